@@ -1,0 +1,169 @@
+/* iron_hip.h -- C ABI of the MI355X (gfx950) Qwen3 int8 decode hot path.
+ *
+ * Every entry point is stream-ordered and asynchronous: it validates its arguments on the host,
+ * launches HIP kernels on `stream` (a hipStream_t passed as void*, NULL = the null stream) and
+ * returns. Device memory is always owned by the caller; the library never allocates. Entry points
+ * that need scratch memory take a caller-provided workspace and export a size query.
+ *
+ * Return value: IRON_OK (0) or a negative iron_status; iron_last_error() then returns a
+ * thread-local message. Validation errors (IRON_ERR_NULL/SHAPE/ALIGN/WORKSPACE/UNSUPPORTED) are
+ * raised before any HIP call is made.
+ *
+ * Data conventions: bf16 tensors are uint16_t bit patterns; int8 weights travel in the reference's
+ * row-block wire (iron/operators/gemv_int8/reference.py:59-80): consecutive blocks of `tile_m`
+ * rows, each = tile_m*K payload bytes then tile_m*(K/G) bf16 scales. `domain` selects the payload
+ * encoding: IRON_DOMAIN_SIGNED (two's-complement q, aie_kernels/aie2p/mv_int8_signed.cc) or
+ * IRON_DOMAIN_BIASED (q+128, aie_kernels/aie2p/mv_int8.cc).
+ */
+#ifndef IRON_HIP_H
+#define IRON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IRON_ABI_VERSION 1
+
+enum iron_status {
+  IRON_OK = 0,
+  IRON_ERR_NULL = -1,        /* a required pointer is NULL */
+  IRON_ERR_SHAPE = -2,       /* a shape / geometry constraint is violated */
+  IRON_ERR_ALIGN = -3,       /* a pointer or wire block is misaligned */
+  IRON_ERR_WORKSPACE = -4,   /* workspace missing or too small */
+  IRON_ERR_HIP = -5,         /* a HIP call or kernel launch failed */
+  IRON_ERR_UNSUPPORTED = -6  /* valid but not implemented for these sizes */
+};
+
+enum iron_domain { IRON_DOMAIN_SIGNED = 0, IRON_DOMAIN_BIASED = 1 };
+enum iron_weight_kind { IRON_WEIGHT_INT8 = 0, IRON_WEIGHT_BF16 = 1 };
+
+/* ABI version of the loaded library (IRON_ABI_VERSION). No reference counterpart. */
+int iron_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). No reference counterpart. */
+const char* iron_last_error(void);
+
+/* Host-only: bytes of an int8 wire of M x K with group G and row-block tile_m.
+ * Replaces the wire sizing in GEMVInt8.get_arg_spec (iron/operators/gemv_int8/op.py:151-171). */
+int iron_wire_bytes(int M, int K, int G, int tile_m, size_t* out_bytes);
+
+/* Bit-exact dequant w[m][k] = bf16(q[m][k] * s[m][k/G]) into a row-major bf16 [M][K].
+ * Replaces the host dequant of SwiGLUMLPDataParallelOurs._dequant_tiles
+ * (iron/operators/swiglu_mlp_dp/op_ours.py:515-541) and _payload_to_q (op_ours.py:31-43). */
+int iron_dequant_w8(const void* wire, uint16_t* w_out, int M, int K, int G, int tile_m,
+                    int domain, void* stream);
+
+/* y[b][m] = bf16(sum_k dequant(W)[m][k] * x[b][k]), fp32 accumulation, B in [1,4].
+ * Replaces GEMVInt8's callable (iron/operators/gemv_int8/op.py:20-178; kernel
+ * aie_kernels/aie2p/mv_int8_signed.cc:60-113). x: [B][K] bf16, y: [B][M] bf16. */
+int iron_gemv_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int M, int K, int G,
+                    int tile_m, int domain, void* stream);
+
+/* y[b][m] = bf16(sum_k W[m][k] * x[b][k]) for bf16 row-major W [M][K], B in [1,4].
+ * Replaces the bf16 GEMV (iron/operators/gemv/op.py) used for a bf16 LM head. */
+int iron_gemv_bf16(const uint16_t* w, const uint16_t* x, uint16_t* y, int B, int M, int K,
+                   void* stream);
+
+/* Weighted RMSNorm y[r][c] = bf16(x[r][c] * rsqrt(mean_c(x^2) + eps) * w[c]).
+ * Replaces RMSNorm (iron/operators/rms_norm/op.py:21-130; kernel rms_norm.cc:83-147). */
+int iron_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols, float eps,
+                 void* stream);
+
+/* LM head: logits[b][v] = bf16(W[v] . xn[b]) with xn = bf16(RMSNorm(x[b]) * norm_w) when
+ * norm_w != NULL (else xn = x), W int8 wire (w_kind IRON_WEIGHT_INT8) or bf16 [V][D]
+ * (IRON_WEIGHT_BF16). When argmax_keys != NULL it must be zeroed before the call; on return
+ * argmax_keys[b] holds (order(bf16 max) << 32) | ~index, the first maximal index on ties.
+ * Replaces the final RMSNorm + GEMVInt8 LM head + host argmax of Qwen3NPU
+ * (iron/applications/qwen3_0.6b/qwen3_npu_int8.py:278-281, 612-621). */
+int iron_lm_head(const void* w, int w_kind, const uint16_t* x, const uint16_t* norm_w, float eps,
+                 uint16_t* logits, unsigned long long* argmax_keys, int B, int V, int D, int G,
+                 int tile_m, int domain, void* stream);
+
+/* Decode the token id from an argmax key written by iron_lm_head, on the device:
+ * tokens[b] = index of keys[b]; then keys[b] = 0 (ready for the next iron_lm_head).
+ * If `emb` != NULL also gathers x[b][:] = emb[tokens[b]][:] (bf16 [vocab][D]) and, when
+ * `token_log` != NULL, appends tokens[b] to token_log[b * log_stride + *step] and increments
+ * *step (device int32). Replaces the host argmax + embedding lookup of the reference decode
+ * loop (qwen3_npu_int8.py:612-621; check_cosine_int8.py:41-52). */
+int iron_next_token(unsigned long long* keys, int32_t* tokens, const uint16_t* emb, uint16_t* x,
+                    int32_t* token_log, int log_stride, int32_t* step, int B, int D, int vocab,
+                    void* stream);
+
+/* Embedding gather x[b][:] = emb[tokens[b]][:] (tokens device int32 [B]). */
+int iron_embed(const int32_t* tokens, const uint16_t* emb, uint16_t* x, int B, int D, int vocab,
+               void* stream);
+
+/* Device-side decode position advance: pos[b] += delta and ctx[b] = pos[b] + 1 (either pointer
+ * may be NULL). Replaces the host writes of k_cache_offset / S_kv_eff before each dispatch
+ * (qwen3_npu_int8.py:606-610), so a captured per-token HIP graph replays without host work. */
+int iron_advance_positions(int32_t* pos, int32_t* ctx, int B, int delta, void* stream);
+
+/* Workspace bytes for iron_qkv_head (raw QKV staging). */
+size_t iron_qkv_head_workspace(int B, int Hq, int Hkv, int HD);
+
+/* Fused decode QKV head, per batch row b:
+ *   hn  = bf16(RMSNorm(cur[b]) * n_in)                                (rms_norm.cc:83-147)
+ *   raw = bf16(Wqkv . hn)          Wqkv rows = [Hq*HD | Hkv*HD | Hkv*HD] int8 wire, K = D
+ *   q   = bf16(RoPE(bf16(RMSNorm_head(raw_q) * n_qn), ang))  -> q_out[b][Hq*HD]
+ *   k   = bf16(RoPE(bf16(RMSNorm_head(raw_k) * n_kn), ang))  -> k cache at position pos[b]
+ *   v   = raw_v                                              -> v cache at position pos[b]
+ * ang: interleaved [cos_i, sin_i] bf16 rows of HD elements; row b is at ang + b*HD, or at
+ * ang + pos[b]*HD when ang_by_pos != 0 (a whole angle table). KV cache addressing (elements):
+ * k_cache + b*kv_sb + h*kv_sh + pos*kv_st (same for v_cache), so both the separate [B,Hkv,S,HD]
+ * layout and the reference's token-interleaved [Hkv][S][K_t|V_t] layout are expressible.
+ * Replaces QKVHeadDataParallelOurs (iron/operators/qkv_head_dp/op_ours.py:31-262, op.py:20-231;
+ * golden qkv_head_dp/reference.py:13-33). */
+int iron_qkv_head(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
+                  const uint16_t* n_qn, const uint16_t* n_kn, const uint16_t* ang, int ang_by_pos,
+                  uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, long long kv_sb,
+                  long long kv_sh, long long kv_st, const int32_t* pos, int B, int D, int HD,
+                  int Hq, int Hkv, int max_seq, int G, int tile_m, int domain, float eps,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes for iron_decode_attn (split-K partials + merge counters). The counters must be
+ * zero before the first call (a zero-filled workspace); the kernel leaves them zero again. */
+size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx);
+
+/* GQA decode attention, one query token per sequence:
+ *   o[b][h] = softmax_j(q[b][h] . K[b][h*KV/H][j] * scale) . V[b][h*KV/H][j],  j < ctx_len[b]
+ * fp32 scores/softmax/accumulation (exp2 form, decode_attn.cc:117-311), bf16 output; a sequence
+ * with ctx_len 0 yields zeros (decode_attn.cc:300-311). q/o: [B][H][D] bf16; K/V addressed as in
+ * iron_qkv_head. ctx_len: device int32 [B] (or NULL: every sequence uses ctx_const).
+ * Replaces DecodeAttention (iron/operators/decode_attn/op.py:20-181; golden
+ * decode_attn/reference.py:26-38). */
+int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                     long long kv_sb, long long kv_sh, long long kv_st, const int32_t* ctx_len,
+                     int ctx_const, uint16_t* out, int B, int H, int KV, int D, int max_ctx,
+                     float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes for iron_swiglu_mlp (x1 residual halves + gh, fp32). */
+size_t iron_swiglu_mlp_workspace(int B, int D, int FF);
+
+/* Fused decode SwiGLU MLP block, per batch row b:
+ *   a   = bf16(Wo . cx[b])   when wo != NULL (fuse_o; cx [B][QD]), else a = a_in[b] ([B][D])
+ *   x1  = cur[b] + a                                      (fp32)
+ *   hf  = RMSNorm(x1) * n_pf                              (fp32)
+ *   gh  = silu(Wg . hf) * (Wu . hf)                       (fp32)
+ *   nxt = bf16(x1 + Wd . gh)
+ * Wo: [D][QD] wire (tile_m_o rows), Wg/Wu: [FF][D] wires (tile_m_gu), Wd: [D][FF] (tile_m_d).
+ * a_out (optional, [B][D] bf16) receives a. Replaces SwiGLUMLPDataParallelOurs
+ * (iron/operators/swiglu_mlp_dp/op_ours.py:46-582, op.py:22-227; golden
+ * swiglu_mlp_dp/reference.py:8-67). */
+int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t* n_pf,
+                    const void* wo, const void* wg, const void* wu, const void* wd,
+                    uint16_t* nxt, uint16_t* a_out, int B, int D, int FF, int QD, int G,
+                    int tile_m_o, int tile_m_gu, int tile_m_d, int domain, float eps,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Host-only check of the device-side divide used for wire row-blocks: returns n / d computed with
+ * the same multiply-shift sequence the kernels use (test hook; no reference counterpart). */
+uint32_t iron_test_fastdiv(uint32_t n, uint32_t d);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IRON_HIP_H */

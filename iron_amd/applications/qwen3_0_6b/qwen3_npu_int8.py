@@ -1,0 +1,290 @@
+"""Qwen3 int8 (W8A16, in-kernel dequant) decode on one MI355X -- the reference's ``Qwen3NPU``.
+
+Drop-in for iron/applications/qwen3_0.6b/qwen3_npu_int8.py:129-621: the same operator set and
+runlist -- per layer the fused QKV head (RMSNorm + QKV GEMV + QK-norm + RoPE + KV append), decode
+attention, and the fused MLP with the output projection folded in (fuse_o); then the final
+RMSNorm and the LM head -- run as one ``OperatorSequence`` whose callable replays a HIP graph
+(one dispatch per token, as the reference's single full-ELF dispatch). ``model(x, seq_pos)``
+keeps the reference call: bf16 hidden state in, argmax token out.
+
+Differences from the reference, all deliberate:
+  * the constructor takes a checkpoint path (GPTQ safetensors), explicit weights, or a config +
+    seed for random-init weights (no checkpoint is available offline);
+  * the KV caches are separate contiguous ``[B, Hkv, max_seq, HD]`` K and V (BASELINE's layout;
+    ``kv_layout="interleaved"`` gives the reference's merged cache);
+  * the LM head carries an argmax epilogue, so the token is chosen on the device (the reference
+    copies the logits out and runs numpy argmax, qwen3_npu_int8.py:612-621);
+  * ``generate()`` runs greedy decoding entirely on the device: each step replays one graph that
+    consumes the previous argmax, gathers its embedding, runs the layers and advances the
+    positions, with no host synchronisation between tokens.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from ... import _lib
+from ...common.context import AIEContext
+from ...common.sequence import OperatorSequence
+from ...operators import (GEMV, DecodeAttention, GEMVInt8, QKVHeadDataParallelOurs, RMSNorm,
+                          SwiGLUMLPDataParallelOurs)
+from ...operators.wire import pack_wire
+from .weights import Qwen3Config, load_gptq_checkpoint, random_qwen3_weights
+
+SIGNED_GEMV_KERNEL = "mv_int8_signed.cc"
+QKV_TSI = 4
+LMHEAD_TSI = 4
+
+
+def rope_angle_table(max_pos: int, head_dim: int, theta: float) -> torch.Tensor:
+    """(max_pos, head_dim) bf16 rows [cos_0, sin_0, cos_1, sin_1, ...] (qwen3_npu_int8.py:580-591)."""
+    half = head_dim // 2
+    inv_freq = 1.0 / (theta ** (torch.arange(0, half, dtype=torch.float32) / half))
+    freqs = torch.outer(torch.arange(max_pos, dtype=torch.float32), inv_freq)
+    emb = torch.cat([freqs, freqs], dim=-1)
+    cos = emb.cos().to(torch.bfloat16)[:, :half]
+    sin = emb.sin().to(torch.bfloat16)[:, :half]
+    return torch.stack([cos, sin], dim=-1).reshape(max_pos, head_dim)
+
+
+def _decode_key(key: int) -> int:
+    return (~key) & 0xFFFFFFFF
+
+
+def _encode_token(tok: int) -> int:
+    return (1 << 32) | ((~int(tok)) & 0xFFFFFFFF)
+
+
+class Qwen3NPU:
+    def __init__(self, weights_path=None, *, config: Qwen3Config | None = None,
+                 weights: dict | None = None, seed: int = 0, max_seq_len: int = 512,
+                 kv_layout: str = "separate", lm_head: str | None = None,
+                 dispatch: str = "auto", context: AIEContext | None = None):
+        self.cfg = cfg = config or Qwen3Config.qwen3_0_6b()
+        self.max_seq_len = max_seq_len
+        self.kv_layout = kv_layout
+        self.context = context or AIEContext()
+        self.device = self.context.device
+        if weights is None:
+            if weights_path is not None:
+                weights = load_gptq_checkpoint(weights_path, cfg, lm_head or "bf16")
+            else:
+                weights = random_qwen3_weights(cfg, seed, lm_head=lm_head or "bf16")
+        self.lm_head_kind = "int8" if isinstance(weights["lm_head"], tuple) else "bf16"
+        self._build_operators()
+        self._build_sequence(dispatch)
+        self._load_weights(weights)
+        self._gen_graph = None
+
+    # ---------------- operators ----------------
+    def _build_operators(self):
+        cfg, c, S = self.cfg, self.context, self.max_seq_len
+        self.rms = RMSNorm(size=cfg.emb_dim, num_aie_columns=1, num_channels=1,
+                           tile_size=cfg.emb_dim, weighted=True, epsilon=cfg.eps, context=c)
+        self.decode_attn = DecodeAttention(
+            num_heads=cfg.n_heads, num_kv_heads=cfg.n_kv_heads, head_dim=cfg.head_dim,
+            seq_len_kv=S, use_runtime_seq_len=True,
+            kv_layout="separate" if self.kv_layout == "separate" else "combined",
+            kv_token_interleaved=True, context=c)
+        self.mlp_xdna = SwiGLUMLPDataParallelOurs(
+            D=cfg.emb_dim, FF=cfg.hidden_dim, group_size=cfg.group_size, epsilon=cfg.eps,
+            fuse_o=True, QD=cfg.q_dim, kernel_source=SIGNED_GEMV_KERNEL, context=c)
+        self.qkv_dp = QKVHeadDataParallelOurs(
+            D=cfg.emb_dim, HD=cfg.head_dim, Hq=cfg.n_heads, Hkv=cfg.n_kv_heads, max_seq=S,
+            num_aie_columns=1, tile_size_input=QKV_TSI, epsilon=cfg.eps,
+            group_size=cfg.group_size, kv_layout=self.kv_layout, angles_from_table=True,
+            kernel_source=SIGNED_GEMV_KERNEL, kv_offset_parameter="k_cache_offset", context=c)
+        if self.lm_head_kind == "bf16":
+            self.lmhead = GEMV(M=cfg.vocab_size, K=cfg.emb_dim, epilogue="argmax", context=c)
+        else:
+            self.lmhead = GEMVInt8(M=cfg.vocab_size, K=cfg.emb_dim, tile_size_input=LMHEAD_TSI,
+                                   group_size=cfg.group_size, kernel_vector_size=16,
+                                   kernel_source=SIGNED_GEMV_KERNEL, epilogue="argmax",
+                                   context=c)
+
+    # ---------------- sequence ----------------
+    def _build_sequence(self, dispatch):
+        cfg = self.cfg
+        runlist = []
+        for i in range(cfg.n_layers):
+            caches = ([f"k_cache_{i}", f"v_cache_{i}"] if self.kv_layout == "separate"
+                      else [f"kv_cache_{i}"])
+            runlist.append((self.qkv_dp, "x", f"W_norm1_{i}", f"W_qkv_{i}", f"W_qn_{i}",
+                            f"W_kn_{i}", "rope_table", "rope_q", *caches))
+            runlist.append((self.decode_attn, "rope_q", *caches, "context"))
+            runlist.append((self.mlp_xdna, "x", "context", f"W_norm2_{i}", f"Wo_{i}", f"Wg_{i}",
+                            f"Wu_{i}", f"Wd_{i}", "gh_scratch", "a_scratch", "x"))
+        runlist += [
+            (self.rms, "x", "W_final_norm", "x_final"),
+            (self.lmhead, "W_out_head", "x_final", "logits", "argmax_key"),
+        ]
+        indep = ["W_out_head"] + [n for entry in runlist for n in entry[1:]
+                                  if n.startswith(("W_qkv_", "Wo_", "Wg_", "Wu_", "Wd_",
+                                                   "k_cache_", "v_cache_", "kv_cache_"))]
+        indep = list(dict.fromkeys(indep))
+        self.seq = OperatorSequence("qwen3_decode", runlist, input_args=["x"],
+                                    output_args=["logits", "argmax_key"],
+                                    independent_buffer_args=indep, dispatch=dispatch,
+                                    context=self.context)
+        self.seq.compile()
+        self.fc = self.seq.get_callable()
+
+    # ---------------- weights ----------------
+    def _set(self, name, t):
+        b = self.fc.get_buffer(name).torch_view(t.dtype if t.dtype != torch.uint8 else torch.uint8)
+        flat = t.reshape(-1)
+        b[: flat.numel()].copy_(flat.to(self.device))
+
+    def _set_wire(self, name, qs, tile_m):
+        w = pack_wire(qs[0], qs[1], tile_m, "signed")
+        self._set(name, w)
+
+    def _load_weights(self, w: dict):
+        cfg = self.cfg
+        mlp = self.mlp_xdna
+        for i, L in enumerate(w["layers"]):
+            self._set(f"W_norm1_{i}", L["input_norm"])
+            self._set_wire(f"W_qkv_{i}", L["qkv"], QKV_TSI)
+            self._set(f"W_qn_{i}", L["q_norm"])
+            self._set(f"W_kn_{i}", L["k_norm"])
+            self._set(f"W_norm2_{i}", L["post_norm"])
+            self._set_wire(f"Wo_{i}", L["o"], mlp.tile_rows_o)
+            self._set_wire(f"Wg_{i}", L["gate"], mlp.tile_rows_gu)
+            self._set_wire(f"Wu_{i}", L["up"], mlp.tile_rows_gu)
+            self._set_wire(f"Wd_{i}", L["down"], mlp.tile_rows_d)
+        self._set("W_final_norm", w["final_norm"])
+        if self.lm_head_kind == "bf16":
+            self._set("W_out_head", w["lm_head"])
+            self.embed = self.fc.get_buffer("W_out_head").torch_view(torch.bfloat16)[
+                : cfg.vocab_size * cfg.emb_dim]
+            if w["embed"] is not w["lm_head"]:
+                self.embed = w["embed"].to(self.device).reshape(-1)
+        else:
+            self._set_wire("W_out_head", w["lm_head"], LMHEAD_TSI)
+            self.embed = w["embed"].to(self.device).reshape(-1)
+        self._set("rope_table", rope_angle_table(self.max_seq_len, cfg.head_dim, cfg.rope_theta))
+        torch.cuda.synchronize(self.device)
+
+    # ---------------- state helpers ----------------
+    def kv_caches(self, layer: int):
+        """(K, V) device views of one layer's cache, each (Hkv, max_seq, HD)."""
+        cfg, S = self.cfg, self.max_seq_len
+        if self.kv_layout == "separate":
+            k = self.fc.get_buffer(f"k_cache_{layer}").torch_view(torch.bfloat16)
+            v = self.fc.get_buffer(f"v_cache_{layer}").torch_view(torch.bfloat16)
+            shape = (cfg.n_kv_heads, S, cfg.head_dim)
+            return k[: np.prod(shape)].reshape(shape), v[: np.prod(shape)].reshape(shape)
+        kv = self.fc.get_buffer(f"kv_cache_{layer}").torch_view(torch.bfloat16)
+        t = kv[: cfg.n_kv_heads * S * 2 * cfg.head_dim].reshape(cfg.n_kv_heads, S, 2, cfg.head_dim)
+        return t[:, :, 0], t[:, :, 1]
+
+    def load_kv(self, k: torch.Tensor, v: torch.Tensor):
+        """Write (n_layers, Hkv, P, HD) K/V into positions [0, P) of every layer's cache."""
+        P = k.shape[2]
+        for i in range(self.cfg.n_layers):
+            kc, vc = self.kv_caches(i)
+            kc[:, :P].copy_(k[i].to(self.device))
+            vc[:, :P].copy_(v[i].to(self.device))
+        torch.cuda.synchronize(self.device)
+
+    def _per_token_offset(self) -> int:
+        return self.cfg.head_dim * (1 if self.kv_layout == "separate" else 2)
+
+    def _set_position(self, seq_pos: int):
+        self.fc.params.write("k_cache_offset", seq_pos * self._per_token_offset())
+        self.fc.params.write("S_kv_eff", seq_pos + 1)
+        self.fc.params.sync()
+
+    def logits(self) -> torch.Tensor:
+        return self.fc.get_buffer("logits").torch_view(torch.bfloat16)[: self.cfg.vocab_size].cpu()
+
+    # ---------------- forward (single token) ----------------
+    def __call__(self, x, seq_pos: int) -> int:
+        """x: (emb_dim,) bf16 hidden state of the new token; returns the argmax token id."""
+        if seq_pos >= self.max_seq_len:
+            raise ValueError(f"seq_pos {seq_pos} >= max_seq_len {self.max_seq_len}")
+        self.fc.get_buffer("x").torch_view(torch.bfloat16)[: self.cfg.emb_dim].copy_(
+            torch.as_tensor(x).reshape(-1).to(self.device, torch.bfloat16))
+        self.fc.get_buffer("argmax_key").torch_view(torch.int64).zero_()
+        self._set_position(seq_pos)
+        self.fc()
+        key = int(self.fc.get_buffer("argmax_key").torch_view(torch.int64)[0].item())
+        return _decode_key(key)
+
+    def step_token(self, token: int, seq_pos: int) -> int:
+        """Embedding lookup + one decode step."""
+        D = self.cfg.emb_dim
+        return self(self.embed[int(token) * D:(int(token) + 1) * D], seq_pos)
+
+    # ---------------- device-resident greedy decoding ----------------
+    def _gen_state(self):
+        if getattr(self, "_gs", None) is None:
+            dev = self.device
+            self._gs = {"tokens": torch.zeros(1, dtype=torch.int32, device=dev),
+                        "step": torch.zeros(1, dtype=torch.int32, device=dev),
+                        "log": torch.zeros(self.max_seq_len + 1, dtype=torch.int32, device=dev)}
+        return self._gs
+
+    def _gen_step_launches(self):
+        cfg, gs = self.cfg, self._gen_state()
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        keys = self.fc.get_buffer("argmax_key").torch_view(torch.int64)
+        x = self.fc.get_buffer("x").torch_view(torch.bfloat16)
+        _lib.call("iron_next_token", keys.data_ptr(), gs["tokens"].data_ptr(),
+                  self.embed.data_ptr(), x.data_ptr(), gs["log"].data_ptr(), 0,
+                  gs["step"].data_ptr(), 1, cfg.emb_dim, cfg.vocab_size, stream)
+        self.fc.run_steps()
+        _lib.call("iron_advance_positions", self.fc.params.tensor("k_cache_offset").data_ptr(),
+                  self.fc.params.tensor("S_kv_eff").data_ptr(), 1, 1, stream)
+
+    def _capture_gen_graph(self):
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream(self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.graph(g, stream=s):
+            self._gen_step_launches()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        self._gen_graph = g
+
+    def start_generation(self, first_token: int, start_pos: int):
+        """Arm the device loop: the next step consumes ``first_token`` at ``start_pos``."""
+        if self._gen_graph is None:
+            self._capture_gen_graph()
+        gs = self._gen_state()
+        gs["step"].zero_()
+        self._set_position(start_pos)
+        self.fc.get_buffer("argmax_key").torch_view(torch.int64)[:1].fill_(
+            _encode_token(first_token))
+        torch.cuda.synchronize(self.device)
+
+    def decode_steps(self, n: int):
+        """Replay the per-token graph n times (no host synchronisation)."""
+        for _ in range(n):
+            self._gen_graph.replay()
+
+    def finish_generation(self) -> list[int]:
+        """Tokens produced since start_generation (the last one decoded from the final key)."""
+        cfg, gs = self.cfg, self._gen_state()
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        keys = self.fc.get_buffer("argmax_key").torch_view(torch.int64)
+        _lib.call("iron_next_token", keys.data_ptr(), gs["tokens"].data_ptr(), None, None,
+                  gs["log"].data_ptr(), 0, gs["step"].data_ptr(), 1, cfg.emb_dim,
+                  cfg.vocab_size, stream)
+        torch.cuda.synchronize(self.device)
+        n = int(gs["step"].item())
+        # log[0] is the armed first token; log[1..n-1] are the generated ones
+        return gs["log"][1:n].cpu().tolist()
+
+    def generate(self, prompt_ids, n_new: int, start_pos: int = 0) -> list[int]:
+        """Greedy decode: prefill ``prompt_ids`` token by token from ``start_pos``, then produce
+        ``n_new`` tokens on the device. Returns the generated token ids."""
+        prompt_ids = list(prompt_ids)
+        pos = start_pos
+        for tok in prompt_ids[:-1]:
+            self.step_token(tok, pos)
+            pos += 1
+        self.start_generation(prompt_ids[-1], pos)
+        self.decode_steps(n_new)
+        return self.finish_generation()

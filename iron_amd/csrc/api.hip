@@ -1,0 +1,161 @@
+// Library plumbing (error state, version, test hooks) and the small kernels around the decode
+// loop: standalone weighted RMSNorm, embedding gather and the on-device next-token step.
+//
+// Reference: RMSNorm (iron/operators/rms_norm/op.py:21-130, kernel rms_norm.cc:83-147, golden
+// rms_norm/reference.py:8-17); the host argmax + embedding lookup of the decode loop
+// (iron/applications/qwen3_0.6b/qwen3_npu_int8.py:612-621, check_cosine_int8.py:41-52).
+#include <string.h>
+#include "common.h"
+#include "internal.h"
+
+namespace iron {
+
+static thread_local char g_err[512] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+}  // namespace iron
+
+namespace {
+
+// One 256-thread workgroup per row: y = bf16(x * rsqrt(mean(x^2) + eps) * w).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ w,
+                                                      uint16_t* __restrict__ y, int cols,
+                                                      float eps) {
+  __shared__ float red[4];
+  const uint16_t* xr = x + (size_t)blockIdx.x * cols;
+  uint16_t* yr = y + (size_t)blockIdx.x * cols;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < cols; i += 256) {
+    const float v = bf16_to_f32(xr[i]);
+    ss = fmaf(v, v, ss);
+  }
+  ss = block_sum_256(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+  for (int i = threadIdx.x; i < cols; i += 256)
+    yr[i] = f32_to_bf16(bf16_to_f32(xr[i]) * inv * (w ? bf16_to_f32(w[i]) : 1.0f));
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tokens,
+                                                    const uint16_t* __restrict__ emb,
+                                                    uint16_t* __restrict__ x, int D, int vocab) {
+  const int b = blockIdx.x;
+  int t = tokens[b];
+  t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+  for (int i = threadIdx.x; i < D; i += 256) x[(size_t)b * D + i] = emb[(size_t)t * D + i];
+}
+
+// Single workgroup: decode every argmax key, reset it, gather the embeddings, log the tokens.
+__global__ __launch_bounds__(256) void next_token_kernel(unsigned long long* keys,
+                                                         int32_t* tokens,
+                                                         const uint16_t* __restrict__ emb,
+                                                         uint16_t* __restrict__ x,
+                                                         int32_t* token_log, int log_stride,
+                                                         int32_t* step, int B, int D, int vocab) {
+  __shared__ int32_t s_tok[64];
+  __shared__ int32_t s_step;
+  if (threadIdx.x < B) {
+    const unsigned long long k = keys[threadIdx.x];
+    int32_t t = k ? (int32_t)(~(uint32_t)(k & 0xffffffffull)) : 0;
+    t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+    s_tok[threadIdx.x] = t;
+    tokens[threadIdx.x] = t;
+  }
+  if (threadIdx.x == 0) s_step = step ? *step : 0;
+  __syncthreads();
+  if (threadIdx.x < B) {
+    keys[threadIdx.x] = 0ull;
+    if (token_log) token_log[(size_t)threadIdx.x * log_stride + s_step] = s_tok[threadIdx.x];
+  }
+  if (threadIdx.x == 0 && step) *step = s_step + 1;
+  if (emb) {
+    for (int b = 0; b < B; ++b) {
+      const uint16_t* src = emb + (size_t)s_tok[b] * D;
+      for (int i = threadIdx.x; i < D; i += 256) x[(size_t)b * D + i] = src[i];
+    }
+  }
+}
+
+__global__ void advance_kernel(int32_t* pos, int32_t* ctx, int B, int delta) {
+  const int b = threadIdx.x;
+  if (b >= B) return;
+  int p = 0;
+  if (pos) {
+    p = pos[b] + delta;
+    pos[b] = p;
+  } else if (ctx) {
+    p = ctx[b] - 1 + delta;
+  }
+  if (ctx) ctx[b] = p + 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int iron_abi_version(void) { return IRON_ABI_VERSION; }
+
+int iron_advance_positions(int32_t* pos, int32_t* ctx, int B, int delta, void* stream) {
+  iron::clear_error();
+  if (!pos && !ctx) return iron::fail(IRON_ERR_NULL, "iron_advance_positions: no buffers");
+  if (B <= 0 || B > 1024)
+    return iron::fail(IRON_ERR_SHAPE, "iron_advance_positions: B=%d must be in [1,1024]", B);
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, pos, ctx, B,
+                     delta);
+  return iron::check_launch("iron_advance_positions");
+}
+
+const char* iron_last_error(void) { return iron::g_err; }
+
+uint32_t iron_test_fastdiv(uint32_t n, uint32_t d) {
+  if (d == 0) return 0xffffffffu;
+  return fastdiv_host(n, make_fastdiv(d));
+}
+
+int iron_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols, float eps,
+                 void* stream) {
+  iron::clear_error();
+  if (!x || !y) return iron::fail(IRON_ERR_NULL, "iron_rmsnorm: null tensor");
+  if (rows <= 0 || cols <= 0)
+    return iron::fail(IRON_ERR_SHAPE, "iron_rmsnorm: bad shape rows=%d cols=%d", rows, cols);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, x, w, y, cols,
+                     eps);
+  return iron::check_launch("iron_rmsnorm");
+}
+
+int iron_embed(const int32_t* tokens, const uint16_t* emb, uint16_t* x, int B, int D, int vocab,
+               void* stream) {
+  iron::clear_error();
+  if (!tokens || !emb || !x) return iron::fail(IRON_ERR_NULL, "iron_embed: null tensor");
+  if (B <= 0 || D <= 0 || vocab <= 0)
+    return iron::fail(IRON_ERR_SHAPE, "iron_embed: bad shape B=%d D=%d vocab=%d", B, D, vocab);
+  hipLaunchKernelGGL(embed_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, tokens, emb, x, D,
+                     vocab);
+  return iron::check_launch("iron_embed");
+}
+
+int iron_next_token(unsigned long long* keys, int32_t* tokens, const uint16_t* emb, uint16_t* x,
+                    int32_t* token_log, int log_stride, int32_t* step, int B, int D, int vocab,
+                    void* stream) {
+  iron::clear_error();
+  if (!keys || !tokens) return iron::fail(IRON_ERR_NULL, "iron_next_token: null keys/tokens");
+  if (B <= 0 || B > 64 || vocab <= 0)
+    return iron::fail(IRON_ERR_SHAPE, "iron_next_token: B=%d must be in [1,64]", B);
+  if (emb && (!x || D <= 0))
+    return iron::fail(IRON_ERR_NULL, "iron_next_token: embedding gather needs x and D > 0");
+  if (token_log && !step)
+    return iron::fail(IRON_ERR_NULL, "iron_next_token: token_log needs a step counter");
+  hipLaunchKernelGGL(next_token_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, keys, tokens,
+                     emb, x, token_log, log_stride, step, B, D, vocab);
+  return iron::check_launch("iron_next_token");
+}
+
+}  // extern "C"

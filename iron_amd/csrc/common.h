@@ -1,0 +1,136 @@
+// Shared device helpers for the gfx950 (MI355X) kernels of the Qwen3 int8 decode path.
+//
+// Conventions used by every kernel in this directory:
+//   * bf16 values travel as uint16_t bit patterns; all arithmetic is fp32.
+//   * fp32 -> bf16 is round-to-nearest-even, the rounding the reference applies at every
+//     operator boundary (iron/common/sequence.py:997-999) and inside its kernels
+//     (aie_kernels/aie2p/mv_int8_signed.cc:66 sets conv_even).
+//   * A wavefront is 64 lanes; reductions use DPP row/bcast controls, not LDS.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#define IRON_DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------------------------------------
+// bf16 <-> fp32
+// ---------------------------------------------------------------------------------------------
+IRON_DEV float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+IRON_DEV float bf16lo_to_f32(uint32_t packed) { return __uint_as_float(packed << 16); }
+IRON_DEV float bf16hi_to_f32(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
+
+IRON_DEV uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+IRON_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ---------------------------------------------------------------------------------------------
+// Wavefront reductions (wave64) with DPP.
+// ---------------------------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+IRON_DEV float dpp_f(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+}
+
+// Sum over each 16-lane row; every lane of the row receives the row's sum.
+IRON_DEV float row16_sum(float v) {
+  v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
+  return v;
+}
+
+// Sum over the full wavefront; every lane receives the total.
+IRON_DEV float wave_sum(float v) {
+  v = row16_sum(v);
+  v += dpp_f<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_f<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+IRON_DEV float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xb1>(v));
+  v = fmaxf(v, dpp_f<0x4e>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+
+IRON_DEV float wave_max(float v) {
+  // Masked rows of the bcast steps read `old` = 0, which would clamp negative maxima, so the
+  // cross-row steps use xor-shuffles instead.
+  v = row16_max(v);
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+// Block-wide sum for blockDim.x == 256 (4 waves). `scratch` holds >= 4 floats of LDS.
+IRON_DEV float block_sum_256(float v, float* scratch) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+  __syncthreads();
+  float t = scratch[0] + scratch[1] + scratch[2] + scratch[3];
+  return t;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Division by a runtime constant (rows -> wire blocks), valid for 0 <= n < 2^31.
+//   l = ceil(log2 d), m = floor(2^32 * (2^l - d) / d) + 1, q = (umulhi(m, n) + n) >> l
+// ---------------------------------------------------------------------------------------------
+struct FastDiv {
+  uint32_t m;
+  uint32_t l;
+  uint32_t d;
+};
+
+static inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  f.l = l;
+  f.m = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1ull);
+  f.d = d;
+  return f;
+}
+
+IRON_DEV uint32_t fastdiv(uint32_t n, FastDiv f) {
+  uint32_t t = __umulhi(f.m, n);
+  return (t + n) >> f.l;
+}
+
+static inline uint32_t fastdiv_host(uint32_t n, FastDiv f) {
+  uint32_t t = (uint32_t)(((uint64_t)f.m * n) >> 32);
+  return (t + n) >> f.l;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Cross-workgroup hand-off: the "last workgroup to finish does the merge" pattern. Writers make
+// their results visible device-wide (agent-scope release), then count in; the workgroup that
+// completes the count acquires and merges, then resets the counter so the next launch (or graph
+// replay) starts from zero without a memset.
+// ---------------------------------------------------------------------------------------------
+IRON_DEV bool arrive_is_last(unsigned int* counter, unsigned int expected) {
+  __shared__ unsigned int s_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    unsigned int prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == expected - 1u) ? 1u : 0u;
+    if (s_last) {
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+  }
+  __syncthreads();
+  return s_last != 0u;
+}

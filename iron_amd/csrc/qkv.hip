@@ -1,0 +1,135 @@
+// Fused decode QKV head: RMSNorm prologue + concatenated int8 QKV GEMV, then a per-head
+// epilogue (QK RMSNorm, two-halves RoPE, KV-cache append).
+//
+// Reference: QKVHeadDataParallelOurs (iron/operators/qkv_head_dp/op_ours.py:31-262, op.py:20-231,
+// design_ours_kvlayout.py:399-447 core, :640-692 KV drains); golden
+// iron/operators/qkv_head_dp/reference.py:13-33, composed of rms_norm/reference.py:8-17 and
+// rope/reference.py:118-154 (method_type 0, TWO_HALVES, interleaved [cos, sin] angle row).
+// Kernel numerics followed: rms_norm.cc:83-147 (fp32, one bf16 rounding), generic/rope.cc:42-83.
+#include "common.h"
+#include "internal.h"
+
+namespace iron {
+int gemv_rms_internal(const void* wire, const uint16_t* x, const uint16_t* nw, uint16_t* y,
+                      int B, int M, int K, int G, int tile_m, int domain, float eps,
+                      hipStream_t stream, const char* fn);
+}
+
+namespace {
+
+constexpr int kHD = 128;
+
+struct QkvEpiParams {
+  const uint16_t* raw;   // [B][(Hq + 2 Hkv) * HD] bf16
+  const uint16_t* n_qn;
+  const uint16_t* n_kn;
+  const uint16_t* ang;
+  int ang_by_pos;
+  uint16_t* q_out;       // [B][Hq*HD]
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  long long sb, sh, st;
+  const int32_t* pos;    // [B]
+  int Hq, Hkv, max_seq;
+  float eps;
+};
+
+// grid (Hq + 2*Hkv, B), 128 threads: one thread per head dimension.
+__global__ __launch_bounds__(128) void qkv_epilogue_kernel(QkvEpiParams p) {
+  const int head = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int nheads = p.Hq + 2 * p.Hkv;
+  const uint16_t hraw = p.raw[((size_t)b * nheads + head) * kHD + d];
+  const int pos = p.pos ? p.pos[b] : 0;
+  const bool pos_ok = pos >= 0 && pos < p.max_seq;
+  if (head >= p.Hq + p.Hkv) {  // v head: copy the raw bf16 value into the cache
+    const int hv = head - p.Hq - p.Hkv;
+    if (pos_ok) p.v_cache[(size_t)b * p.sb + (size_t)hv * p.sh + (size_t)pos * p.st + d] = hraw;
+    return;
+  }
+  __shared__ float s_red[2];
+  __shared__ float s_y[kHD];
+  const float x = bf16_to_f32(hraw);
+  float ss = wave_sum(x * x);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  ss = s_red[0] + s_red[1];
+  const float inv = 1.0f / sqrtf(ss / (float)kHD + p.eps);
+  const uint16_t* nw = head < p.Hq ? p.n_qn : p.n_kn;
+  const float y = round_bf16(x * inv * bf16_to_f32(nw[d]));
+  s_y[d] = y;
+  __syncthreads();
+  const int i = d & (kHD / 2 - 1);
+  const uint16_t* arow = p.ang + (size_t)(p.ang_by_pos ? (pos_ok ? pos : 0) : b) * kHD;
+  const float c = bf16_to_f32(arow[2 * i]);
+  const float s = bf16_to_f32(arow[2 * i + 1]);
+  float r;
+  if (d < kHD / 2) {
+    r = y * c - s_y[d + kHD / 2] * s;   // y1*cos - y2*sin
+  } else {
+    r = y * c + s_y[d - kHD / 2] * s;   // y2*cos + y1*sin
+  }
+  const uint16_t hr = f32_to_bf16(r);
+  if (head < p.Hq) {
+    p.q_out[((size_t)b * p.Hq + head) * kHD + d] = hr;
+  } else if (pos_ok) {
+    const int hk = head - p.Hq;
+    p.k_cache[(size_t)b * p.sb + (size_t)hk * p.sh + (size_t)pos * p.st + d] = hr;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t iron_qkv_head_workspace(int B, int Hq, int Hkv, int HD) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || HD <= 0) return 0;
+  return ((size_t)B * (Hq + 2 * Hkv) * HD * 2 + 255) & ~(size_t)255;
+}
+
+int iron_qkv_head(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
+                  const uint16_t* n_qn, const uint16_t* n_kn, const uint16_t* ang, int ang_by_pos,
+                  uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, long long kv_sb,
+                  long long kv_sh, long long kv_st, const int32_t* pos, int B, int D, int HD,
+                  int Hq, int Hkv, int max_seq, int G, int tile_m, int domain, float eps,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  iron::clear_error();
+  const char* fn = "iron_qkv_head";
+  if (!cur || !n_in || !n_qn || !n_kn || !ang || !q_out || !k_cache || !v_cache || !pos)
+    return iron::fail(IRON_ERR_NULL, "%s: null tensor", fn);
+  if (HD != kHD) return iron::fail(IRON_ERR_UNSUPPORTED, "%s: head_dim %d (only 128)", fn, HD);
+  if (B <= 0 || D <= 0 || Hq <= 0 || Hkv <= 0 || max_seq <= 0 || D % 16)
+    return iron::fail(IRON_ERR_SHAPE, "%s: bad shape B=%d D=%d Hq=%d Hkv=%d S=%d", fn, B, D, Hq,
+                      Hkv, max_seq);
+  const int M = (Hq + 2 * Hkv) * HD;
+  int st = iron::check_wire(fn, wqkv, M, D, G, tile_m, domain);
+  if (st) return st;
+  const size_t need = iron_qkv_head_workspace(B, Hq, Hkv, HD);
+  if (!workspace || workspace_bytes < need)
+    return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes,
+                      need);
+  hipStream_t s = (hipStream_t)stream;
+  uint16_t* raw = (uint16_t*)workspace;
+  st = iron::gemv_rms_internal(wqkv, cur, n_in, raw, B, M, D, G, tile_m, domain, eps, s, fn);
+  if (st) return st;
+  QkvEpiParams p = {};
+  p.raw = raw;
+  p.n_qn = n_qn;
+  p.n_kn = n_kn;
+  p.ang = ang;
+  p.ang_by_pos = ang_by_pos;
+  p.q_out = q_out;
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.sb = kv_sb;
+  p.sh = kv_sh;
+  p.st = kv_st;
+  p.pos = pos;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.max_seq = max_seq;
+  p.eps = eps;
+  hipLaunchKernelGGL(qkv_epilogue_kernel, dim3(Hq + 2 * Hkv, B), dim3(kHD), 0, s, p);
+  return iron::check_launch(fn);
+}
+
+}  // extern "C"

@@ -1,0 +1,132 @@
+"""DecodeAttention: single-query GQA attention over a bf16 KV cache on gfx950.
+
+Drop-in for iron/operators/decode_attn/op.py:20-181: same fields and validation, the same arg
+specs for both KV layouts, and the runtime causal bound ``S_kv_eff`` (the number of valid cached
+tokens, written per dispatch) when ``use_runtime_seq_len`` is set; the static arm uses every
+cached position, as the reference's does.
+
+KV layouts (all head-major, addressed by strides in one kernel):
+  * ``kv_layout="separate"``: K and V args of (KV, S*D) each -- the reference's separate arm and
+    BASELINE's contiguous ``[B, KV, L, D]`` caches.
+  * ``kv_layout="combined"``, ``kv_token_interleaved=True``: one (KV, 2*S*D) arg with token t's K
+    at 2*t*D and V at 2*t*D + D (the shipped chain's layout).
+  * ``kv_layout="combined"``, ``kv_token_interleaved=False``: one (KV, 2*S*D) arg with a K half
+    then a V half per head -- the layout of the reference golden (decode_attn/reference.py:41-60).
+New fields: ``batch`` (sequences per call; Q/O become (batch*H, D), K/V (batch*KV, ...), and
+``S_kv_eff`` holds one count per sequence, so ragged batches are one call) and ``scale``
+(default 1/sqrt(D)). The speculative-verify batch mode (``batch_queries``) is not implemented.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import ClassVar, Dict
+
+from ... import _lib
+from ...common.base import AIERuntimeArgSpec, MLIROperator, check_args
+from .._common import RuntimeParams, Workspace, stream_ptr
+
+
+@dataclass
+class DecodeAttention(MLIROperator):
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    seq_len_kv: int
+    num_aie_columns: int = 8
+    block_kv: int = 64
+    use_runtime_seq_len: bool = field(default=False, repr=False)
+    batch_queries: int = 0
+    num_new_tokens: int = 0
+    causal: bool = True
+    kv_token_interleaved: bool = True
+    out_buffer_tokens: int = 0
+    kv_layout: str = "combined"
+    batch: int = 1
+    scale: float | None = None
+    context: object = field(default=None, repr=False)
+
+    _name_aliases: ClassVar[Dict[str, str]] = {
+        "num_heads": "h",
+        "num_kv_heads": "kv",
+        "head_dim": "d",
+        "seq_len_kv": "skv",
+        "num_aie_columns": "col",
+        "block_kv": "bkv",
+        "batch_queries": "m",
+        "num_new_tokens": "new",
+        "kv_layout": "kvl",
+    }
+
+    def __post_init__(self):
+        if self.seq_len_kv % 64 != 0:
+            raise ValueError("seq_len_kv must be a multiple of 64")
+        if self.block_kv % 16 != 0:
+            raise ValueError("block_kv must be a multiple of 16")
+        if self.batch_queries > 0:
+            raise NotImplementedError("batch (speculative verify) mode is not implemented")
+        if self.kv_layout not in ("combined", "separate"):
+            raise ValueError(f"unknown kv_layout {self.kv_layout!r}")
+        if self.num_heads % self.num_kv_heads:
+            raise ValueError("num_heads must be a multiple of num_kv_heads")
+        if self.batch < 1:
+            raise ValueError("batch must be >= 1")
+        MLIROperator.__init__(self, context=self.context)
+
+    @property
+    def softmax_scale(self) -> float:
+        return self.scale if self.scale is not None else 1.0 / math.sqrt(self.head_dim)
+
+    def kv_strides(self) -> tuple[int, int, int, int]:
+        """(v_offset, batch stride, head stride, token stride) in elements."""
+        S, D, KV = self.seq_len_kv, self.head_dim, self.num_kv_heads
+        if self.kv_layout == "separate":
+            return 0, KV * S * D, S * D, D
+        if self.kv_token_interleaved:
+            return D, KV * 2 * S * D, 2 * S * D, 2 * D
+        return S * D, KV * 2 * S * D, 2 * S * D, D
+
+    def get_arg_spec(self):
+        H, KV, D, S, B = self.num_heads, self.num_kv_heads, self.head_dim, self.seq_len_kv, self.batch
+        if self.kv_layout == "separate":
+            return [
+                AIERuntimeArgSpec("in", (B * H, D)),         # Q
+                AIERuntimeArgSpec("in", (B * KV, S * D)),    # K cache (head-major)
+                AIERuntimeArgSpec("in", (B * KV, S * D)),    # V cache (head-major)
+                AIERuntimeArgSpec("out", (B * H, D)),        # O
+            ]
+        return [
+            AIERuntimeArgSpec("in", (B * H, D)),             # Q
+            AIERuntimeArgSpec("in", (B * KV, 2 * S * D)),    # KV combined
+            AIERuntimeArgSpec("out", (B * H, D)),            # O
+        ]
+
+    def get_callable(self, params: RuntimeParams | None = None):
+        """``params``: a shared runtime-parameter store holding ``S_kv_eff`` (one is created if
+        None and ``use_runtime_seq_len`` is set)."""
+        lib = _lib.load()
+        H, KV, D, S, B = self.num_heads, self.num_kv_heads, self.head_dim, self.seq_len_kv, self.batch
+        ws = Workspace(lib.iron_decode_attn_workspace(B, H, KV, D, S), self.context.device)
+        voff, sb, sh, st = self.kv_strides()
+        params = params if params is not None else RuntimeParams(self.context.device)
+        if self.use_runtime_seq_len and "S_kv_eff" not in params:
+            params.define("S_kv_eff", B)
+            params.write("S_kv_eff", [S] * B)
+
+        def call(*args):
+            args = check_args(self, args)
+            if self.kv_layout == "separate":
+                q, k, v, o = args
+                kp, vp = k.data_ptr(), v.data_ptr()
+            else:
+                q, kv, o = args
+                kp, vp = kv.data_ptr(), kv.data_ptr() + 2 * voff
+            ctx = params.tensor("S_kv_eff", B) if self.use_runtime_seq_len else None
+            _lib.check(lib.iron_decode_attn(
+                q.data_ptr(), kp, vp, sb, sh, st, _lib.ptr(ctx), S, o.data_ptr(), B, H, KV, D, S,
+                float(self.softmax_scale), ws.ptr, ws.nbytes, stream_ptr()), "DecodeAttention")
+
+        call.params = params
+        call.workspace = ws
+        return call

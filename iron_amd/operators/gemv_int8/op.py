@@ -1,0 +1,133 @@
+"""GEMVInt8: int8-weight GEMV with in-kernel per-group dequant (W8A16) on gfx950.
+
+Drop-in for the reference operator (iron/operators/gemv_int8/op.py:20-178): same dataclass
+fields, same validation, same three-argument spec ``[packed wire (bf16 view), x, y]``. The NPU
+tiling knobs (``num_aie_columns``, ``tile_size_output``, ``weight_depth``,
+``kernel_vector_size``) are accepted and validated as before but select no code path;
+``tile_size_input`` fixes the wire's row-block height, and ``kernel_source`` the payload domain
+(``"mv_int8_signed.cc"`` = signed, default = biased), exactly the pairing the reference uses.
+``group_size`` is new: the reference hard-wires 128 (op.py:83-84), the graded configs use 32.
+``batch_size`` (also new) streams the weights once for up to 4 activation vectors, and
+``epilogue="argmax"`` (new; the LM-head use) appends a ``(batch_size,)`` int64 output that must
+be zero before the call and receives the packed argmax key of each bf16 output row vector.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import ClassVar, Dict
+
+import torch
+
+from ... import _lib
+from ...common.base import AIERuntimeArgSpec, MLIROperator, check_args
+from .._common import domain_code, stream_ptr
+from ..wire import domain_of, wire_nbytes
+
+
+@dataclass
+class GEMVInt8(MLIROperator):
+    M: int
+    K: int
+    num_aie_columns: int = 1
+    tile_size_input: int = 2
+    tile_size_output: int | None = None
+    num_batches: int = 1
+    group_size: int = 128
+    batch_size: int = 1
+    kernel_vector_size: int = field(default=128, repr=False)
+    weight_depth: int = field(default=2, repr=False)
+    kernel_source: str | None = field(default=None, repr=False)
+    epilogue: str = field(default="none", repr=False)
+    context: object = field(default=None, repr=False)
+
+    _name_aliases: ClassVar[Dict[str, str]] = {
+        **MLIROperator._name_aliases,
+        "num_aie_columns": "col",
+        "tile_size_input": "tsi",
+        "tile_size_output": "tso",
+        "num_batches": "batch",
+        "group_size": "g",
+        "batch_size": "bs",
+    }
+
+    def __post_init__(self):
+        if self.tile_size_output is None:
+            self.tile_size_output = self.tile_size_input
+        if not (self.tile_size_output % self.tile_size_input == 0
+                and self.tile_size_output >= self.tile_size_input):
+            raise ValueError("tile_size_output must be a multiple of tile_size_input")
+        if not (self.K >= self.kernel_vector_size and self.K % self.kernel_vector_size == 0):
+            raise ValueError("K must be multiple of kernel_vector_size")
+        if self.group_size < 16 or self.group_size & (self.group_size - 1):
+            raise ValueError("group_size must be a power of two >= 16")
+        if self.K % self.group_size != 0:
+            raise ValueError(f"K must be a multiple of GROUP_SIZE={self.group_size}")
+        if self.M % self.tile_size_input != 0:
+            raise ValueError("tile_size_input must divide M")
+        if not 1 <= self.batch_size <= 4:
+            raise ValueError("batch_size must be in [1, 4]")
+        if self.epilogue not in ("none", "argmax"):
+            raise ValueError(f"unknown epilogue {self.epilogue!r}")
+        if self.epilogue == "argmax" and self.num_batches != 1:
+            raise ValueError("the argmax epilogue needs num_batches == 1")
+        MLIROperator.__init__(self, context=self.context)
+
+    def _kernel_source(self) -> str:
+        if self.kernel_source is not None:
+            return self.kernel_source
+        return getattr(self.context, "gemv_int8_kernel_source", None) or "mv_int8.cc"
+
+    @property
+    def name(self) -> str:
+        base = super().name
+        return base if self.epilogue == "none" else f"{base}_epi{self.epilogue}"
+
+    @property
+    def domain(self) -> str:
+        return domain_of(self._kernel_source())
+
+    @property
+    def wire_bytes(self) -> int:
+        return wire_nbytes(self.M, self.K, self.group_size, self.tile_size_input)
+
+    def get_arg_spec(self):
+        batch_dim = (self.num_batches,) if self.num_batches > 1 else ()
+        vec_dim = (self.batch_size,) if self.batch_size > 1 else ()
+        w_elems = self.num_batches * self.wire_bytes // 2
+        spec = [
+            AIERuntimeArgSpec("in", (w_elems,)),                       # packed wire (bf16 view)
+            AIERuntimeArgSpec("in", batch_dim + vec_dim + (self.K,)),  # bf16 vector(s)
+            AIERuntimeArgSpec("out", batch_dim + vec_dim + (self.M,)),  # output
+        ]
+        if self.epilogue == "argmax":
+            spec.append(AIERuntimeArgSpec("inout", (self.batch_size,), dtype=torch.int64))
+        return spec
+
+    def get_callable(self):
+        lib = _lib.load()
+        dom = domain_code(self.domain)
+        wb = self.wire_bytes
+        M, K, G, tm, B = self.M, self.K, self.group_size, self.tile_size_input, self.batch_size
+
+        def call(*args):
+            w, x, y = check_args(self, args)[:3]
+            s = stream_ptr()
+            if self.epilogue == "argmax":
+                _lib.check(lib.iron_lm_head(
+                    w.data_ptr(), _lib.IRON_WEIGHT_INT8, x.data_ptr(), None, 0.0, y.data_ptr(),
+                    args[3].data_ptr(), B, M, K, G, tm, dom, s), "GEMVInt8")
+                return
+            for nb in range(self.num_batches):
+                _lib.check(lib.iron_gemv_w8a16(
+                    w.data_ptr() + nb * wb, x.data_ptr() + nb * B * K * 2,
+                    y.data_ptr() + nb * B * M * 2, B, M, K, G, tm, dom, s), "GEMVInt8")
+
+        return call
+
+    def dequantize(self, w: torch.Tensor) -> torch.Tensor:
+        """Device-side bit-exact dequant of one wire into a (M, K) bf16 matrix."""
+        out = torch.empty((self.M, self.K), dtype=torch.bfloat16, device=w.device)
+        _lib.call("iron_dequant_w8", w.data_ptr(), out.data_ptr(), self.M, self.K,
+                  self.group_size, self.tile_size_input, domain_code(self.domain), stream_ptr())
+        return out

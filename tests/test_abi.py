@@ -1,0 +1,111 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol, and rejects bad
+arguments with the documented status before touching the GPU (the reference raises ValueError
+for shape constraints, iron/operators/gemv_int8/op.py:74-84)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from iron_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "iron_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:[\w\*\s]+?)\b(iron_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = _declared()
+    assert "iron_gemv_w8a16" in names and "iron_decode_attn" in names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in iron_hip.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) <= set(names)
+
+
+def test_abi_version(lib):
+    assert lib.iron_abi_version() == 1
+
+
+def test_wire_bytes(lib):
+    out = ctypes.c_size_t()
+    assert lib.iron_wire_bytes(4096, 1024, 32, 4, ctypes.byref(out)) == 0
+    assert out.value == 1024 * (4 * 1024 + 4 * 32 * 2)
+    assert lib.iron_wire_bytes(4096, 1000, 32, 4, ctypes.byref(out)) == _lib.IRON_ERR_SHAPE
+    assert b"bad geometry" in lib.iron_last_error()
+
+
+@pytest.mark.parametrize("d", [1, 2, 3, 4, 12, 16, 37, 1000, 65535])
+def test_fastdiv_matches_integer_division(lib, d):
+    for n in list(range(0, 5000, 7)) + [2**20 - 1, 2**24 + 5, 2**31 - 1, 151936]:
+        assert lib.iron_test_fastdiv(n, d) == n // d
+
+
+def test_gemv_rejects_bad_arguments(lib):
+    f = lib.iron_gemv_w8a16
+    # null wire
+    assert f(None, 16, 16, 1, 64, 128, 32, 4, 0, None) == _lib.IRON_ERR_NULL
+    fake = 1 << 20  # an aligned non-null address; validation fails before any use
+    # K not a multiple of G
+    assert f(fake, fake, fake, 1, 64, 100, 32, 4, 0, None) == _lib.IRON_ERR_SHAPE
+    # tile_m does not divide M
+    assert f(fake, fake, fake, 1, 66, 128, 32, 4, 0, None) == _lib.IRON_ERR_SHAPE
+    # non power-of-two group
+    assert f(fake, fake, fake, 1, 64, 144, 48, 4, 0, None) == _lib.IRON_ERR_SHAPE
+    # misaligned wire
+    assert f(fake + 2, fake, fake, 1, 64, 128, 32, 4, 0, None) == _lib.IRON_ERR_ALIGN
+    # batch > 4 -> unsupported (MFMA path)
+    assert f(fake, fake, fake, 8, 64, 128, 32, 4, 0, None) == _lib.IRON_ERR_UNSUPPORTED
+    # unknown domain
+    assert f(fake, fake, fake, 1, 64, 128, 32, 4, 7, None) == _lib.IRON_ERR_SHAPE
+
+
+def test_attention_rejects_bad_arguments(lib):
+    f = lib.iron_decode_attn
+    fake = 1 << 20
+    args = lambda **kw: dict(dict(q=fake, k=fake, v=fake, sb=0, sh=0, st=128, ctx=None, cc=1,  # noqa
+                                  o=fake, B=1, H=16, KV=8, D=128, L=64, scale=0.1, ws=None,
+                                  wsb=0), **kw)
+
+    def call(**kw):
+        a = args(**kw)
+        return f(a["q"], a["k"], a["v"], a["sb"], a["sh"], a["st"], a["ctx"], a["cc"], a["o"],
+                 a["B"], a["H"], a["KV"], a["D"], a["L"], a["scale"], a["ws"], a["wsb"], None)
+
+    assert call(q=None) == _lib.IRON_ERR_NULL
+    assert call(D=64) == _lib.IRON_ERR_UNSUPPORTED
+    assert call(H=12, KV=8) == _lib.IRON_ERR_SHAPE
+    assert call(cc=65) == _lib.IRON_ERR_SHAPE
+    assert call(st=100) == _lib.IRON_ERR_ALIGN
+    # a long context needs split-K scratch: missing workspace is reported, not ignored
+    assert call(L=4096, cc=4096) == _lib.IRON_ERR_WORKSPACE
+    assert lib.iron_decode_attn_workspace(1, 16, 8, 128, 4096) > 0
+    assert lib.iron_decode_attn_workspace(1, 16, 8, 64, 4096) == 0
+
+
+def test_status_to_exception(lib):
+    lib.iron_wire_bytes(1, 1, 3, 4, ctypes.byref(ctypes.c_size_t()))
+    with pytest.raises(ValueError, match="bad geometry"):
+        _lib.check(_lib.IRON_ERR_SHAPE, "iron_wire_bytes")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.IRON_ERR_HIP, "x")
+
+
+def test_mlp_and_qkv_reject_bad_arguments(lib):
+    fake = 1 << 20
+    # MLP: FF not divisible by tile_m_gu
+    rc = lib.iron_swiglu_mlp(fake, fake, fake, None, fake, fake, fake, fake, None, 1, 1024, 3000,
+                             0, 32, 4, 12, 4, 0, 1e-6, fake, 1 << 20, None)
+    assert rc == _lib.IRON_ERR_SHAPE
+    # QKV: head_dim 64 unsupported
+    rc = lib.iron_qkv_head(fake, fake, fake, fake, fake, fake, 0, fake, fake, fake, 0, 0, 0,
+                           fake, 1, 1024, 64, 16, 8, 512, 32, 4, 0, 1e-6, fake, 1 << 20, None)
+    assert rc == _lib.IRON_ERR_UNSUPPORTED
+    # QKV: workspace too small
+    rc = lib.iron_qkv_head(fake, fake, fake, fake, fake, fake, 0, fake, fake, fake, 0, 0, 0,
+                           fake, 1, 1024, 128, 16, 8, 512, 32, 4, 0, 1e-6, fake, 16, None)
+    assert rc == _lib.IRON_ERR_WORKSPACE

@@ -1,0 +1,181 @@
+"""Whole-model GPU parity: the Qwen3 decode chain (HIP) against the CPU oracle chain.
+
+* tiny model: logits within tolerance of the CPU chain at every step, same argmax;
+* dispatch modes: the graph-replayed ("fused") and eager ("separate") sequences give
+  bit-identical logits (the reference checks the same across its dispatch modes,
+  iron/tests/infrastructure/sequence.py:183-203);
+* the device-resident greedy loop reproduces the host-driven loop token for token;
+* compare mode raises on a planted wrong reference (sequence.py:284-324 in the reference tests);
+* Qwen3-0.6B architecture, int8 G=32, bf16 LM head, KV prefilled to 2048 positions, 128 greedy
+  steps: greedy-token agreement with the CPU chain >= 99% under teacher forcing.
+"""
+
+import pytest
+import torch
+
+from iron_amd.applications.qwen3_0_6b.qwen3_npu_int8 import Qwen3NPU
+from iron_amd.applications.qwen3_0_6b.weights import (Qwen3Config, random_qwen3_weights,
+                                                       synthetic_kv)
+from iron_amd.common.test_utils import verify_buffer
+from oracle.qwen3 import Qwen3CpuChain
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    cfg = Qwen3Config.tiny()
+    return cfg, random_qwen3_weights(cfg, seed=99)
+
+
+@pytest.mark.parametrize("kv_layout,lm_head", [("separate", "bf16"), ("interleaved", "int8")])
+def test_tiny_model_matches_cpu_chain(kv_layout, lm_head):
+    _say(f"tiny model kv_layout={kv_layout} lm_head={lm_head}")
+    cfg = Qwen3Config.tiny()
+    w = random_qwen3_weights(cfg, seed=5, lm_head=lm_head)
+    S = 128
+    model = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, kv_layout=kv_layout)
+    chain = Qwen3CpuChain(cfg, w, S)
+    tok = 3
+    for pos in range(8):
+        g = model.step_token(tok, pos)
+        lg = model.logits()
+        lc = chain.step(tok, pos)
+        # logits are O(3); 1e-2 abs + 1e-2 rel on the bf16 logits of a 2-layer chain
+        assert not verify_buffer(lg, f"logits@{pos}", lc, rel_tol=1e-2, abs_tol=1e-2)
+        assert g == int(torch.argmax(lg.float())), "device argmax != argmax of device logits"
+        assert g == Qwen3CpuChain.argmax(lc)
+        tok = g
+
+
+def test_dispatch_modes_bit_identical(tiny):
+    _say("fused vs separate dispatch")
+    cfg, w = tiny
+    outs = []
+    for dispatch in ("fused", "separate"):
+        m = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, dispatch=dispatch)
+        toks, logits = [], []
+        tok = 11
+        for pos in range(5):
+            tok = m.step_token(tok, pos)
+            toks.append(tok)
+            logits.append(m.logits())
+        outs.append((toks, torch.stack(logits)))
+    assert outs[0][0] == outs[1][0]
+    assert torch.equal(outs[0][1].view(torch.int16), outs[1][1].view(torch.int16))
+
+
+def test_device_generate_matches_host_loop(tiny):
+    _say("device generate vs host loop")
+    cfg, w = tiny
+    prompt = [7, 19, 23, 5]
+    n_new = 20
+    a = Qwen3NPU(config=cfg, weights=w, max_seq_len=64)
+    dev_tokens = a.generate(prompt, n_new)
+    b = Qwen3NPU(config=cfg, weights=w, max_seq_len=64)
+    pos = 0
+    for t in prompt[:-1]:
+        b.step_token(t, pos)
+        pos += 1
+    host = []
+    tok = prompt[-1]
+    for _ in range(n_new):
+        tok = b.step_token(tok, pos)
+        pos += 1
+        host.append(tok)
+    assert dev_tokens == host
+    # replaying again from a re-armed state gives the same tokens (graph replay is repeatable)
+    a2 = a.generate(prompt, n_new)
+    assert a2 == dev_tokens
+
+
+def test_compare_mode_raises_on_wrong_reference(tiny, oracle_provider):
+    """Plant a mistake in the oracle (CPU side): compare dispatch must raise."""
+    from iron_amd.common.base import register_reference_provider
+    from iron_amd.common.sequence import CompareDispatch, OperatorSequence
+    from iron_amd.operators import RMSNorm
+
+    _say("compare mode")
+    op = RMSNorm(size=256, num_aie_columns=1, num_channels=1, tile_size=256, weighted=True,
+                 epsilon=1e-6)
+    seq = OperatorSequence("cmp", [(op, "x", "w", "y")], input_args=["x", "w"],
+                           output_args=["y"], dispatch=CompareDispatch(1e-2, 1e-2))
+    fc = seq.get_callable()
+    fc.get_buffer("x").torch_view()[:256].copy_(torch.randn(256).to(torch.bfloat16))
+    fc.get_buffer("w").torch_view()[:256].fill_(1.0)
+    fc()  # correct reference: passes
+    assert not any(s["mismatch"] for s in fc.last_step_stats)
+
+    def wrong(op_, *inputs):
+        return oracle_provider(op_, *inputs) * 1.5
+
+    register_reference_provider(wrong)
+    try:
+        with pytest.raises(RuntimeError, match="deviates"):
+            fc()
+    finally:
+        register_reference_provider(oracle_provider)
+
+
+def test_reference_dispatch_matches_hip(tiny, oracle_provider):
+    _say("reference dispatch vs hip on one layer step")
+    from iron_amd.common.sequence import OperatorSequence
+    from iron_amd.operators import GEMVInt8
+    from iron_amd.operators.wire import pack_wire
+    from oracle.gemv import rtn_quantize
+
+    M, K = 512, 256
+    op = GEMVInt8(M=M, K=K, tile_size_input=4, group_size=32, kernel_source="mv_int8_signed.cc")
+    q, s = rtn_quantize(torch.randn(M, K) * 0.05, 32)
+    wire = pack_wire(q, s, 4, "signed")
+    x = torch.randn(K).to(torch.bfloat16)
+    ys = []
+    for dispatch in ("fused", "reference"):
+        seq = OperatorSequence("g", [(op, "w", "x", "y")], input_args=["w", "x"],
+                               output_args=["y"], dispatch=dispatch)
+        fc = seq.get_callable()
+        fc.get_buffer("w").torch_view(torch.uint8)[: wire.numel()].copy_(wire)
+        fc.get_buffer("x").torch_view()[:K].copy_(x)
+        fc()
+        ys.append(fc.get_buffer("y").torch_view()[:M].cpu())
+    assert not verify_buffer(ys[0], "y", ys[1], rel_tol=1e-2, abs_tol=1e-2)
+
+
+@pytest.mark.slow
+def test_qwen3_0_6b_greedy_agreement():
+    """BASELINE config 4 shape at full size; agreement measured under teacher forcing."""
+    cfg = Qwen3Config.qwen3_0_6b()
+    P0, n_prompt, n_new = 1984, 64, 128
+    S = P0 + n_prompt + n_new
+    _say(f"qwen3-0.6b: weights G={cfg.group_size}, KV prefill {P0}+{n_prompt}, {n_new} steps")
+    w = random_qwen3_weights(cfg, seed=2024)
+    k0, v0 = synthetic_kv(cfg, P0, seed=7)
+    model = Qwen3NPU(config=cfg, weights=w, max_seq_len=S)
+    model.load_kv(k0, v0)
+    gen = torch.Generator().manual_seed(64)
+    prompt = torch.randint(0, cfg.vocab_size, (n_prompt,), generator=gen).tolist()
+    toks = model.generate(prompt, n_new, start_pos=P0)
+    assert len(toks) == n_new
+    _say("qwen3-0.6b: CPU chain (teacher forced)")
+    chain = Qwen3CpuChain(cfg, w, S, kv_init=(k0, v0))
+    pos = P0
+    for t in prompt[:-1]:
+        chain.step(t, pos)
+        pos += 1
+    agree, margins = 0, []
+    tok = prompt[-1]
+    for i in range(n_new):
+        lc = chain.step(tok, pos).float()
+        top = torch.topk(lc, 2).values
+        margins.append(float(top[0] - top[1]))
+        agree += int(Qwen3CpuChain.argmax(lc) == toks[i])
+        tok = toks[i]
+        pos += 1
+    rate = agree / n_new
+    print(f"greedy agreement {agree}/{n_new} = {rate:.4f}; top1-top2 margin min "
+          f"{min(margins):.4g} median {sorted(margins)[len(margins) // 2]:.4g}", flush=True)
+    assert rate >= 0.99

@@ -1,0 +1,331 @@
+"""GPU parity of every hot-path operator against the CPU oracle, through the operator API.
+
+Tolerances (written per test): bit-exact for dequant; rel 1e-2 / abs 1e-2 for GEMV and attention
+outputs in bf16; the fused blocks use the same 1e-2 bar on their final bf16
+outputs. Every case prints its name and shape before the GPU call.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from iron_amd.common.test_utils import verify_buffer
+from iron_amd.operators import (DecodeAttention, GEMVInt8, QKVHeadDataParallelOurs, RMSNorm,
+                                SwiGLUMLPDataParallelOurs)
+from iron_amd.operators.qkv_head_dp.op import QKVHeadDataParallel
+from iron_amd.operators.wire import pack_wire
+from oracle import attention as oatt
+from oracle import blocks as oblk
+from oracle import cref
+from oracle import gemv as ogemv
+from oracle import norms as onorm
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL = ATOL = 1e-2
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _baseline_weights(M, K, G, gen):
+    """BASELINE-config weights: q ~ U{-127..127}, s = bf16(|N(0, 0.02)|) per group."""
+    q = torch.randint(-127, 128, (M, K), generator=gen, dtype=torch.int16)
+    s = (torch.randn(M, K // G, generator=gen) * 0.02).abs().to(torch.bfloat16)
+    return q, s
+
+
+def _src(domain):
+    return "mv_int8_signed.cc" if domain == "signed" else None
+
+
+@pytest.mark.parametrize("M,K,G,tile_m,domain", [
+    (4096, 1024, 32, 4, "signed"),
+    (4096, 1024, 128, 4, "biased"),
+    (96, 256, 32, 12, "signed"),
+    (128, 2048, 64, 1, "biased"),
+])
+def test_dequant_bit_exact(M, K, G, tile_m, domain):
+    _say(f"dequant M={M} K={K} G={G} tile_m={tile_m} {domain}")
+    gen = torch.Generator().manual_seed(M + K + G)
+    q, s = _baseline_weights(M, K, G, gen)
+    op = GEMVInt8(M=M, K=K, tile_size_input=tile_m, group_size=G, kernel_vector_size=min(128, K),
+                  kernel_source=_src(domain))
+    wire = pack_wire(q, s, tile_m, domain).to(DEV)
+    got = op.dequantize(wire).cpu()
+    want = ogemv.dequant(q, s)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(want.view(torch.int16), cref.dequant(q, s).view(torch.int16))
+
+
+@pytest.mark.parametrize("M,K,G,tile_m,B,domain", [
+    (4096, 1024, 32, 4, 1, "signed"),
+    (4096, 1024, 128, 4, 1, "biased"),    # reference group
+    (6144, 2048, 32, 12, 1, "signed"),    # 1.7B gate/up shape
+    (2048, 6144, 32, 4, 1, "signed"),     # 1.7B down shape
+    (1024, 3072, 32, 4, 2, "signed"),
+    (512, 4096, 32, 4, 3, "biased"),
+    (640, 1024, 32, 16, 4, "signed"),
+    (64, 128, 32, 2, 1, "signed"),
+    (200, 1040, 16, 8, 1, "signed"),       # K not a multiple of 1024, odd row count per grid
+])
+def test_gemv_int8(M, K, G, tile_m, B, domain):
+    _say(f"gemv M={M} K={K} G={G} tile_m={tile_m} B={B} {domain}")
+    gen = torch.Generator().manual_seed(7 * M + K + B)
+    q, s = _baseline_weights(M, K, G, gen)
+    x = torch.randn(B, K, generator=gen).to(torch.bfloat16)
+    op = GEMVInt8(M=M, K=K, tile_size_input=tile_m, group_size=G, batch_size=B,
+                  kernel_vector_size=16, kernel_source=_src(domain))
+    op.compile()
+    fn = op.get_callable()
+    wire = pack_wire(q, s, tile_m, domain).view(torch.bfloat16).to(DEV)
+    xd = x.reshape(op.get_arg_spec()[1].shape).to(DEV)
+    y = torch.zeros(op.get_arg_spec()[2].shape, dtype=torch.bfloat16, device=DEV)
+    fn(wire, xd, y)
+    torch.cuda.synchronize()
+    want = ogemv.gemv_exact(q, s, x).to(torch.bfloat16)
+    assert not verify_buffer(y.cpu(), "y", want, rel_tol=RTOL, abs_tol=ATOL)
+    # independent fp64 witness
+    want64 = cref.gemv_f64(q, s, x)
+    assert not verify_buffer(y.cpu().float().reshape(B, M), "y64", want64, RTOL, ATOL)
+
+
+def test_gemv_num_batches():
+    _say("gemv num_batches=3")
+    M, K, G, tm = 256, 512, 32, 4
+    gen = torch.Generator().manual_seed(3)
+    ws, xs, ys = [], [], []
+    for _ in range(3):
+        q, s = _baseline_weights(M, K, G, gen)
+        x = torch.randn(K, generator=gen).to(torch.bfloat16)
+        ws.append(pack_wire(q, s, tm, "signed"))
+        xs.append(x)
+        ys.append(ogemv.gemv_exact(q, s, x).to(torch.bfloat16))
+    op = GEMVInt8(M=M, K=K, tile_size_input=tm, group_size=G, num_batches=3,
+                  kernel_source="mv_int8_signed.cc")
+    y = torch.zeros(3, M, dtype=torch.bfloat16, device=DEV)
+    op.get_callable()(torch.cat(ws).view(torch.bfloat16).to(DEV), torch.stack(xs).to(DEV), y)
+    torch.cuda.synchronize()
+    assert not verify_buffer(y.cpu(), "y", torch.stack(ys), RTOL, ATOL)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1024), (4, 2048), (16, 128), (3, 1000)])
+def test_rmsnorm(rows, cols):
+    _say(f"rmsnorm rows={rows} cols={cols}")
+    gen = torch.Generator().manual_seed(rows * cols)
+    x = (torch.randn(rows, cols, generator=gen) * 3).to(torch.bfloat16)
+    w = (torch.rand(cols, generator=gen) + 0.5).to(torch.bfloat16)
+    op = RMSNorm(size=rows * cols, num_aie_columns=1, num_channels=1, tile_size=cols,
+                 weighted=True, epsilon=1e-6)
+    y = torch.zeros(rows, cols, dtype=torch.bfloat16, device=DEV)
+    op.get_callable()(x.to(DEV), w.to(DEV), y)
+    torch.cuda.synchronize()
+    want = onorm.rms_norm(x, w, 1e-6)
+    # one fp32 rounding path apart: at most one bf16 ulp
+    assert not verify_buffer(y.cpu(), "y", want, rel_tol=2 ** -8, abs_tol=1e-6)
+
+
+def _kv(B, KV, L, D, gen, scale=1.0):
+    k = (torch.randn(B, KV, L, D, generator=gen) * scale).to(torch.bfloat16)
+    v = (torch.randn(B, KV, L, D, generator=gen) * scale).to(torch.bfloat16)
+    return k, v
+
+
+@pytest.mark.parametrize("B,H,KV,L,ctx", [
+    (1, 16, 8, 4096, [4096]),                 # BASELINE config 3, B=1
+    (8, 16, 8, 4096, "ragged"),               # BASELINE config 3, B=8 ragged
+    (1, 32, 8, 512, [300]),                   # GQA 4 (Qwen3-8B heads)
+    (2, 8, 8, 256, [1, 65]),                  # MHA, tiny contexts
+    (3, 16, 2, 128, [0, 63, 64]),             # GQA 8, empty sequence
+    (1, 16, 16, 8192, [8191]),                # long context, GQA 1
+])
+def test_decode_attention(B, H, KV, L, ctx):
+    gen = torch.Generator().manual_seed(B * 100 + L)
+    if ctx == "ragged":
+        ctx = torch.randint(512, 4097, (B,), generator=gen).tolist()
+    _say(f"decode_attn B={B} H={H} KV={KV} L={L} ctx={ctx}")
+    D = 128
+    q = torch.randn(B, H, D, generator=gen).to(torch.bfloat16)
+    k, v = _kv(B, KV, L, D, gen)
+    op = DecodeAttention(num_heads=H, num_kv_heads=KV, head_dim=D, seq_len_kv=L,
+                         use_runtime_seq_len=True, kv_layout="separate", batch=B)
+    fn = op.get_callable()
+    fn.params.write("S_kv_eff", ctx)
+    o = torch.zeros(B * H, D, dtype=torch.bfloat16, device=DEV)
+    fn(q.reshape(B * H, D).to(DEV), k.reshape(B * KV, L * D).to(DEV),
+       v.reshape(B * KV, L * D).to(DEV), o)
+    torch.cuda.synchronize()
+    want = oatt.decode_attention(q, k, v, ctx).reshape(B * H, D)
+    assert not verify_buffer(o.cpu(), "o", want, RTOL, ATOL)
+    # call again (split-K counters must have been reset by the previous call)
+    o2 = torch.zeros_like(o)
+    fn(q.reshape(B * H, D).to(DEV), k.reshape(B * KV, L * D).to(DEV),
+       v.reshape(B * KV, L * D).to(DEV), o2)
+    torch.cuda.synchronize()
+    assert torch.equal(o.cpu(), o2.cpu())
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+def test_decode_attention_combined_layouts(interleaved, oracle_provider):
+    _say(f"decode_attn combined interleaved={interleaved}")
+    H, KV, D, S = 16, 8, 128, 512
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn(H, D, generator=gen).to(torch.bfloat16)
+    kv = (torch.randn(KV, 2 * S * D, generator=gen) * 0.3).to(torch.bfloat16)
+    op = DecodeAttention(num_heads=H, num_kv_heads=KV, head_dim=D, seq_len_kv=S,
+                         kv_token_interleaved=interleaved)
+    o = torch.zeros(H, D, dtype=torch.bfloat16, device=DEV)
+    op.get_callable()(q.to(DEV), kv.to(DEV), o)
+    torch.cuda.synchronize()
+    want = op.reference(q, kv)
+    assert not verify_buffer(o.cpu(), "o", want, RTOL, ATOL)
+
+
+def _qkv_case(D, Hq, Hkv, S, G, tm, layout, B, seed):
+    HD = 128
+    gen = torch.Generator().manual_seed(seed)
+    M = (Hq + 2 * Hkv) * HD
+    w = torch.randn(M, D, generator=gen) * 0.05
+    q8, s = ogemv.rtn_quantize(w, G)
+    cur = torch.randn(B, D, generator=gen).to(torch.bfloat16)
+    n_in = (torch.rand(D, generator=gen) + 0.5).to(torch.bfloat16)
+    n_qn = (torch.rand(HD, generator=gen) + 0.5).to(torch.bfloat16)
+    n_kn = (torch.rand(HD, generator=gen) + 0.5).to(torch.bfloat16)
+    table = onorm.rope_angle_table(S, HD, 1e6)
+    pos = torch.randint(0, S, (B,), generator=gen)
+    ang = table[pos]
+    return dict(HD=HD, M=M, q8=q8, s=s, cur=cur, n_in=n_in, n_qn=n_qn, n_kn=n_kn, ang=ang,
+                pos=pos)
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,S,G,tm,layout,B", [
+    (1024, 16, 8, 512, 32, 4, "interleaved", 1),    # Qwen3-0.6B, reference cache layout
+    (1024, 16, 8, 2048, 128, 4, "separate", 1),
+    (4096, 32, 8, 256, 32, 16, "separate", 2),      # Qwen3-8B head shape, batch 2
+    (256, 2, 1, 64, 32, 4, "separate", 4),
+])
+def test_qkv_head(D, Hq, Hkv, S, G, tm, layout, B):
+    _say(f"qkv_head D={D} Hq={Hq} Hkv={Hkv} S={S} G={G} layout={layout} B={B}")
+    c = _qkv_case(D, Hq, Hkv, S, G, tm, layout, B, seed=D + S + B)
+    HD = c["HD"]
+    op = QKVHeadDataParallelOurs(D=D, HD=HD, Hq=Hq, Hkv=Hkv, max_seq=S, group_size=G,
+                                 tile_size_input=tm, kv_layout=layout, batch=B,
+                                 num_aie_columns=1, kernel_source="mv_int8_signed.cc")
+    fn = op.get_callable()
+    pname = op.kv_offset_parameter
+    per_tok = HD if layout == "separate" else 2 * HD
+    fn.params.write(pname, (c["pos"] * per_tok).numpy())
+    wire = pack_wire(c["q8"], c["s"], tm, "signed").view(torch.bfloat16).to(DEV)
+    qo = torch.zeros(B * Hq * HD, dtype=torch.bfloat16, device=DEV)
+    if layout == "separate":
+        kc = torch.zeros(B, Hkv, S, HD, dtype=torch.bfloat16, device=DEV)
+        vc = torch.zeros_like(kc)
+        caches = (kc.reshape(-1), vc.reshape(-1))
+    else:
+        kvc = torch.zeros(B, Hkv, S, 2, HD, dtype=torch.bfloat16, device=DEV)
+        caches = (kvc.reshape(-1),)
+    fn(c["cur"].reshape(-1).to(DEV), c["n_in"].to(DEV), wire, c["n_qn"].to(DEV),
+       c["n_kn"].to(DEV), c["ang"].reshape(-1).to(DEV), qo, *caches)
+    torch.cuda.synchronize()
+    wq, wk, wv = oblk.qkv_head(c["cur"], c["n_in"], c["q8"], c["s"], c["n_qn"], c["n_kn"],
+                               c["ang"], Hq, Hkv, HD, 1e-6)
+    assert not verify_buffer(qo.cpu(), "q", wq, RTOL, ATOL)
+    if layout == "separate":
+        kcc, vcc = kc.cpu(), vc.cpu()
+    else:
+        kcc, vcc = kvc.cpu()[:, :, :, 0], kvc.cpu()[:, :, :, 1]
+    for b in range(B):
+        p = int(c["pos"][b])
+        assert not verify_buffer(kcc[b, :, p].reshape(-1), "k", wk[b], RTOL, ATOL)
+        assert not verify_buffer(vcc[b, :, p].reshape(-1), "v", wv[b], RTOL, ATOL)
+        # nothing else in the cache was touched
+        mask = torch.ones(S, dtype=torch.bool)
+        mask[p] = False
+        assert kcc[b][:, mask].abs().sum() == 0 and vcc[b][:, mask].abs().sum() == 0
+
+
+@pytest.mark.parametrize("D,FF,QD,fuse_o,G,B", [
+    (1024, 3072, 2048, True, 32, 1),    # Qwen3-0.6B chain arm
+    (2048, 6144, 0, False, 32, 1),      # BASELINE config 2, B=1
+    (2048, 6144, 0, False, 32, 4),
+    (1024, 3072, 2048, True, 128, 2),   # reference group size
+])
+def test_swiglu_mlp(D, FF, QD, fuse_o, G, B):
+    _say(f"swiglu D={D} FF={FF} QD={QD} fuse_o={fuse_o} G={G} B={B}")
+    gen = torch.Generator().manual_seed(D + FF + B)
+    op = SwiGLUMLPDataParallelOurs(D=D, FF=FF, QD=QD or None, fuse_o=fuse_o, group_size=G,
+                                   epsilon=1e-6, batch=B, kernel_source="mv_int8_signed.cc")
+
+    def lin(M, K, std):
+        return ogemv.rtn_quantize(torch.randn(M, K, generator=gen) * std, G)
+
+    wg, wu, wd = lin(FF, D, 0.05), lin(FF, D, 0.05), lin(D, FF, 0.05)
+    cur = torch.randn(B, D, generator=gen).to(torch.bfloat16)
+    n_pf = (torch.rand(D, generator=gen) + 0.5).to(torch.bfloat16)
+    if fuse_o:
+        wo = lin(D, QD, 0.05)
+        cx = torch.randn(B, QD, generator=gen).to(torch.bfloat16)
+    else:
+        wo = None
+        cx = torch.randn(B, D, generator=gen).to(torch.bfloat16)
+    wires = {}
+    if fuse_o:
+        wires["Wo"] = pack_wire(*wo, op.tile_rows_o, "signed")
+    wires["Wg"] = pack_wire(*wg, op.tile_rows_gu, "signed")
+    wires["Wu"] = pack_wire(*wu, op.tile_rows_gu, "signed")
+    wires["Wd"] = pack_wire(*wd, op.tile_rows_d, "signed")
+    ws = torch.zeros(op.workspace_bytes(), dtype=torch.uint8, device=DEV)
+    nxt = torch.zeros(B * D, dtype=torch.bfloat16, device=DEV)
+    args = [cur.reshape(-1).to(DEV), cx.reshape(-1).to(DEV), n_pf.to(DEV)]
+    args += [wires[k].view(torch.bfloat16).to(DEV) for k in ("Wo", "Wg", "Wu", "Wd") if k in wires]
+    args.append(ws)
+    a_s = torch.zeros(B * D, dtype=torch.bfloat16, device=DEV)
+    if fuse_o:
+        args.append(a_s)
+    args.append(nxt)
+    op.get_callable()(*args)
+    torch.cuda.synchronize()
+    want, want_a = oblk.swiglu_mlp(cur, cx, n_pf, wg, wu, wd, 1e-6, wo=wo)
+    assert not verify_buffer(nxt.cpu(), "nxt", want, RTOL, ATOL)
+    if fuse_o:
+        assert not verify_buffer(a_s.cpu(), "a", want_a, RTOL, ATOL)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "int8"])
+def test_lm_head_argmax(kind, lib):
+    from iron_amd import _lib
+
+    V, D, G, tm = 151936, 1024, 32, 4
+    _say(f"lm_head {kind} V={V} D={D}")
+    gen = torch.Generator().manual_seed(5)
+    emb = (torch.randn(V, D, generator=gen) * 0.1).to(torch.bfloat16)
+    x = torch.randn(1, D, generator=gen).to(torch.bfloat16)
+    nw = (torch.rand(D, generator=gen) + 0.5).to(torch.bfloat16)
+    xn = onorm.rms_norm(x, nw, 1e-6)
+    if kind == "bf16":
+        w = emb.to(DEV)
+        wk = _lib.IRON_WEIGHT_BF16
+        want = (xn.float() @ emb.float().t()).to(torch.bfloat16).reshape(-1)
+    else:
+        q8, s = ogemv.rtn_quantize(emb, G)
+        w = pack_wire(q8, s, tm, "signed").to(DEV)
+        wk = _lib.IRON_WEIGHT_INT8
+        want = ogemv.gemv_exact(q8, s, xn.reshape(-1)).to(torch.bfloat16)
+    logits = torch.zeros(V, dtype=torch.bfloat16, device=DEV)
+    keys = torch.zeros(1, dtype=torch.int64, device=DEV)
+    xd, nwd = x.to(DEV), nw.to(DEV)  # keep the device copies alive across the async launch
+    _lib.call("iron_lm_head", w.data_ptr(), wk, xd.data_ptr(), nwd.data_ptr(),
+              1e-6, logits.data_ptr(), keys.data_ptr(), 1, V, D, G, tm, 0,
+              torch.cuda.current_stream().cuda_stream)
+    tokens = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _lib.call("iron_next_token", keys.data_ptr(), tokens.data_ptr(), None, None, None, 0, None, 1,
+              D, V, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = logits.cpu()
+    assert not verify_buffer(got, "logits", want, RTOL, ATOL)
+    # device argmax == first index of the max of the device's own bf16 logits
+    assert int(tokens.item()) == int(torch.argmax(got.float()))
+    assert int(keys.item()) == 0  # consumed and reset
