@@ -239,6 +239,9 @@ class Qwen3NPU:
                   self.fc.params.tensor("S_kv_eff").data_ptr(), 1, 1, stream)
 
     def _capture_gen_graph(self):
+        # State tensors must exist before capture: a tensor created inside the capture would
+        # come from the graph's pool and its zero-fill would be recorded into every replay.
+        self._gen_state()
         torch.cuda.synchronize(self.device)
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream(self.device)

@@ -81,22 +81,25 @@ class Qwen3Config:
 
 
 def random_qwen3_weights(cfg: Qwen3Config, seed: int = 0, lin_std: float = 0.02,
-                         emb_std: float = 0.1, lm_head: str = "bf16") -> dict:
+                         emb_std: float = 0.1, lm_head: str = "bf16", device=None) -> dict:
     """Seeded random-init weights of the given architecture (no checkpoint needed).
 
     Linear weights are drawn N(0, lin_std) and RTN-quantized to int8 per-group (the
     reference's own quantizer, qwen3_npu_int8.py:457-491); norms are U[0.8, 1.2]; the
     embedding is N(0, emb_std) and the LM head is tied to it (Qwen3-0.6B ties them), either as
     bf16 or RTN int8. ``emb_std`` sets the logit spread; 0.1 gives logit std ~3 at D=1024.
+    ``device`` selects where the numbers are drawn (a GPU generator is much faster at full
+    size); the values are deterministic per (seed, device type).
     """
-    gen = torch.Generator().manual_seed(seed)
+    dev = torch.device(device) if device is not None else torch.device("cpu")
+    gen = torch.Generator(device=dev).manual_seed(seed)
     D, FF, HD, G = cfg.emb_dim, cfg.hidden_dim, cfg.head_dim, cfg.group_size
 
     def lin(M, K):
-        return rtn_quantize(torch.randn(M, K, generator=gen) * lin_std, G)
+        return rtn_quantize(torch.randn(M, K, generator=gen, device=dev) * lin_std, G)
 
     def norm(n):
-        return (0.8 + 0.4 * torch.rand(n, generator=gen)).to(torch.bfloat16)
+        return (0.8 + 0.4 * torch.rand(n, generator=gen, device=dev)).to(torch.bfloat16)
 
     layers = []
     for _ in range(cfg.n_layers):
@@ -105,9 +108,20 @@ def random_qwen3_weights(cfg: Qwen3Config, seed: int = 0, lin_std: float = 0.02,
             "qkv": lin(cfg.qkv_dim, D), "o": lin(D, cfg.q_dim),
             "gate": lin(FF, D), "up": lin(FF, D), "down": lin(D, FF),
         })
-    embed = (torch.randn(cfg.vocab_size, D, generator=gen) * emb_std).to(torch.bfloat16)
+    embed = (torch.randn(cfg.vocab_size, D, generator=gen, device=dev) * emb_std).to(torch.bfloat16)
     head = embed if lm_head == "bf16" else rtn_quantize(embed, G)
     return {"embed": embed, "final_norm": norm(D), "lm_head": head, "layers": layers}
+
+
+def weights_to(w: dict, device) -> dict:
+    """Copy of a neutral weight dict on ``device`` (tied embedding/head stay tied)."""
+    def mv(t):
+        return tuple(x.to(device) for x in t) if isinstance(t, tuple) else t.to(device)
+
+    out = {"embed": mv(w["embed"]), "final_norm": mv(w["final_norm"]),
+           "layers": [{k: mv(v) for k, v in L.items()} for L in w["layers"]]}
+    out["lm_head"] = out["embed"] if w["lm_head"] is w["embed"] else mv(w["lm_head"])
+    return out
 
 
 def load_gptq_checkpoint(path, cfg: Qwen3Config, lm_head: str = "bf16") -> dict:

@@ -25,23 +25,26 @@ void clear_error() { g_err[0] = 0; }
 
 namespace {
 
-// One 256-thread workgroup per row: y = bf16(x * rsqrt(mean(x^2) + eps) * w).
+// One 256-thread workgroup per row: y = bf16((x * (1 / sqrt(mean(x^2) + eps))) * w), the
+// golden's closed form evaluated in fp64 and rounded once.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ w,
                                                       uint16_t* __restrict__ y, int cols,
                                                       float eps) {
-  __shared__ float red[4];
+  __shared__ double red[4];
   const uint16_t* xr = x + (size_t)blockIdx.x * cols;
   uint16_t* yr = y + (size_t)blockIdx.x * cols;
-  float ss = 0.f;
+  double ss = 0.0;
   for (int i = threadIdx.x; i < cols; i += 256) {
-    const float v = bf16_to_f32(xr[i]);
-    ss = fmaf(v, v, ss);
+    const double v = bf16_to_f32(xr[i]);
+    ss = fma(v, v, ss);
   }
-  ss = block_sum_256(ss, red);
-  const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
-  for (int i = threadIdx.x; i < cols; i += 256)
-    yr[i] = f32_to_bf16(bf16_to_f32(xr[i]) * inv * (w ? bf16_to_f32(w[i]) : 1.0f));
+  ss = block_sum_256_d(ss, red);
+  const double inv = 1.0 / sqrt(ss / (double)cols + (double)eps);
+  for (int i = threadIdx.x; i < cols; i += 256) {
+    const double v = (double)bf16_to_f32(xr[i]) * inv;
+    yr[i] = f64_to_bf16(w ? v * (double)bf16_to_f32(w[i]) : v);
+  }
 }
 
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tokens,

@@ -1,18 +1,24 @@
-// GQA decode attention (one query token per sequence) over a bf16 KV cache, split-K across
-// workgroups (flash-decoding) with an in-kernel merge by the last workgroup of each (b, kv head).
+// GQA decode attention (one query token per sequence) over a bf16 KV cache: split-K across
+// workgroups (flash-decoding), then a merge kernel.
 //
 // Reference: DecodeAttention (iron/operators/decode_attn/op.py:20-181), kernels
-// aie_kernels/aie2p/decode_attn.cc:117-311 (scores with scale log2(e)/sqrt(D), exp2 online
-// softmax over KV blocks, finalize out/l with l == 0 -> 0), golden
-// iron/operators/decode_attn/reference.py:26-38 (fp32, exp2 form, kv = h*KV//H).
-// Numerics here: fp32 scores, fp32 probabilities (no bf16 rounding of p), fp32 accumulation,
-// one bf16 rounding of the output.
+// aie_kernels/aie2p/decode_attn.cc:117-311 (scores with scale log2(e)/sqrt(D), online softmax over
+// KV blocks, finalize out/l with l == 0 -> 0), golden iron/operators/decode_attn/reference.py:
+// 26-38 (kv = h*KV//H).
 //
-// Mapping: grid (split, kv, b), 256 threads = 4 wavefronts. Lane l works on token row l/16 of a
-// 4-token group and on head dims [8*(l%16), +8): one 128-bit load per lane reads 4 consecutive
-// K (or V) rows = 1 KiB per wavefront instruction. The HG = H/KV query heads of the GQA group
-// share every K/V load. Each 16-lane row keeps its own online-softmax state; rows, wavefronts
-// and finally splits are merged with the standard (m, l, o) rescaling.
+// Arithmetic: the exact value of the golden, o = sum_j e^(s_j - m) v_j / sum_j e^(s_j - m) with
+// s_j = (q . k_j) / sqrt(D), evaluated in fp64 (scores, exponentials, sums, accumulation) and
+// rounded once to bf16. The exp2/log2(e) form of the reference is the same function.
+//
+// Mapping: grid (split, kv * head_groups, b), 256 threads = 4 wavefronts. Lane l works on token
+// row l/16 of a 4-token group and on head dims [8*(l%16), +8): one 128-bit load per lane reads 4
+// consecutive K (or V) rows = 1 KiB per wavefront instruction. HB query heads of the GQA group
+// share every K/V load. Per 16 tokens (4 rows x 4 unrolled groups) a row keeps one online-softmax
+// state per head; the row's lanes split the block's exponentials between them (one exp per
+// (token, head) instead of sixteen) and share the results with DPP row broadcasts. Rows and
+// wavefronts merge through shuffles and LDS; splits merge in a second kernel.
+#include <utility>
+
 #include "common.h"
 #include "internal.h"
 
@@ -30,21 +36,48 @@ struct AttnParams {
   int ctx_const;
   int max_ctx;
   uint16_t* out;
-  int H, KV;
+  int H, KV, HG, HB;   // heads, kv heads, GQA group, heads per workgroup
   int chunk, nsplit;
-  float scale_log2;
-  float* part;         // [B][KV][nsplit][HG*(D+2)]
-  unsigned int* cnt;   // [B][KV]
+  double scale;
+  double* part;        // [B][H][nsplit][D + 2]: o (unnormalised), m, l
 };
 
-IRON_DEV float safe_exp2_diff(float a, float m) {
-  // exp2(a - m) with a == -inf -> 0 (m is finite whenever this is called)
-  return exp2f(a - m);
+template <int N>
+IRON_DEV double row_share_d(double v) {
+  // every lane of a 16-lane row receives lane N of that row
+  return dpp_d<0x150 + N>(v);
 }
 
-template <int HG>
+// Lane N of each row evaluated exponential N; every lane of the row receives it.
+template <int N, int HB>
+IRON_DEV void share_one(double ev, double (&pe)[4][HB], double (&corr)[HB]) {
+  if constexpr (N < 4 * HB) {
+    pe[N / HB][N % HB] = row_share_d<N>(ev);
+  } else if constexpr (N < 5 * HB) {
+    corr[N - 4 * HB] = row_share_d<N>(ev);
+  }
+}
+
+template <int HB, int... Ns>
+IRON_DEV void share_all(double ev, double (&pe)[4][HB], double (&corr)[HB],
+                        std::integer_sequence<int, Ns...>) {
+  (share_one<Ns, HB>(ev, pe, corr), ...);
+}
+
+IRON_DEV double pick(const double* vals, int idx, int n) {
+  double r = vals[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i)
+    if (i < n && idx == i) r = vals[i];
+  return r;
+}
+
+template <int HB>
 __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
-  const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
+  const int split = blockIdx.x, b = blockIdx.z;
+  const int groups = p.HG / HB;
+  const int kv = blockIdx.y / groups, hg = blockIdx.y % groups;
+  const int h0 = kv * p.HG + hg * HB;  // first query head of this workgroup
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row = lane >> 4, dl = lane & 15;
 
@@ -53,25 +86,25 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   const int t_begin = split * p.chunk;
   const int t_end = min(ctx, t_begin + p.chunk);
 
-  float qf[HG][8];
+  double qf[HB][8];
 #pragma unroll
-  for (int h = 0; h < HG; ++h) {
-    const uint4 qq = *(const uint4*)(p.q + ((size_t)b * p.H + (size_t)kv * HG + h) * kD + dl * 8);
+  for (int h = 0; h < HB; ++h) {
+    const uint4 qq = *(const uint4*)(p.q + ((size_t)b * p.H + h0 + h) * kD + dl * 8);
     const uint32_t qd[4] = {qq.x, qq.y, qq.z, qq.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      qf[h][2 * j] = bf16lo_to_f32(qd[j]) * p.scale_log2;
-      qf[h][2 * j + 1] = bf16hi_to_f32(qd[j]) * p.scale_log2;
+      qf[h][2 * j] = bf16lo_to_f32(qd[j]);
+      qf[h][2 * j + 1] = bf16hi_to_f32(qd[j]);
     }
   }
 
-  float m[HG], l[HG], o[HG][8];
+  double m[HB], l[HB], o[HB][8];
 #pragma unroll
-  for (int h = 0; h < HG; ++h) {
+  for (int h = 0; h < HB; ++h) {
     m[h] = -INFINITY;
-    l[h] = 0.f;
+    l[h] = 0.0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[h][j] = 0.f;
+    for (int j = 0; j < 8; ++j) o[h][j] = 0.0;
   }
 
   const uint16_t* kbase = p.k + (size_t)b * p.sb + (size_t)kv * p.sh + dl * 8;
@@ -92,78 +125,116 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
         vr[u] = make_uint4(0u, 0u, 0u, 0u);
       }
     }
-    float s[4][HG];
+    // scores s[u][h], identical in every lane of the row
+    double s[4][HB];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const uint32_t kd[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
-      float kf[8];
+      double kf[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         kf[2 * j] = bf16lo_to_f32(kd[j]);
         kf[2 * j + 1] = bf16hi_to_f32(kd[j]);
       }
 #pragma unroll
-      for (int h = 0; h < HG; ++h) {
-        float a = 0.f;
+      for (int h = 0; h < HB; ++h) {
+        double a = 0.0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a = fmaf(qf[h][j], kf[j], a);
-        a = row16_sum(a);
+        for (int j = 0; j < 8; ++j) a = fma(qf[h][j], kf[j], a);
+        a = row16_sum_d(a) * p.scale;
         s[u][h] = tv[u] ? a : -INFINITY;
       }
     }
+    // new running max per head (row-uniform)
+    double mn[HB];
+    bool any = false;
 #pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      const float mb = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
-      const float mn = fmaxf(m[h], mb);
-      if (mn == -INFINITY) continue;  // row-uniform: no valid token yet
-      const float c = safe_exp2_diff(m[h], mn);
-      l[h] *= c;
+    for (int h = 0; h < HB; ++h) {
+      const double mb = fmax(fmax(s[0][h], s[1][h]), fmax(s[2][h], s[3][h]));
+      mn[h] = fmax(m[h], mb);
+      any |= mn[h] != -INFINITY;
+    }
+    if (!any) continue;  // row-uniform: no valid token in this row yet
+    // lane dl evaluates one exponential: (u, h) = (dl / HB, dl % HB) for dl < 4*HB, the
+    // correction e^(m_old - m_new) of head dl - 4*HB for 4*HB <= dl < 5*HB
+    double arg = -INFINITY;
+    {
+      double vals[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) vals[i] = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int h = 0; h < HB; ++h) vals[u * HB + h] = s[u][h] - mn[h];
+#pragma unroll
+      for (int h = 0; h < HB; ++h)
+        if (4 * HB + h < 16) vals[4 * HB + h] = (m[h] == -INFINITY) ? -INFINITY : m[h] - mn[h];
+      arg = pick(vals, dl, 5 * HB);
+    }
+    // exp(-inf) = 0 covers invalid tokens and heads with no valid token (mn == -inf makes the
+    // argument NaN only when both sides are -inf, which the guard above excludes for m)
+    const double ev = (arg == -INFINITY || arg != arg) ? 0.0 : exp(arg);
+    double pe[4][HB], corr[HB];
+    share_all<HB>(ev, pe, corr, std::make_integer_sequence<int, 16>{});
+    if constexpr (HB >= 4) {
+      // 5*HB = 20 > 16 lanes: the last four corrections are computed directly
+#pragma unroll
+      for (int h = 0; h < HB; ++h)
+        if (4 * HB + h >= 16) corr[h] = (m[h] == -INFINITY) ? 0.0 : exp(m[h] - mn[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      if (mn[h] == -INFINITY) continue;
+      const double c = (m[h] == -INFINITY) ? 0.0 : corr[h];
+      l[h] = l[h] * c + ((pe[0][h] + pe[1][h]) + (pe[2][h] + pe[3][h]));
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[h][j] *= c;
+      m[h] = mn[h];
+    }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float pu = safe_exp2_diff(s[u][h], mn);
-        l[h] += pu;
-        const uint32_t vd[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t vd[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+      double vf[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          o[h][2 * j] = fmaf(pu, bf16lo_to_f32(vd[j]), o[h][2 * j]);
-          o[h][2 * j + 1] = fmaf(pu, bf16hi_to_f32(vd[j]), o[h][2 * j + 1]);
-        }
+      for (int j = 0; j < 4; ++j) {
+        vf[2 * j] = bf16lo_to_f32(vd[j]);
+        vf[2 * j + 1] = bf16hi_to_f32(vd[j]);
       }
-      m[h] = mn;
+#pragma unroll
+      for (int h = 0; h < HB; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[h][j] = fma(pe[u][h], vf[j], o[h][j]);
     }
   }
 
-  // Merge the 4 token rows of this wavefront (lanes l, l^16, l^32, l^48 share head dims).
+  // merge the 4 token rows of this wavefront (lanes l, l^16, l^32, l^48 share head dims)
 #pragma unroll
   for (int step = 16; step <= 32; step <<= 1) {
 #pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      const float mo = __shfl_xor(m[h], step);
-      const float lo = __shfl_xor(l[h], step);
-      float oo[8];
+    for (int h = 0; h < HB; ++h) {
+      const double mo = __shfl_xor(m[h], step);
+      const double lo = __shfl_xor(l[h], step);
+      double oo[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) oo[j] = __shfl_xor(o[h][j], step);
-      const float mn = fmaxf(m[h], mo);
-      if (mn != -INFINITY) {
-        const float c1 = safe_exp2_diff(m[h], mn), c2 = safe_exp2_diff(mo, mn);
+      const double mm = fmax(m[h], mo);
+      if (mm != -INFINITY) {
+        const double c1 = m[h] == -INFINITY ? 0.0 : exp(m[h] - mm);
+        const double c2 = mo == -INFINITY ? 0.0 : exp(mo - mm);
         l[h] = l[h] * c1 + lo * c2;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[h][j] = o[h][j] * c1 + oo[j] * c2;
-        m[h] = mn;
+        m[h] = mm;
       }
     }
   }
 
-  // Merge the 4 wavefronts through LDS.
-  __shared__ float s_o[4][HG][kD];
-  __shared__ float s_m[4][HG], s_l[4][HG];
-  __shared__ float s_f[64][HG];  // split weights for the final merge
-  __shared__ float s_L[HG];
+  // merge the 4 wavefronts through LDS
+  __shared__ double s_o[4][HB][kD];
+  __shared__ double s_m[4][HB], s_l[4][HB];
   if (row == 0) {
 #pragma unroll
-    for (int h = 0; h < HG; ++h) {
+    for (int h = 0; h < HB; ++h) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) s_o[wave][h][dl * 8 + j] = o[h][j];
       if (dl == 0) {
@@ -173,102 +244,93 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-
-  const int HGD = HG * kD;
-  // Each thread owns HGD/256 outputs (one for HG <= 2).
-  for (int t = threadIdx.x; t < HGD; t += 256) {
-    const int oh = t / kD;
-    const int od = t % kD;
-    float M = -INFINITY;
+  for (int t = threadIdx.x; t < HB * kD; t += 256) {
+    const int oh = t / kD, od = t % kD;
+    double M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w][oh]);
-    float L = 0.f, O = 0.f;
+    for (int w = 0; w < 4; ++w) M = fmax(M, s_m[w][oh]);
+    double L = 0.0, O = 0.0;
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const float f = safe_exp2_diff(s_m[w][oh], M);
+        const double f = s_m[w][oh] == -INFINITY ? 0.0 : exp(s_m[w][oh] - M);
         L += f * s_l[w][oh];
         O += f * s_o[w][oh][od];
       }
     }
+    const int hq = h0 + oh;
     if (p.nsplit == 1) {
-      const float r = L > 0.f ? O / L : 0.f;
-      p.out[((size_t)b * p.H + (size_t)kv * HG + oh) * kD + od] = f32_to_bf16(r);
+      p.out[((size_t)b * p.H + hq) * kD + od] = f64_to_bf16(L > 0.0 ? O / L : 0.0);
     } else {
-      float* part = p.part + (((size_t)b * p.KV + kv) * p.nsplit + split) * (HG * (kD + 2));
-      part[oh * kD + od] = O;
+      double* part = p.part + (((size_t)b * p.H + hq) * p.nsplit + split) * (kD + 2);
+      part[od] = O;
       if (od == 0) {
-        part[HGD + oh] = M;
-        part[HGD + HG + oh] = L;
+        part[kD] = M;
+        part[kD + 1] = L;
       }
     }
   }
-  if (p.nsplit == 1) return;
+}
 
-  if (!arrive_is_last(p.cnt + (size_t)b * p.KV + kv, (unsigned)p.nsplit)) return;
-
-  // Last workgroup of this (b, kv): merge the nsplit partials.
-  const float* base = p.part + ((size_t)b * p.KV + kv) * p.nsplit * (HG * (kD + 2));
+// grid (H, B), 128 threads: o = sum_s f_s O_s / sum_s f_s L_s, f_s = e^(m_s - max m).
+__global__ __launch_bounds__(128) void attn_merge_kernel(AttnParams p) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int ns = p.nsplit;
-  __shared__ float s_red[4];
-  for (int h = 0; h < HG; ++h) {
-    // split weights f_s = exp2(m_s - M), L = sum f_s l_s
-    float mloc = -INFINITY;
-    for (int sidx = threadIdx.x; sidx < ns; sidx += 256)
-      mloc = fmaxf(mloc, base[(size_t)sidx * (HG * (kD + 2)) + HGD + h]);
-    mloc = wave_max(mloc);
-    if (lane == 0) s_red[wave] = mloc;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    __syncthreads();
-    float lloc = 0.f;
-    for (int sidx = threadIdx.x; sidx < ns; sidx += 256) {
-      const float* ps = base + (size_t)sidx * (HG * (kD + 2));
-      const float ms = ps[HGD + h];
-      const float f = (M == -INFINITY || ms == -INFINITY) ? 0.f : exp2f(ms - M);
-      s_f[sidx][h] = f;
-      lloc += f * ps[HGD + HG + h];
-    }
-    lloc = block_sum_256(lloc, s_red);
-    if (threadIdx.x == 0) s_L[h] = lloc;
-    __syncthreads();
+  const double* base = p.part + ((size_t)b * p.H + h) * ns * (kD + 2);
+  __shared__ double s_f[256];
+  __shared__ double s_red[2];
+  double mloc = -INFINITY;
+  for (int s = d; s < ns; s += 128) mloc = fmax(mloc, base[(size_t)s * (kD + 2) + kD]);
+  // block max over 2 wavefronts
+  mloc = fmax(mloc, __shfl_xor(mloc, 1));
+  mloc = fmax(mloc, __shfl_xor(mloc, 2));
+  mloc = fmax(mloc, __shfl_xor(mloc, 4));
+  mloc = fmax(mloc, __shfl_xor(mloc, 8));
+  mloc = fmax(mloc, __shfl_xor(mloc, 16));
+  mloc = fmax(mloc, __shfl_xor(mloc, 32));
+  if ((d & 63) == 0) s_red[d >> 6] = mloc;
+  __syncthreads();
+  const double M = fmax(s_red[0], s_red[1]);
+  __syncthreads();
+  double lloc = 0.0;
+  for (int s = d; s < ns; s += 128) {
+    const double ms = base[(size_t)s * (kD + 2) + kD];
+    const double f = (M == -INFINITY || ms == -INFINITY) ? 0.0 : exp(ms - M);
+    s_f[s] = f;
+    lloc += f * base[(size_t)s * (kD + 2) + kD + 1];
   }
-  for (int t = threadIdx.x; t < HGD; t += 256) {
-    const int h = t / kD, d = t % kD;
-    float O0 = 0.f, O1 = 0.f, O2 = 0.f, O3 = 0.f;
-    int sidx = 0;
-    for (; sidx + 4 <= ns; sidx += 4) {
-      const float* ps = base + (size_t)sidx * (HG * (kD + 2)) + h * kD + d;
-      const size_t S = HG * (kD + 2);
-      O0 = fmaf(s_f[sidx][h], ps[0], O0);
-      O1 = fmaf(s_f[sidx + 1][h], ps[S], O1);
-      O2 = fmaf(s_f[sidx + 2][h], ps[2 * S], O2);
-      O3 = fmaf(s_f[sidx + 3][h], ps[3 * S], O3);
-    }
-    for (; sidx < ns; ++sidx)
-      O0 = fmaf(s_f[sidx][h], base[(size_t)sidx * (HG * (kD + 2)) + h * kD + d], O0);
-    const float L = s_L[h];
-    const float O = (O0 + O1) + (O2 + O3);
-    const float r = L > 0.f ? O / L : 0.f;
-    p.out[((size_t)b * p.H + (size_t)kv * HG + h) * kD + d] = f32_to_bf16(r);
+  lloc = wave_sum_d(lloc);
+  if ((d & 63) == 0) s_red[d >> 6] = lloc;
+  __syncthreads();
+  const double L = s_red[0] + s_red[1];
+  double O0 = 0.0, O1 = 0.0;
+  int s = 0;
+  for (; s + 2 <= ns; s += 2) {
+    O0 = fma(s_f[s], base[(size_t)s * (kD + 2) + d], O0);
+    O1 = fma(s_f[s + 1], base[(size_t)(s + 1) * (kD + 2) + d], O1);
   }
+  if (s < ns) O0 = fma(s_f[s], base[(size_t)s * (kD + 2) + d], O0);
+  const double O = O0 + O1;
+  p.out[((size_t)b * p.H + h) * kD + d] = f64_to_bf16(L > 0.0 ? O / L : 0.0);
 }
 
 struct SplitPlan {
-  int nsplit, chunk;
+  int nsplit, chunk, hb;
 };
 
-SplitPlan plan_split(int B, int KV, int max_ctx) {
+SplitPlan plan_split(int B, int H, int KV, int max_ctx) {
   SplitPlan sp;
-  const int target_wgs = 256;
-  int ns = (target_wgs + B * KV - 1) / (B * KV);
-  const int max_ns = (max_ctx + 63) / 64;
+  const int HG = H / KV;
+  sp.hb = HG >= 4 ? 4 : HG;
+  const int wg_per_split = B * KV * (HG / sp.hb);
+  const int target_wgs = 512;
+  int ns = (target_wgs + wg_per_split - 1) / wg_per_split;
+  const int max_ns = (max_ctx + kTokensPerIter - 1) / kTokensPerIter;
   if (ns > max_ns) ns = max_ns;
-  if (ns > 64) ns = 64;
+  if (ns > 256) ns = 256;
   if (ns < 1) ns = 1;
   int chunk = (max_ctx + ns - 1) / ns;
-  chunk = ((chunk + 63) / 64) * 64;
-  if (chunk < 64) chunk = 64;
+  chunk = ((chunk + kTokensPerIter - 1) / kTokensPerIter) * kTokensPerIter;
   ns = (max_ctx + chunk - 1) / chunk;
   if (ns < 1) ns = 1;
   sp.nsplit = ns;
@@ -277,11 +339,9 @@ SplitPlan plan_split(int B, int KV, int max_ctx) {
 }
 
 size_t attn_ws_bytes(int B, int H, int KV, int max_ctx) {
-  const SplitPlan sp = plan_split(B, KV, max_ctx);
-  const int HG = H / KV;
-  size_t part = (size_t)B * KV * sp.nsplit * HG * (kD + 2) * sizeof(float);
-  part = (part + 255) & ~(size_t)255;
-  return part + (size_t)B * KV * sizeof(unsigned int) + 256;
+  const SplitPlan sp = plan_split(B, H, KV, max_ctx);
+  if (sp.nsplit == 1) return 0;
+  return (((size_t)B * H * sp.nsplit * (kD + 2) * sizeof(double)) + 255) & ~(size_t)255;
 }
 
 }  // namespace
@@ -290,7 +350,8 @@ extern "C" {
 
 size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx) {
   if (B <= 0 || H <= 0 || KV <= 0 || D != kD || H % KV || max_ctx <= 0) return 0;
-  return attn_ws_bytes(B, H, KV, max_ctx);
+  const size_t n = attn_ws_bytes(B, H, KV, max_ctx);
+  return n ? n : 256;
 }
 
 int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
@@ -306,14 +367,15 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
   if (D != kD) return iron::fail(IRON_ERR_UNSUPPORTED, "%s: head_dim %d (only 128)", fn, D);
   if (H % KV) return iron::fail(IRON_ERR_SHAPE, "%s: H=%d not a multiple of KV=%d", fn, H, KV);
   const int HG = H / KV;
-  if (HG != 1 && HG != 2 && HG != 4 && HG != 8)
-    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: GQA group %d not in {1,2,4,8}", fn, HG);
+  if (HG != 1 && HG != 2 && HG % 4 != 0)
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: GQA group %d not 1, 2 or a multiple of 4", fn,
+                      HG);
   if (kv_st % 8 || kv_sh % 8 || kv_sb % 8 || !iron::aligned(k_cache, 16) ||
       !iron::aligned(v_cache, 16) || !iron::aligned(q, 16))
     return iron::fail(IRON_ERR_ALIGN, "%s: K/V/Q rows must be 16-byte aligned", fn);
   if (!ctx_len && (ctx_const < 0 || ctx_const > max_ctx))
     return iron::fail(IRON_ERR_SHAPE, "%s: ctx_const=%d outside [0, %d]", fn, ctx_const, max_ctx);
-  const SplitPlan sp = plan_split(B, KV, max_ctx);
+  const SplitPlan sp = plan_split(B, H, KV, max_ctx);
   AttnParams p = {};
   p.q = q;
   p.k = k_cache;
@@ -327,9 +389,11 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
   p.out = out;
   p.H = H;
   p.KV = KV;
+  p.HG = HG;
+  p.HB = sp.hb;
   p.chunk = sp.chunk;
   p.nsplit = sp.nsplit;
-  p.scale_log2 = scale * 1.4426950408889634f;
+  p.scale = (double)scale;
   if (sp.nsplit > 1) {
     const size_t need = attn_ws_bytes(B, H, KV, max_ctx);
     if (!workspace || workspace_bytes < need)
@@ -337,19 +401,18 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
                         need);
     if (!iron::aligned(workspace, 256))
       return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
-    size_t part = (size_t)B * KV * sp.nsplit * HG * (kD + 2) * sizeof(float);
-    part = (part + 255) & ~(size_t)255;
-    p.part = (float*)workspace;
-    p.cnt = (unsigned int*)((char*)workspace + part);
+    p.part = (double*)workspace;
   }
-  dim3 grid(sp.nsplit, KV, B);
+  dim3 grid(sp.nsplit, KV * (HG / sp.hb), B);
   hipStream_t s = (hipStream_t)stream;
-  switch (HG) {
+  switch (sp.hb) {
     case 1: hipLaunchKernelGGL(decode_attn_kernel<1>, grid, dim3(256), 0, s, p); break;
     case 2: hipLaunchKernelGGL(decode_attn_kernel<2>, grid, dim3(256), 0, s, p); break;
-    case 4: hipLaunchKernelGGL(decode_attn_kernel<4>, grid, dim3(256), 0, s, p); break;
-    default: hipLaunchKernelGGL(decode_attn_kernel<8>, grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL(decode_attn_kernel<4>, grid, dim3(256), 0, s, p); break;
   }
+  int st = iron::check_launch(fn);
+  if (st || sp.nsplit == 1) return st;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(H, B), dim3(128), 0, s, p);
   return iron::check_launch(fn);
 }
 

@@ -28,6 +28,10 @@ IRON_DEV uint16_t f32_to_bf16(float f) {
 }
 IRON_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// fp64 -> bf16 goes through fp32 (RNE at each step), the conversion path torch uses for a
+// float64 tensor cast to bfloat16, so device results and the fp64 oracle round identically.
+IRON_DEV uint16_t f64_to_bf16(double d) { return f32_to_bf16((float)d); }
+
 // ---------------------------------------------------------------------------------------------
 // Wavefront reductions (wave64) with DPP.
 // ---------------------------------------------------------------------------------------------
@@ -69,6 +73,49 @@ IRON_DEV float wave_max(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
   v = fmaxf(v, __shfl_xor(v, 32));
   return v;
+}
+
+// ---- fp64 variants: DPP moves 32 bits, so a double is moved as two halves.
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+IRON_DEV double dpp_d(double v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, ROW_MASK, BANK_MASK, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, ROW_MASK, BANK_MASK, false);
+  return __hiloint2double(hi, lo);
+}
+
+IRON_DEV double row16_sum_d(double v) {
+  v += dpp_d<0xb1>(v);
+  v += dpp_d<0x4e>(v);
+  v += dpp_d<0x141>(v);
+  v += dpp_d<0x140>(v);
+  return v;
+}
+
+IRON_DEV double wave_sum_d(double v) {
+  v = row16_sum_d(v);
+  v += dpp_d<0x142, 0xa>(v);
+  v += dpp_d<0x143, 0xc>(v);
+  const int lo = __builtin_amdgcn_readlane(__double2loint(v), 63);
+  const int hi = __builtin_amdgcn_readlane(__double2hiint(v), 63);
+  return __hiloint2double(hi, lo);
+}
+
+IRON_DEV double row16_max_d(double v) {
+  v = fmax(v, dpp_d<0xb1>(v));
+  v = fmax(v, dpp_d<0x4e>(v));
+  v = fmax(v, dpp_d<0x141>(v));
+  v = fmax(v, dpp_d<0x140>(v));
+  return v;
+}
+
+// Block-wide fp64 sum for blockDim.x == 256. `scratch` holds >= 4 doubles of LDS.
+IRON_DEV double block_sum_256_d(double v, double* scratch) {
+  v = wave_sum_d(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+  __syncthreads();
+  return (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
 }
 
 // Block-wide sum for blockDim.x == 256 (4 waves). `scratch` holds >= 4 floats of LDS.

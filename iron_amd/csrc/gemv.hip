@@ -8,19 +8,20 @@
 // Weight wire (the reference's own packing, gemv_int8/reference.py:59-80): consecutive
 // row-blocks of `tile_m` rows, each block = tile_m*K int8 payload (row-major) followed by
 // tile_m*(K/G) bf16 group scales (row-major). The payload domain is signed two's-complement q or
-// biased q+128; both feed the same integer q.
+// biased q+128; both carry the same integer q.
 //
-// Arithmetic (the exact-dequant golden of GEMVInt8.reference, gemv_int8/op.py:173-178):
-//     y[b][m] = sum_g s[m][g] * sum_{k in g} q[m][k] * x[b][k]     (fp32), one bf16 rounding.
-// Every product q*s*x is exact in fp32 (8 x 8 x 8 significant bits), so this matches the golden
-// to fp32 summation order. The inner loop reads the payload as u = q+128 (XOR 0x80 for the
-// signed domain, a single v_cvt_f32_ubyteN per weight) and removes the bias per group with the
-// lane's precomputed sum of x: sum q*x = sum u*x - 128*sum x.
+// Arithmetic: the exact value of the reference golden GEMVInt8.reference (gemv_int8/op.py:
+// 173-178), y[b][m] = sum_g s[m][g] * sum_{k in g} q[m][k] * x[b][k], accumulated in fp64 (every
+// product q*x is exact in fp64 and so is the accumulation to within 2^-53), then one rounding to
+// the output type. Non-packed fp64 FMA issues at the fp32 FMA rate on CDNA4, so exactness costs
+// one extra convert per weight, and it makes the device result equal the correctly rounded
+// value the fp64 oracle computes, not merely close to it.
 //
-// Mapping: 256-thread workgroups, 4 wavefronts, each wavefront owns R consecutive rows; lane l
-// reads 16 consecutive K elements (one 128-bit load) per 1024-wide chunk, so one wavefront load
-// instruction covers 1 KiB of one row, fully coalesced. x is staged once per workgroup in LDS
-// as fp32 by a prologue that can also fuse RMSNorm / residual adds.
+// Mapping: 256-thread workgroups (4 wavefronts); each wavefront owns R consecutive rows and each
+// lane one 16-byte slice of every 1024-wide (int8) or 512-wide (bf16) chunk of those rows, so a
+// wavefront load instruction reads 1 KiB of one row. A workgroup owns one group of 4*R rows: it
+// first issues every weight/scale load of the group (R*NCH 128-bit loads per lane, all in
+// flight), then stages x into LDS (the prologue, overlapping the weight latency), then reduces.
 #include "common.h"
 #include "internal.h"
 
@@ -29,16 +30,16 @@ namespace {
 enum Prologue : int {
   PRO_BF16 = 0,        // xs = x                                   (x bf16)
   PRO_RMS_BF16 = 1,    // xs = bf16(rmsnorm(x) * w)                (fused RMSNorm, bf16 boundary)
-  PRO_RES_RMS_F32 = 2, // xs = rmsnorm(x + x2) * w  in fp32        (SwiGLU MLP: x1 = cur + a)
+  PRO_RES_RMS_F32 = 2, // xs = f32(rmsnorm(f32(x + x2)) * w)       (SwiGLU MLP: x1 = cur + a)
   PRO_F32 = 3,         // xs = x                                   (x fp32)
 };
 
 enum Epilogue : int {
   EPI_BF16 = 0,        // y = bf16(acc)
-  EPI_F32 = 1,         // y = acc (fp32)
-  EPI_RES_BF16 = 2,    // y = bf16((r1 + r2) + acc)                (down GEMV + residual)
-  EPI_SWIGLU_F32 = 3,  // y = silu(acc_gate) * acc_up (fp32)       (dual matrix)
-  EPI_BF16_ARGMAX = 4, // y = bf16(acc), plus atomic argmax of the bf16 value
+  EPI_F32 = 1,         // y = f32(acc)
+  EPI_RES_BF16 = 2,    // y = bf16(f32(r1 + r2) + acc)             (down GEMV + residual)
+  EPI_SWIGLU_F32 = 3,  // y = f32(silu(acc_gate) * acc_up)         (dual matrix)
+  EPI_BF16_ARGMAX = 4, // y = bf16(acc), plus the argmax key of the bf16 values
 };
 
 struct GemvParams {
@@ -47,7 +48,7 @@ struct GemvParams {
   int M, K, gshift, tile_m;
   FastDiv tdiv;
   uint32_t blk_bytes;
-  uint32_t xor_mask;    // 0x80808080 for the signed domain, 0 for biased
+  uint32_t xor_mask;    // 0x80808080 for the biased domain (turns q+128 into q), 0 for signed
   // prologue
   int pro;
   const void* x;        // [B][x_stride] bf16 or fp32
@@ -66,34 +67,67 @@ struct GemvParams {
 };
 
 // ------------------------------------------------------------------------------------------
-// Prologue: stage B vectors of length K into LDS as fp32.
+// Prologue: stage B vectors of length K into LDS as fp64 (K % 8 == 0, 16-byte aligned rows).
 // ------------------------------------------------------------------------------------------
+IRON_DEV void unpack8(const uint4 v, float (&f)[8]) {
+  f[0] = bf16lo_to_f32(v.x); f[1] = bf16hi_to_f32(v.x);
+  f[2] = bf16lo_to_f32(v.y); f[3] = bf16hi_to_f32(v.y);
+  f[4] = bf16lo_to_f32(v.z); f[5] = bf16hi_to_f32(v.z);
+  f[6] = bf16lo_to_f32(v.w); f[7] = bf16hi_to_f32(v.w);
+}
+
 template <int B>
-__device__ void stage_x(const GemvParams& p, float* __restrict__ xs, float* red) {
+__device__ void stage_x(const GemvParams& p, double* __restrict__ xs, double* red) {
   const int K = p.K;
+  const int n8 = K >> 3;
   for (int b = 0; b < B; ++b) {
-    float* dst = xs + (size_t)b * K;
+    double* dst = xs + (size_t)b * K;
     if (p.pro == PRO_F32) {
-      const float* src = (const float*)p.x + (size_t)b * p.x_stride;
-      for (int i = threadIdx.x; i < K; i += blockDim.x) dst[i] = src[i];
-    } else if (p.pro == PRO_BF16) {
-      const uint16_t* src = (const uint16_t*)p.x + (size_t)b * p.x_stride;
-      for (int i = threadIdx.x; i < K; i += blockDim.x) dst[i] = bf16_to_f32(src[i]);
-    } else {
-      const uint16_t* src = (const uint16_t*)p.x + (size_t)b * p.x_stride;
-      const uint16_t* src2 = p.x2 ? p.x2 + (size_t)b * p.x2_stride : nullptr;
-      float ss = 0.f;
-      for (int i = threadIdx.x; i < K; i += blockDim.x) {
-        float v = bf16_to_f32(src[i]);
-        if (src2) v += bf16_to_f32(src2[i]);
-        dst[i] = v;
-        ss = fmaf(v, v, ss);
+      const float4* src = (const float4*)((const float*)p.x + (size_t)b * p.x_stride);
+      for (int i = threadIdx.x; i < (K >> 2); i += 256) {
+        const float4 v = src[i];
+        dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
       }
-      ss = block_sum_256(ss, red);
-      const float inv = 1.0f / sqrtf(ss / (float)K + p.eps);
-      for (int i = threadIdx.x; i < K; i += blockDim.x) {
-        float v = dst[i] * inv * bf16_to_f32(p.nw[i]);
-        dst[i] = (p.pro == PRO_RMS_BF16) ? round_bf16(v) : v;
+      continue;
+    }
+    const uint4* src = (const uint4*)((const uint16_t*)p.x + (size_t)b * p.x_stride);
+    if (p.pro == PRO_BF16) {
+      for (int i = threadIdx.x; i < n8; i += 256) {
+        float f[8];
+        unpack8(src[i], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[8 * i + j] = f[j];
+      }
+      continue;
+    }
+    const uint4* src2 = p.x2 ? (const uint4*)(p.x2 + (size_t)b * p.x2_stride) : nullptr;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n8; i += 256) {
+      float f[8];
+      unpack8(src[i], f);
+      if (src2) {
+        float g[8];
+        unpack8(src2[i], g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = f[j] + g[j];   // x1 = cur + a, one fp32 rounding
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const double d = f[j];
+        dst[8 * i + j] = d;
+        ss = fma(d, d, ss);
+      }
+    }
+    ss = block_sum_256_d(ss, red);
+    const double inv = 1.0 / sqrt(ss / (double)K + (double)p.eps);
+    const uint4* wsrc = (const uint4*)p.nw;
+    for (int i = threadIdx.x; i < n8; i += 256) {
+      float wf[8];
+      unpack8(wsrc[i], wf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const double y = (dst[8 * i + j] * inv) * (double)wf[j];
+        dst[8 * i + j] = (p.pro == PRO_RMS_BF16) ? (double)round_bf16((float)y) : (double)(float)y;
       }
     }
   }
@@ -101,238 +135,275 @@ __device__ void stage_x(const GemvParams& p, float* __restrict__ xs, float* red)
 }
 
 // ------------------------------------------------------------------------------------------
-// int8 core: R rows x B vectors, full-row dot products (every lane ends with the totals).
+// Weight fetch: lane-resident 16-byte slices of R rows x NCH chunks (+ their group scales).
 // ------------------------------------------------------------------------------------------
-template <int B, int R>
-__device__ __forceinline__ void w8_rows(const GemvParams& p, const uint8_t* __restrict__ wire,
-                                        int row0, const float* __restrict__ xs, int lane,
-                                        float (&acc)[R][B]) {
+template <int R, int NCH>
+IRON_DEV void fetch_w8(const GemvParams& p, const uint8_t* __restrict__ wire, int row0, int lane,
+                       uint4 (&w)[R][NCH], float (&sc)[R][NCH]) {
   const int K = p.K;
   const int ng = K >> p.gshift;
-  const uint8_t* qrow[R];
-  const uint16_t* srow[R];
-  bool rv[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r;
-    rv[r] = row < p.M;
-    const uint32_t rr = rv[r] ? (uint32_t)row : 0u;
+    const bool rv = row < p.M;
+    const uint32_t rr = rv ? (uint32_t)row : 0u;
     const uint32_t blk = fastdiv(rr, p.tdiv);
     const uint32_t in = rr - blk * (uint32_t)p.tile_m;
     const uint8_t* base = wire + (size_t)blk * p.blk_bytes;
-    qrow[r] = base + (size_t)in * K;
-    srow[r] = (const uint16_t*)(base + (size_t)p.tile_m * K) + (size_t)in * ng;
+    const uint8_t* qrow = base + (size_t)in * K;
+    const uint16_t* srow = (const uint16_t*)(base + (size_t)p.tile_m * K) + (size_t)in * ng;
 #pragma unroll
-    for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
-  }
-
-  for (int c0 = 0; c0 < K; c0 += 1024) {
-    const int e = c0 + lane * 16;
-    const bool ev = e < K;
-    uint4 w[R];
-    float s[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (ev && rv[r]) {
-        w[r] = *(const uint4*)(qrow[r] + e);
-        s[r] = bf16_to_f32(srow[r][e >> p.gshift]);
+    for (int c = 0; c < NCH; ++c) {
+      const int e = c * 1024 + lane * 16;
+      if (rv && e < K) {
+        w[r][c] = *(const uint4*)(qrow + e);
+        sc[r][c] = bf16_to_f32(srow[e >> p.gshift]);
       } else {
-        w[r] = make_uint4(0x80808080u ^ p.xor_mask, 0x80808080u ^ p.xor_mask,
-                          0x80808080u ^ p.xor_mask, 0x80808080u ^ p.xor_mask);
-        s[r] = 0.f;
-      }
-    }
-    float xv[B][16];
-    float xsum[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      if (ev) {
-        const float4* src = (const float4*)(xs + (size_t)b * K + e);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float4 t = src[j];
-          xv[b][4 * j + 0] = t.x;
-          xv[b][4 * j + 1] = t.y;
-          xv[b][4 * j + 2] = t.z;
-          xv[b][4 * j + 3] = t.w;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) xv[b][j] = 0.f;
-      }
-      float t0 = 0.f, t1 = 0.f;
-#pragma unroll
-      for (int j = 0; j < 16; j += 2) {
-        t0 += xv[b][j];
-        t1 += xv[b][j + 1];
-      }
-      xsum[b] = t0 + t1;
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t d0 = w[r].x ^ p.xor_mask, d1 = w[r].y ^ p.xor_mask;
-      const uint32_t d2 = w[r].z ^ p.xor_mask, d3 = w[r].w ^ p.xor_mask;
-      const uint32_t dd[4] = {d0, d1, d2, d3};
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        float pa = 0.f, pb = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t d = dd[j];
-          pa = fmaf((float)(d & 0xffu), xv[b][4 * j + 0], pa);
-          pb = fmaf((float)((d >> 8) & 0xffu), xv[b][4 * j + 1], pb);
-          pa = fmaf((float)((d >> 16) & 0xffu), xv[b][4 * j + 2], pa);
-          pb = fmaf((float)(d >> 24), xv[b][4 * j + 3], pb);
-        }
-        acc[r][b] = fmaf(s[r], (pa + pb) - 128.f * xsum[b], acc[r][b]);
+        w[r][c] = make_uint4(p.xor_mask, p.xor_mask, p.xor_mask, p.xor_mask);  // q == 0
+        sc[r][c] = 0.f;
       }
     }
   }
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int b = 0; b < B; ++b) acc[r][b] = wave_sum(acc[r][b]);
 }
 
-// ------------------------------------------------------------------------------------------
-// bf16-weight core (row-major [M][K] bf16): lane l reads 8 consecutive K per 512-wide chunk.
-// ------------------------------------------------------------------------------------------
-template <int B, int R>
-__device__ __forceinline__ void w16_rows(const GemvParams& p, int row0,
-                                         const float* __restrict__ xs, int lane,
-                                         float (&acc)[R][B]) {
+IRON_DEV double sbyte(uint32_t d, int j) {
+  return (double)(int)(((int32_t)(d << (24 - 8 * j))) >> 24);
+}
+
+template <int B, int R, int NCH>
+IRON_DEV void dot_w8(const GemvParams& p, const uint4 (&w)[R][NCH], const float (&sc)[R][NCH],
+                     const double* __restrict__ xs, int lane, double (&acc)[R][B]) {
   const int K = p.K;
-  const uint16_t* W = (const uint16_t*)p.w;
-  bool rv[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    rv[r] = (row0 + r) < p.M;
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
-  }
-  for (int c0 = 0; c0 < K; c0 += 512) {
-    const int e = c0 + lane * 8;
-    const bool ev = e < K;
-    uint4 w[R];
+    for (int b = 0; b < B; ++b) acc[r][b] = 0.0;
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      w[r] = (ev && rv[r]) ? *(const uint4*)(W + (size_t)(row0 + r) * K + e)
-                           : make_uint4(0u, 0u, 0u, 0u);
-    float xv[B][8];
+  for (int c = 0; c < NCH; ++c) {
+    const int e = c * 1024 + lane * 16;
+    if (c * 1024 >= K) break;
+    double xv[B][16];
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      if (ev) {
-        const float4* src = (const float4*)(xs + (size_t)b * K + e);
-        float4 t0 = src[0], t1 = src[1];
-        xv[b][0] = t0.x; xv[b][1] = t0.y; xv[b][2] = t0.z; xv[b][3] = t0.w;
-        xv[b][4] = t1.x; xv[b][5] = t1.y; xv[b][6] = t1.z; xv[b][7] = t1.w;
+      if (e < K) {
+        const double2* src = (const double2*)(xs + (size_t)b * K + e);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const double2 t = src[j];
+          xv[b][2 * j] = t.x;
+          xv[b][2 * j + 1] = t.y;
+        }
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xv[b][j] = 0.f;
+        for (int j = 0; j < 16; ++j) xv[b][j] = 0.0;
       }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint32_t dd[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+      const uint32_t dd[4] = {w[r][c].x ^ p.xor_mask, w[r][c].y ^ p.xor_mask,
+                              w[r][c].z ^ p.xor_mask, w[r][c].w ^ p.xor_mask};
+      const double s = (double)sc[r][c];
 #pragma unroll
       for (int b = 0; b < B; ++b) {
-        float a = acc[r][b];
+        double pa = 0.0, pb = 0.0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          a = fmaf(bf16lo_to_f32(dd[j]), xv[b][2 * j], a);
-          a = fmaf(bf16hi_to_f32(dd[j]), xv[b][2 * j + 1], a);
+          pa = fma(sbyte(dd[j], 0), xv[b][4 * j + 0], pa);
+          pb = fma(sbyte(dd[j], 1), xv[b][4 * j + 1], pb);
+          pa = fma(sbyte(dd[j], 2), xv[b][4 * j + 2], pa);
+          pb = fma(sbyte(dd[j], 3), xv[b][4 * j + 3], pb);
         }
-        acc[r][b] = a;
+        acc[r][b] = fma(s, pa + pb, acc[r][b]);
       }
     }
   }
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int b = 0; b < B; ++b) acc[r][b] = wave_sum(acc[r][b]);
+    for (int b = 0; b < B; ++b) acc[r][b] = wave_sum_d(acc[r][b]);
+}
+
+// bf16 row-major weights: lane slices of 8 bf16 per 512-wide chunk.
+template <int R, int NCH>
+IRON_DEV void fetch_w16(const GemvParams& p, int row0, int lane, uint4 (&w)[R][NCH]) {
+  const uint16_t* W = (const uint16_t*)p.w;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int e = c * 512 + lane * 8;
+      w[r][c] = (row < p.M && e < p.K) ? *(const uint4*)(W + (size_t)row * p.K + e)
+                                       : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+}
+
+template <int B, int R, int NCH>
+IRON_DEV void dot_w16(const GemvParams& p, const uint4 (&w)[R][NCH],
+                      const double* __restrict__ xs, int lane, double (&acc)[R][B]) {
+  const int K = p.K;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < B; ++b) acc[r][b] = 0.0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e = c * 512 + lane * 8;
+    if (c * 512 >= K) break;
+    double xv[B][8];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      if (e < K) {
+        const double2* src = (const double2*)(xs + (size_t)b * K + e);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const double2 t = src[j];
+          xv[b][2 * j] = t.x;
+          xv[b][2 * j + 1] = t.y;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[b][j] = 0.0;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t dd[4] = {w[r][c].x, w[r][c].y, w[r][c].z, w[r][c].w};
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        double pa = 0.0, pb = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          pa = fma((double)bf16lo_to_f32(dd[j]), xv[b][2 * j], pa);
+          pb = fma((double)bf16hi_to_f32(dd[j]), xv[b][2 * j + 1], pb);
+        }
+        acc[r][b] += pa + pb;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < B; ++b) acc[r][b] = wave_sum_d(acc[r][b]);
 }
 
 IRON_DEV uint32_t bf16_order_key(uint16_t h) {
   return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);
 }
 
+// SiLU(g) * u in fp64 with the golden's numerically stable sigmoid
+// (iron/operators/swiglu_mlp_dp/reference.py:28-33).
+IRON_DEV double silu_mul(double g, double u) {
+  double sig;
+  if (g >= 0.0) {
+    sig = 1.0 / (1.0 + exp(-g));
+  } else {
+    const double e = exp(g);
+    sig = e / (1.0 + e);
+  }
+  return (g * sig) * u;
+}
+
 template <int B, int R>
-__device__ __forceinline__ void store_rows(const GemvParams& p, int row0, int lane,
-                                           const float (&acc)[R][B], const float (&acc2)[R][B],
-                                           unsigned long long (&best)[B]) {
+IRON_DEV void store_rows(const GemvParams& p, int row0, int lane, const double (&acc)[R][B],
+                         const double (&acc2)[R][B], unsigned long long (&best)[B]) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r;
     if (row >= p.M) continue;
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      const float v = acc[r][b];
+      const double v = acc[r][b];
       const size_t o = (size_t)b * p.y_stride + row;
       if (p.epi == EPI_BF16_ARGMAX) {
-        const uint16_t h = f32_to_bf16(v);
+        const uint16_t h = f64_to_bf16(v);
         const unsigned long long key =
             ((unsigned long long)bf16_order_key(h) << 32) | (unsigned long long)(~(uint32_t)row);
         best[b] = key > best[b] ? key : best[b];
         if (lane == r * B + b) ((uint16_t*)p.y)[o] = h;
       } else if (lane == r * B + b) {
         if (p.epi == EPI_BF16) {
-          ((uint16_t*)p.y)[o] = f32_to_bf16(v);
+          ((uint16_t*)p.y)[o] = f64_to_bf16(v);
         } else if (p.epi == EPI_F32) {
-          ((float*)p.y)[o] = v;
+          ((float*)p.y)[o] = (float)v;
         } else if (p.epi == EPI_RES_BF16) {
           const size_t ro = (size_t)b * p.r_stride + row;
           float x1 = bf16_to_f32(p.r1[ro]);
-          if (p.r2) x1 += bf16_to_f32(p.r2[ro]);
-          ((uint16_t*)p.y)[o] = f32_to_bf16(x1 + v);
+          if (p.r2) x1 = x1 + bf16_to_f32(p.r2[ro]);
+          ((uint16_t*)p.y)[o] = f64_to_bf16((double)x1 + v);
         } else {  // EPI_SWIGLU_F32
-          const float g = v;
-          const float sg = g / (1.0f + expf(-g));
-          ((float*)p.y)[o] = sg * acc2[r][b];
+          ((float*)p.y)[o] = (float)silu_mul(v, acc2[r][b]);
         }
       }
     }
   }
 }
 
-template <int B, int R, bool INT8>
+template <int B, int R, int NCH, bool INT8, bool DUAL>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
-  extern __shared__ float xs[];
-  __shared__ float red[8];
-  stage_x<B>(p, xs, red);
+  extern __shared__ double xs[];
+  __shared__ double red[4];
+  __shared__ unsigned long long s_best[4][4];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  unsigned long long best[B];
-#pragma unroll
-  for (int b = 0; b < B; ++b) best[b] = 0ull;
-  const int rows_per_wg = 4 * R;
-  for (int grp = blockIdx.x; grp * rows_per_wg < p.M; grp += gridDim.x) {
-    const int row0 = grp * rows_per_wg + wave * R;
-    if (row0 >= p.M) continue;
-    float acc[R][B];
-    float acc2[R][B];
-    if constexpr (INT8) {
-      w8_rows<B, R>(p, p.w, row0, xs, lane, acc);
-      if (p.epi == EPI_SWIGLU_F32) {
-        w8_rows<B, R>(p, p.w2, row0, xs, lane, acc2);
-      } else {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int b = 0; b < B; ++b) acc2[r][b] = 0.f;
-      }
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+
+  // 1. every weight load of this wavefront's rows goes out before the prologue
+  uint4 w[R][NCH];
+  float sc[R][NCH];
+  uint4 w2[DUAL ? R : 1][DUAL ? NCH : 1];
+  float sc2[DUAL ? R : 1][DUAL ? NCH : 1];
+  if constexpr (INT8) {
+    fetch_w8<R, NCH>(p, p.w, row0, lane, w, sc);
+    if constexpr (DUAL) fetch_w8<R, NCH>(p, p.w2, row0, lane, w2, sc2);
+  } else {
+    fetch_w16<R, NCH>(p, row0, lane, w);
+  }
+
+  // 2. stage x (its global-load latency overlaps the weight loads in flight)
+  stage_x<B>(p, xs, red);
+
+  // 3. reduce and store
+  double acc[R][B], acc2[R][B];
+  if constexpr (INT8) {
+    dot_w8<B, R, NCH>(p, w, sc, xs, lane, acc);
+    if constexpr (DUAL) {
+      dot_w8<B, R, NCH>(p, w2, sc2, xs, lane, acc2);
     } else {
-      w16_rows<B, R>(p, row0, xs, lane, acc);
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int b = 0; b < B; ++b) acc2[r][b] = 0.f;
+        for (int b = 0; b < B; ++b) acc2[r][b] = 0.0;
     }
-    store_rows<B, R>(p, row0, lane, acc, acc2, best);
-  }
-  if (p.epi == EPI_BF16_ARGMAX && lane == 0) {
+  } else {
+    dot_w16<B, R, NCH>(p, w, xs, lane, acc);
 #pragma unroll
-    for (int b = 0; b < B; ++b)
-      if (best[b]) atomicMax(p.argmax + b, best[b]);
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < B; ++b) acc2[r][b] = 0.0;
+  }
+  unsigned long long best[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) best[b] = 0ull;
+  if (row0 < p.M) store_rows<B, R>(p, row0, lane, acc, acc2, best);
+
+  if (p.epi == EPI_BF16_ARGMAX) {
+    // One candidate per workgroup; an atomic only when it beats the value already published
+    // (a stale read costs at most a redundant atomicMax, never a wrong result).
+    if (lane == 0) {
+#pragma unroll
+      for (int b = 0; b < B; ++b) s_best[wave][b] = best[b];
+    }
+    __syncthreads();
+    if (threadIdx.x < B) {
+      const int b = threadIdx.x;
+      unsigned long long k = s_best[0][b];
+      for (int i = 1; i < 4; ++i) k = s_best[i][b] > k ? s_best[i][b] : k;
+      const unsigned long long cur =
+          __hip_atomic_load(p.argmax + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (k > cur) atomicMax(p.argmax + b, k);
+    }
   }
 }
 
@@ -362,10 +433,10 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t d = dd[j];
-      const float q0 = (float)(int)((d & 0xffu)) - 128.f;
-      const float q1 = (float)(int)((d >> 8) & 0xffu) - 128.f;
-      const float q2 = (float)(int)((d >> 16) & 0xffu) - 128.f;
-      const float q3 = (float)(int)(d >> 24) - 128.f;
+      const float q0 = (float)(int)(((int32_t)(d << 24)) >> 24);
+      const float q1 = (float)(int)(((int32_t)(d << 16)) >> 24);
+      const float q2 = (float)(int)(((int32_t)(d << 8)) >> 24);
+      const float q3 = (float)(int)(((int32_t)d) >> 24);
       o[2 * j] = (uint32_t)f32_to_bf16(q0 * s) | ((uint32_t)f32_to_bf16(q1 * s) << 16);
       o[2 * j + 1] = (uint32_t)f32_to_bf16(q2 * s) | ((uint32_t)f32_to_bf16(q3 * s) << 16);
     }
@@ -376,37 +447,78 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
 }
 
 // ------------------------------------------------------------------------------------------
-// Host launch helpers
+// Host launch: choose (R, NCH) so that every lane keeps at most 16 weight slices in flight and
+// the grid has enough workgroups to cover the chip.
 // ------------------------------------------------------------------------------------------
-constexpr int kMaxLdsBytes = 131072;
+constexpr int kMaxLdsBytes = 147456;
+constexpr int kMaxSlices = 16;
 
-template <bool INT8>
+int round_pow2(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+template <bool INT8, bool DUAL, int B, int R, int NCH>
+void launch_one(const GemvParams& p, int grid, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((gemv_kernel<B, R, NCH, INT8, DUAL>), dim3(grid), dim3(256), lds, s, p);
+}
+
+template <bool INT8, bool DUAL, int B, int NCH>
+bool launch_r(const GemvParams& p, int R, int grid, size_t lds, hipStream_t s) {
+  constexpr int slices = DUAL ? 2 * NCH : NCH;
+  switch (R) {
+    case 1: launch_one<INT8, DUAL, B, 1, NCH>(p, grid, lds, s); return true;
+    case 2: if constexpr (2 * slices <= kMaxSlices) { launch_one<INT8, DUAL, B, 2, NCH>(p, grid, lds, s); return true; } break;
+    case 4: if constexpr (4 * slices <= kMaxSlices) { launch_one<INT8, DUAL, B, 4, NCH>(p, grid, lds, s); return true; } break;
+    case 8: if constexpr (8 * slices <= kMaxSlices) { launch_one<INT8, DUAL, B, 8, NCH>(p, grid, lds, s); return true; } break;
+  }
+  return false;
+}
+
+template <bool INT8, bool DUAL, int B>
+bool launch_nch(const GemvParams& p, int NCH, int R, int grid, size_t lds, hipStream_t s) {
+  switch (NCH) {
+    case 1: return launch_r<INT8, DUAL, B, 1>(p, R, grid, lds, s);
+    case 2: return launch_r<INT8, DUAL, B, 2>(p, R, grid, lds, s);
+    case 4: return launch_r<INT8, DUAL, B, 4>(p, R, grid, lds, s);
+    case 8: return launch_r<INT8, DUAL, B, 8>(p, R, grid, lds, s);
+    case 16: if constexpr (!DUAL) return launch_r<INT8, DUAL, B, 16>(p, R, grid, lds, s);
+  }
+  return false;
+}
+
+template <bool INT8, bool DUAL>
 int launch_gemv(const GemvParams& p, int B, hipStream_t stream, const char* fn) {
-  const size_t lds = (size_t)B * p.K * sizeof(float);
+  const size_t lds = (size_t)B * p.K * sizeof(double);
   if (lds > (size_t)kMaxLdsBytes)
     return iron::fail(IRON_ERR_UNSUPPORTED, "%s: B*K = %d*%d exceeds the LDS-staged GEMV limit",
                       fn, B, p.K);
-  // R = 4 rows per wavefront for small M (more workgroups), 8 for large M (more bytes in flight).
-  const bool big = p.M >= 65536;
-  const int rows_per_wg = 4 * (big ? 8 : 4);
-  long long groups = ((long long)p.M + rows_per_wg - 1) / rows_per_wg;
-  const int grid = (int)(groups < 16384 ? groups : 16384);
-#define IRON_GEMV_CASE(BB)                                                                     \
-  case BB:                                                                                     \
-    if (big)                                                                                   \
-      hipLaunchKernelGGL((gemv_kernel<BB, 8, INT8>), dim3(grid), dim3(256), lds, stream, p);   \
-    else                                                                                       \
-      hipLaunchKernelGGL((gemv_kernel<BB, 4, INT8>), dim3(grid), dim3(256), lds, stream, p);   \
-    break;
+  const int chunk = INT8 ? 1024 : 512;
+  const int NCH = round_pow2((p.K + chunk - 1) / chunk);
+  const int slices = (DUAL ? 2 : 1) * NCH;
+  if (slices > kMaxSlices)
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: K=%d too long for the resident-slice GEMV", fn,
+                      p.K);
+  // rows per wavefront: as many as the slice budget allows while the grid stays >= 2 waves of
+  // workgroups over the 256 CUs
+  int R = 1;
+  while (R < 8 && 2 * R * slices <= kMaxSlices &&
+         (long long)p.M >= (long long)4 * (2 * R) * 512)
+    R *= 2;
+  const long long groups = ((long long)p.M + 4 * R - 1) / (4 * R);
+  if (groups > (1ll << 30)) return iron::fail(IRON_ERR_SHAPE, "%s: M too large", fn);
+  const int grid = (int)groups;
+  bool ok = false;
   switch (B) {
-    IRON_GEMV_CASE(1)
-    IRON_GEMV_CASE(2)
-    IRON_GEMV_CASE(3)
-    IRON_GEMV_CASE(4)
+    case 1: ok = launch_nch<INT8, DUAL, 1>(p, NCH, R, grid, lds, stream); break;
+    case 2: ok = launch_nch<INT8, DUAL, 2>(p, NCH, R, grid, lds, stream); break;
+    case 3: ok = launch_nch<INT8, DUAL, 3>(p, NCH, R, grid, lds, stream); break;
+    case 4: ok = launch_nch<INT8, DUAL, 4>(p, NCH, R, grid, lds, stream); break;
     default:
       return iron::fail(IRON_ERR_UNSUPPORTED, "%s: batch %d > 4 needs the MFMA path", fn, B);
   }
-#undef IRON_GEMV_CASE
+  if (!ok) return iron::fail(IRON_ERR_UNSUPPORTED, "%s: no kernel for K=%d R=%d", fn, p.K, R);
   return iron::check_launch(fn);
 }
 
@@ -419,7 +531,7 @@ GemvParams wire_params(const void* wire, int M, int K, int G, int tile_m, int do
   p.tile_m = tile_m;
   p.tdiv = make_fastdiv((uint32_t)tile_m);
   p.blk_bytes = (uint32_t)iron::wire_block_bytes(K, G, tile_m);
-  p.xor_mask = domain == IRON_DOMAIN_SIGNED ? 0x80808080u : 0u;
+  p.xor_mask = domain == IRON_DOMAIN_BIASED ? 0x80808080u : 0u;
   return p;
 }
 
@@ -441,7 +553,7 @@ int gemv_swiglu_internal(const void* wg, const void* wu, const uint16_t* cur,
   p.epi = EPI_SWIGLU_F32;
   p.y = gh;
   p.y_stride = FF;
-  return launch_gemv<true>(p, B, stream, "iron_swiglu_mlp(gate/up)");
+  return launch_gemv<true, true>(p, B, stream, "iron_swiglu_mlp(gate/up)");
 }
 
 int gemv_down_internal(const void* wd, const float* gh, const uint16_t* cur, const uint16_t* a,
@@ -457,7 +569,7 @@ int gemv_down_internal(const void* wd, const float* gh, const uint16_t* cur, con
   p.r1 = cur;
   p.r2 = a;
   p.r_stride = D;
-  return launch_gemv<true>(p, B, stream, "iron_swiglu_mlp(down)");
+  return launch_gemv<true, false>(p, B, stream, "iron_swiglu_mlp(down)");
 }
 
 int gemv_rms_internal(const void* wire, const uint16_t* x, const uint16_t* nw, uint16_t* y,
@@ -472,7 +584,7 @@ int gemv_rms_internal(const void* wire, const uint16_t* x, const uint16_t* nw, u
   p.epi = EPI_BF16;
   p.y = y;
   p.y_stride = M;
-  return launch_gemv<true>(p, B, stream, fn);
+  return launch_gemv<true, false>(p, B, stream, fn);
 }
 
 int check_wire(const char* fn, const void* wire, int M, int K, int G, int tile_m, int domain) {
@@ -522,7 +634,7 @@ int iron_dequant_w8(const void* wire, uint16_t* w_out, int M, int K, int G, int 
                      (const uint8_t*)wire, w_out, M, K, iron::ilog2(G), tile_m,
                      make_fastdiv((uint32_t)tile_m),
                      (uint32_t)iron::wire_block_bytes(K, G, tile_m),
-                     domain == IRON_DOMAIN_SIGNED ? 0x80808080u : 0u);
+                     domain == IRON_DOMAIN_BIASED ? 0x80808080u : 0u);
   return iron::check_launch("iron_dequant_w8");
 }
 
@@ -534,6 +646,8 @@ int iron_gemv_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int
   if (!x || !y) return iron::fail(IRON_ERR_NULL, "iron_gemv_w8a16: x or y is null");
   if (B <= 0) return iron::fail(IRON_ERR_SHAPE, "iron_gemv_w8a16: batch %d must be positive", B);
   if (K % 16) return iron::fail(IRON_ERR_SHAPE, "iron_gemv_w8a16: K=%d must be a multiple of 16", K);
+  if (!iron::aligned(x, 16))
+    return iron::fail(IRON_ERR_ALIGN, "iron_gemv_w8a16: x not 16-byte aligned");
   GemvParams p = wire_params(wire, M, K, G, tile_m, domain);
   p.pro = PRO_BF16;
   p.x = x;
@@ -541,7 +655,7 @@ int iron_gemv_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int
   p.epi = EPI_BF16;
   p.y = y;
   p.y_stride = M;
-  return launch_gemv<true>(p, B, (hipStream_t)stream, "iron_gemv_w8a16");
+  return launch_gemv<true, false>(p, B, (hipStream_t)stream, "iron_gemv_w8a16");
 }
 
 int iron_gemv_bf16(const uint16_t* w, const uint16_t* x, uint16_t* y, int B, int M, int K,
@@ -550,7 +664,8 @@ int iron_gemv_bf16(const uint16_t* w, const uint16_t* x, uint16_t* y, int B, int
   if (!w || !x || !y) return iron::fail(IRON_ERR_NULL, "iron_gemv_bf16: null pointer");
   if (B <= 0 || M <= 0 || K <= 0 || K % 8)
     return iron::fail(IRON_ERR_SHAPE, "iron_gemv_bf16: bad shape B=%d M=%d K=%d", B, M, K);
-  if (!iron::aligned(w, 16)) return iron::fail(IRON_ERR_ALIGN, "iron_gemv_bf16: W not 16B aligned");
+  if (!iron::aligned(w, 16) || !iron::aligned(x, 16))
+    return iron::fail(IRON_ERR_ALIGN, "iron_gemv_bf16: W or x not 16B aligned");
   GemvParams p = {};
   p.w = (const uint8_t*)w;
   p.M = M;
@@ -561,7 +676,7 @@ int iron_gemv_bf16(const uint16_t* w, const uint16_t* x, uint16_t* y, int B, int
   p.epi = EPI_BF16;
   p.y = y;
   p.y_stride = M;
-  return launch_gemv<false>(p, B, (hipStream_t)stream, "iron_gemv_bf16");
+  return launch_gemv<false, false>(p, B, (hipStream_t)stream, "iron_gemv_bf16");
 }
 
 int iron_lm_head(const void* w, int w_kind, const uint16_t* x, const uint16_t* norm_w, float eps,
@@ -571,6 +686,8 @@ int iron_lm_head(const void* w, int w_kind, const uint16_t* x, const uint16_t* n
   if (!w || !x || !logits) return iron::fail(IRON_ERR_NULL, "iron_lm_head: null pointer");
   if (B <= 0 || V <= 0 || D <= 0 || D % 16)
     return iron::fail(IRON_ERR_SHAPE, "iron_lm_head: bad shape B=%d V=%d D=%d", B, V, D);
+  if (!iron::aligned(x, 16) || (norm_w && !iron::aligned(norm_w, 16)))
+    return iron::fail(IRON_ERR_ALIGN, "iron_lm_head: x / norm weight not 16B aligned");
   GemvParams p = {};
   if (w_kind == IRON_WEIGHT_INT8) {
     int st = iron::check_wire("iron_lm_head", w, V, D, G, tile_m, domain);
@@ -593,8 +710,9 @@ int iron_lm_head(const void* w, int w_kind, const uint16_t* x, const uint16_t* n
   p.y = logits;
   p.y_stride = V;
   p.argmax = argmax_keys;
-  if (w_kind == IRON_WEIGHT_INT8) return launch_gemv<true>(p, B, (hipStream_t)stream, "iron_lm_head");
-  return launch_gemv<false>(p, B, (hipStream_t)stream, "iron_lm_head");
+  if (w_kind == IRON_WEIGHT_INT8)
+    return launch_gemv<true, false>(p, B, (hipStream_t)stream, "iron_lm_head");
+  return launch_gemv<false, false>(p, B, (hipStream_t)stream, "iron_lm_head");
 }
 
 }  // extern "C"

@@ -34,41 +34,47 @@ struct QkvEpiParams {
   float eps;
 };
 
-// grid (Hq + 2*Hkv, B), 128 threads: one thread per head dimension.
+// grid (Hq + 2*Hkv, B), 128 threads: one thread per head dimension. fp64 math (the exact value
+// of the golden's closed forms), bf16 at the reference's boundaries: the normalised head and the
+// rotated head are each rounded once (qkv_head_dp/reference.py:27-32).
 __global__ __launch_bounds__(128) void qkv_epilogue_kernel(QkvEpiParams p) {
   const int head = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int nheads = p.Hq + 2 * p.Hkv;
+  // every global load is issued before the first reduction
   const uint16_t hraw = p.raw[((size_t)b * nheads + head) * kHD + d];
   const int pos = p.pos ? p.pos[b] : 0;
   const bool pos_ok = pos >= 0 && pos < p.max_seq;
-  if (head >= p.Hq + p.Hkv) {  // v head: copy the raw bf16 value into the cache
+  const bool is_v = head >= p.Hq + p.Hkv;
+  const uint16_t* nw = head < p.Hq ? p.n_qn : p.n_kn;
+  const uint16_t hw = is_v ? (uint16_t)0 : nw[d];
+  const int i = d & (kHD / 2 - 1);
+  const uint16_t* arow = p.ang + (size_t)(p.ang_by_pos ? (pos_ok ? pos : 0) : b) * kHD;
+  const uint16_t hc = is_v ? (uint16_t)0 : arow[2 * i];
+  const uint16_t hs = is_v ? (uint16_t)0 : arow[2 * i + 1];
+  if (is_v) {  // v head: the raw bf16 value goes to the cache unchanged
     const int hv = head - p.Hq - p.Hkv;
     if (pos_ok) p.v_cache[(size_t)b * p.sb + (size_t)hv * p.sh + (size_t)pos * p.st + d] = hraw;
     return;
   }
-  __shared__ float s_red[2];
-  __shared__ float s_y[kHD];
-  const float x = bf16_to_f32(hraw);
-  float ss = wave_sum(x * x);
+  __shared__ double s_red[2];
+  __shared__ double s_y[kHD];
+  const double x = bf16_to_f32(hraw);
+  double ss = wave_sum_d(x * x);
   if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
   __syncthreads();
   ss = s_red[0] + s_red[1];
-  const float inv = 1.0f / sqrtf(ss / (float)kHD + p.eps);
-  const uint16_t* nw = head < p.Hq ? p.n_qn : p.n_kn;
-  const float y = round_bf16(x * inv * bf16_to_f32(nw[d]));
+  const double inv = 1.0 / sqrt(ss / (double)kHD + (double)p.eps);
+  const double y = bf16_to_f32(f64_to_bf16((x * inv) * (double)bf16_to_f32(hw)));
   s_y[d] = y;
   __syncthreads();
-  const int i = d & (kHD / 2 - 1);
-  const uint16_t* arow = p.ang + (size_t)(p.ang_by_pos ? (pos_ok ? pos : 0) : b) * kHD;
-  const float c = bf16_to_f32(arow[2 * i]);
-  const float s = bf16_to_f32(arow[2 * i + 1]);
-  float r;
+  const double c = bf16_to_f32(hc), s = bf16_to_f32(hs);
+  double r;
   if (d < kHD / 2) {
-    r = y * c - s_y[d + kHD / 2] * s;   // y1*cos - y2*sin
+    r = y * c - s_y[d + kHD / 2] * s;   // y1*cos - y2*sin  (exact in fp64)
   } else {
     r = y * c + s_y[d - kHD / 2] * s;   // y2*cos + y1*sin
   }
-  const uint16_t hr = f32_to_bf16(r);
+  const uint16_t hr = f64_to_bf16(r);
   if (head < p.Hq) {
     p.q_out[((size_t)b * p.Hq + head) * kHD + d] = hr;
   } else if (pos_ok) {

@@ -7,7 +7,8 @@ Follows:
     q + 128 (biased) or q as int8 (signed);
   * dequant -- op_ours.py:31-43 (``_payload_to_q``) and :515-541 (``_dequant_tiles``):
     w = q * s, exact in fp32; one RNE rounding gives the bit-exact bf16 weight;
-  * exact GEMV golden -- GEMVInt8.reference, iron/operators/gemv_int8/op.py:173-178;
+  * exact GEMV golden -- GEMVInt8.reference, iron/operators/gemv_int8/op.py:173-178
+    (dequantize, then matvec), evaluated in ``dt``;
   * premul GEMV golden -- iron/operators/gemv_int8/reference.py:25-40 (x*s rounded to bf16);
   * RTN quantizer -- qwen3_npu_int8.py:457-491; GPTQ unpack -- qwen3_npu_int8.py:350-379.
 The wire pack/unpack here is written with explicit per-block loops on purpose, independent of
@@ -16,6 +17,8 @@ the product's vectorized packer.
 
 import numpy as np
 import torch
+
+from .numerics import EXACT
 
 
 def pack_wire(q: torch.Tensor, s: torch.Tensor, tile_m: int, domain: str = "signed") -> np.ndarray:
@@ -55,27 +58,29 @@ def unpack_wire(wire, M: int, K: int, G: int, tile_m: int, domain: str = "signed
 
 def dequant(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
     """Bit-exact bf16 dequant: bf16(f32(q) * f32(s)), s broadcast over each group of K."""
-    M, K = q.shape
-    G = K // s.shape[1]
+    G = q.shape[1] // s.shape[1]
     return (q.float() * s.float().repeat_interleave(G, dim=1)).to(torch.bfloat16)
 
 
-def dequant_f32(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
-    """fp32 dequant q * s (exact: 8-bit x 8-bit significands)."""
+def dequant_f(q: torch.Tensor, s: torch.Tensor, dt=EXACT) -> torch.Tensor:
+    """q * s in ``dt`` (exact in fp32 already: 8-bit x 8-bit significands)."""
     G = q.shape[1] // s.shape[1]
-    return q.float() * s.float().repeat_interleave(G, dim=1)
+    return q.to(dt) * s.to(dt).repeat_interleave(G, dim=1)
 
 
-def gemv_exact(q: torch.Tensor, s: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-    """GEMVInt8.reference (op.py:173-178): (q*s in fp32) @ x, fp32 result. x: (K,) or (B,K)."""
-    W = dequant_f32(q, s)
-    return x.float() @ W.t() if x.dim() == 2 else W @ x.float()
+def dequant_f32(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    return dequant_f(q, s, torch.float32)
 
 
-def gemv_exact_f64(q: torch.Tensor, s: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-    """fp64 brute force of the same sum (every product exact in fp64)."""
-    W = q.double() * s.double().repeat_interleave(q.shape[1] // s.shape[1], dim=1)
-    return x.double() @ W.t() if x.dim() == 2 else W @ x.double()
+def gemv(W: torch.Tensor, x: torch.Tensor, dt=EXACT) -> torch.Tensor:
+    """Dequantized (M,K) weight times x (K,) or (B,K), in ``dt`` (no rounding)."""
+    W = W.to(dt)
+    return x.to(dt) @ W.t() if x.dim() == 2 else W @ x.to(dt)
+
+
+def gemv_exact(q: torch.Tensor, s: torch.Tensor, x: torch.Tensor, dt=EXACT) -> torch.Tensor:
+    """GEMVInt8.reference (op.py:173-178): (q*s) @ x in ``dt``. x: (K,) or (B,K)."""
+    return gemv(dequant_f(q, s, dt), x, dt)
 
 
 def gemv_premul(q: torch.Tensor, s: torch.Tensor, x: torch.Tensor) -> torch.Tensor:

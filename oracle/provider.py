@@ -36,7 +36,7 @@ def reference(op, *inputs):
     if name == "GEMVInt8":
         w, x = inputs
         q, s = _unpack(w, op.M, op.K, op.group_size, op.tile_size_input, _domain(op))
-        return gemv_exact(q, s, x.reshape(-1, op.K)).to(torch.bfloat16).reshape(-1)
+        return gemv_exact(q, s, x.reshape(-1, op.K)).float().to(torch.bfloat16).reshape(-1)
     if name == "RMSNorm":
         x = inputs[0]
         w = inputs[1] if op.weighted else None
