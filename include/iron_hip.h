@@ -56,7 +56,8 @@ int iron_wire_bytes(int M, int K, int G, int tile_m, size_t* out_bytes);
 int iron_dequant_w8(const void* wire, uint16_t* w_out, int M, int K, int G, int tile_m,
                     int domain, void* stream);
 
-/* y[b][m] = bf16(sum_k dequant(W)[m][k] * x[b][k]), fp32 accumulation, B in [1,4].
+/* y[b][m] = bf16(sum_k dequant(W)[m][k] * x[b][k]), B in [1,4]. The sum is accumulated in fp64
+ * and rounded once, so y is the correctly rounded bf16 of the exact dot product.
  * Replaces GEMVInt8's callable (iron/operators/gemv_int8/op.py:20-178; kernel
  * aie_kernels/aie2p/mv_int8_signed.cc:60-113). x: [B][K] bf16, y: [B][M] bf16. */
 int iron_gemv_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int M, int K, int G,
@@ -123,13 +124,13 @@ int iron_qkv_head(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
                   int Hq, int Hkv, int max_seq, int G, int tile_m, int domain, float eps,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes for iron_decode_attn (split-K partials + merge counters). The counters must be
- * zero before the first call (a zero-filled workspace); the kernel leaves them zero again. */
+/* Workspace bytes for iron_decode_attn (fp64 split-K partials; contents need no initialisation). */
 size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx);
 
 /* GQA decode attention, one query token per sequence:
  *   o[b][h] = softmax_j(q[b][h] . K[b][h*KV/H][j] * scale) . V[b][h*KV/H][j],  j < ctx_len[b]
- * fp32 scores/softmax/accumulation (exp2 form, decode_attn.cc:117-311), bf16 output; a sequence
+ * fp64 scores/softmax/accumulation (the exp2-form golden of decode_attn.cc:117-311 in exact
+ * arithmetic), rounded once to bf16 output; a sequence
  * with ctx_len 0 yields zeros (decode_attn.cc:300-311). q/o: [B][H][D] bf16; K/V addressed as in
  * iron_qkv_head. ctx_len: device int32 [B] (or NULL: every sequence uses ctx_const).
  * Replaces DecodeAttention (iron/operators/decode_attn/op.py:20-181; golden
