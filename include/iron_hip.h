@@ -97,10 +97,16 @@ int iron_next_token(unsigned long long* keys, int32_t* tokens, const uint16_t* e
 int iron_embed(const int32_t* tokens, const uint16_t* emb, uint16_t* x, int B, int D, int vocab,
                void* stream);
 
-/* Device-side decode position advance: pos[b] += delta and ctx[b] = pos[b] + 1 (either pointer
- * may be NULL). Replaces the host writes of k_cache_offset / S_kv_eff before each dispatch
- * (qwen3_npu_int8.py:606-610), so a captured per-token HIP graph replays without host work. */
-int iron_advance_positions(int32_t* pos, int32_t* ctx, int B, int delta, void* stream);
+/* Device-side decode position advance, per row b: pos[b] += delta and ctx[b] = pos[b] + 1
+ * (either pointer may be NULL; with pos NULL the position is ctx[b] - 1). When `table` is not
+ * NULL it also copies the RoPE angle row of the new position, ang_rows[b][:] = table[pos[b]][:]
+ * (bf16 [max_pos][HD] -> [B][HD]; positions outside [0, max_pos) leave the row unchanged).
+ * Replaces the host writes of k_cache_offset / S_kv_eff and of the angle row before each
+ * dispatch (qwen3_npu_int8.py:580-591, 598-610), so a captured per-token HIP graph replays
+ * without host work. */
+int iron_advance_positions(int32_t* pos, int32_t* ctx, const uint16_t* table,
+                           uint16_t* ang_rows, int HD, int max_pos, int B, int delta,
+                           void* stream);
 
 /* Workspace bytes for iron_qkv_head (raw QKV staging). */
 size_t iron_qkv_head_workspace(int B, int Hq, int Hkv, int HD);
@@ -139,6 +145,26 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
                      long long kv_sb, long long kv_sh, long long kv_st, const int32_t* ctx_len,
                      int ctx_const, uint16_t* out, int B, int H, int KV, int D, int max_ctx,
                      float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes for iron_qkv_attn (raw QKV staging + split-K partials). */
+size_t iron_qkv_attn_workspace(int B, int Hq, int Hkv, int HD, int max_seq);
+
+/* Fused QKV head + decode attention for one decode step, per batch row b (ctx = pos[b] + 1):
+ *   q, k, v  exactly as iron_qkv_head computes them (the k and v rows are appended to the caches
+ *            at pos[b]; q is consumed in registers and not written out)
+ *   out[b]   exactly as iron_decode_attn computes it over positions 0..pos[b] with ctx_len = pos+1
+ * i.e. the composition of iron_qkv_head and iron_decode_attn with the per-head epilogue moved
+ * into the attention kernel (two launches plus the split merge instead of four). out: [B][Hq][HD].
+ * ang holds one angle row per batch row ([B][HD], the position's row; no table lookup).
+ * Replaces the QKVHeadDataParallelOurs -> DecodeAttention pair of the reference runlist
+ * (iron/applications/qwen3_0.6b/qwen3_npu_int8.py:249-281; qkv_head_dp/op_ours.py:31-262,
+ * decode_attn/op.py:20-181). */
+int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
+                  const uint16_t* n_qn, const uint16_t* n_kn, const uint16_t* ang,
+                  uint16_t* k_cache, uint16_t* v_cache, long long kv_sb, long long kv_sh,
+                  long long kv_st, const int32_t* pos, uint16_t* out, int B, int D, int HD, int Hq,
+                  int Hkv, int max_seq, int G, int tile_m, int domain, float eps, float scale,
+                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes for iron_swiglu_mlp (x1 residual halves + gh, fp32). */
 size_t iron_swiglu_mlp_workspace(int B, int D, int FF);

@@ -49,7 +49,8 @@ SIGNATURES = {
     "iron_next_token": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_int,
                                  _c_int, _c_int, _c_vp]),
     "iron_embed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
-    "iron_advance_positions": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_vp]),
+    "iron_advance_positions": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int,
+                                        _c_int, _c_vp]),
     "iron_qkv_head_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),
     "iron_qkv_head": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp,
                                _c_vp, _c_ll, _c_ll, _c_ll, _c_vp, _c_int, _c_int, _c_int, _c_int,
@@ -59,6 +60,11 @@ SIGNATURES = {
     "iron_decode_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_ll, _c_ll, _c_ll, _c_vp, _c_int,
                                   _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_vp,
                                   _c_sz, _c_vp]),
+    "iron_qkv_attn_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "iron_qkv_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                               _c_ll, _c_ll, _c_ll, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
+                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_f, _c_vp, _c_sz,
+                               _c_vp]),
     "iron_swiglu_mlp_workspace": (_c_sz, [_c_int, _c_int, _c_int]),
     "iron_swiglu_mlp": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,

@@ -12,6 +12,9 @@ Differences from the reference, all deliberate:
     seed for random-init weights (no checkpoint is available offline);
   * the KV caches are separate contiguous ``[B, Hkv, max_seq, HD]`` K and V (BASELINE's layout;
     ``kv_layout="interleaved"`` gives the reference's merged cache);
+  * by default (``fuse_attention=True``) the QKV head and decode attention run as one operator
+    (``QKVHeadAttention``) whose attention kernel performs the QK-norm/RoPE/KV-append epilogue;
+    ``fuse_attention=False`` keeps the reference's two runlist entries (identical results);
   * the LM head carries an argmax epilogue, so the token is chosen on the device (the reference
     copies the logits out and runs numpy argmax, qwen3_npu_int8.py:612-621);
   * ``generate()`` runs greedy decoding entirely on the device: each step replays one graph that
@@ -27,8 +30,8 @@ import torch
 from ... import _lib
 from ...common.context import AIEContext
 from ...common.sequence import OperatorSequence
-from ...operators import (GEMV, DecodeAttention, GEMVInt8, QKVHeadDataParallelOurs, RMSNorm,
-                          SwiGLUMLPDataParallelOurs)
+from ...operators import (GEMV, DecodeAttention, GEMVInt8, QKVHeadAttention,
+                          QKVHeadDataParallelOurs, RMSNorm, SwiGLUMLPDataParallelOurs)
 from ...operators.wire import pack_wire
 from .weights import Qwen3Config, load_gptq_checkpoint, random_qwen3_weights
 
@@ -60,10 +63,12 @@ class Qwen3NPU:
     def __init__(self, weights_path=None, *, config: Qwen3Config | None = None,
                  weights: dict | None = None, seed: int = 0, max_seq_len: int = 512,
                  kv_layout: str = "separate", lm_head: str | None = None,
-                 dispatch: str = "auto", context: AIEContext | None = None):
+                 dispatch: str = "auto", context: AIEContext | None = None,
+                 fuse_attention: bool = True):
         self.cfg = cfg = config or Qwen3Config.qwen3_0_6b()
         self.max_seq_len = max_seq_len
         self.kv_layout = kv_layout
+        self.fuse_attention = fuse_attention
         self.context = context or AIEContext()
         self.device = self.context.device
         if weights is None:
@@ -93,7 +98,12 @@ class Qwen3NPU:
         self.qkv_dp = QKVHeadDataParallelOurs(
             D=cfg.emb_dim, HD=cfg.head_dim, Hq=cfg.n_heads, Hkv=cfg.n_kv_heads, max_seq=S,
             num_aie_columns=1, tile_size_input=QKV_TSI, epsilon=cfg.eps,
-            group_size=cfg.group_size, kv_layout=self.kv_layout, angles_from_table=True,
+            group_size=cfg.group_size, kv_layout=self.kv_layout,
+            kernel_source=SIGNED_GEMV_KERNEL, kv_offset_parameter="k_cache_offset", context=c)
+        self.qkv_attn = QKVHeadAttention(
+            D=cfg.emb_dim, HD=cfg.head_dim, Hq=cfg.n_heads, Hkv=cfg.n_kv_heads, max_seq=S,
+            num_aie_columns=1, tile_size_input=QKV_TSI, epsilon=cfg.eps,
+            group_size=cfg.group_size, kv_layout=self.kv_layout,
             kernel_source=SIGNED_GEMV_KERNEL, kv_offset_parameter="k_cache_offset", context=c)
         if self.lm_head_kind == "bf16":
             self.lmhead = GEMV(M=cfg.vocab_size, K=cfg.emb_dim, epilogue="argmax", context=c)
@@ -110,9 +120,13 @@ class Qwen3NPU:
         for i in range(cfg.n_layers):
             caches = ([f"k_cache_{i}", f"v_cache_{i}"] if self.kv_layout == "separate"
                       else [f"kv_cache_{i}"])
-            runlist.append((self.qkv_dp, "x", f"W_norm1_{i}", f"W_qkv_{i}", f"W_qn_{i}",
-                            f"W_kn_{i}", "rope_table", "rope_q", *caches))
-            runlist.append((self.decode_attn, "rope_q", *caches, "context"))
+            if self.fuse_attention:
+                runlist.append((self.qkv_attn, "x", f"W_norm1_{i}", f"W_qkv_{i}", f"W_qn_{i}",
+                                f"W_kn_{i}", "rope_row", *caches, "context"))
+            else:
+                runlist.append((self.qkv_dp, "x", f"W_norm1_{i}", f"W_qkv_{i}", f"W_qn_{i}",
+                                f"W_kn_{i}", "rope_row", "rope_q", *caches))
+                runlist.append((self.decode_attn, "rope_q", *caches, "context"))
             runlist.append((self.mlp_xdna, "x", "context", f"W_norm2_{i}", f"Wo_{i}", f"Wg_{i}",
                             f"Wu_{i}", f"Wd_{i}", "gh_scratch", "a_scratch", "x"))
         runlist += [
@@ -163,7 +177,10 @@ class Qwen3NPU:
         else:
             self._set_wire("W_out_head", w["lm_head"], LMHEAD_TSI)
             self.embed = w["embed"].to(self.device).reshape(-1)
-        self._set("rope_table", rope_angle_table(self.max_seq_len, cfg.head_dim, cfg.rope_theta))
+        # the RoPE table stays on the device; the runlist reads the current position's row
+        # ("rope_row"), written per token like the reference's angle input
+        self.rope_table = rope_angle_table(self.max_seq_len, cfg.head_dim,
+                                           cfg.rope_theta).to(self.device).reshape(-1)
         torch.cuda.synchronize(self.device)
 
     # ---------------- state helpers ----------------
@@ -192,6 +209,9 @@ class Qwen3NPU:
         return self.cfg.head_dim * (1 if self.kv_layout == "separate" else 2)
 
     def _set_position(self, seq_pos: int):
+        HD = self.cfg.head_dim
+        self.fc.get_buffer("rope_row").torch_view(torch.bfloat16)[:HD].copy_(
+            self.rope_table[seq_pos * HD:(seq_pos + 1) * HD])
         self.fc.params.write("k_cache_offset", seq_pos * self._per_token_offset())
         self.fc.params.write("S_kv_eff", seq_pos + 1)
         self.fc.params.sync()
@@ -236,7 +256,9 @@ class Qwen3NPU:
                   gs["step"].data_ptr(), 1, cfg.emb_dim, cfg.vocab_size, stream)
         self.fc.run_steps()
         _lib.call("iron_advance_positions", self.fc.params.tensor("k_cache_offset").data_ptr(),
-                  self.fc.params.tensor("S_kv_eff").data_ptr(), 1, 1, stream)
+                  self.fc.params.tensor("S_kv_eff").data_ptr(), self.rope_table.data_ptr(),
+                  self.fc.get_buffer("rope_row").torch_view(torch.bfloat16).data_ptr(),
+                  cfg.head_dim, self.max_seq_len, 1, 1, stream)
 
     def _capture_gen_graph(self):
         # State tensors must exist before capture: a tensor created inside the capture would

@@ -87,17 +87,24 @@ __global__ __launch_bounds__(256) void next_token_kernel(unsigned long long* key
   }
 }
 
-__global__ void advance_kernel(int32_t* pos, int32_t* ctx, int B, int delta) {
-  const int b = threadIdx.x;
-  if (b >= B) return;
+// grid (B), 64 threads: pos[b] += delta, ctx[b] = pos[b] + 1, ang_rows[b] = table[pos[b]].
+__global__ __launch_bounds__(64) void advance_kernel(int32_t* pos, int32_t* ctx,
+                                                     const uint16_t* table, uint16_t* ang_rows,
+                                                     int HD, int max_pos, int delta) {
+  const int b = blockIdx.x;
   int p = 0;
-  if (pos) {
-    p = pos[b] + delta;
-    pos[b] = p;
-  } else if (ctx) {
-    p = ctx[b] - 1 + delta;
+  if (pos) p = pos[b] + delta;
+  else if (ctx) p = ctx[b] - 1 + delta;
+  __syncthreads();  // every thread has read the old value before it is replaced
+  if (threadIdx.x == 0) {
+    if (pos) pos[b] = p;
+    if (ctx) ctx[b] = p + 1;
   }
-  if (ctx) ctx[b] = p + 1;
+  if (table && p >= 0 && p < max_pos) {
+    const uint4* src = (const uint4*)(table + (size_t)p * HD);
+    uint4* dst = (uint4*)(ang_rows + (size_t)b * HD);
+    for (int i = threadIdx.x; i < HD / 8; i += 64) dst[i] = src[i];
+  }
 }
 
 }  // namespace
@@ -106,14 +113,23 @@ extern "C" {
 
 int iron_abi_version(void) { return IRON_ABI_VERSION; }
 
-int iron_advance_positions(int32_t* pos, int32_t* ctx, int B, int delta, void* stream) {
+int iron_advance_positions(int32_t* pos, int32_t* ctx, const uint16_t* table,
+                           uint16_t* ang_rows, int HD, int max_pos, int B, int delta,
+                           void* stream) {
   iron::clear_error();
-  if (!pos && !ctx) return iron::fail(IRON_ERR_NULL, "iron_advance_positions: no buffers");
-  if (B <= 0 || B > 1024)
-    return iron::fail(IRON_ERR_SHAPE, "iron_advance_positions: B=%d must be in [1,1024]", B);
-  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, pos, ctx, B,
-                     delta);
-  return iron::check_launch("iron_advance_positions");
+  const char* fn = "iron_advance_positions";
+  if (!pos && !ctx) return iron::fail(IRON_ERR_NULL, "%s: no buffers", fn);
+  if (B <= 0) return iron::fail(IRON_ERR_SHAPE, "%s: B=%d must be positive", fn, B);
+  if (table) {
+    if (!ang_rows) return iron::fail(IRON_ERR_NULL, "%s: table without ang_rows", fn);
+    if (HD <= 0 || HD % 8 || max_pos <= 0)
+      return iron::fail(IRON_ERR_SHAPE, "%s: HD=%d max_pos=%d", fn, HD, max_pos);
+    if (!iron::aligned(table, 16) || !iron::aligned(ang_rows, 16))
+      return iron::fail(IRON_ERR_ALIGN, "%s: table / ang_rows must be 16-byte aligned", fn);
+  }
+  hipLaunchKernelGGL(advance_kernel, dim3(B), dim3(64), 0, (hipStream_t)stream, pos, ctx, table,
+                     ang_rows, HD, max_pos, delta);
+  return iron::check_launch(fn);
 }
 
 const char* iron_last_error(void) { return iron::g_err; }

@@ -1,22 +1,31 @@
 // GQA decode attention (one query token per sequence) over a bf16 KV cache: split-K across
-// workgroups (flash-decoding), then a merge kernel.
+// workgroups (flash-decoding), then a merge kernel. A fused variant also performs the QKV head's
+// per-head epilogue (QK RMSNorm, RoPE, KV-cache append) so that the QKV GEMV output feeds
+// attention directly.
 //
 // Reference: DecodeAttention (iron/operators/decode_attn/op.py:20-181), kernels
 // aie_kernels/aie2p/decode_attn.cc:117-311 (scores with scale log2(e)/sqrt(D), online softmax over
 // KV blocks, finalize out/l with l == 0 -> 0), golden iron/operators/decode_attn/reference.py:
-// 26-38 (kv = h*KV//H).
+// 26-38 (kv = h*KV//H). Fused epilogue: QKVHeadDataParallelOurs (qkv_head_dp/op_ours.py:31-262),
+// golden qkv_head_dp/reference.py:13-33 (rms_norm/reference.py:8-17, rope/reference.py:118-154).
 //
 // Arithmetic: the exact value of the golden, o = sum_j e^(s_j - m) v_j / sum_j e^(s_j - m) with
 // s_j = (q . k_j) / sqrt(D), evaluated in fp64 (scores, exponentials, sums, accumulation) and
 // rounded once to bf16. The exp2/log2(e) form of the reference is the same function.
 //
-// Mapping: grid (split, kv * head_groups, b), 256 threads = 4 wavefronts. Lane l works on token
-// row l/16 of a 4-token group and on head dims [8*(l%16), +8): one 128-bit load per lane reads 4
-// consecutive K (or V) rows = 1 KiB per wavefront instruction. HB query heads of the GQA group
-// share every K/V load. Per 16 tokens (4 rows x 4 unrolled groups) a row keeps one online-softmax
-// state per head; the row's lanes split the block's exponentials between them (one exp per
-// (token, head) instead of sixteen) and share the results with DPP row broadcasts. Rows and
-// wavefronts merge through shuffles and LDS; splits merge in a second kernel.
+// Mapping: grid (split, kv * head_groups, b), 256 threads = 4 wavefronts. A tile is 64 tokens:
+// lane l of wavefront w works on tokens t0 + 16u + 4w + l/16 (u = 0..3) and on head dims
+// [8*(l%16), +8), so one 128-bit load per lane reads 4 consecutive K (or V) rows = 1 KiB per
+// wavefront instruction, and HB query heads of the GQA group share every K/V load. The softmax
+// offset of a tile is the workgroup-wide maximum (one LDS exchange), so the token rows and the
+// wavefronts hold partial sums under the same offset and combine by plain addition. A row's lanes
+// split the tile's exponentials between them (one exp per (token, head)) and share them with DPP
+// row broadcasts. Splits merge in a second kernel.
+//
+// With one sequence (B == 1) the first tile's K/V loads are issued before the context length is
+// known (bounded by max_ctx, masked afterwards), which takes the length's load off the critical
+// path; with several sequences the length is read first so that short sequences read nothing
+// beyond their context.
 #include <utility>
 
 #include "common.h"
@@ -25,54 +34,96 @@
 namespace {
 
 constexpr int kD = 128;
-constexpr int kTokensPerIter = 64;  // 4 waves x 4 rows x 4 unrolled groups
+constexpr int kTile = 64;  // 4 waves x 4 rows x 4 unrolled groups
 
 struct AttnParams {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
+  const uint16_t* q;       // [B][H][D] (plain mode)
+  // fused mode: q and the current token's K/V come from the raw QKV GEMV output
+  const uint16_t* raw;     // [B][(H + 2 KV) * D]
+  const uint16_t* n_qn;
+  const uint16_t* n_kn;
+  const uint16_t* ang;     // [B][D] angle rows (fused mode)
+  const int32_t* pos;      // [B]
+  double eps;
+  uint16_t* k;
+  uint16_t* v;
   long long sb, sh, st;
-  const int32_t* ctx_len;
+  const int32_t* ctx_len;  // plain mode
   int ctx_const;
   int max_ctx;
+  int spec;                // issue the first tile before the context length is known
   uint16_t* out;
-  int H, KV, HG, HB;   // heads, kv heads, GQA group, heads per workgroup
+  int H, KV, HG, HB;       // heads, kv heads, GQA group, heads per workgroup
   int chunk, nsplit;
   double scale;
-  double* part;        // [B][H][nsplit][D + 2]: o (unnormalised), m, l
+  double* part;            // [B][H][nsplit][D + 2]: o (unnormalised), m, l
 };
 
 template <int N>
 IRON_DEV double row_share_d(double v) {
-  // every lane of a 16-lane row receives lane N of that row
+  // every lane of a 16-lane row receives lane N of that row (row_newbcast)
   return dpp_d<0x150 + N>(v);
 }
 
-// Lane N of each row evaluated exponential N; every lane of the row receives it.
 template <int N, int HB>
-IRON_DEV void share_one(double ev, double (&pe)[4][HB], double (&corr)[HB]) {
-  if constexpr (N < 4 * HB) {
-    pe[N / HB][N % HB] = row_share_d<N>(ev);
-  } else if constexpr (N < 5 * HB) {
-    corr[N - 4 * HB] = row_share_d<N>(ev);
-  }
+IRON_DEV void share_one(double ev, double (&pe)[4][HB]) {
+  if constexpr (N < 4 * HB) pe[N / HB][N % HB] = row_share_d<N>(ev);
 }
 
 template <int HB, int... Ns>
-IRON_DEV void share_all(double ev, double (&pe)[4][HB], double (&corr)[HB],
-                        std::integer_sequence<int, Ns...>) {
-  (share_one<Ns, HB>(ev, pe, corr), ...);
+IRON_DEV void share_all(double ev, double (&pe)[4][HB], std::integer_sequence<int, Ns...>) {
+  (share_one<Ns, HB>(ev, pe), ...);
 }
 
-IRON_DEV double pick(const double* vals, int idx, int n) {
-  double r = vals[0];
+IRON_DEV void unpack8d(const uint4 v, double (&f)[8]) {
+  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-  for (int i = 1; i < 16; ++i)
-    if (i < n && idx == i) r = vals[i];
-  return r;
+  for (int j = 0; j < 4; ++j) {
+    f[2 * j] = bf16lo_to_f32(d[j]);
+    f[2 * j + 1] = bf16hi_to_f32(d[j]);
+  }
 }
 
-template <int HB>
+IRON_DEV uint4 pack8_bf16(const double (&f)[8]) {
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = (uint32_t)f64_to_bf16(f[2 * j]) | ((uint32_t)f64_to_bf16(f[2 * j + 1]) << 16);
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// The QKV head epilogue for one head held by a 16-lane row (lane dl owns dims 8*dl..8*dl+7):
+//   y = bf16(RMSNorm(x) * w), r = bf16(RoPE(y)) with the two-halves rotation
+//   r[i] = y[i] cos_i - y[i+64] sin_i, r[i+64] = y[i+64] cos_i + y[i] sin_i (i < 64).
+// a0/a1: this lane's 8 (cos, sin) bf16 pairs of the interleaved angle row (indices (dl%8)*8..+8).
+// The same operations and roundings as the standalone epilogue kernel (qkv.hip).
+IRON_DEV void norm_rope8(const uint4 xr, const uint4 wr, const uint4 a0, const uint4 a1, int dl,
+                         double eps, double (&out)[8]) {
+  double x[8], w[8];
+  unpack8d(xr, x);
+  unpack8d(wr, w);
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss = fma(x[j], x[j], ss);
+  ss = row16_sum_d(ss);
+  const double inv = 1.0 / sqrt(ss / (double)kD + eps);
+  float y[8], yp[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = bf16_to_f32(f64_to_bf16((x[j] * inv) * w[j]));
+  // the partner dims (+-64) live in lane dl ^ 8 of the same row (row_ror:8)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) yp[j] = dpp_f<0x128>(y[j]);
+  const uint32_t ad[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const double c = bf16lo_to_f32(ad[j]), s = bf16hi_to_f32(ad[j]);
+    const double r = dl < 8 ? (double)y[j] * c - (double)yp[j] * s
+                            : (double)y[j] * c + (double)yp[j] * s;
+    out[j] = bf16_to_f32(f64_to_bf16(r));
+  }
+}
+
+template <int HB, bool FUSED>
 __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   const int split = blockIdx.x, b = blockIdx.z;
   const int groups = p.HG / HB;
@@ -80,22 +131,89 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   const int h0 = kv * p.HG + hg * HB;  // first query head of this workgroup
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row = lane >> 4, dl = lane & 15;
-
-  int ctx = p.ctx_len ? p.ctx_len[b] : p.ctx_const;
-  ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
   const int t_begin = split * p.chunk;
-  const int t_end = min(ctx, t_begin + p.chunk);
+  const int t_lim = min(p.max_ctx, t_begin + p.chunk);
+
+  const uint16_t* kbase = p.k + (size_t)b * p.sb + (size_t)kv * p.sh + dl * 8;
+  const uint16_t* vbase = p.v + (size_t)b * p.sb + (size_t)kv * p.sh + dl * 8;
+  uint4 kr[4], vr[4];
+  // Rows past `bound` (> t0) are clamped to bound - 1: every load is issued unconditionally, so
+  // the compiler's wait counts stay exact; those rows are masked where they are used.
+  auto load_tile = [&](int t0, int bound) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      int t = t0 + u * 16 + wave * 4 + row;
+      t = t < bound ? t : bound - 1;
+      kr[u] = *(const uint4*)(kbase + (size_t)t * p.st);
+      vr[u] = *(const uint4*)(vbase + (size_t)t * p.st);
+    }
+  };
+  // Issue order: the position / context length and the query-side rows, then (B == 1) the
+  // first K/V tile. Loads complete in issue order, so the query-side work below waits only for
+  // the first group while the tile is still in flight.
+  uint4 xq[HB];
+  int ctx, pos = -1;
+  uint4 nq, nk, xk, xv, a0, a1;
+  if constexpr (FUSED) {
+    pos = p.pos[b];
+    const uint16_t* rawb = p.raw + (size_t)b * (p.H + 2 * p.KV) * kD;
+#pragma unroll
+    for (int h = 0; h < HB; ++h) xq[h] = *(const uint4*)(rawb + (size_t)(h0 + h) * kD + dl * 8);
+    xk = *(const uint4*)(rawb + (size_t)(p.H + kv) * kD + dl * 8);
+    xv = *(const uint4*)(rawb + (size_t)(p.H + p.KV + kv) * kD + dl * 8);
+    nq = *(const uint4*)(p.n_qn + dl * 8);
+    nk = *(const uint4*)(p.n_kn + dl * 8);
+    const uint16_t* arow = p.ang + (size_t)b * kD + 16 * (dl & 7);
+    a0 = *(const uint4*)arow;
+    a1 = *(const uint4*)(arow + 8);
+    ctx = pos + 1;
+  } else {
+#pragma unroll
+    for (int h = 0; h < HB; ++h)
+      xq[h] = *(const uint4*)(p.q + ((size_t)b * p.H + h0 + h) * kD + dl * 8);
+    ctx = p.ctx_len ? p.ctx_len[b] : p.ctx_const;
+  }
+  if (p.spec) load_tile(t_begin, t_lim);
+  ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
+  const int t_end = min(ctx, t_lim);
 
   double qf[HB][8];
+  __shared__ uint4 s_new[2][16];   // the current token's K and V rows (fused mode)
+  __shared__ uint4 s_q[HB][16];    // the rotated query rows (fused mode)
+  bool has_new = false;
+  if constexpr (FUSED) {
+    const bool pos_ok = pos >= 0 && pos < p.max_ctx;
+    has_new = pos_ok && pos >= t_begin && pos < t_lim;  // workgroup-uniform
+    // the per-head epilogues run in parallel: wave h < HB rotates query head h, wave HB % 4
+    // (wave 0 when HB == 4, after its query head) builds the current token's K row
+    if (wave < HB) {
+      uint4 mine = xq[0];
 #pragma unroll
-  for (int h = 0; h < HB; ++h) {
-    const uint4 qq = *(const uint4*)(p.q + ((size_t)b * p.H + h0 + h) * kD + dl * 8);
-    const uint32_t qd[4] = {qq.x, qq.y, qq.z, qq.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      qf[h][2 * j] = bf16lo_to_f32(qd[j]);
-      qf[h][2 * j + 1] = bf16hi_to_f32(qd[j]);
+      for (int h = 1; h < HB; ++h)
+        if (wave == h) mine = xq[h];
+      double qn[8];
+      norm_rope8(mine, nq, a0, a1, dl, p.eps, qn);
+      if (row == 0) s_q[wave][dl] = pack8_bf16(qn);
     }
+    if (has_new && wave == HB % 4) {
+      double kn[8];
+      norm_rope8(xk, nk, a0, a1, dl, p.eps, kn);
+      const uint4 kp = pack8_bf16(kn);
+      if (row == 0) {
+        s_new[0][dl] = kp;
+        s_new[1][dl] = xv;
+        if (hg == 0) {  // one writer per (b, kv head)
+          *(uint4*)(p.k + (size_t)b * p.sb + (size_t)kv * p.sh + (size_t)pos * p.st + dl * 8) = kp;
+          *(uint4*)(p.v + (size_t)b * p.sb + (size_t)kv * p.sh + (size_t)pos * p.st + dl * 8) = xv;
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < HB; ++h) unpack8d(s_q[h][dl], qf[h]);
+  } else {
+#pragma unroll
+    for (int h = 0; h < HB; ++h) unpack8d(xq[h], qf[h]);
   }
 
   double m[HB], l[HB], o[HB][8];
@@ -107,35 +225,29 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
     for (int j = 0; j < 8; ++j) o[h][j] = 0.0;
   }
 
-  const uint16_t* kbase = p.k + (size_t)b * p.sb + (size_t)kv * p.sh + dl * 8;
-  const uint16_t* vbase = p.v + (size_t)b * p.sb + (size_t)kv * p.sh + dl * 8;
-
-  for (int t0 = t_begin; t0 < t_end; t0 += kTokensPerIter) {
-    uint4 kr[4], vr[4];
+  __shared__ double s_mx[2][4][HB];
+  int it = 0;
+  for (int t0 = t_begin; t0 < t_end; t0 += kTile, ++it) {
+    if (!(p.spec && t0 == t_begin)) load_tile(t0, t_end);
     bool tv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = t0 + u * 16 + wave * 4 + row;
       tv[u] = t < t_end;
-      if (tv[u]) {
-        kr[u] = *(const uint4*)(kbase + (size_t)t * p.st);
-        vr[u] = *(const uint4*)(vbase + (size_t)t * p.st);
-      } else {
-        kr[u] = make_uint4(0u, 0u, 0u, 0u);
-        vr[u] = make_uint4(0u, 0u, 0u, 0u);
+      if constexpr (FUSED) {
+        if (has_new && t == pos) {
+          kr[u] = s_new[0][dl];
+          vr[u] = s_new[1][dl];
+        }
       }
+      if (!tv[u]) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // rows past the context may hold NaNs
     }
     // scores s[u][h], identical in every lane of the row
     double s[4][HB];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const uint32_t kd[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
       double kf[8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        kf[2 * j] = bf16lo_to_f32(kd[j]);
-        kf[2 * j + 1] = bf16hi_to_f32(kd[j]);
-      }
+      unpack8d(kr[u], kf);
 #pragma unroll
       for (int h = 0; h < HB; ++h) {
         double a = 0.0;
@@ -145,47 +257,41 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
         s[u][h] = tv[u] ? a : -INFINITY;
       }
     }
-    // new running max per head (row-uniform)
+    // workgroup-wide tile maximum per head
+    double mx[HB];
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      double v = fmax(fmax(s[0][h], s[1][h]), fmax(s[2][h], s[3][h]));
+      v = fmax(v, __shfl_xor(v, 16));
+      v = fmax(v, __shfl_xor(v, 32));
+      mx[h] = v;
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int h = 0; h < HB; ++h) s_mx[it & 1][wave][h] = mx[h];
+    }
+    __syncthreads();
     double mn[HB];
-    bool any = false;
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
-      const double mb = fmax(fmax(s[0][h], s[1][h]), fmax(s[2][h], s[3][h]));
-      mn[h] = fmax(m[h], mb);
-      any |= mn[h] != -INFINITY;
+      const double t = fmax(fmax(s_mx[it & 1][0][h], s_mx[it & 1][1][h]),
+                            fmax(s_mx[it & 1][2][h], s_mx[it & 1][3][h]));
+      mn[h] = fmax(m[h], t);
     }
-    if (!any) continue;  // row-uniform: no valid token in this row yet
-    // lane dl evaluates one exponential: (u, h) = (dl / HB, dl % HB) for dl < 4*HB, the
-    // correction e^(m_old - m_new) of head dl - 4*HB for 4*HB <= dl < 5*HB
+    // every tile of the loop holds at least one valid token, so mn is finite here
+    // lane dl < 4*HB evaluates exponential (u, h) = (dl / HB, dl % HB)
     double arg = -INFINITY;
-    {
-      double vals[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) vals[i] = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int h = 0; h < HB; ++h) vals[u * HB + h] = s[u][h] - mn[h];
+    for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int h = 0; h < HB; ++h)
-        if (4 * HB + h < 16) vals[4 * HB + h] = (m[h] == -INFINITY) ? -INFINITY : m[h] - mn[h];
-      arg = pick(vals, dl, 5 * HB);
-    }
-    // exp(-inf) = 0 covers invalid tokens and heads with no valid token (mn == -inf makes the
-    // argument NaN only when both sides are -inf, which the guard above excludes for m)
-    const double ev = (arg == -INFINITY || arg != arg) ? 0.0 : exp(arg);
-    double pe[4][HB], corr[HB];
-    share_all<HB>(ev, pe, corr, std::make_integer_sequence<int, 16>{});
-    if constexpr (HB >= 4) {
-      // 5*HB = 20 > 16 lanes: the last four corrections are computed directly
-#pragma unroll
-      for (int h = 0; h < HB; ++h)
-        if (4 * HB + h >= 16) corr[h] = (m[h] == -INFINITY) ? 0.0 : exp(m[h] - mn[h]);
-    }
+        if (dl == u * HB + h) arg = s[u][h] - mn[h];
+    const double ev = arg == -INFINITY ? 0.0 : exp(arg);
+    double pe[4][HB];
+    share_all<HB>(ev, pe, std::make_integer_sequence<int, 16>{});
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
-      if (mn[h] == -INFINITY) continue;
-      const double c = (m[h] == -INFINITY) ? 0.0 : corr[h];
+      const double c = m[h] == -INFINITY ? 0.0 : exp(m[h] - mn[h]);
       l[h] = l[h] * c + ((pe[0][h] + pe[1][h]) + (pe[2][h] + pe[3][h]));
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[h][j] *= c;
@@ -193,13 +299,8 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const uint32_t vd[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
       double vf[8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vf[2 * j] = bf16lo_to_f32(vd[j]);
-        vf[2 * j + 1] = bf16hi_to_f32(vd[j]);
-      }
+      unpack8d(vr[u], vf);
 #pragma unroll
       for (int h = 0; h < HB; ++h)
 #pragma unroll
@@ -207,57 +308,30 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
     }
   }
 
-  // merge the 4 token rows of this wavefront (lanes l, l^16, l^32, l^48 share head dims)
+  // 16 token rows (4 per wavefront) share the offset m: their partial sums add
+  __shared__ double s_o[16][HB][kD];
+  __shared__ double s_l[16][HB];
+  const int rr = wave * 4 + row;
 #pragma unroll
-  for (int step = 16; step <= 32; step <<= 1) {
+  for (int h = 0; h < HB; ++h) {
 #pragma unroll
-    for (int h = 0; h < HB; ++h) {
-      const double mo = __shfl_xor(m[h], step);
-      const double lo = __shfl_xor(l[h], step);
-      double oo[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) oo[j] = __shfl_xor(o[h][j], step);
-      const double mm = fmax(m[h], mo);
-      if (mm != -INFINITY) {
-        const double c1 = m[h] == -INFINITY ? 0.0 : exp(m[h] - mm);
-        const double c2 = mo == -INFINITY ? 0.0 : exp(mo - mm);
-        l[h] = l[h] * c1 + lo * c2;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[h][j] = o[h][j] * c1 + oo[j] * c2;
-        m[h] = mm;
-      }
-    }
-  }
-
-  // merge the 4 wavefronts through LDS
-  __shared__ double s_o[4][HB][kD];
-  __shared__ double s_m[4][HB], s_l[4][HB];
-  if (row == 0) {
-#pragma unroll
-    for (int h = 0; h < HB; ++h) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s_o[wave][h][dl * 8 + j] = o[h][j];
-      if (dl == 0) {
-        s_m[wave][h] = m[h];
-        s_l[wave][h] = l[h];
-      }
-    }
+    for (int j = 0; j < 8; j += 2)
+      *(double2*)&s_o[rr][h][dl * 8 + j] = make_double2(o[h][j], o[h][j + 1]);
+    if (dl == 0) s_l[rr][h] = l[h];
   }
   __syncthreads();
   for (int t = threadIdx.x; t < HB * kD; t += 256) {
     const int oh = t / kD, od = t % kD;
-    double M = -INFINITY;
+    double O = 0.0, L = 0.0;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmax(M, s_m[w][oh]);
-    double L = 0.0, O = 0.0;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const double f = s_m[w][oh] == -INFINITY ? 0.0 : exp(s_m[w][oh] - M);
-        L += f * s_l[w][oh];
-        O += f * s_o[w][oh][od];
-      }
+    for (int r = 0; r < 16; ++r) {
+      O += s_o[r][oh][od];
+      L += s_l[r][oh];
     }
+    double M = m[0];
+#pragma unroll
+    for (int h = 1; h < HB; ++h)
+      if (oh == h) M = m[h];
     const int hq = h0 + oh;
     if (p.nsplit == 1) {
       p.out[((size_t)b * p.H + hq) * kD + od] = f64_to_bf16(L > 0.0 ? O / L : 0.0);
@@ -272,44 +346,58 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   }
 }
 
-// grid (H, B), 128 threads: o = sum_s f_s O_s / sum_s f_s L_s, f_s = e^(m_s - max m).
+// grid (H, B), 128 threads: o = sum_s f_s O_s / sum_s f_s L_s, f_s = e^(m_s - max m). Every
+// partial of the first kReg splits is loaded before the first reduction.
+constexpr int kReg = 64;
+constexpr int kMaxSplit = 256;
+
 __global__ __launch_bounds__(128) void attn_merge_kernel(AttnParams p) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int ns = p.nsplit;
   const double* base = p.part + ((size_t)b * p.H + h) * ns * (kD + 2);
-  __shared__ double s_f[256];
-  __shared__ double s_red[2];
-  double mloc = -INFINITY;
-  for (int s = d; s < ns; s += 128) mloc = fmax(mloc, base[(size_t)s * (kD + 2) + kD]);
-  // block max over 2 wavefronts
+  double ov[kReg];
+#pragma unroll
+  for (int s = 0; s < kReg; ++s) ov[s] = s < ns ? base[(size_t)s * (kD + 2) + d] : 0.0;
+  double ms[2], ls[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int s = d + 128 * i;
+    ms[i] = s < ns ? base[(size_t)s * (kD + 2) + kD] : -INFINITY;
+    ls[i] = s < ns ? base[(size_t)s * (kD + 2) + kD + 1] : 0.0;
+  }
+  __shared__ double s_f[kMaxSplit];
+  __shared__ double s_red[2][2];
+  double mloc = fmax(ms[0], ms[1]);
   mloc = fmax(mloc, __shfl_xor(mloc, 1));
   mloc = fmax(mloc, __shfl_xor(mloc, 2));
   mloc = fmax(mloc, __shfl_xor(mloc, 4));
   mloc = fmax(mloc, __shfl_xor(mloc, 8));
   mloc = fmax(mloc, __shfl_xor(mloc, 16));
   mloc = fmax(mloc, __shfl_xor(mloc, 32));
-  if ((d & 63) == 0) s_red[d >> 6] = mloc;
+  if ((d & 63) == 0) s_red[0][d >> 6] = mloc;
   __syncthreads();
-  const double M = fmax(s_red[0], s_red[1]);
-  __syncthreads();
+  const double M = fmax(s_red[0][0], s_red[0][1]);
   double lloc = 0.0;
-  for (int s = d; s < ns; s += 128) {
-    const double ms = base[(size_t)s * (kD + 2) + kD];
-    const double f = (M == -INFINITY || ms == -INFINITY) ? 0.0 : exp(ms - M);
-    s_f[s] = f;
-    lloc += f * base[(size_t)s * (kD + 2) + kD + 1];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int s = d + 128 * i;
+    if (s < ns) {
+      const double f = (M == -INFINITY || ms[i] == -INFINITY) ? 0.0 : exp(ms[i] - M);
+      s_f[s] = f;
+      lloc += f * ls[i];
+    }
   }
   lloc = wave_sum_d(lloc);
-  if ((d & 63) == 0) s_red[d >> 6] = lloc;
+  if ((d & 63) == 0) s_red[1][d >> 6] = lloc;
   __syncthreads();
-  const double L = s_red[0] + s_red[1];
+  const double L = s_red[1][0] + s_red[1][1];
   double O0 = 0.0, O1 = 0.0;
-  int s = 0;
-  for (; s + 2 <= ns; s += 2) {
-    O0 = fma(s_f[s], base[(size_t)s * (kD + 2) + d], O0);
-    O1 = fma(s_f[s + 1], base[(size_t)(s + 1) * (kD + 2) + d], O1);
+#pragma unroll
+  for (int s = 0; s < kReg; s += 2) {
+    if (s < ns) O0 = fma(s_f[s], ov[s], O0);
+    if (s + 1 < ns) O1 = fma(s_f[s + 1], ov[s + 1], O1);
   }
-  if (s < ns) O0 = fma(s_f[s], base[(size_t)s * (kD + 2) + d], O0);
+  for (int s = kReg; s < ns; ++s) O0 = fma(s_f[s], base[(size_t)s * (kD + 2) + d], O0);
   const double O = O0 + O1;
   p.out[((size_t)b * p.H + h) * kD + d] = f64_to_bf16(L > 0.0 ? O / L : 0.0);
 }
@@ -325,12 +413,12 @@ SplitPlan plan_split(int B, int H, int KV, int max_ctx) {
   const int wg_per_split = B * KV * (HG / sp.hb);
   const int target_wgs = 512;
   int ns = (target_wgs + wg_per_split - 1) / wg_per_split;
-  const int max_ns = (max_ctx + kTokensPerIter - 1) / kTokensPerIter;
+  const int max_ns = (max_ctx + kTile - 1) / kTile;
   if (ns > max_ns) ns = max_ns;
-  if (ns > 256) ns = 256;
+  if (ns > kMaxSplit) ns = kMaxSplit;
   if (ns < 1) ns = 1;
   int chunk = (max_ctx + ns - 1) / ns;
-  chunk = ((chunk + kTokensPerIter - 1) / kTokensPerIter) * kTokensPerIter;
+  chunk = ((chunk + kTile - 1) / kTile) * kTile;
   ns = (max_ctx + chunk - 1) / chunk;
   if (ns < 1) ns = 1;
   sp.nsplit = ns;
@@ -344,7 +432,64 @@ size_t attn_ws_bytes(int B, int H, int KV, int max_ctx) {
   return (((size_t)B * H * sp.nsplit * (kD + 2) * sizeof(double)) + 255) & ~(size_t)255;
 }
 
+int check_attn_shape(const char* fn, int B, int H, int KV, int D, int max_ctx) {
+  if (B <= 0 || H <= 0 || KV <= 0 || max_ctx <= 0)
+    return iron::fail(IRON_ERR_SHAPE, "%s: bad shape B=%d H=%d KV=%d max_ctx=%d", fn, B, H, KV,
+                      max_ctx);
+  if (D != kD) return iron::fail(IRON_ERR_UNSUPPORTED, "%s: head_dim %d (only 128)", fn, D);
+  if (H % KV) return iron::fail(IRON_ERR_SHAPE, "%s: H=%d not a multiple of KV=%d", fn, H, KV);
+  const int HG = H / KV;
+  if (HG != 1 && HG != 2 && HG % 4 != 0)
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: GQA group %d not 1, 2 or a multiple of 4", fn,
+                      HG);
+  return IRON_OK;
+}
+
+// Launches the split kernel (and the merge when the context is split). `p` carries the inputs;
+// the split plan, partial buffer and head blocking are filled in here.
+int launch_attention(AttnParams p, bool fused, int B, void* part_ws, size_t part_bytes,
+                     hipStream_t s, const char* fn) {
+  const SplitPlan sp = plan_split(B, p.H, p.KV, p.max_ctx);
+  p.HG = p.H / p.KV;
+  p.HB = sp.hb;
+  p.chunk = sp.chunk;
+  p.nsplit = sp.nsplit;
+  p.spec = B == 1 ? 1 : 0;
+  if (sp.nsplit > 1) {
+    const size_t need = attn_ws_bytes(B, p.H, p.KV, p.max_ctx);
+    if (!part_ws || part_bytes < need)
+      return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, part_bytes, need);
+    if (!iron::aligned(part_ws, 256))
+      return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
+    p.part = (double*)part_ws;
+  }
+  dim3 grid(sp.nsplit, p.KV * (p.HG / sp.hb), B);
+#define IRON_ATTN_LAUNCH(HBV)                                                                  \
+  do {                                                                                         \
+    if (fused)                                                                                 \
+      hipLaunchKernelGGL((decode_attn_kernel<HBV, true>), grid, dim3(256), 0, s, p);           \
+    else                                                                                       \
+      hipLaunchKernelGGL((decode_attn_kernel<HBV, false>), grid, dim3(256), 0, s, p);          \
+  } while (0)
+  switch (sp.hb) {
+    case 1: IRON_ATTN_LAUNCH(1); break;
+    case 2: IRON_ATTN_LAUNCH(2); break;
+    default: IRON_ATTN_LAUNCH(4); break;
+  }
+#undef IRON_ATTN_LAUNCH
+  int st = iron::check_launch(fn);
+  if (st || sp.nsplit == 1) return st;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.H, B), dim3(128), 0, s, p);
+  return iron::check_launch(fn);
+}
+
 }  // namespace
+
+namespace iron {
+int gemv_rms_internal(const void* wire, const uint16_t* x, const uint16_t* nw, uint16_t* y,
+                      int B, int M, int K, int G, int tile_m, int domain, float eps,
+                      hipStream_t stream, const char* fn);
+}
 
 extern "C" {
 
@@ -361,25 +506,17 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
   iron::clear_error();
   const char* fn = "iron_decode_attn";
   if (!q || !k_cache || !v_cache || !out) return iron::fail(IRON_ERR_NULL, "%s: null tensor", fn);
-  if (B <= 0 || H <= 0 || KV <= 0 || max_ctx <= 0)
-    return iron::fail(IRON_ERR_SHAPE, "%s: bad shape B=%d H=%d KV=%d max_ctx=%d", fn, B, H, KV,
-                      max_ctx);
-  if (D != kD) return iron::fail(IRON_ERR_UNSUPPORTED, "%s: head_dim %d (only 128)", fn, D);
-  if (H % KV) return iron::fail(IRON_ERR_SHAPE, "%s: H=%d not a multiple of KV=%d", fn, H, KV);
-  const int HG = H / KV;
-  if (HG != 1 && HG != 2 && HG % 4 != 0)
-    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: GQA group %d not 1, 2 or a multiple of 4", fn,
-                      HG);
+  int st = check_attn_shape(fn, B, H, KV, D, max_ctx);
+  if (st) return st;
   if (kv_st % 8 || kv_sh % 8 || kv_sb % 8 || !iron::aligned(k_cache, 16) ||
       !iron::aligned(v_cache, 16) || !iron::aligned(q, 16))
     return iron::fail(IRON_ERR_ALIGN, "%s: K/V/Q rows must be 16-byte aligned", fn);
   if (!ctx_len && (ctx_const < 0 || ctx_const > max_ctx))
     return iron::fail(IRON_ERR_SHAPE, "%s: ctx_const=%d outside [0, %d]", fn, ctx_const, max_ctx);
-  const SplitPlan sp = plan_split(B, H, KV, max_ctx);
   AttnParams p = {};
   p.q = q;
-  p.k = k_cache;
-  p.v = v_cache;
+  p.k = const_cast<uint16_t*>(k_cache);
+  p.v = const_cast<uint16_t*>(v_cache);
   p.sb = kv_sb;
   p.sh = kv_sh;
   p.st = kv_st;
@@ -389,31 +526,67 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
   p.out = out;
   p.H = H;
   p.KV = KV;
-  p.HG = HG;
-  p.HB = sp.hb;
-  p.chunk = sp.chunk;
-  p.nsplit = sp.nsplit;
   p.scale = (double)scale;
-  if (sp.nsplit > 1) {
-    const size_t need = attn_ws_bytes(B, H, KV, max_ctx);
-    if (!workspace || workspace_bytes < need)
-      return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes,
-                        need);
-    if (!iron::aligned(workspace, 256))
-      return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
-    p.part = (double*)workspace;
-  }
-  dim3 grid(sp.nsplit, KV * (HG / sp.hb), B);
+  return launch_attention(p, false, B, workspace, workspace_bytes, (hipStream_t)stream, fn);
+}
+
+size_t iron_qkv_attn_workspace(int B, int Hq, int Hkv, int HD, int max_seq) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || HD != kD || Hq % Hkv || max_seq <= 0) return 0;
+  const size_t raw = ((size_t)B * (Hq + 2 * Hkv) * HD * 2 + 255) & ~(size_t)255;
+  return raw + attn_ws_bytes(B, Hq, Hkv, max_seq) + 256;
+}
+
+int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
+                  const uint16_t* n_qn, const uint16_t* n_kn, const uint16_t* ang,
+                  uint16_t* k_cache, uint16_t* v_cache, long long kv_sb, long long kv_sh,
+                  long long kv_st, const int32_t* pos, uint16_t* out, int B, int D, int HD, int Hq,
+                  int Hkv, int max_seq, int G, int tile_m, int domain, float eps, float scale,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  iron::clear_error();
+  const char* fn = "iron_qkv_attn";
+  if (!cur || !n_in || !n_qn || !n_kn || !ang || !k_cache || !v_cache || !pos || !out)
+    return iron::fail(IRON_ERR_NULL, "%s: null tensor", fn);
+  int st = check_attn_shape(fn, B, Hq, Hkv, HD, max_seq);
+  if (st) return st;
+  if (D <= 0 || D % 16) return iron::fail(IRON_ERR_SHAPE, "%s: bad hidden size D=%d", fn, D);
+  if (kv_st % 8 || kv_sh % 8 || kv_sb % 8 || !iron::aligned(k_cache, 16) ||
+      !iron::aligned(v_cache, 16) || !iron::aligned(ang, 16) || !iron::aligned(n_qn, 16) ||
+      !iron::aligned(n_kn, 16))
+    return iron::fail(IRON_ERR_ALIGN, "%s: K/V rows, angles and norm weights must be 16-byte "
+                      "aligned", fn);
+  const int M = (Hq + 2 * Hkv) * HD;
+  st = iron::check_wire(fn, wqkv, M, D, G, tile_m, domain);
+  if (st) return st;
+  const size_t need = iron_qkv_attn_workspace(B, Hq, Hkv, HD, max_seq);
+  if (!workspace || workspace_bytes < need)
+    return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes,
+                      need);
+  if (!iron::aligned(workspace, 256))
+    return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
   hipStream_t s = (hipStream_t)stream;
-  switch (sp.hb) {
-    case 1: hipLaunchKernelGGL(decode_attn_kernel<1>, grid, dim3(256), 0, s, p); break;
-    case 2: hipLaunchKernelGGL(decode_attn_kernel<2>, grid, dim3(256), 0, s, p); break;
-    default: hipLaunchKernelGGL(decode_attn_kernel<4>, grid, dim3(256), 0, s, p); break;
-  }
-  int st = iron::check_launch(fn);
-  if (st || sp.nsplit == 1) return st;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(H, B), dim3(128), 0, s, p);
-  return iron::check_launch(fn);
+  uint16_t* raw = (uint16_t*)workspace;
+  const size_t raw_bytes = ((size_t)B * M * 2 + 255) & ~(size_t)255;
+  st = iron::gemv_rms_internal(wqkv, cur, n_in, raw, B, M, D, G, tile_m, domain, eps, s, fn);
+  if (st) return st;
+  AttnParams p = {};
+  p.raw = raw;
+  p.n_qn = n_qn;
+  p.n_kn = n_kn;
+  p.ang = ang;
+  p.pos = pos;
+  p.eps = (double)eps;
+  p.k = k_cache;
+  p.v = v_cache;
+  p.sb = kv_sb;
+  p.sh = kv_sh;
+  p.st = kv_st;
+  p.max_ctx = max_seq;
+  p.out = out;
+  p.H = Hq;
+  p.KV = Hkv;
+  p.scale = (double)scale;
+  return launch_attention(p, true, B, (char*)workspace + raw_bytes, workspace_bytes - raw_bytes, s,
+                          fn);
 }
 
 }  // extern "C"

@@ -21,7 +21,8 @@
 // lane one 16-byte slice of every 1024-wide (int8) or 512-wide (bf16) chunk of those rows, so a
 // wavefront load instruction reads 1 KiB of one row. A workgroup owns one group of 4*R rows: it
 // first issues every weight/scale load of the group (R*NCH 128-bit loads per lane, all in
-// flight), then stages x into LDS (the prologue, overlapping the weight latency), then reduces.
+// flight) behind the activation loads, then stages x into LDS (the prologue, overlapping the
+// weight latency), then reduces.
 #include "common.h"
 #include "internal.h"
 
@@ -68,6 +69,12 @@ struct GemvParams {
 
 // ------------------------------------------------------------------------------------------
 // Prologue: stage B vectors of length K into LDS as fp64 (K % 8 == 0, 16-byte aligned rows).
+//
+// LDS layout: lane-contiguous pairs. A lane of the dot product consumes J consecutive pairs
+// (x[2P], x[2P+1]) per chunk (J = 8 for int8 chunks of 1024, 4 for bf16 chunks of 512); pair P
+// lives at slot (c*J + j)*64 + lane with c = P / (64*J), lane = (P % (64*J)) / J, j = P % J, so
+// one ds_read_b128 of a wavefront reads 64 consecutive 16-byte slots (no bank conflicts). A
+// vector occupies ceil(K / chunk) * chunk doubles.
 // ------------------------------------------------------------------------------------------
 IRON_DEV void unpack8(const uint4 v, float (&f)[8]) {
   f[0] = bf16lo_to_f32(v.x); f[1] = bf16hi_to_f32(v.x);
@@ -76,58 +83,176 @@ IRON_DEV void unpack8(const uint4 v, float (&f)[8]) {
   f[6] = bf16lo_to_f32(v.w); f[7] = bf16hi_to_f32(v.w);
 }
 
+template <bool INT8>
+IRON_DEV int pair_slot(int P) {
+  constexpr int J = INT8 ? 8 : 4;
+  constexpr int PC = 64 * J;  // pairs per chunk
+  const int c = P / PC, rem = P % PC;
+  return (c * J + (rem % J)) * 64 + rem / J;
+}
+
+template <bool INT8>
+IRON_DEV int padded_k(int K) {
+  constexpr int chunk = INT8 ? 1024 : 512;
+  return (K + chunk - 1) / chunk * chunk;
+}
+
+// thread t's 8 elements x[8t..8t+7] are pairs 4t..4t+3
+template <bool INT8>
+IRON_DEV void put8(double2* dst, int i, const double (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) dst[pair_slot<INT8>(4 * i + j)] = make_double2(v[2 * j], v[2 * j + 1]);
+}
+
+// The activation side is loaded into registers before the weight loads are issued: loads
+// complete in issue order, so the prologue (and its block reduction) then runs while the weight
+// stream is still in flight. Each thread owns up to S 8-element slots per batch row
+// (i = threadIdx.x + 256*r); slots beyond S (K > 2048*S) are loaded in the compute pass.
+//   xa: bf16 x, or the low half of fp32 x;  xb: the high half of fp32 x (PRO_F32) or the
+//   residual term x2 (PRO_RES_RMS_F32);  xn: the RMSNorm weight.
 template <int B>
-__device__ void stage_x(const GemvParams& p, double* __restrict__ xs, double* red) {
+constexpr int x_slots() { return B == 1 ? 4 : (B == 2 ? 2 : 1); }
+
+template <int B, int S>
+IRON_DEV void load_x(const GemvParams& p, uint4 (&xa)[B][S], uint4 (&xb)[B][S], uint4 (&xn)[S]) {
+  const int n8 = p.K >> 3;
+  const bool rms = p.pro == PRO_RMS_BF16 || p.pro == PRO_RES_RMS_F32;
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+#pragma unroll
+    for (int r = 0; r < S; ++r) {
+      const int i = threadIdx.x + 256 * r;
+      xa[b][r] = make_uint4(0u, 0u, 0u, 0u);
+      xb[b][r] = make_uint4(0u, 0u, 0u, 0u);
+      if (i < n8) {
+        if (p.pro == PRO_F32) {
+          const uint4* src = (const uint4*)((const float*)p.x + (size_t)b * p.x_stride);
+          xa[b][r] = src[2 * i];
+          xb[b][r] = src[2 * i + 1];
+        } else {
+          xa[b][r] = ((const uint4*)((const uint16_t*)p.x + (size_t)b * p.x_stride))[i];
+          if (p.x2) xb[b][r] = ((const uint4*)(p.x2 + (size_t)b * p.x2_stride))[i];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < S; ++r) {
+    const int i = threadIdx.x + 256 * r;
+    xn[r] = make_uint4(0u, 0u, 0u, 0u);
+    if (rms && i < n8) xn[r] = ((const uint4*)p.nw)[i];
+  }
+}
+
+// x (+ x2) of one slot as exact fp32 values (x1 = cur + a is the one fp32 rounding)
+IRON_DEV void slot_values(uint4 xv, uint4 x2v, bool has_x2, float (&f)[8]) {
+  unpack8(xv, f);
+  if (has_x2) {
+    float g[8];
+    unpack8(x2v, g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = f[j] + g[j];
+  }
+}
+
+template <int B, int S, bool INT8>
+IRON_DEV void stage_x(const GemvParams& p, const uint4 (&xa)[B][S], const uint4 (&xb)[B][S],
+                      const uint4 (&xn)[S], double* __restrict__ xs, double* red) {
   const int K = p.K;
   const int n8 = K >> 3;
+  const int KP = padded_k<INT8>(K);
+  const int tid = threadIdx.x;
+#pragma unroll
   for (int b = 0; b < B; ++b) {
-    double* dst = xs + (size_t)b * K;
+    double2* dst = (double2*)(xs + (size_t)b * KP);
     if (p.pro == PRO_F32) {
-      const float4* src = (const float4*)((const float*)p.x + (size_t)b * p.x_stride);
-      for (int i = threadIdx.x; i < (K >> 2); i += 256) {
-        const float4 v = src[i];
-        dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
+      const uint4* src = (const uint4*)((const float*)p.x + (size_t)b * p.x_stride);
+#pragma unroll
+      for (int r = 0; r < S; ++r) {
+        const int i = tid + 256 * r;
+        if (i < n8) {
+          const uint4 lo = xa[b][r], hi = xb[b][r];
+          const double v[8] = {__uint_as_float(lo.x), __uint_as_float(lo.y), __uint_as_float(lo.z),
+                               __uint_as_float(lo.w), __uint_as_float(hi.x), __uint_as_float(hi.y),
+                               __uint_as_float(hi.z), __uint_as_float(hi.w)};
+          put8<INT8>(dst, i, v);
+        }
+      }
+      for (int i = tid + 256 * S; i < n8; i += 256) {
+        const uint4 lo = src[2 * i], hi = src[2 * i + 1];
+        const double v[8] = {__uint_as_float(lo.x), __uint_as_float(lo.y), __uint_as_float(lo.z),
+                             __uint_as_float(lo.w), __uint_as_float(hi.x), __uint_as_float(hi.y),
+                             __uint_as_float(hi.z), __uint_as_float(hi.w)};
+        put8<INT8>(dst, i, v);
       }
       continue;
     }
     const uint4* src = (const uint4*)((const uint16_t*)p.x + (size_t)b * p.x_stride);
     if (p.pro == PRO_BF16) {
-      for (int i = threadIdx.x; i < n8; i += 256) {
+#pragma unroll
+      for (int r = 0; r < S; ++r) {
+        const int i = tid + 256 * r;
+        if (i < n8) {
+          float f[8];
+          unpack8(xa[b][r], f);
+          double v[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = f[j];
+          put8<INT8>(dst, i, v);
+        }
+      }
+      for (int i = tid + 256 * S; i < n8; i += 256) {
         float f[8];
         unpack8(src[i], f);
+        double v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dst[8 * i + j] = f[j];
+        for (int j = 0; j < 8; ++j) v[j] = f[j];
+        put8<INT8>(dst, i, v);
       }
       continue;
     }
-    const uint4* src2 = p.x2 ? (const uint4*)(p.x2 + (size_t)b * p.x2_stride) : nullptr;
+    // RMS prologues
+    const bool has_x2 = p.x2 != nullptr;
+    const uint4* src2 = (const uint4*)(p.x2 + (size_t)b * p.x2_stride);
+    const uint4* wsrc = (const uint4*)p.nw;
     double ss = 0.0;
-    for (int i = threadIdx.x; i < n8; i += 256) {
+#pragma unroll
+    for (int r = 0; r < S; ++r) {
+      if (tid + 256 * r < n8) {
+        float f[8];
+        slot_values(xa[b][r], xb[b][r], has_x2, f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
+      }
+    }
+    for (int i = tid + 256 * S; i < n8; i += 256) {
       float f[8];
-      unpack8(src[i], f);
-      if (src2) {
-        float g[8];
-        unpack8(src2[i], g);
+      slot_values(src[i], has_x2 ? src2[i] : make_uint4(0u, 0u, 0u, 0u), has_x2, f);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) f[j] = f[j] + g[j];   // x1 = cur + a, one fp32 rounding
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const double d = f[j];
-        dst[8 * i + j] = d;
-        ss = fma(d, d, ss);
-      }
+      for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
     }
     ss = block_sum_256_d(ss, red);
     const double inv = 1.0 / sqrt(ss / (double)K + (double)p.eps);
-    const uint4* wsrc = (const uint4*)p.nw;
-    for (int i = threadIdx.x; i < n8; i += 256) {
-      float wf[8];
-      unpack8(wsrc[i], wf);
+    const bool to_bf16 = p.pro == PRO_RMS_BF16;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const double y = (dst[8 * i + j] * inv) * (double)wf[j];
-        dst[8 * i + j] = (p.pro == PRO_RMS_BF16) ? (double)round_bf16((float)y) : (double)(float)y;
+    for (int r = 0; r < S + 1; ++r) {
+      // r < S: register slots; r == S: the remaining slots, loaded here
+      for (int i = tid + 256 * r; i < n8; i += (r < S ? n8 : 256)) {
+        float f[8], wf[8];
+        if (r < S) {
+          slot_values(xa[b][r], xb[b][r], has_x2, f);
+          unpack8(xn[r], wf);
+        } else {
+          slot_values(src[i], has_x2 ? src2[i] : make_uint4(0u, 0u, 0u, 0u), has_x2, f);
+          unpack8(wsrc[i], wf);
+        }
+        double v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const double y = ((double)f[j] * inv) * (double)wf[j];
+          v[j] = to_bf16 ? (double)round_bf16((float)y) : (double)(float)y;
+        }
+        put8<INT8>(dst, i, v);
       }
     }
   }
@@ -137,16 +262,19 @@ __device__ void stage_x(const GemvParams& p, double* __restrict__ xs, double* re
 // ------------------------------------------------------------------------------------------
 // Weight fetch: lane-resident 16-byte slices of R rows x NCH chunks (+ their group scales).
 // ------------------------------------------------------------------------------------------
+// Loads go to clamped addresses with no branch and no use of the loaded value, so every load of
+// the group is in flight at once (a value read right after its load would make the wavefront
+// wait for all earlier loads). Out-of-range slices are masked where they are used: their scale
+// counts as 0 and their rows are never stored.
 template <int R, int NCH>
 IRON_DEV void fetch_w8(const GemvParams& p, const uint8_t* __restrict__ wire, int row0, int lane,
-                       uint4 (&w)[R][NCH], float (&sc)[R][NCH]) {
+                       uint4 (&w)[R][NCH], uint32_t (&sraw)[R][NCH]) {
   const int K = p.K;
   const int ng = K >> p.gshift;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int row = row0 + r;
-    const bool rv = row < p.M;
-    const uint32_t rr = rv ? (uint32_t)row : 0u;
+    const uint32_t rr = row < p.M ? (uint32_t)row : 0u;
     const uint32_t blk = fastdiv(rr, p.tdiv);
     const uint32_t in = rr - blk * (uint32_t)p.tile_m;
     const uint8_t* base = wire + (size_t)blk * p.blk_bytes;
@@ -155,15 +283,16 @@ IRON_DEV void fetch_w8(const GemvParams& p, const uint8_t* __restrict__ wire, in
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const int e = c * 1024 + lane * 16;
-      if (rv && e < K) {
-        w[r][c] = *(const uint4*)(qrow + e);
-        sc[r][c] = bf16_to_f32(srow[e >> p.gshift]);
-      } else {
-        w[r][c] = make_uint4(p.xor_mask, p.xor_mask, p.xor_mask, p.xor_mask);  // q == 0
-        sc[r][c] = 0.f;
-      }
+      const int ec = e < K ? e : 0;
+      w[r][c] = *(const uint4*)(qrow + ec);
+      sraw[r][c] = srow[ec >> p.gshift];
     }
   }
+}
+
+// scale of slice (r, c) as used by the dot product: 0 outside the matrix
+IRON_DEV double slice_scale(const GemvParams& p, uint32_t sraw, int row, int e) {
+  return (row < p.M && e < p.K) ? (double)bf16_to_f32(sraw) : 0.0;
 }
 
 IRON_DEV double sbyte(uint32_t d, int j) {
@@ -171,8 +300,8 @@ IRON_DEV double sbyte(uint32_t d, int j) {
 }
 
 template <int B, int R, int NCH>
-IRON_DEV void dot_w8(const GemvParams& p, const uint4 (&w)[R][NCH], const float (&sc)[R][NCH],
-                     const double* __restrict__ xs, int lane, double (&acc)[R][B]) {
+IRON_DEV void dot_w8(const GemvParams& p, const uint4 (&w)[R][NCH], const uint32_t (&sc)[R][NCH],
+                     const double* __restrict__ xs, int row0, int lane, double (&acc)[R][B]) {
   const int K = p.K;
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -186,10 +315,11 @@ IRON_DEV void dot_w8(const GemvParams& p, const uint4 (&w)[R][NCH], const float 
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       if (e < K) {
-        const double2* src = (const double2*)(xs + (size_t)b * K + e);
+        // pairs (c*8 + j)*64 + lane, j = 0..7 (the lane-contiguous staging layout)
+        const double2* src = (const double2*)(xs + (size_t)b * padded_k<true>(K)) + c * 512 + lane;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const double2 t = src[j];
+          const double2 t = src[j * 64];
           xv[b][2 * j] = t.x;
           xv[b][2 * j + 1] = t.y;
         }
@@ -202,7 +332,7 @@ IRON_DEV void dot_w8(const GemvParams& p, const uint4 (&w)[R][NCH], const float 
     for (int r = 0; r < R; ++r) {
       const uint32_t dd[4] = {w[r][c].x ^ p.xor_mask, w[r][c].y ^ p.xor_mask,
                               w[r][c].z ^ p.xor_mask, w[r][c].w ^ p.xor_mask};
-      const double s = (double)sc[r][c];
+      const double s = slice_scale(p, sc[r][c], row0 + r, e);
 #pragma unroll
       for (int b = 0; b < B; ++b) {
         double pa = 0.0, pb = 0.0;
@@ -233,8 +363,8 @@ IRON_DEV void fetch_w16(const GemvParams& p, int row0, int lane, uint4 (&w)[R][N
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const int e = c * 512 + lane * 8;
-      w[r][c] = (row < p.M && e < p.K) ? *(const uint4*)(W + (size_t)row * p.K + e)
-                                       : make_uint4(0u, 0u, 0u, 0u);
+      // clamped address; an out-of-range row is never stored and x is 0 past K
+      w[r][c] = *(const uint4*)(W + (size_t)(row < p.M ? row : 0) * p.K + (e < p.K ? e : 0));
     }
   }
 }
@@ -255,10 +385,11 @@ IRON_DEV void dot_w16(const GemvParams& p, const uint4 (&w)[R][NCH],
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       if (e < K) {
-        const double2* src = (const double2*)(xs + (size_t)b * K + e);
+        // pairs (c*4 + j)*64 + lane, j = 0..3
+        const double2* src = (const double2*)(xs + (size_t)b * padded_k<false>(K)) + c * 256 + lane;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const double2 t = src[j];
+          const double2 t = src[j * 64];
           xv[b][2 * j] = t.x;
           xv[b][2 * j + 1] = t.y;
         }
@@ -286,6 +417,156 @@ IRON_DEV void dot_w16(const GemvParams& p, const uint4 (&w)[R][NCH],
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int b = 0; b < B; ++b) acc[r][b] = wave_sum_d(acc[r][b]);
+}
+
+// ------------------------------------------------------------------------------------------
+// Batch-1 path with the activation in registers: lane l of a wavefront multiplies elements
+// [c*CH + l*EPL, +EPL) of every chunk c (CH = 1024, EPL = 16 for int8; 512 and 8 for bf16), so
+// it loads exactly those x (and norm-weight / residual) elements, and the RMSNorm statistic is a
+// wavefront reduction: no LDS staging and no workgroup barrier. Every wavefront of a workgroup
+// computes the (identical) statistic itself.
+// ------------------------------------------------------------------------------------------
+template <int NCH, int EPL>
+IRON_DEV void load_x_lane(const GemvParams& p, int lane, uint4 (&xl)[NCH][EPL / 4],
+                          uint4 (&x2l)[NCH][EPL / 8], uint4 (&nwl)[NCH][EPL / 8]) {
+  const bool rms = p.pro == PRO_RMS_BF16 || p.pro == PRO_RES_RMS_F32;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e = c * 64 * EPL + lane * EPL;
+#pragma unroll
+    for (int u = 0; u < EPL / 4; ++u) xl[c][u] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int u = 0; u < EPL / 8; ++u) {
+      x2l[c][u] = make_uint4(0u, 0u, 0u, 0u);
+      nwl[c][u] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (e < p.K) {
+      if (p.pro == PRO_F32) {
+        const uint4* src = (const uint4*)((const float*)p.x + e);
+#pragma unroll
+        for (int u = 0; u < EPL / 4; ++u) xl[c][u] = src[u];
+      } else {
+        const uint4* src = (const uint4*)((const uint16_t*)p.x + e);
+#pragma unroll
+        for (int u = 0; u < EPL / 8; ++u) xl[c][u] = src[u];
+        if (p.x2) {
+#pragma unroll
+          for (int u = 0; u < EPL / 8; ++u) x2l[c][u] = ((const uint4*)(p.x2 + e))[u];
+        }
+      }
+      if (rms) {
+#pragma unroll
+        for (int u = 0; u < EPL / 8; ++u) nwl[c][u] = ((const uint4*)(p.nw + e))[u];
+      }
+    }
+  }
+}
+
+// The prologue of the lane's elements: xf = the (exact fp32) value the dot product multiplies.
+template <int NCH, int EPL>
+IRON_DEV void prologue_lane(const GemvParams& p, int lane, const uint4 (&xl)[NCH][EPL / 4],
+                            const uint4 (&x2l)[NCH][EPL / 8], const uint4 (&nwl)[NCH][EPL / 8],
+                            float (&xf)[NCH][EPL]) {
+  const bool has_x2 = p.x2 != nullptr;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (p.pro == PRO_F32) {
+#pragma unroll
+      for (int u = 0; u < EPL / 4; ++u) {
+        xf[c][4 * u] = __uint_as_float(xl[c][u].x);
+        xf[c][4 * u + 1] = __uint_as_float(xl[c][u].y);
+        xf[c][4 * u + 2] = __uint_as_float(xl[c][u].z);
+        xf[c][4 * u + 3] = __uint_as_float(xl[c][u].w);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < EPL / 8; ++u) {
+        float f[8];
+        slot_values(xl[c][u], x2l[c][u], has_x2, f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xf[c][8 * u + j] = f[j];
+      }
+    }
+  }
+  if (p.pro != PRO_RMS_BF16 && p.pro != PRO_RES_RMS_F32) return;
+  double ss = 0.0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) ss = fma((double)xf[c][j], (double)xf[c][j], ss);
+  ss = wave_sum_d(ss);
+  const double inv = 1.0 / sqrt(ss / (double)p.K + (double)p.eps);
+  const bool to_bf16 = p.pro == PRO_RMS_BF16;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int u = 0; u < EPL / 8; ++u) {
+      float wf[8];
+      unpack8(nwl[c][u], wf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const double y = ((double)xf[c][8 * u + j] * inv) * (double)wf[j];
+        xf[c][8 * u + j] = to_bf16 ? round_bf16((float)y) : (float)y;
+      }
+    }
+  }
+}
+
+template <int R, int NCH>
+IRON_DEV void dot_w8_lane(const GemvParams& p, const uint4 (&w)[R][NCH],
+                          const uint32_t (&sc)[R][NCH], const float (&xf)[NCH][16], int row0,
+                          int lane, double (&acc)[R][1]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r][0] = 0.0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    double xv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) xv[j] = xf[c][j];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t dd[4] = {w[r][c].x ^ p.xor_mask, w[r][c].y ^ p.xor_mask,
+                              w[r][c].z ^ p.xor_mask, w[r][c].w ^ p.xor_mask};
+      double pa = 0.0, pb = 0.0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pa = fma(sbyte(dd[j], 0), xv[4 * j + 0], pa);
+        pb = fma(sbyte(dd[j], 1), xv[4 * j + 1], pb);
+        pa = fma(sbyte(dd[j], 2), xv[4 * j + 2], pa);
+        pb = fma(sbyte(dd[j], 3), xv[4 * j + 3], pb);
+      }
+      acc[r][0] = fma(slice_scale(p, sc[r][c], row0 + r, c * 1024 + lane * 16), pa + pb,
+                      acc[r][0]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r][0] = wave_sum_d(acc[r][0]);
+}
+
+template <int R, int NCH>
+IRON_DEV void dot_w16_lane(const uint4 (&w)[R][NCH], const float (&xf)[NCH][8],
+                           double (&acc)[R][1]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r][0] = 0.0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    double xv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[j] = xf[c][j];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t dd[4] = {w[r][c].x, w[r][c].y, w[r][c].z, w[r][c].w};
+      double pa = 0.0, pb = 0.0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pa = fma((double)bf16lo_to_f32(dd[j]), xv[2 * j], pa);
+        pb = fma((double)bf16hi_to_f32(dd[j]), xv[2 * j + 1], pb);
+      }
+      acc[r][0] += pa + pb;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r][0] = wave_sum_d(acc[r][0]);
 }
 
 IRON_DEV uint32_t bf16_order_key(uint16_t h) {
@@ -340,6 +621,9 @@ IRON_DEV void store_rows(const GemvParams& p, int row0, int lane, const double (
   }
 }
 
+// Batch 1 with at most four chunks per lane keeps the activation in registers.
+constexpr bool xreg_path(int B, int NCH) { return B == 1 && NCH <= 4; }
+
 template <int B, int R, int NCH, bool INT8, bool DUAL>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   extern __shared__ double xs[];
@@ -349,39 +633,56 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + wave) * R;
 
-  // 1. every weight load of this wavefront's rows goes out before the prologue
   uint4 w[R][NCH];
-  float sc[R][NCH];
+  uint32_t sc[R][NCH];
   uint4 w2[DUAL ? R : 1][DUAL ? NCH : 1];
-  float sc2[DUAL ? R : 1][DUAL ? NCH : 1];
-  if constexpr (INT8) {
-    fetch_w8<R, NCH>(p, p.w, row0, lane, w, sc);
-    if constexpr (DUAL) fetch_w8<R, NCH>(p, p.w2, row0, lane, w2, sc2);
-  } else {
-    fetch_w16<R, NCH>(p, row0, lane, w);
-  }
-
-  // 2. stage x (its global-load latency overlaps the weight loads in flight)
-  stage_x<B>(p, xs, red);
-
-  // 3. reduce and store
-  double acc[R][B], acc2[R][B];
-  if constexpr (INT8) {
-    dot_w8<B, R, NCH>(p, w, sc, xs, lane, acc);
-    if constexpr (DUAL) {
-      dot_w8<B, R, NCH>(p, w2, sc2, xs, lane, acc2);
+  uint32_t sc2[DUAL ? R : 1][DUAL ? NCH : 1];
+  auto fetch_weights = [&]() {
+    if constexpr (INT8) {
+      fetch_w8<R, NCH>(p, p.w, row0, lane, w, sc);
+      if constexpr (DUAL) fetch_w8<R, NCH>(p, p.w2, row0, lane, w2, sc2);
     } else {
+      fetch_w16<R, NCH>(p, row0, lane, w);
+    }
+  };
+  double acc[R][B], acc2[R][B];
 #pragma unroll
-      for (int r = 0; r < R; ++r)
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int b = 0; b < B; ++b) acc2[r][b] = 0.0;
+    for (int b = 0; b < B; ++b) acc2[r][b] = 0.0;
+
+  if constexpr (xreg_path(B, NCH)) {
+    // 1. this lane's activation elements, then the weights; 2. the prologue in registers
+    constexpr int EPL = INT8 ? 16 : 8;
+    uint4 xl[NCH][EPL / 4], x2l[NCH][EPL / 8], nwl[NCH][EPL / 8];
+    load_x_lane<NCH, EPL>(p, lane, xl, x2l, nwl);
+    fetch_weights();
+    float xf[NCH][EPL];
+    prologue_lane<NCH, EPL>(p, lane, xl, x2l, nwl, xf);
+    // 3. reduce
+    if constexpr (INT8) {
+      dot_w8_lane<R, NCH>(p, w, sc, xf, row0, lane, acc);
+      if constexpr (DUAL) dot_w8_lane<R, NCH>(p, w2, sc2, xf, row0, lane, acc2);
+    } else {
+      dot_w16_lane<R, NCH>(w, xf, acc);
     }
   } else {
+  // 1. the activation side first, then every weight load of this wavefront's rows
+  constexpr int S = x_slots<B>();
+  uint4 xa[B][S], xb[B][S], xn[S];
+  load_x<B, S>(p, xa, xb, xn);
+  fetch_weights();
+
+  // 2. the prologue runs while the weights are in flight
+  stage_x<B, S, INT8>(p, xa, xb, xn, xs, red);
+
+  // 3. reduce
+  if constexpr (INT8) {
+    dot_w8<B, R, NCH>(p, w, sc, xs, row0, lane, acc);
+    if constexpr (DUAL) dot_w8<B, R, NCH>(p, w2, sc2, xs, row0, lane, acc2);
+  } else {
     dot_w16<B, R, NCH>(p, w, xs, lane, acc);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int b = 0; b < B; ++b) acc2[r][b] = 0.0;
+  }
   }
   unsigned long long best[B];
 #pragma unroll
@@ -490,12 +791,13 @@ bool launch_nch(const GemvParams& p, int NCH, int R, int grid, size_t lds, hipSt
 
 template <bool INT8, bool DUAL>
 int launch_gemv(const GemvParams& p, int B, hipStream_t stream, const char* fn) {
-  const size_t lds = (size_t)B * p.K * sizeof(double);
+  const int chunk = INT8 ? 1024 : 512;
+  size_t lds = (size_t)B * ((p.K + chunk - 1) / chunk * chunk) * sizeof(double);
   if (lds > (size_t)kMaxLdsBytes)
     return iron::fail(IRON_ERR_UNSUPPORTED, "%s: B*K = %d*%d exceeds the LDS-staged GEMV limit",
                       fn, B, p.K);
-  const int chunk = INT8 ? 1024 : 512;
   const int NCH = round_pow2((p.K + chunk - 1) / chunk);
+  if (xreg_path(B, NCH)) lds = 0;  // the activation stays in registers
   const int slices = (DUAL ? 2 : 1) * NCH;
   if (slices > kMaxSlices)
     return iron::fail(IRON_ERR_UNSUPPORTED, "%s: K=%d too long for the resident-slice GEMV", fn,

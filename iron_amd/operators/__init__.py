@@ -9,6 +9,7 @@ _OPERATOR_MODULES = {
     "DecodeAttention": "decode_attn",
     "GEMV": "gemv",
     "GEMVInt8": "gemv_int8",
+    "QKVHeadAttention": "qkv_attn",
     "QKVHeadDataParallel": "qkv_head_dp",
     "QKVHeadDataParallelOurs": "qkv_head_dp:op_ours",
     "RMSNorm": "rms_norm",

@@ -14,8 +14,8 @@ import pytest
 import torch
 
 from iron_amd.common.test_utils import verify_buffer
-from iron_amd.operators import (DecodeAttention, GEMVInt8, QKVHeadDataParallelOurs, RMSNorm,
-                                SwiGLUMLPDataParallelOurs)
+from iron_amd.operators import (DecodeAttention, GEMVInt8, QKVHeadAttention,
+                                QKVHeadDataParallelOurs, RMSNorm, SwiGLUMLPDataParallelOurs)
 from iron_amd.operators.wire import pack_wire
 from oracle import attention as oatt
 from oracle import blocks as oblk
@@ -256,6 +256,75 @@ def test_qkv_head(D, Hq, Hkv, S, G, tm, layout, B):
         mask = torch.ones(S, dtype=torch.bool)          # nothing else in the cache was touched
         mask[p] = False
         assert kcc[b][:, mask].abs().sum() == 0 and vcc[b][:, mask].abs().sum() == 0
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,S,G,tm,layout,pos", [
+    (1024, 16, 8, 2240, 32, 4, "separate", [2048]),      # the bench step (B=1, speculative)
+    (1024, 16, 8, 512, 32, 4, "interleaved", [0]),       # first position, reference cache layout
+    (1024, 16, 8, 512, 32, 4, "separate", [64]),         # first token of a tile
+    (4096, 32, 8, 1024, 32, 16, "separate", [1000, 63]), # Qwen3-8B heads (4 per workgroup), B=2
+    (256, 2, 1, 128, 32, 4, "separate", [127, 5, 64]),   # GQA 2, B=3, last position
+])
+def test_qkv_attention_fused(D, Hq, Hkv, S, G, tm, layout, pos):
+    """QKVHeadAttention == QKVHeadDataParallelOurs -> DecodeAttention(S_kv_eff = pos + 1), bit for
+    bit (output and caches), and == the exact oracle. Cache rows past each position hold NaN/inf
+    bit patterns: they are read by the speculative first tile and must not leak into the result."""
+    B = len(pos)
+    _say(f"qkv_attn D={D} Hq={Hq} Hkv={Hkv} S={S} G={G} layout={layout} pos={pos}")
+    c = _qkv_case(D, Hq, Hkv, S, G, B, seed=D + S + 7 * B)
+    HD = c["HD"]
+    gen = torch.Generator().manual_seed(S + B)
+    k0, v0 = _kv(B, Hkv, S, HD, gen)
+    for b, p in enumerate(pos):                     # garbage past the context
+        k0[b, :, p:] = torch.tensor([0x7FC0, 0x7F80, -0x80, 0x7FFF], dtype=torch.int16).view(
+            torch.bfloat16).repeat(HD // 4)
+        v0[b, :, p:] = k0[b, :, p:]
+    table = onorm.rope_angle_table(S, HD, 1e6)
+    common = dict(D=D, HD=HD, Hq=Hq, Hkv=Hkv, max_seq=S, group_size=G, tile_size_input=tm,
+                  kv_layout=layout, batch=B, num_aie_columns=1, kernel_source="mv_int8_signed.cc")
+    fused = QKVHeadAttention(**common)                           # one angle row per batch row
+    qkv = QKVHeadDataParallelOurs(**common, angles_from_table=True)  # the whole table
+    attn = DecodeAttention(num_heads=Hq, num_kv_heads=Hkv, head_dim=HD, seq_len_kv=S,
+                           use_runtime_seq_len=True, batch=B,
+                           kv_layout="separate" if layout == "separate" else "combined")
+    per_tok = HD if layout == "separate" else 2 * HD
+    offs = np.asarray(pos) * per_tok
+    wire = pack_wire(c["q8"], c["s"], tm, "signed").view(torch.bfloat16).to(DEV)
+    ins = (c["cur"].reshape(-1).to(DEV), c["n_in"].to(DEV), wire, c["n_qn"].to(DEV),
+           c["n_kn"].to(DEV))
+    rows = table[torch.tensor(pos)].reshape(-1).to(DEV)
+
+    def caches():
+        if layout == "separate":
+            return [k0.clone().reshape(-1).to(DEV), v0.clone().reshape(-1).to(DEV)]
+        return [torch.stack([k0, v0], dim=3).reshape(-1).to(DEV)]
+
+    ca, cb = caches(), caches()
+    fa = fused.get_callable()
+    fa.params.write(fused.kv_offset_parameter, offs)
+    out_a = torch.zeros(B * Hq * HD, dtype=torch.bfloat16, device=DEV)
+    fa(*ins, rows, *ca, out_a)
+    fq = qkv.get_callable()
+    fq.params.write(qkv.kv_offset_parameter, offs)
+    fattn = attn.get_callable()
+    fattn.params.write("S_kv_eff", [p + 1 for p in pos])
+    qo = torch.zeros(B * Hq * HD, dtype=torch.bfloat16, device=DEV)
+    out_b = torch.zeros_like(out_a)
+    fq(*ins, table.reshape(-1).to(DEV), qo, *cb)
+    fattn(qo.reshape(B * Hq, HD), *[t.reshape(B * Hkv, -1) for t in cb], out_b.reshape(B * Hq, HD))
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.cpu().view(torch.int16), out_b.cpu().view(torch.int16)), "output"
+    for x, y in zip(ca, cb):
+        assert torch.equal(x.cpu().view(torch.int16), y.cpu().view(torch.int16)), "caches"
+    # exact oracle: QKV head, append, attention over 0..pos
+    wq, wk, wv = oblk.qkv_head(c["cur"], c["n_in"], c["q8"], c["s"], c["n_qn"], c["n_kn"],
+                               table[torch.tensor(pos)], Hq, Hkv, HD, 1e-6)
+    kk, vv = k0.clone(), v0.clone()
+    for b, p in enumerate(pos):
+        kk[b, :, p] = wk[b].reshape(Hkv, HD)
+        vv[b, :, p] = wv[b].reshape(Hkv, HD)
+    want = oatt.decode_attention(wq.reshape(B, Hq, HD), kk, vv, [p + 1 for p in pos])
+    assert_bit_exact(out_a, want, "fused attention")
 
 
 @pytest.mark.parametrize("D,FF,QD,fuse_o,G,B", [
