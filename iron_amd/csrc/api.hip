@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
     ss = fma(v, v, ss);
   }
   ss = block_sum_256_d(ss, red);
-  const double inv = 1.0 / sqrt(ss / (double)cols + (double)eps);
+  const double inv = inv_rms(ss, cols, (double)eps);
   for (int i = threadIdx.x; i < cols; i += 256) {
     const double v = (double)bf16_to_f32(xr[i]) * inv;
     yr[i] = f64_to_bf16(w ? v * (double)bf16_to_f32(w[i]) : v);

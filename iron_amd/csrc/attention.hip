@@ -102,11 +102,8 @@ IRON_DEV void norm_rope8(const uint4 xr, const uint4 wr, const uint4 a0, const u
   double x[8], w[8];
   unpack8d(xr, x);
   unpack8d(wr, w);
-  double ss = 0.0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ss = fma(x[j], x[j], ss);
-  ss = row16_sum_d(ss);
-  const double inv = 1.0 / sqrt(ss / (double)kD + eps);
+  const double ss = row16_sum_d(sum_sq_tree(x));
+  const double inv = inv_rms(ss, kD, eps);
   float y[8], yp[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) y[j] = bf16_to_f32(f64_to_bf16((x[j] * inv) * w[j]));
@@ -289,12 +286,18 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
     const double ev = arg == -INFINITY ? 0.0 : exp(arg);
     double pe[4][HB];
     share_all<HB>(ev, pe, std::make_integer_sequence<int, 16>{});
+    if (it > 0) {  // rescale the running sums (the first tile starts from zero)
+#pragma unroll
+      for (int h = 0; h < HB; ++h) {
+        const double c = m[h] == -INFINITY ? 0.0 : exp(m[h] - mn[h]);
+        l[h] *= c;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[h][j] *= c;
+      }
+    }
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
-      const double c = m[h] == -INFINITY ? 0.0 : exp(m[h] - mn[h]);
-      l[h] = l[h] * c + ((pe[0][h] + pe[1][h]) + (pe[2][h] + pe[3][h]));
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[h][j] *= c;
+      l[h] += (pe[0][h] + pe[1][h]) + (pe[2][h] + pe[3][h]);
       m[h] = mn[h];
     }
 #pragma unroll
@@ -322,12 +325,20 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   __syncthreads();
   for (int t = threadIdx.x; t < HB * kD; t += 256) {
     const int oh = t / kD, od = t % kD;
-    double O = 0.0, L = 0.0;
+    double so[16], sl[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      O += s_o[r][oh][od];
-      L += s_l[r][oh];
+      so[r] = s_o[r][oh][od];
+      sl[r] = s_l[r][oh];
     }
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int r = 0; r < w; ++r) {
+        so[r] += so[r + w];
+        sl[r] += sl[r + w];
+      }
+    const double O = so[0], L = sl[0];
     double M = m[0];
 #pragma unroll
     for (int h = 1; h < HB; ++h)
@@ -367,11 +378,7 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(AttnParams p) {
   }
   __shared__ double s_f[kMaxSplit];
   __shared__ double s_red[2][2];
-  double mloc = fmax(ms[0], ms[1]);
-  mloc = fmax(mloc, __shfl_xor(mloc, 1));
-  mloc = fmax(mloc, __shfl_xor(mloc, 2));
-  mloc = fmax(mloc, __shfl_xor(mloc, 4));
-  mloc = fmax(mloc, __shfl_xor(mloc, 8));
+  double mloc = row16_max_d(fmax(ms[0], ms[1]));
   mloc = fmax(mloc, __shfl_xor(mloc, 16));
   mloc = fmax(mloc, __shfl_xor(mloc, 32));
   if ((d & 63) == 0) s_red[0][d >> 6] = mloc;
@@ -391,12 +398,11 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(AttnParams p) {
   if ((d & 63) == 0) s_red[1][d >> 6] = lloc;
   __syncthreads();
   const double L = s_red[1][0] + s_red[1][1];
-  double O0 = 0.0, O1 = 0.0;
+  double Oa[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-  for (int s = 0; s < kReg; s += 2) {
-    if (s < ns) O0 = fma(s_f[s], ov[s], O0);
-    if (s + 1 < ns) O1 = fma(s_f[s + 1], ov[s + 1], O1);
-  }
+  for (int s = 0; s < kReg; ++s)
+    if (s < ns) Oa[s & 3] = fma(s_f[s], ov[s], Oa[s & 3]);
+  double O0 = Oa[0] + Oa[2], O1 = Oa[1] + Oa[3];
   for (int s = kReg; s < ns; ++s) O0 = fma(s_f[s], base[(size_t)s * (kD + 2) + d], O0);
   const double O = O0 + O1;
   p.out[((size_t)b * p.H + h) * kD + d] = f64_to_bf16(L > 0.0 ? O / L : 0.0);

@@ -108,6 +108,40 @@ IRON_DEV double row16_max_d(double v) {
   return v;
 }
 
+// 1 / sqrt(v) in fp64 for v > 0: the hardware reciprocal square root (about 24 correct bits)
+// refined by two Newton steps, y <- y + y (1 - v y^2) / 2, to within a few units of 2^-53 of the
+// correctly rounded value. The bf16 / fp32 values the kernels compute from it then round exactly
+// like the correctly rounded form except when they sit that close to a rounding boundary.
+IRON_DEV double rsqrt_d(double v) {
+  double y = __builtin_amdgcn_rsq(v);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const double e = fma(-v * y, y, 1.0);
+    y = fma(0.5 * y, e, y);
+  }
+  return y;
+}
+
+// The RMSNorm factor 1 / sqrt(ss / n + eps); for n a power of two the mean is an exact scaling.
+IRON_DEV double inv_rms(double ss, int n, double eps) {
+  const double mean = (n & (n - 1)) == 0 ? ldexp(ss, -(31 - __clz(n))) : ss / (double)n;
+  return rsqrt_d(mean + eps);
+}
+
+// Sum of squares of N exact fp32 values in fp64 as a balanced tree (depth log2 N; every square
+// and partial sum of bf16-derived values is exact in fp64 for the magnitudes involved).
+template <int N>
+IRON_DEV double sum_sq_tree(const double (&v)[N]) {
+  double t[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = v[i] * v[i];
+#pragma unroll
+  for (int w = N / 2; w >= 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; ++i) t[i] += t[i + w];
+  return t[0];
+}
+
 // Block-wide fp64 sum for blockDim.x == 256. `scratch` holds >= 4 doubles of LDS.
 IRON_DEV double block_sum_256_d(double v, double* scratch) {
   v = wave_sum_d(v);

@@ -232,7 +232,7 @@ IRON_DEV void stage_x(const GemvParams& p, const uint4 (&xa)[B][S], const uint4 
       for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
     }
     ss = block_sum_256_d(ss, red);
-    const double inv = 1.0 / sqrt(ss / (double)K + (double)p.eps);
+    const double inv = inv_rms(ss, K, (double)p.eps);
     const bool to_bf16 = p.pro == PRO_RMS_BF16;
 #pragma unroll
     for (int r = 0; r < S + 1; ++r) {
@@ -491,11 +491,14 @@ IRON_DEV void prologue_lane(const GemvParams& p, int lane, const uint4 (&xl)[NCH
   if (p.pro != PRO_RMS_BF16 && p.pro != PRO_RES_RMS_F32) return;
   double ss = 0.0;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c)
+  for (int c = 0; c < NCH; ++c) {
+    double v[EPL];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) ss = fma((double)xf[c][j], (double)xf[c][j], ss);
+    for (int j = 0; j < EPL; ++j) v[j] = xf[c][j];
+    ss += sum_sq_tree(v);
+  }
   ss = wave_sum_d(ss);
-  const double inv = 1.0 / sqrt(ss / (double)p.K + (double)p.eps);
+  const double inv = inv_rms(ss, p.K, (double)p.eps);
   const bool to_bf16 = p.pro == PRO_RMS_BF16;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -621,8 +624,9 @@ IRON_DEV void store_rows(const GemvParams& p, int row0, int lane, const double (
   }
 }
 
-// Batch 1 with at most four chunks per lane keeps the activation in registers.
-constexpr bool xreg_path(int B, int NCH) { return B == 1 && NCH <= 4; }
+// Batch 1 with at most two chunks per lane keeps the activation in registers (longer rows
+// stage it once per workgroup in LDS: every wavefront loading the whole vector costs more).
+constexpr bool xreg_path(int B, int NCH) { return B == 1 && NCH <= 2; }
 
 template <int B, int R, int NCH, bool INT8, bool DUAL>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {

@@ -63,7 +63,7 @@ __global__ __launch_bounds__(128) void qkv_epilogue_kernel(QkvEpiParams p) {
   if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
   __syncthreads();
   ss = s_red[0] + s_red[1];
-  const double inv = 1.0 / sqrt(ss / (double)kHD + (double)p.eps);
+  const double inv = inv_rms(ss, kHD, (double)p.eps);
   const double y = bf16_to_f32(f64_to_bf16((x * inv) * (double)bf16_to_f32(hw)));
   s_y[d] = y;
   __syncthreads();
