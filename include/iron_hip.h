@@ -68,6 +68,19 @@ int iron_gemv_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int
 int iron_gemv_bf16(const uint16_t* w, const uint16_t* x, uint16_t* y, int B, int M, int K,
                    void* stream);
 
+/* Workspace bytes for iron_gemm_w8a16 (MFMA split-K partials; 256 when none are needed). */
+size_t iron_gemm_w8a16_workspace(int B, int M, int K, int G);
+
+/* Batched decode GEMM on MFMA: y[b][m] = bf16(sum_g s[m][g] * sum_{k in g} q[m][k] x[b][k]) for
+ * B in [1,16] (the batch sizes above the GEMV path), M % 64 == 0, K % 128 == 0, G in {32,64,128}.
+ * q is exact in bf16, each 32-wide k step is one v_mfma_f32_16x16x32_bf16 (fp32 sums of exact
+ * products), and the group scales apply in fp64; x: [B][K] bf16, y: [B][M] bf16. No reference
+ * counterpart (the reference has a bf16 GEMM operator, iron/operators/gemm/op.py:23-80, golden
+ * gemm/reference.py:8-19, and the int8 GEMV golden gemv_int8/op.py:173-178 it generalises). */
+int iron_gemm_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int M, int K, int G,
+                    int tile_m, int domain, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* Weighted RMSNorm y[r][c] = bf16(x[r][c] * rsqrt(mean_c(x^2) + eps) * w[c]).
  * Replaces RMSNorm (iron/operators/rms_norm/op.py:21-130; kernel rms_norm.cc:83-147). */
 int iron_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols, float eps,
@@ -108,8 +121,9 @@ int iron_advance_positions(int32_t* pos, int32_t* ctx, const uint16_t* table,
                            uint16_t* ang_rows, int HD, int max_pos, int B, int delta,
                            void* stream);
 
-/* Workspace bytes for iron_qkv_head (raw QKV staging). */
-size_t iron_qkv_head_workspace(int B, int Hq, int Hkv, int HD);
+/* Workspace bytes for iron_qkv_head (raw QKV staging; for B > 4 also the normalised input and
+ * the MFMA split-K partials). */
+size_t iron_qkv_head_workspace(int B, int D, int Hq, int Hkv, int HD);
 
 /* Fused decode QKV head, per batch row b:
  *   hn  = bf16(RMSNorm(cur[b]) * n_in)                                (rms_norm.cc:83-147)
@@ -147,7 +161,7 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
                      float scale, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes for iron_qkv_attn (raw QKV staging + split-K partials). */
-size_t iron_qkv_attn_workspace(int B, int Hq, int Hkv, int HD, int max_seq);
+size_t iron_qkv_attn_workspace(int B, int D, int Hq, int Hkv, int HD, int max_seq);
 
 /* Fused QKV head + decode attention for one decode step, per batch row b (ctx = pos[b] + 1):
  *   q, k, v  exactly as iron_qkv_head computes them (the k and v rows are appended to the caches
@@ -176,7 +190,9 @@ size_t iron_swiglu_mlp_workspace(int B, int D, int FF);
  *   gh  = silu(Wg . hf) * (Wu . hf)                       (fp32)
  *   nxt = bf16(x1 + Wd . gh)
  * Wo: [D][QD] wire (tile_m_o rows), Wg/Wu: [FF][D] wires (tile_m_gu), Wd: [D][FF] (tile_m_d).
- * a_out (optional, [B][D] bf16) receives a. Replaces SwiGLUMLPDataParallelOurs
+ * a_out (optional, [B][D] bf16) receives a. B <= 4 runs the fused GEMV kernels; B in [5,16] runs
+ * the prologue once per row and the three products on MFMA (fp32 hf and gh enter the MFMA as
+ * three exact bf16 planes, hi + mid + lo). Replaces SwiGLUMLPDataParallelOurs
  * (iron/operators/swiglu_mlp_dp/op_ours.py:46-582, op.py:22-227; golden
  * swiglu_mlp_dp/reference.py:8-67). */
 int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t* n_pf,

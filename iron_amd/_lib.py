@@ -43,6 +43,9 @@ SIGNATURES = {
     "iron_gemv_w8a16": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                  _c_int, _c_vp]),
     "iron_gemv_bf16": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
+    "iron_gemm_w8a16_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),
+    "iron_gemm_w8a16": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                 _c_int, _c_vp, _c_sz, _c_vp]),
     "iron_rmsnorm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_f, _c_vp]),
     "iron_lm_head": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_int, _c_int,
                               _c_int, _c_int, _c_int, _c_int, _c_vp]),
@@ -51,7 +54,7 @@ SIGNATURES = {
     "iron_embed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
     "iron_advance_positions": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int,
                                         _c_int, _c_vp]),
-    "iron_qkv_head_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),
+    "iron_qkv_head_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "iron_qkv_head": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_vp,
                                _c_vp, _c_ll, _c_ll, _c_ll, _c_vp, _c_int, _c_int, _c_int, _c_int,
                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_vp, _c_sz,
@@ -60,7 +63,7 @@ SIGNATURES = {
     "iron_decode_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_ll, _c_ll, _c_ll, _c_vp, _c_int,
                                   _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_vp,
                                   _c_sz, _c_vp]),
-    "iron_qkv_attn_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "iron_qkv_attn_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "iron_qkv_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                _c_ll, _c_ll, _c_ll, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_f, _c_vp, _c_sz,

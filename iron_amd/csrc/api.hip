@@ -47,6 +47,28 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   }
 }
 
+// One 256-thread workgroup per row: x1 = f32(cur + a), y = f32((x1 * inv_rms(x1)) * w), the
+// SwiGLU MLP's fp32 hf (swiglu_mlp_dp/reference.py:54-67) for batches on the MFMA path.
+__global__ __launch_bounds__(256) void res_rmsnorm_f32_kernel(const uint16_t* __restrict__ cur,
+                                                              const uint16_t* __restrict__ a,
+                                                              const uint16_t* __restrict__ w,
+                                                              float* __restrict__ y, int cols,
+                                                              float eps) {
+  __shared__ double red[4];
+  const size_t r = (size_t)blockIdx.x * cols;
+  double ss = 0.0;
+  for (int i = threadIdx.x; i < cols; i += 256) {
+    const double v = bf16_to_f32(cur[r + i]) + bf16_to_f32(a[r + i]);
+    ss = fma(v, v, ss);
+  }
+  ss = block_sum_256_d(ss, red);
+  const double inv = inv_rms(ss, cols, (double)eps);
+  for (int i = threadIdx.x; i < cols; i += 256) {
+    const double v = (double)(bf16_to_f32(cur[r + i]) + bf16_to_f32(a[r + i]));
+    y[r + i] = (float)((v * inv) * (double)bf16_to_f32(w[i]));
+  }
+}
+
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tokens,
                                                     const uint16_t* __restrict__ emb,
                                                     uint16_t* __restrict__ x, int D, int vocab) {
@@ -108,6 +130,23 @@ __global__ __launch_bounds__(64) void advance_kernel(int32_t* pos, int32_t* ctx,
 }
 
 }  // namespace
+
+namespace iron {
+
+int rmsnorm_launch(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols,
+                   float eps, hipStream_t stream) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream, x, w, y, cols, eps);
+  return check_launch("rmsnorm");
+}
+
+int res_rmsnorm_f32_launch(const uint16_t* cur, const uint16_t* a, const uint16_t* w, float* y,
+                           int rows, int cols, float eps, hipStream_t stream) {
+  hipLaunchKernelGGL(res_rmsnorm_f32_kernel, dim3(rows), dim3(256), 0, stream, cur, a, w, y,
+                     cols, eps);
+  return check_launch("res_rmsnorm_f32");
+}
+
+}  // namespace iron
 
 extern "C" {
 

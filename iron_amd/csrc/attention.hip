@@ -491,12 +491,6 @@ int launch_attention(AttnParams p, bool fused, int B, void* part_ws, size_t part
 
 }  // namespace
 
-namespace iron {
-int gemv_rms_internal(const void* wire, const uint16_t* x, const uint16_t* nw, uint16_t* y,
-                      int B, int M, int K, int G, int tile_m, int domain, float eps,
-                      hipStream_t stream, const char* fn);
-}
-
 extern "C" {
 
 size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx) {
@@ -536,10 +530,10 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
   return launch_attention(p, false, B, workspace, workspace_bytes, (hipStream_t)stream, fn);
 }
 
-size_t iron_qkv_attn_workspace(int B, int Hq, int Hkv, int HD, int max_seq) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || HD != kD || Hq % Hkv || max_seq <= 0) return 0;
-  const size_t raw = ((size_t)B * (Hq + 2 * Hkv) * HD * 2 + 255) & ~(size_t)255;
-  return raw + attn_ws_bytes(B, Hq, Hkv, max_seq) + 256;
+size_t iron_qkv_attn_workspace(int B, int D, int Hq, int Hkv, int HD, int max_seq) {
+  if (B <= 0 || D <= 0 || Hq <= 0 || Hkv <= 0 || HD != kD || Hq % Hkv || max_seq <= 0) return 0;
+  return iron::qkv_raw_bytes(B, D, (Hq + 2 * Hkv) * HD) + attn_ws_bytes(B, Hq, Hkv, max_seq) +
+         256;
 }
 
 int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
@@ -563,7 +557,7 @@ int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
   const int M = (Hq + 2 * Hkv) * HD;
   st = iron::check_wire(fn, wqkv, M, D, G, tile_m, domain);
   if (st) return st;
-  const size_t need = iron_qkv_attn_workspace(B, Hq, Hkv, HD, max_seq);
+  const size_t need = iron_qkv_attn_workspace(B, D, Hq, Hkv, HD, max_seq);
   if (!workspace || workspace_bytes < need)
     return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes,
                       need);
@@ -571,8 +565,9 @@ int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
     return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
   hipStream_t s = (hipStream_t)stream;
   uint16_t* raw = (uint16_t*)workspace;
-  const size_t raw_bytes = ((size_t)B * M * 2 + 255) & ~(size_t)255;
-  st = iron::gemv_rms_internal(wqkv, cur, n_in, raw, B, M, D, G, tile_m, domain, eps, s, fn);
+  const size_t raw_bytes = iron::qkv_raw_bytes(B, D, M);
+  st = iron::qkv_raw_internal(wqkv, cur, n_in, workspace, raw_bytes, B, M, D, G, tile_m, domain,
+                              eps, s, fn);
   if (st) return st;
   AttnParams p = {};
   p.raw = raw;

@@ -1,0 +1,407 @@
+// Batched int8-weight GEMM on MFMA for decode batches above the GEMV path (B = 5..16):
+//   Y[b][m] = EPI( sum_g s[m][g] * sum_{k in g} q[m][k] * x[b][k] )
+//
+// Reference: there is no int8 batched GEMM in the reference; its bf16 GEMM operator
+// (iron/operators/gemm/op.py:23-80, golden gemm/reference.py:8-19) and the int8 GEMV golden
+// (gemv_int8/op.py:173-178: dequantize, matmul, bf16) define the arithmetic. The weights are the
+// same row-block wire as the GEMV (gemv_int8/reference.py:59-80).
+//
+// Arithmetic: q is exact in bf16 (|q| <= 127), so one v_mfma_f32_16x16x32_bf16 per 32-wide k
+// step multiplies q by x exactly and sums 32 products in fp32; at the end of each quantization
+// group the fp32 partial is scaled by s (in fp64) and added to an fp64 accumulator. fp32 inputs
+// (the MLP's hf and gh) are split exactly into three bf16 planes (hi + mid + lo), three MFMAs
+// per step. The result is within the fp32 rounding of the per-group sums of the exact value (the
+// parity bar is the north star's rel/abs 1e-2; measured errors are a few fp32 ulps).
+//
+// Mapping: a workgroup (4 wavefronts) owns 64 rows x 16 batch columns over a K range (split-K
+// when the row tiles alone do not cover the chip). Per 128-wide K step the workgroup stages the
+// weight tile (64 rows x 128 int8 per matrix), its group scales and x (16 x 128, bf16 planes) in LDS
+// (double buffered: the next step's global loads are in flight while this one computes).
+// Wavefront w multiplies rows 16w..16w+15: lane l reads A = 8 int8 of row l%16 at k = (l/16)*8
+// and B = 8 bf16 of batch column l%16 at the same k; its 4 accumulators are rows (l/16)*4 + i,
+// column l%16 (the gfx950 16x16x32 operand layout, checked on the device).
+#include "common.h"
+#include "internal.h"
+
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+constexpr int kTM = 64;           // rows per workgroup
+constexpr int kKS = 128;          // K per pipeline step
+constexpr int kBN = 16;           // batch columns
+constexpr int kWRow = kKS + 16;   // LDS bytes per weight row (padded)
+constexpr int kXRow = kKS + 8;    // LDS bf16 per x row (padded)
+
+// epilogues (iron::GEMM_EPI_*): bf16(acc) | f32(acc) | f32(silu(acc0) * acc1) (dual) |
+// bf16(f32(r1 + r2) + acc)
+
+struct GemmParams {
+  const uint8_t* w0;
+  const uint8_t* w1;      // second matrix (dual) or null
+  int M, K, gshift, tile_m;
+  FastDiv tdiv;
+  uint32_t blk_bytes, xor_mask;
+  const void* x;          // [B][x_stride] bf16, or fp32 when x_f32
+  int x_f32, B, x_stride;
+  int splits, ksteps;     // split s covers pipeline steps [s*ksteps, (s+1)*ksteps)
+  double* part;           // [2][splits][kBN][M] fp64 partials (splits > 1)
+  int epi;
+  void* y;
+  int y_stride;
+  const uint16_t* r1;
+  const uint16_t* r2;
+  int r_stride;
+};
+
+IRON_DEV double silu_mul_d(double g, double u) {
+  double sig;
+  if (g >= 0.0) {
+    sig = 1.0 / (1.0 + exp(-g));
+  } else {
+    const double e = exp(g);
+    sig = e / (1.0 + e);
+  }
+  return (g * sig) * u;
+}
+
+IRON_DEV void store_out(const GemmParams& p, int b, int m, double a0, double a1) {
+  const size_t o = (size_t)b * p.y_stride + m;
+  switch (p.epi) {
+    case iron::GEMM_EPI_BF16: ((uint16_t*)p.y)[o] = f64_to_bf16(a0); break;
+    case iron::GEMM_EPI_F32: ((float*)p.y)[o] = (float)a0; break;
+    case iron::GEMM_EPI_SWIGLU_F32: ((float*)p.y)[o] = (float)silu_mul_d(a0, a1); break;
+    default: {
+      const size_t ro = (size_t)b * p.r_stride + m;
+      float x1 = bf16_to_f32(p.r1[ro]);
+      if (p.r2) x1 = x1 + bf16_to_f32(p.r2[ro]);
+      ((uint16_t*)p.y)[o] = f64_to_bf16((double)x1 + a0);
+    }
+  }
+}
+
+// 8 int8 (two dwords, signed after the domain xor) -> 8 bf16 (exact)
+IRON_DEV bf16x8 q8_to_bf16(uint32_t lo, uint32_t hi, uint32_t xm) {
+  lo ^= xm;
+  hi ^= xm;
+  bf16x8 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float f0 = (float)(int)(((int32_t)(lo << (24 - 8 * j))) >> 24);
+    const float f1 = (float)(int)(((int32_t)(hi << (24 - 8 * j))) >> 24);
+    r[j] = __builtin_bit_cast(__bf16, (uint16_t)(__float_as_uint(f0) >> 16));
+    r[4 + j] = __builtin_bit_cast(__bf16, (uint16_t)(__float_as_uint(f1) >> 16));
+  }
+  return r;
+}
+
+// 8 fp32 -> 8 bf16 of one of three planes: hi = the value truncated to bf16, mid = the remainder
+// truncated to bf16, lo = what is left (at most 8 significant bits, so exact in bf16). Every
+// plane value is exact and hi + mid + lo == the fp32 value.
+IRON_DEV uint4 split_plane(const uint4 a, const uint4 b, bool valid, int plane) {
+  const uint32_t f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t h2[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float v = __uint_as_float(valid ? f[2 * j + t] : 0u);
+      const float hi = __uint_as_float(__float_as_uint(v) & 0xffff0000u);
+      const float r1 = v - hi;
+      const float mid = __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
+      const float lo = r1 - mid;
+      const float pick = plane == 0 ? hi : (plane == 1 ? mid : lo);
+      h2[t] = __float_as_uint(pick) >> 16;
+    }
+    o[j] = h2[0] | (h2[1] << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+template <bool DUAL, bool XF32>
+__global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
+  constexpr int NM = DUAL ? 2 : 1;
+  constexpr int NX = XF32 ? 3 : 1;   // bf16 planes of x (fp32 x: hi, mid, lo)
+  __shared__ __align__(16) uint8_t s_w[2][NM][kTM][kWRow];
+  __shared__ __align__(16) uint16_t s_s[2][NM][kTM][kKS / 32];
+  __shared__ __align__(16) uint16_t s_x[2][NX][kBN][kXRow];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row0 = blockIdx.x * kTM;
+  const int split = blockIdx.y;
+  const int step0 = split * p.ksteps;
+  const int nsteps = p.ksteps;
+  const int ng = p.K >> p.gshift;
+  const int G = 1 << p.gshift;
+
+  // ---- global -> register staging of one pipeline step
+  const int lrow = tid >> 2, lpart = tid & 3;  // weight tile: row, 32-byte quarter
+  const uint8_t* wbase[NM];
+  const uint16_t* sbase[NM];
+  {
+    const uint32_t row = (uint32_t)(row0 + lrow);
+    const uint32_t blk = fastdiv(row, p.tdiv);
+    const uint32_t in = row - blk * (uint32_t)p.tile_m;
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      const uint8_t* base = (mi == 0 ? p.w0 : p.w1) + (size_t)blk * p.blk_bytes;
+      wbase[mi] = base + (size_t)in * p.K;
+      sbase[mi] = (const uint16_t*)(base + (size_t)p.tile_m * p.K) + (size_t)in * ng;
+    }
+  }
+  const int xb = tid >> 4, xk = (tid & 15) * 8;  // x tile: batch row, 8-element chunk
+  // registers of one pipeline step: the weight quarter-rows of matrix 0 (and 1), their
+  // scales, and x (bf16, or the two halves of 8 fp32)
+  uint4 wa0, wa1, wb0, wb1, rx0, rx1;
+  uint32_t sa, sb;
+  const int gpr = kKS / G;  // groups per step (G <= kKS)
+  const uint8_t* wsrc0 = wbase[0];
+  const uint8_t* wsrc1 = wbase[NM - 1];
+  const uint16_t* ssrc0 = sbase[0];
+  const uint16_t* ssrc1 = sbase[NM - 1];
+  const size_t xrow = (size_t)(xb < p.B ? xb : 0) * p.x_stride;
+#define GEMM_GLOAD(step_)                                                                      \
+  do {                                                                                         \
+    const int k0_ = (step_) * kKS;                                                             \
+    const int gi_ = (k0_ >> p.gshift) + (lpart < gpr ? lpart : 0);                             \
+    const uint4* s0_ = (const uint4*)(wsrc0 + k0_ + lpart * 32);                               \
+    wa0 = s0_[0];                                                                              \
+    wa1 = s0_[1];                                                                              \
+    sa = ssrc0[gi_];                                                                           \
+    if (DUAL) {                                                                                \
+      const uint4* s1_ = (const uint4*)(wsrc1 + k0_ + lpart * 32);                             \
+      wb0 = s1_[0];                                                                            \
+      wb1 = s1_[1];                                                                            \
+      sb = ssrc1[gi_];                                                                         \
+    }                                                                                          \
+    if (XF32) {                                                                                \
+      const uint4* xr_ = (const uint4*)((const float*)p.x + xrow + k0_ + xk);                  \
+      rx0 = xr_[0];                                                                            \
+      rx1 = xr_[1];                                                                            \
+    } else {                                                                                   \
+      rx0 = *(const uint4*)((const uint16_t*)p.x + xrow + k0_ + xk);                           \
+    }                                                                                          \
+  } while (0)
+#define GEMM_LSTORE(buf_)                                                                      \
+  do {                                                                                         \
+    uint4* d0_ = (uint4*)&s_w[(buf_)][0][lrow][lpart * 32];                                    \
+    d0_[0] = wa0;                                                                              \
+    d0_[1] = wa1;                                                                              \
+    if (lpart < kKS / 32) s_s[(buf_)][0][lrow][lpart] = (uint16_t)sa;                          \
+    if (DUAL) {                                                                                \
+      uint4* d1_ = (uint4*)&s_w[(buf_)][NM - 1][lrow][lpart * 32];                             \
+      d1_[0] = wb0;                                                                            \
+      d1_[1] = wb1;                                                                            \
+      if (lpart < kKS / 32) s_s[(buf_)][NM - 1][lrow][lpart] = (uint16_t)sb;                   \
+    }                                                                                          \
+    if (XF32) {                                                                                \
+      _Pragma("unroll") for (int pl_ = 0; pl_ < NX; ++pl_)                                     \
+        *(uint4*)&s_x[(buf_)][pl_][xb][xk] = split_plane(rx0, rx1, xb < p.B, pl_);              \
+    } else {                                                                                   \
+      *(uint4*)&s_x[(buf_)][0][xb][xk] = xb < p.B ? rx0 : make_uint4(0u, 0u, 0u, 0u);          \
+    }                                                                                          \
+  } while (0)
+
+  // ---- compute state
+  double acc[NM][4];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[mi][i] = 0.0;
+  f32x4 c[NM];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi) c[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int arow = wave * 16 + (lane & 15);      // A operand row (tile-relative)
+  const int kq = (lane >> 4) * 8;                // k offset of this lane in a 32-step
+  const int bcol = lane & 15;                    // B operand / C column (batch)
+  const int crow = wave * 16 + (lane >> 4) * 4;  // first C row (tile-relative)
+
+  GEMM_GLOAD(step0);
+  GEMM_LSTORE(0);
+  __syncthreads();
+  for (int it = 0; it < nsteps; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < nsteps) GEMM_GLOAD(step0 + it + 1);
+    const int k0 = (step0 + it) * kKS;
+#pragma unroll
+    for (int j = 0; j < kKS / 32; ++j) {
+      bf16x8 bx[NX];
+#pragma unroll
+      for (int xi = 0; xi < NX; ++xi)
+        bx[xi] = __builtin_bit_cast(bf16x8, *(const uint4*)&s_x[buf][xi][bcol][32 * j + kq]);
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) {
+        const uint2 qa = *(const uint2*)&s_w[buf][mi][arow][32 * j + kq];
+        const bf16x8 a = q8_to_bf16(qa.x, qa.y, p.xor_mask);
+#pragma unroll
+        for (int xi = 0; xi < NX; ++xi)
+          c[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bx[xi], c[mi], 0, 0, 0);
+      }
+      if (((k0 + 32 * (j + 1)) & (G - 1)) == 0) {  // end of a quantization group
+        const int gl = (32 * j) >> p.gshift;        // group index within this step
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const double s = bf16_to_f32(s_s[buf][mi][crow + i][gl]);
+            acc[mi][i] = fma(s, (double)c[mi][i], acc[mi][i]);
+          }
+          c[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
+    if (it + 1 < nsteps) GEMM_LSTORE(buf ^ 1);
+    __syncthreads();
+  }
+
+#undef GEMM_GLOAD
+#undef GEMM_LSTORE
+  // ---- write
+  if (bcol >= p.B) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = row0 + crow + i;
+    if (p.splits == 1) {
+      store_out(p, bcol, m, acc[0][i], NM > 1 ? acc[NM - 1][i] : 0.0);
+    } else {
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi)
+        p.part[(((size_t)mi * p.splits + split) * kBN + bcol) * p.M + m] = acc[mi][i];
+    }
+  }
+}
+
+// Split-K reduction in split order, then the epilogue. grid (M / 256, B), 256 threads.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p, int dual) {
+  const int m = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+  if (m >= p.M) return;
+  double a[2] = {0.0, 0.0};
+  for (int mi = 0; mi <= dual; ++mi)
+    for (int s = 0; s < p.splits; ++s)
+      a[mi] += p.part[(((size_t)mi * p.splits + s) * kBN + b) * p.M + m];
+  store_out(p, b, m, a[0], a[1]);
+}
+
+struct GemmPlan {
+  int splits, ksteps;
+};
+
+GemmPlan plan_gemm(int M, int K) {
+  const int tiles = M / kTM;
+  const int steps = K / kKS;
+  int splits = (256 + tiles - 1) / tiles;  // about one workgroup per CU
+  if (splits > steps) splits = steps;
+  while (splits > 1 && steps % splits) --splits;
+  return {splits, steps / splits};
+}
+
+}  // namespace
+
+namespace iron {
+
+size_t gemm_workspace_bytes(int M, int K, bool dual) {
+  const GemmPlan pl = plan_gemm(M, K);
+  if (pl.splits == 1) return 0;
+  return (size_t)(dual ? 2 : 1) * pl.splits * kBN * M * sizeof(double);
+}
+
+// An upper bound over every K (the split count never exceeds ceil(256 / (M / 64))).
+size_t gemm_workspace_bound(int M, bool dual) {
+  if (M <= 0 || M % kTM) return 0;
+  const size_t splits = (256 + M / kTM - 1) / (M / kTM);
+  return ((size_t)(dual ? 2 : 1) * splits * kBN * M * sizeof(double) + 255) & ~(size_t)255;
+}
+
+// Y = EPI(W0 [, W1] . x), B in [1, 16]; validation of M/K/G/B is the caller's (gemm_check).
+int gemm_check(const char* fn, int B, int M, int K, int G) {
+  if (B < 1 || B > kBN)
+    return fail(IRON_ERR_UNSUPPORTED, "%s: MFMA batch %d outside [1, %d]", fn, B, kBN);
+  if (M % kTM) return fail(IRON_ERR_UNSUPPORTED, "%s: M=%d not a multiple of %d", fn, M, kTM);
+  if (K % kKS) return fail(IRON_ERR_UNSUPPORTED, "%s: K=%d not a multiple of %d", fn, K, kKS);
+  if (G < 32 || G > kKS)
+    return fail(IRON_ERR_UNSUPPORTED, "%s: group size %d outside [32, %d] on the MFMA path", fn,
+                G, kKS);
+  return IRON_OK;
+}
+
+int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile_m, int domain,
+                   const void* x, bool x_f32, int B, int x_stride, int epi, void* y, int y_stride,
+                   const uint16_t* r1, const uint16_t* r2, int r_stride, void* ws,
+                   size_t ws_bytes, hipStream_t stream, const char* fn) {
+  int st = gemm_check(fn, B, M, K, G);
+  if (st) return st;
+  const bool dual = w1 != nullptr;
+  const GemmPlan pl = plan_gemm(M, K);
+  GemmParams p = {};
+  p.w0 = (const uint8_t*)w0;
+  p.w1 = (const uint8_t*)w1;
+  p.M = M;
+  p.K = K;
+  p.gshift = ilog2(G);
+  p.tile_m = tile_m;
+  p.tdiv = make_fastdiv((uint32_t)tile_m);
+  p.blk_bytes = (uint32_t)wire_block_bytes(K, G, tile_m);
+  p.xor_mask = domain == IRON_DOMAIN_BIASED ? 0x80808080u : 0u;
+  p.x = x;
+  p.x_f32 = x_f32;
+  p.B = B;
+  p.x_stride = x_stride;
+  p.splits = pl.splits;
+  p.ksteps = pl.ksteps;
+  p.epi = epi;
+  p.y = y;
+  p.y_stride = y_stride;
+  p.r1 = r1;
+  p.r2 = r2;
+  p.r_stride = r_stride;
+  if (pl.splits > 1) {
+    const size_t need = gemm_workspace_bytes(M, K, dual);
+    if (!ws || ws_bytes < need)
+      return fail(IRON_ERR_WORKSPACE, "%s: MFMA workspace %zu < %zu bytes", fn, ws_bytes, need);
+    if (!aligned(ws, 256)) return fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
+    p.part = (double*)ws;
+  }
+  dim3 grid(M / kTM, pl.splits);
+  if (dual) {
+    if (x_f32) hipLaunchKernelGGL((gemm_w8_mfma_kernel<true, true>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((gemm_w8_mfma_kernel<true, false>), grid, dim3(256), 0, stream, p);
+  } else {
+    if (x_f32) hipLaunchKernelGGL((gemm_w8_mfma_kernel<false, true>), grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((gemm_w8_mfma_kernel<false, false>), grid, dim3(256), 0, stream, p);
+  }
+  st = check_launch(fn);
+  if (st || pl.splits == 1) return st;
+  hipLaunchKernelGGL(gemm_reduce_kernel, dim3((M + 255) / 256, B), dim3(256), 0, stream, p,
+                     dual ? 1 : 0);
+  return check_launch(fn);
+}
+
+}  // namespace iron
+
+extern "C" {
+
+size_t iron_gemm_w8a16_workspace(int B, int M, int K, int G) {
+  (void)B;
+  (void)G;
+  if (M <= 0 || K <= 0 || M % kTM || K % kKS) return 0;
+  const size_t n = iron::gemm_workspace_bytes(M, K, false);
+  return n ? n : 256;
+}
+
+int iron_gemm_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int M, int K, int G,
+                    int tile_m, int domain, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  iron::clear_error();
+  const char* fn = "iron_gemm_w8a16";
+  if (!x || !y) return iron::fail(IRON_ERR_NULL, "%s: null tensor", fn);
+  int st = iron::check_wire(fn, wire, M, K, G, tile_m, domain);
+  if (st) return st;
+  if (!iron::aligned(x, 16)) return iron::fail(IRON_ERR_ALIGN, "%s: x not 16-byte aligned", fn);
+  return iron::gemm_w8_launch(wire, nullptr, M, K, G, tile_m, domain, x, false, B, K,
+                              iron::GEMM_EPI_BF16, y, M, nullptr, nullptr, 0, workspace,
+                              workspace_bytes, (hipStream_t)stream, fn);
+}
+
+}  // extern "C"

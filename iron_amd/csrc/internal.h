@@ -42,4 +42,31 @@ inline size_t wire_block_bytes(int K, int G, int tile_m) {
 // Validates the int8 wire geometry shared by every int8 entry point.
 int check_wire(const char* fn, const void* wire, int M, int K, int G, int tile_m, int domain);
 
+// Small prologue kernels (api.hip).
+int rmsnorm_launch(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols,
+                   float eps, hipStream_t stream);
+int res_rmsnorm_f32_launch(const uint16_t* cur, const uint16_t* a, const uint16_t* w, float* y,
+                           int rows, int cols, float eps, hipStream_t stream);
+
+// MFMA batched GEMM (gemm_mfma.hip) for decode batches above the GEMV limit.
+constexpr int kGemvMaxBatch = 4;
+constexpr int kGemmMaxBatch = 16;
+enum : int { GEMM_EPI_BF16 = 0, GEMM_EPI_F32 = 1, GEMM_EPI_SWIGLU_F32 = 2, GEMM_EPI_RES_BF16 = 3 };
+int gemm_check(const char* fn, int B, int M, int K, int G);
+size_t gemm_workspace_bound(int M, bool dual);
+int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile_m, int domain,
+                   const void* x, bool x_f32, int B, int x_stride, int epi, void* y, int y_stride,
+                   const uint16_t* r1, const uint16_t* r2, int r_stride, void* ws,
+                   size_t ws_bytes, hipStream_t stream, const char* fn);
+
+
+// The raw-QKV stage shared by the QKV head and the fused QKV head + attention (qkv.hip).
+size_t qkv_raw_bytes(int B, int D, int M);
+int qkv_raw_internal(const void* wqkv, const uint16_t* cur, const uint16_t* n_in, void* ws,
+                     size_t ws_bytes, int B, int M, int D, int G, int tile_m, int domain,
+                     float eps, hipStream_t s, const char* fn);
+int gemv_rms_internal(const void* wire, const uint16_t* x, const uint16_t* nw, uint16_t* y,
+                      int B, int M, int K, int G, int tile_m, int domain, float eps,
+                      hipStream_t stream, const char* fn);
+
 }  // namespace iron

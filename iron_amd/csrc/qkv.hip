@@ -9,12 +9,6 @@
 #include "common.h"
 #include "internal.h"
 
-namespace iron {
-int gemv_rms_internal(const void* wire, const uint16_t* x, const uint16_t* nw, uint16_t* y,
-                      int B, int M, int K, int G, int tile_m, int domain, float eps,
-                      hipStream_t stream, const char* fn);
-}
-
 namespace {
 
 constexpr int kHD = 128;
@@ -85,11 +79,44 @@ __global__ __launch_bounds__(128) void qkv_epilogue_kernel(QkvEpiParams p) {
 
 }  // namespace
 
+namespace iron {
+
+static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Bytes of the raw-QKV stage: raw (bf16 [B][M]), and for B > 4 the normalised input (bf16
+// [B][D]) and the MFMA split-K partials.
+size_t qkv_raw_bytes(int B, int D, int M) {
+  size_t n = round256((size_t)B * M * 2);
+  if (B > kGemvMaxBatch) n += round256((size_t)B * D * 2) + gemm_workspace_bound(M, false);
+  return n;
+}
+
+// raw = bf16(Wqkv . bf16(RMSNorm(cur) * n_in)): the fused-prologue GEMV for B <= 4; for larger
+// batches the normalisation runs once per row and the product on MFMA.
+int qkv_raw_internal(const void* wqkv, const uint16_t* cur, const uint16_t* n_in, void* ws,
+                     size_t ws_bytes, int B, int M, int D, int G, int tile_m, int domain,
+                     float eps, hipStream_t s, const char* fn) {
+  uint16_t* raw = (uint16_t*)ws;
+  if (B <= kGemvMaxBatch)
+    return gemv_rms_internal(wqkv, cur, n_in, raw, B, M, D, G, tile_m, domain, eps, s, fn);
+  int st = gemm_check(fn, B, M, D, G);
+  if (st) return st;
+  uint16_t* hn = (uint16_t*)((char*)ws + round256((size_t)B * M * 2));
+  char* part = (char*)hn + round256((size_t)B * D * 2);
+  st = rmsnorm_launch(cur, n_in, hn, B, D, eps, s);
+  if (st) return st;
+  return gemm_w8_launch(wqkv, nullptr, M, D, G, tile_m, domain, hn, false, B, D, GEMM_EPI_BF16,
+                        raw, M, nullptr, nullptr, 0, part, ws_bytes - (size_t)(part - (char*)ws),
+                        s, fn);
+}
+
+}  // namespace iron
+
 extern "C" {
 
-size_t iron_qkv_head_workspace(int B, int Hq, int Hkv, int HD) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || HD <= 0) return 0;
-  return ((size_t)B * (Hq + 2 * Hkv) * HD * 2 + 255) & ~(size_t)255;
+size_t iron_qkv_head_workspace(int B, int D, int Hq, int Hkv, int HD) {
+  if (B <= 0 || D <= 0 || Hq <= 0 || Hkv <= 0 || HD <= 0) return 0;
+  return iron::qkv_raw_bytes(B, D, (Hq + 2 * Hkv) * HD);
 }
 
 int iron_qkv_head(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
@@ -109,13 +136,16 @@ int iron_qkv_head(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
   const int M = (Hq + 2 * Hkv) * HD;
   int st = iron::check_wire(fn, wqkv, M, D, G, tile_m, domain);
   if (st) return st;
-  const size_t need = iron_qkv_head_workspace(B, Hq, Hkv, HD);
+  const size_t need = iron_qkv_head_workspace(B, D, Hq, Hkv, HD);
   if (!workspace || workspace_bytes < need)
     return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes,
                       need);
+  if (!iron::aligned(workspace, 256))
+    return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
   hipStream_t s = (hipStream_t)stream;
   uint16_t* raw = (uint16_t*)workspace;
-  st = iron::gemv_rms_internal(wqkv, cur, n_in, raw, B, M, D, G, tile_m, domain, eps, s, fn);
+  st = iron::qkv_raw_internal(wqkv, cur, n_in, workspace, workspace_bytes, B, M, D, G, tile_m,
+                              domain, eps, s, fn);
   if (st) return st;
   QkvEpiParams p = {};
   p.raw = raw;

@@ -7,7 +7,8 @@ tiling knobs (``num_aie_columns``, ``tile_size_output``, ``weight_depth``,
 ``tile_size_input`` fixes the wire's row-block height, and ``kernel_source`` the payload domain
 (``"mv_int8_signed.cc"`` = signed, default = biased), exactly the pairing the reference uses.
 ``group_size`` is new: the reference hard-wires 128 (op.py:83-84), the graded configs use 32.
-``batch_size`` (also new) streams the weights once for up to 4 activation vectors, and
+``batch_size`` (also new) streams the weights once for up to 16 activation vectors (1-4 on the
+GEMV kernels, 5-16 on the MFMA GEMM, iron_gemm_w8a16), and
 ``epilogue="argmax"`` (new; the LM-head use) appends a ``(batch_size,)`` int64 output that must
 be zero before the call and receives the packed argmax key of each bf16 output row vector.
 """
@@ -21,7 +22,7 @@ import torch
 
 from ... import _lib
 from ...common.base import AIERuntimeArgSpec, MLIROperator, check_args
-from .._common import domain_code, stream_ptr
+from .._common import Workspace, domain_code, stream_ptr
 from ..wire import domain_of, wire_nbytes
 
 
@@ -65,8 +66,10 @@ class GEMVInt8(MLIROperator):
             raise ValueError(f"K must be a multiple of GROUP_SIZE={self.group_size}")
         if self.M % self.tile_size_input != 0:
             raise ValueError("tile_size_input must divide M")
-        if not 1 <= self.batch_size <= 4:
-            raise ValueError("batch_size must be in [1, 4]")
+        if not 1 <= self.batch_size <= 16:
+            raise ValueError("batch_size must be in [1, 16]")
+        if self.batch_size > 4 and self.epilogue != "none":
+            raise ValueError("the argmax epilogue needs batch_size <= 4")
         if self.epilogue not in ("none", "argmax"):
             raise ValueError(f"unknown epilogue {self.epilogue!r}")
         if self.epilogue == "argmax" and self.num_batches != 1:
@@ -109,6 +112,8 @@ class GEMVInt8(MLIROperator):
         dom = domain_code(self.domain)
         wb = self.wire_bytes
         M, K, G, tm, B = self.M, self.K, self.group_size, self.tile_size_input, self.batch_size
+        ws = (Workspace(lib.iron_gemm_w8a16_workspace(B, M, K, G), self.context.device)
+              if B > 4 else None)
 
         def call(*args):
             w, x, y = check_args(self, args)[:3]
@@ -119,9 +124,15 @@ class GEMVInt8(MLIROperator):
                     args[3].data_ptr(), B, M, K, G, tm, dom, s), "GEMVInt8")
                 return
             for nb in range(self.num_batches):
-                _lib.check(lib.iron_gemv_w8a16(
-                    w.data_ptr() + nb * wb, x.data_ptr() + nb * B * K * 2,
-                    y.data_ptr() + nb * B * M * 2, B, M, K, G, tm, dom, s), "GEMVInt8")
+                if ws is not None:
+                    _lib.check(lib.iron_gemm_w8a16(
+                        w.data_ptr() + nb * wb, x.data_ptr() + nb * B * K * 2,
+                        y.data_ptr() + nb * B * M * 2, B, M, K, G, tm, dom, ws.ptr, ws.nbytes,
+                        s), "GEMVInt8")
+                else:
+                    _lib.check(lib.iron_gemv_w8a16(
+                        w.data_ptr() + nb * wb, x.data_ptr() + nb * B * K * 2,
+                        y.data_ptr() + nb * B * M * 2, B, M, K, G, tm, dom, s), "GEMVInt8")
 
         return call
 

@@ -51,7 +51,8 @@ class QKVHeadAttention(QKVHeadDataParallel):
     def get_callable(self, params: RuntimeParams | None = None):
         lib = _lib.load()
         B = self.batch
-        ws = Workspace(lib.iron_qkv_attn_workspace(B, self.Hq, self.Hkv, self.HD, self.max_seq),
+        ws = Workspace(lib.iron_qkv_attn_workspace(B, self.D, self.Hq, self.Hkv, self.HD,
+                                                   self.max_seq),
                        self.context.device)
         dom = domain_code(self.domain)
         voff, sb, sh, st = self.kv_strides()

@@ -135,7 +135,7 @@ class QKVHeadDataParallel(MLIROperator):
         element-offset semantics while the kernel reads positions."""
         lib = _lib.load()
         B = self.batch
-        ws = Workspace(lib.iron_qkv_head_workspace(B, self.Hq, self.Hkv, self.HD),
+        ws = Workspace(lib.iron_qkv_head_workspace(B, self.D, self.Hq, self.Hkv, self.HD),
                        self.context.device)
         dom = domain_code(self.domain)
         voff, sb, sh, st = self.kv_strides()

@@ -11,7 +11,8 @@ qwen3_npu_int8.py:525-530). Wo uses a plain ``tile_rows_o``-row wire instead of 
 NPU per-core overlap windows (op_ours.py:357-369) -- those duplicated pad rows only exist to
 feed eight AIE columns. ``gh_scratch`` is the operator's device workspace (fp32 gh, which the
 golden keeps unrounded) sized by ``iron_swiglu_mlp_workspace``; ``a_scratch`` receives
-``a = bf16(Wo @ cx)`` under fuse_o. ``batch`` (new) runs up to 4 rows with one weight pass.
+``a = bf16(Wo @ cx)`` under fuse_o. ``batch`` (new) runs up to 16 rows with one weight pass (1-4 on the fused GEMV kernels, 5-16
+on the MFMA GEMMs).
 """
 
 from __future__ import annotations
@@ -59,8 +60,8 @@ class SwiGLUMLPDataParallelOurs(SwiGLUMLPDataParallel):
         for what, K in (("D", self.D), ("FF", self.FF)) + ((("QD", self.QD),) if self.fuse_o else ()):
             if K % self.group_size:
                 raise ValueError(f"{what}={K} not a multiple of group_size={self.group_size}")
-        if not 1 <= self.batch <= 4:
-            raise ValueError("batch must be in [1, 4]")
+        if not 1 <= self.batch <= 16:
+            raise ValueError("batch must be in [1, 16]")
         self.ff_pad = self.FF
 
     @property

@@ -1,0 +1,165 @@
+"""GPU parity of the MFMA batched-decode path (B = 5..16) against the CPU oracle.
+
+The MFMA path sums each 32-wide group of exact q*x products in fp32 (v_mfma_f32_16x16x32_bf16)
+and applies the group scales in fp64, so its results are within the fp32 rounding of the exact
+value rather than correctly rounded. Two bars per case, both written here:
+  * the north-star tolerance rel 1e-2 / abs 1e-2 against the exact oracle and the literal golden;
+  * every bf16 output within one bf16 ulp of the exact oracle's (the fp32 group sums can move a
+    value across a bf16 rounding boundary, never further), with the count of bit-exact outputs
+    printed.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from iron_amd.common.test_utils import verify_buffer
+from iron_amd.operators import (GEMVInt8, QKVHeadAttention, SwiGLUMLPDataParallelOurs)
+from iron_amd.operators.wire import pack_wire
+from oracle import attention as oatt
+from oracle import blocks as oblk
+from oracle import gemv as ogemv
+from oracle import norms as onorm
+from oracle.numerics import LITERAL
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL = ATOL = 1e-2
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def assert_within_one_ulp(got: torch.Tensor, want: torch.Tensor, what: str):
+    g = got.cpu().float().reshape(-1)
+    w = want.cpu().float().reshape(-1)
+    exact = int((g == w).sum())
+    # one bf16 ulp of the larger magnitude (8 significant bits)
+    mag = torch.maximum(g.abs(), w.abs()).clamp_min(2.0 ** -126)
+    ulp = torch.exp2(torch.floor(torch.log2(mag)) - 7)
+    bad = int(((g - w).abs() > ulp).sum())
+    print(f"{what}: {exact}/{w.numel()} bit-exact, {bad} beyond one ulp", flush=True)
+    assert bad == 0, f"{what}: {bad} of {w.numel()} outputs differ by more than one bf16 ulp"
+
+
+def _weights(M, K, G, gen):
+    q = torch.randint(-127, 128, (M, K), generator=gen, dtype=torch.int16)
+    s = (torch.randn(M, K // G, generator=gen) * 0.02).abs().to(torch.bfloat16)
+    return q, s
+
+
+@pytest.mark.parametrize("M,K,G,tile_m,B,domain", [
+    (6144, 4096, 32, 4, 16, "signed"),    # Qwen3-8B fused QKV, BASELINE config 5 batch
+    (4096, 12288, 32, 4, 16, "signed"),   # Qwen3-8B down projection
+    (6144, 2048, 32, 12, 8, "signed"),    # Qwen3-1.7B gate/up at BASELINE config 2 batch 8
+    (256, 512, 64, 16, 5, "biased"),
+    (64, 128, 128, 8, 11, "signed"),
+])
+def test_gemm_mfma(M, K, G, tile_m, B, domain):
+    _say(f"gemm_mfma M={M} K={K} G={G} tile_m={tile_m} B={B} {domain}")
+    gen = torch.Generator().manual_seed(M + K + B)
+    q, s = _weights(M, K, G, gen)
+    x = torch.randn(B, K, generator=gen).to(torch.bfloat16)
+    op = GEMVInt8(M=M, K=K, tile_size_input=tile_m, group_size=G, batch_size=B,
+                  kernel_vector_size=16,
+                  kernel_source="mv_int8_signed.cc" if domain == "signed" else None)
+    wire = pack_wire(q, s, tile_m, domain).view(torch.bfloat16).to(DEV)
+    y = torch.zeros(B, M, dtype=torch.bfloat16, device=DEV)
+    fn = op.get_callable()
+    fn(wire, x.to(DEV), y)
+    torch.cuda.synchronize()
+    exact = ogemv.gemv_exact(q, s, x).float().to(torch.bfloat16)
+    assert not verify_buffer(y.cpu(), "y", exact, rel_tol=RTOL, abs_tol=ATOL)
+    literal = ogemv.gemv_exact(q, s, x, dt=LITERAL).to(torch.bfloat16)
+    assert not verify_buffer(y.cpu(), "y", literal, rel_tol=RTOL, abs_tol=ATOL)
+    assert_within_one_ulp(y, exact, "gemm")
+    y2 = torch.zeros_like(y)                  # deterministic: a second call gives the same bits
+    fn(wire, x.to(DEV), y2)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu().view(torch.int16), y2.cpu().view(torch.int16))
+
+
+@pytest.mark.parametrize("D,FF,QD,fuse_o,G,B", [
+    (2048, 6144, 0, False, 32, 8),      # BASELINE config 2, batch 8 (Qwen3-1.7B MLP)
+    (1024, 3072, 2048, True, 32, 16),   # Qwen3-0.6B chain arm at batch 16
+])
+def test_swiglu_mlp_mfma(D, FF, QD, fuse_o, G, B):
+    _say(f"swiglu mfma D={D} FF={FF} QD={QD} fuse_o={fuse_o} G={G} B={B}")
+    gen = torch.Generator().manual_seed(D + FF + B)
+    op = SwiGLUMLPDataParallelOurs(D=D, FF=FF, QD=QD or None, fuse_o=fuse_o, group_size=G,
+                                   epsilon=1e-6, batch=B, kernel_source="mv_int8_signed.cc")
+
+    def lin(M, K, std):
+        return ogemv.rtn_quantize(torch.randn(M, K, generator=gen) * std, G)
+
+    wg, wu, wd = lin(FF, D, 0.05), lin(FF, D, 0.05), lin(D, FF, 0.05)
+    cur = torch.randn(B, D, generator=gen).to(torch.bfloat16)
+    n_pf = (torch.rand(D, generator=gen) + 0.5).to(torch.bfloat16)
+    wo = lin(D, QD, 0.05) if fuse_o else None
+    cx = torch.randn(B, QD if fuse_o else D, generator=gen).to(torch.bfloat16)
+    wires = {}
+    if fuse_o:
+        wires["Wo"] = pack_wire(*wo, op.tile_rows_o, "signed")
+    wires["Wg"] = pack_wire(*wg, op.tile_rows_gu, "signed")
+    wires["Wu"] = pack_wire(*wu, op.tile_rows_gu, "signed")
+    wires["Wd"] = pack_wire(*wd, op.tile_rows_d, "signed")
+    ws = torch.zeros(op.workspace_bytes(), dtype=torch.uint8, device=DEV)
+    nxt = torch.zeros(B * D, dtype=torch.bfloat16, device=DEV)
+    args = [cur.reshape(-1).to(DEV), cx.reshape(-1).to(DEV), n_pf.to(DEV)]
+    args += [wires[k].view(torch.bfloat16).to(DEV) for k in ("Wo", "Wg", "Wu", "Wd") if k in wires]
+    args.append(ws)
+    a_s = torch.zeros(B * D, dtype=torch.bfloat16, device=DEV)
+    if fuse_o:
+        args.append(a_s)
+    args.append(nxt)
+    op.get_callable()(*args)
+    torch.cuda.synchronize()
+    want, want_a = oblk.swiglu_mlp(cur, cx, n_pf, wg, wu, wd, 1e-6, wo=wo)
+    assert not verify_buffer(nxt.cpu(), "nxt", want, RTOL, ATOL)
+    lit, _ = oblk.swiglu_mlp(cur, cx, n_pf, wg, wu, wd, 1e-6, wo=wo, dt=LITERAL)
+    assert not verify_buffer(nxt.cpu(), "nxt", lit, RTOL, ATOL)
+    assert_within_one_ulp(nxt, want, "mlp nxt")
+    if fuse_o:
+        assert_within_one_ulp(a_s, want_a, "mlp a")
+
+
+def test_qkv_attention_mfma_batch16():
+    """Qwen3-8B heads (32 Q / 8 KV x 128, D = 4096) at batch 16: the raw QKV on MFMA, then the
+    fused epilogue + attention; ragged positions."""
+    D, Hq, Hkv, HD, S, G, tm, B = 4096, 32, 8, 128, 512, 32, 16, 16
+    _say(f"qkv_attn mfma D={D} Hq={Hq} Hkv={Hkv} S={S} B={B}")
+    gen = torch.Generator().manual_seed(4242)
+    M = (Hq + 2 * Hkv) * HD
+    q8, s = ogemv.rtn_quantize(torch.randn(M, D, generator=gen) * 0.05, G)
+    cur = torch.randn(B, D, generator=gen).to(torch.bfloat16)
+    n_in = (torch.rand(D, generator=gen) + 0.5).to(torch.bfloat16)
+    n_qn = (torch.rand(HD, generator=gen) + 0.5).to(torch.bfloat16)
+    n_kn = (torch.rand(HD, generator=gen) + 0.5).to(torch.bfloat16)
+    pos = torch.randint(0, S, (B,), generator=gen)
+    table = onorm.rope_angle_table(S, HD, 1e6)
+    k0 = torch.randn(B, Hkv, S, HD, generator=gen).to(torch.bfloat16)
+    v0 = torch.randn(B, Hkv, S, HD, generator=gen).to(torch.bfloat16)
+    op = QKVHeadAttention(D=D, HD=HD, Hq=Hq, Hkv=Hkv, max_seq=S, group_size=G,
+                          tile_size_input=tm, kv_layout="separate", batch=B, num_aie_columns=1,
+                          kernel_source="mv_int8_signed.cc")
+    fn = op.get_callable()
+    fn.params.write(op.kv_offset_parameter, (pos * HD).numpy())
+    kc, vc = k0.clone().to(DEV), v0.clone().to(DEV)
+    out = torch.zeros(B * Hq * HD, dtype=torch.bfloat16, device=DEV)
+    fn(cur.reshape(-1).to(DEV), n_in.to(DEV),
+       pack_wire(q8, s, tm, "signed").view(torch.bfloat16).to(DEV), n_qn.to(DEV), n_kn.to(DEV),
+       table[pos].reshape(-1).to(DEV), kc.reshape(-1), vc.reshape(-1), out)
+    torch.cuda.synchronize()
+    wq, wk, wv = oblk.qkv_head(cur, n_in, q8, s, n_qn, n_kn, table[pos], Hq, Hkv, HD, 1e-6)
+    kk, vv = k0.clone(), v0.clone()
+    for b in range(B):
+        kk[b, :, int(pos[b])] = wk[b].reshape(Hkv, HD)
+        vv[b, :, int(pos[b])] = wv[b].reshape(Hkv, HD)
+    want = oatt.decode_attention(wq.reshape(B, Hq, HD), kk, vv, (pos + 1).tolist())
+    assert not verify_buffer(out.cpu(), "attn", want.reshape(-1), RTOL, ATOL)
+    # the cache rows written at each position hold the oracle's k and v (to one ulp: raw QKV
+    # comes from the MFMA sums)
+    for b in range(B):
+        p = int(pos[b])
+        assert_within_one_ulp(kc[b, :, p].cpu(), wk[b].reshape(Hkv, HD), f"k@{b}")
