@@ -180,6 +180,15 @@ int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
                   int Hkv, int max_seq, int G, int tile_m, int domain, float eps, float scale,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* Causal prefill attention (GQA) on MFMA:
+ *   o[b][h][i] = sum_{j <= i} softmax_j(q[b][h][i] . k[b][h*KV/H][j] * scale) v[b][h*KV/H][j]
+ * q/o: [B][H][S][D] bf16, k/v: [B][KV][S][D] bf16, D in {64, 128}, S a multiple of 64 (the
+ * reference pads to 64), H/KV in {1, 2} or a multiple of 4. Scores, softmax and accumulation in
+ * fp32 (bf16 MFMAs), probabilities rounded to bf16 for the P.V product, bf16 output.
+ * Replaces MHA (iron/operators/mha/op.py:20-153; golden mha/reference.py:27-94, causal SDPA). */
+int iron_prefill_attn(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, int B,
+                      int H, int KV, int S, int D, float scale, void* stream);
+
 /* Workspace bytes for iron_swiglu_mlp (x1 residual halves + gh, fp32). */
 size_t iron_swiglu_mlp_workspace(int B, int D, int FF);
 

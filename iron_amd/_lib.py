@@ -68,6 +68,8 @@ SIGNATURES = {
                                _c_ll, _c_ll, _c_ll, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_f, _c_vp, _c_sz,
                                _c_vp]),
+    "iron_prefill_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
+                                   _c_int, _c_f, _c_vp]),
     "iron_swiglu_mlp_workspace": (_c_sz, [_c_int, _c_int, _c_int]),
     "iron_swiglu_mlp": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,

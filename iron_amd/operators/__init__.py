@@ -9,6 +9,7 @@ _OPERATOR_MODULES = {
     "DecodeAttention": "decode_attn",
     "GEMV": "gemv",
     "GEMVInt8": "gemv_int8",
+    "MHA": "mha",
     "QKVHeadAttention": "qkv_attn",
     "QKVHeadDataParallel": "qkv_head_dp",
     "QKVHeadDataParallelOurs": "qkv_head_dp:op_ours",

@@ -8,6 +8,7 @@ reference operator's own ``reference()`` method:
   DecodeAttention             -- decode_attn/reference.py:26-38 (static arm: every key valid)
   QKVHeadDataParallel(Ours)   -- qkv_head_dp/op.py:225-231 (concatenated [q | k | v])
   SwiGLUMLPDataParallelOurs   -- swiglu_mlp_dp/op_ours.py:543-582
+  MHA                         -- mha/reference.py:73-81 (causal SDPA, scale 1/sqrt(d))
 Operators are recognised by class name and read only their public fields.
 """
 
@@ -15,7 +16,7 @@ from __future__ import annotations
 
 import torch
 
-from .attention import decode_attention
+from .attention import causal_prefill_attention, decode_attention
 from .blocks import qkv_head, swiglu_mlp
 from .gemv import gemv_exact, unpack_wire
 from .norms import rms_norm
@@ -76,6 +77,12 @@ def reference(op, *inputs):
         nxt, _ = swiglu_mlp(cur.reshape(op.batch, op.D), cx, n_pf, wg, wu, wd, op.epsilon,
                             wo=wo)
         return nxt.reshape(-1)
+    if name == "MHA":
+        H, KV, D, S = op.num_heads, op.kv_heads, op.d, op.seq_padded
+        q = inputs[0].reshape(H, S, D)
+        k = inputs[1].reshape(KV, S, D)
+        v = inputs[2].reshape(KV, S, D)
+        return causal_prefill_attention(q, k, v).to(torch.bfloat16).reshape(-1)
     if name == "QKVHeadAttention":
         # The fused operator has no reference counterpart (the reference runs the QKV head and
         # DecodeAttention as two entries); its result is checked against that composition.

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from iron_amd.common.test_utils import verify_buffer
-from iron_amd.operators import (GEMVInt8, QKVHeadAttention, SwiGLUMLPDataParallelOurs)
+from iron_amd.operators import MHA, GEMVInt8, QKVHeadAttention, SwiGLUMLPDataParallelOurs
 from iron_amd.operators.wire import pack_wire
 from oracle import attention as oatt
 from oracle import blocks as oblk
@@ -163,3 +163,36 @@ def test_qkv_attention_mfma_batch16():
     for b in range(B):
         p = int(pos[b])
         assert_within_one_ulp(kc[b, :, p].cpu(), wk[b].reshape(Hkv, HD), f"k@{b}")
+
+
+@pytest.mark.parametrize("H,KV,S,D,dist", [
+    (32, 8, 2048, 128, "normal"),   # BASELINE config 5 prefill: Qwen3-8B heads, S = 2048
+    (4, 2, 256, 64, "rand4"),       # the reference golden's input distribution, d = 64
+    (8, 8, 128, 128, "normal"),     # plain MHA
+    (16, 8, 512, 64, "normal"),     # GQA 2
+    (4, 1, 192, 128, "normal"),     # S padded from 150 (the reference's 64-padding)
+])
+def test_prefill_attention(H, KV, S, D, dist, oracle_provider):
+    _say(f"prefill H={H} KV={KV} S={S} D={D} {dist}")
+    gen = torch.Generator().manual_seed(H * S + D)
+    seq = 150 if S == 192 else S
+    op = MHA(num_heads=H, seq_len=seq, d=D, num_KV_heads=KV)
+    Sp = op.seq_padded
+    assert Sp == S
+
+    def draw(*shape):
+        if dist == "rand4":
+            return (torch.rand(*shape, generator=gen) * 4).to(torch.bfloat16)
+        return torch.randn(*shape, generator=gen).to(torch.bfloat16)
+
+    q, k, v = draw(H, Sp, D), draw(KV, Sp, D), draw(KV, Sp, D)
+    o = torch.zeros(H * Sp * D, dtype=torch.bfloat16, device=DEV)
+    op.get_callable()(q.reshape(-1).to(DEV), k.reshape(-1).to(DEV), v.reshape(-1).to(DEV), o)
+    torch.cuda.synchronize()
+    want = op.reference(q.reshape(-1), k.reshape(-1), v.reshape(-1)).reshape(H, Sp, D)
+    got = o.cpu().reshape(H, Sp, D)
+    err = (got.float() - want.float()).abs()
+    print(f"prefill max abs err {float(err.max()):.3g} (rows < seq_len)", flush=True)
+    # rows past seq_len are padding (their outputs are defined but unused, as in the reference)
+    assert not verify_buffer(got[:, :seq].contiguous(), "o", want[:, :seq].contiguous(), RTOL,
+                             ATOL)
