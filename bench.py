@@ -32,6 +32,10 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the bf16 LM-head GEMV from two rocprofv3 --pmc passes over this bench:
+# FETCH_SIZE 152040.19 KiB x 2.0 + WRITE_SIZE 310.56 KiB x 1.0, the factors being what the same
+# counters read for a plain 256 MiB device copy (profiles/decode_qwen3_0_6b_hbm_traffic.md).
+LM_HEAD_BF16_TRAFFIC = 311_696_320
 
 
 def parse():
@@ -41,6 +45,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--cpu-sample-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the standalone measurements of BASELINE configs 1, 2, 3 and 5")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--lm-head", default="bf16", choices=["bf16", "int8"])
     return ap.parse_args()
@@ -56,7 +62,7 @@ def main():
 
     from iron_amd.applications.qwen3_0_6b.qwen3_npu_int8 import Qwen3NPU
     from iron_amd.applications.qwen3_0_6b.weights import (Qwen3Config, random_qwen3_weights,
-                                                           synthetic_kv)
+                                                           synthetic_kv, weights_to)
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     cfg = Qwen3Config.qwen3_0_6b(group_size=32)
@@ -66,6 +72,7 @@ def main():
     S = (S + 63) // 64 * 64
     t0 = time.time()
     w = random_qwen3_weights(cfg, seed=args.seed, lm_head=args.lm_head, device="cuda")
+    w_cpu = None if args.no_cpu_baseline else weights_to(w, "cpu")
     k0, v0 = synthetic_kv(cfg, P0, seed=7)
     print(f"[bench] weights ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
     model = Qwen3NPU(config=cfg, weights=w, max_seq_len=S)
@@ -134,7 +141,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 weights x bf16 activations, fp32 accumulate",
+        "dtype": "int8 x bf16 -> f64 accumulate (bf16/fp32 operator boundaries)",
         "data": "synthetic (seeded random-init weights, synthetic KV prefill, seeded prompt)",
         "config": {"workload": "BASELINE config 4: Qwen3-0.6B-architecture int8 (G=32) decode, "
                                f"B=1, {args.lm_head} LM head, context {start + 1}.."
@@ -145,15 +152,24 @@ def main():
                                                 "epilogue)" if args.lm_head == "bf16" else
                      "lm_head GEMV (int8 G=32, argmax epilogue)",
                      "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": LM_HEAD_BF16_TRAFFIC if args.lm_head == "bf16" else None,
                      "bytes_per_launch": lm_bytes, "avg_launch_us": round(lm_us, 2)},
         "step_roofline": {"bytes_per_step": int(step_bytes), "achieved": round(step_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
     }
 
+    if not args.no_configs:
+        # the other BASELINE configurations, each timed standalone over >= 512 MiB of rotating
+        # operands (iron_amd/benchmarks.py); config 5 includes the 36-layer Qwen3-8B B=16 stack
+        del model, w
+        torch.cuda.empty_cache()
+        from iron_amd import benchmarks
+        print("[bench] configs 1, 2, 3, 5", file=sys.stderr, flush=True)
+        result["configs"] = benchmarks.run_all()
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, w, (k0, v0), prompt, tokens, start, S,
+        result["cpu_baseline"] = cpu_baseline(cfg, w_cpu, (k0, v0), prompt, tokens, start, S,
                                               args.cpu_sample_steps)
     print(json.dumps(result), flush=True)
 

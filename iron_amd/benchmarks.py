@@ -1,0 +1,256 @@
+"""Standalone measurements of the hot-path kernels at the BASELINE configurations (1, 2, 3, 5).
+
+    python -m iron_amd.benchmarks            # prints one JSON object
+
+Every measurement replays a captured HIP graph of back-to-back launches that cycle over distinct
+copies of the streamed operands (at least 512 MiB in total, twice the 256 MiB Infinity Cache), so
+the bytes come from HBM; the per-launch time is the graph time divided by the launches, and the
+figure reported is the median (with p10/p90) over the replays. Algorithmic bytes are the
+operands each launch must read plus what it writes; ``frac`` is against the 8 TB/s HBM peak, or
+against the 2.5 PFLOP/s dense bf16 MFMA peak for the prefill attention.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import math
+import statistics
+
+import torch
+
+from . import _lib
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+ROTATE_BYTES = 512 << 20
+DEV = "cuda"
+
+
+def _wire(lib, M, K, G, tm, n):
+    sz = ctypes.c_size_t()
+    _lib.check(lib.iron_wire_bytes(M, K, G, tm, ctypes.byref(sz)))
+    out = []
+    for _ in range(n):
+        t = torch.randint(-127, 128, (sz.value,), dtype=torch.int8, device=DEV).view(torch.uint8)
+        # the scale bytes become small positive bf16 values (|N(0, 0.02)|-like magnitudes)
+        out.append(t)
+    return out, sz.value
+
+
+def _time_graph(fn, launches: int, replays: int = 40):
+    """fn() issues `launches` launches; returns (median, p10, p90) microseconds per launch."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(replays):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3 / launches)
+    ts.sort()
+    return statistics.median(ts), ts[len(ts) // 10], ts[(9 * len(ts)) // 10]
+
+
+def _result(us, nbytes, extra=None):
+    med, p10, p90 = us
+    gbs = nbytes / (med * 1e-6) / 1e9
+    r = {"us_median": round(med, 3), "us_p10": round(p10, 3), "us_p90": round(p90, 3),
+         "bytes": int(nbytes), "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if extra:
+        r.update(extra)
+    return r
+
+
+def _st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def config1(lib):
+    """QKV GEMV, int8 G=32, B=1: x [1,1024], W [4096,1024] -> y [1,4096]."""
+    M, K, G, tm = 4096, 1024, 32, 4
+    n = math.ceil(ROTATE_BYTES / (M * K))
+    ws, wbytes = _wire(lib, M, K, G, tm, n)
+    x = torch.randn(K, device=DEV).to(torch.bfloat16)
+    y = torch.empty(M, dtype=torch.bfloat16, device=DEV)
+
+    def run():
+        for w in ws:
+            _lib.check(lib.iron_gemv_w8a16(w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, M, K, G,
+                                           tm, 0, _st()))
+
+    return _result(_time_graph(run, n), wbytes + 2 * K + 2 * M,
+                   {"shape": "M=4096 K=1024 G=32 B=1", "copies": n})
+
+
+def config2(lib, B):
+    """SwiGLU MLP at Qwen3-1.7B shape (D=2048, FF=6144), B rows."""
+    D, FF, G = 2048, 6144, 32
+    per = 3 * FF * D
+    n = max(2, math.ceil(ROTATE_BYTES / per))
+    gate, gb = _wire(lib, FF, D, G, 12, n)
+    up, _ = _wire(lib, FF, D, G, 12, n)
+    down, db = _wire(lib, D, FF, G, 4, n)
+    cur = torch.randn(B, D, device=DEV).to(torch.bfloat16)
+    a = torch.randn(B, D, device=DEV).to(torch.bfloat16)
+    nw = torch.ones(D, dtype=torch.bfloat16, device=DEV)
+    nxt = torch.empty(B, D, dtype=torch.bfloat16, device=DEV)
+    wsz = lib.iron_swiglu_mlp_workspace(B, D, FF)
+    ws = torch.zeros(wsz, dtype=torch.uint8, device=DEV)
+
+    def run():
+        for i in range(n):
+            _lib.check(lib.iron_swiglu_mlp(cur.data_ptr(), a.data_ptr(), nw.data_ptr(), None,
+                                           gate[i].data_ptr(), up[i].data_ptr(),
+                                           down[i].data_ptr(), nxt.data_ptr(), None, B, D, FF, 0,
+                                           G, 4, 12, 4, 0, ctypes.c_float(1e-6), ws.data_ptr(),
+                                           wsz, _st()))
+
+    return _result(_time_graph(run, n), 2 * gb + db + B * (3 * 2 * D),
+                   {"shape": f"D=2048 FF=6144 G=32 B={B}", "copies": n,
+                    "path": "GEMV" if B <= 4 else "MFMA"})
+
+
+def config3(lib, B, ragged):
+    """GQA decode attention, 16 Q / 8 KV x 128, contiguous [B, 8, L, 128] caches."""
+    H, KV, D, L = 16, 8, 128, 4096
+    g = torch.Generator().manual_seed(3)
+    ctx = (torch.randint(512, L + 1, (B,), generator=g) if ragged
+           else torch.full((B,), L, dtype=torch.int64))
+    per = B * KV * L * D * 2 * 2
+    n = max(2, math.ceil(ROTATE_BYTES / per))
+    ks = [torch.randn(B * KV * L * D, device=DEV).to(torch.bfloat16) for _ in range(n)]
+    vs = [torch.randn(B * KV * L * D, device=DEV).to(torch.bfloat16) for _ in range(n)]
+    q = torch.randn(B * H * D, device=DEV).to(torch.bfloat16)
+    o = torch.empty(B * H * D, dtype=torch.bfloat16, device=DEV)
+    c = ctx.to(torch.int32).to(DEV)
+    wsz = lib.iron_decode_attn_workspace(B, H, KV, D, L)
+    ws = torch.zeros(wsz, dtype=torch.uint8, device=DEV)
+    scale = ctypes.c_float(D ** -0.5)
+
+    def run():
+        for i in range(n):
+            _lib.check(lib.iron_decode_attn(q.data_ptr(), ks[i].data_ptr(), vs[i].data_ptr(),
+                                            KV * L * D, L * D, D, c.data_ptr(), 0, o.data_ptr(), B,
+                                            H, KV, D, L, scale, ws.data_ptr(), wsz, _st()))
+
+    nbytes = KV * D * 2 * 2 * int(ctx.sum()) + 2 * 2 * B * H * D
+    return _result(_time_graph(run, n), nbytes,
+                   {"shape": f"B={B} L={'U[512,4096]' if ragged else L}", "copies": n,
+                    "context_sum": int(ctx.sum())})
+
+
+def config5_decode(lib, steps: int = 3):
+    """Qwen3-8B layer stack (36 layers, D=4096, 32 Q / 8 KV x 128, FF=12288, int8 G=32) decode
+    at B=16 with every sequence at context 8192: per step, each layer runs the fused QKV head +
+    attention (raw QKV on MFMA) and the MLP with the output projection (three MFMA GEMMs)."""
+    NL, D, Hq, Hkv, HD, FF, G, B, L = 36, 4096, 32, 8, 128, 12288, 32, 16, 8192
+    QD, M = Hq * HD, (Hq + 2 * Hkv) * HD
+    layers = []
+    for _ in range(NL):
+        layers.append({
+            "qkv": _wire(lib, M, D, G, 16, 1)[0][0], "o": _wire(lib, D, QD, G, 4, 1)[0][0],
+            "g": _wire(lib, FF, D, G, 12, 1)[0][0], "u": _wire(lib, FF, D, G, 12, 1)[0][0],
+            "d": _wire(lib, D, FF, G, 4, 1)[0][0],
+            "k": torch.randn(B * Hkv * L * HD, device=DEV).to(torch.bfloat16),
+            "v": torch.randn(B * Hkv * L * HD, device=DEV).to(torch.bfloat16),
+        })
+    x = torch.randn(B, D, device=DEV).to(torch.bfloat16)
+    nw = torch.ones(D, dtype=torch.bfloat16, device=DEV)
+    nh = torch.ones(HD, dtype=torch.bfloat16, device=DEV)
+    ang = torch.randn(B * HD, device=DEV).to(torch.bfloat16)
+    pos = torch.full((B,), L - 1, dtype=torch.int32, device=DEV)
+    attn = torch.empty(B, QD, dtype=torch.bfloat16, device=DEV)
+    wq = lib.iron_qkv_attn_workspace(B, D, Hq, Hkv, HD, L)
+    wsq = torch.zeros(wq, dtype=torch.uint8, device=DEV)
+    wm = lib.iron_swiglu_mlp_workspace(B, D, FF)
+    wsm = torch.zeros(wm, dtype=torch.uint8, device=DEV)
+    eps, scale = ctypes.c_float(1e-6), ctypes.c_float(HD ** -0.5)
+
+    def step():
+        for ly in layers:
+            _lib.check(lib.iron_qkv_attn(x.data_ptr(), nw.data_ptr(), ly["qkv"].data_ptr(),
+                                         nh.data_ptr(), nh.data_ptr(), ang.data_ptr(),
+                                         ly["k"].data_ptr(), ly["v"].data_ptr(), Hkv * L * HD,
+                                         L * HD, HD, pos.data_ptr(), attn.data_ptr(), B, D, HD,
+                                         Hq, Hkv, L, G, 16, 0, eps, scale, wsq.data_ptr(), wq,
+                                         _st()))
+            _lib.check(lib.iron_swiglu_mlp(x.data_ptr(), attn.data_ptr(), nw.data_ptr(),
+                                           ly["o"].data_ptr(), ly["g"].data_ptr(),
+                                           ly["u"].data_ptr(), ly["d"].data_ptr(), x.data_ptr(),
+                                           None, B, D, FF, QD, G, 4, 12, 4, 0, eps,
+                                           wsm.data_ptr(), wm, _st()))
+
+    med, p10, p90 = _time_graph(step, 1, replays=steps + 2)
+    wbytes = sum(t.numel() for ly in layers for key, t in ly.items() if key not in ("k", "v"))
+    kvbytes = NL * B * Hkv * L * HD * 2 * 2
+    nbytes = wbytes + kvbytes
+    gbs = nbytes / (med * 1e-6) / 1e9
+    return {"ms_per_step": round(med / 1e3, 3), "tokens_per_s": round(B / (med * 1e-6), 1),
+            "bytes_per_step": int(nbytes), "GB_s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "shape": "Qwen3-8B int8 G=32, 36 layers, B=16, context 8192"}
+
+
+def config5_prefill(lib):
+    """Causal bf16 prefill attention, Qwen3-8B heads (32 Q / 8 KV x 128), S = 2048, B = 1."""
+    H, KV, S, D = 32, 8, 2048, 128
+    q = torch.randn(H * S * D, device=DEV).to(torch.bfloat16)
+    k = torch.randn(KV * S * D, device=DEV).to(torch.bfloat16)
+    v = torch.randn(KV * S * D, device=DEV).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    reps = 20
+
+    def run():
+        for _ in range(reps):
+            _lib.check(lib.iron_prefill_attn(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                             o.data_ptr(), 1, H, KV, S, D,
+                                             ctypes.c_float(D ** -0.5), _st()))
+
+    med, p10, p90 = _time_graph(run, reps, replays=10)
+    flops = 4 * D * H * (S * (S + 1) // 2)
+    tf = flops / (med * 1e-6) / 1e12
+    return {"us_median": round(med, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
+            "flops": flops, "TFLOP_s": round(tf, 1), "frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+            "shape": "H=32 KV=8 S=2048 D=128 causal"}
+
+
+def run_all(include_c5: bool = True) -> dict:
+    lib = _lib.load()
+    out = {"c1_qkv_gemv": config1(lib),
+           "c2_mlp_b1": config2(lib, 1), "c2_mlp_b8": config2(lib, 8),
+           "c3_attn_b1": config3(lib, 1, False), "c3_attn_b8_ragged": config3(lib, 8, True)}
+    torch.cuda.empty_cache()
+    if include_c5:
+        out["c5_prefill_mha"] = config5_prefill(lib)
+        out["c5_decode_b16"] = config5_decode(lib)
+        torch.cuda.empty_cache()
+    return out
+
+
+def copy_probe(mib: int = 256, reps: int = 4) -> dict:
+    """A plain device copy of a known size: the calibration run for the HBM byte counters
+    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE read this kernel as mib MiB fetched / written)."""
+    src = torch.randn(mib << 18, device=DEV)   # mib MiB of fp32
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"copy_bytes": mib << 20, "reps": reps}
+
+
+if __name__ == "__main__":
+    import sys
+
+    if "--copy-probe" in sys.argv:
+        print(json.dumps(copy_probe()), flush=True)
+    else:
+        print(json.dumps(run_all()), flush=True)

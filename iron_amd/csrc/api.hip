@@ -26,11 +26,113 @@ void clear_error() { g_err[0] = 0; }
 namespace {
 
 // One 256-thread workgroup per row: y = bf16((x * (1 / sqrt(mean(x^2) + eps))) * w), the
-// golden's closed form evaluated in fp64 and rounded once.
+// golden's closed form evaluated in fp64 and rounded once. A thread holds up to kRegSlots 8-element
+// slices of the row in registers (one vector load each); longer rows reload the rest.
+constexpr int kRegSlots = 4;
+
+IRON_DEV void unpack8_f(const uint4 v, float (&f)[8]) {
+  f[0] = bf16lo_to_f32(v.x); f[1] = bf16hi_to_f32(v.x);
+  f[2] = bf16lo_to_f32(v.y); f[3] = bf16hi_to_f32(v.y);
+  f[4] = bf16lo_to_f32(v.z); f[5] = bf16hi_to_f32(v.z);
+  f[6] = bf16lo_to_f32(v.w); f[7] = bf16hi_to_f32(v.w);
+}
+
+// x (and x2 when given, added in fp32) of slice i, as exact fp32
+IRON_DEV void row_slice(const uint4* x, const uint4* x2, int i, float (&f)[8]) {
+  unpack8_f(x[i], f);
+  if (x2) {
+    float g[8];
+    unpack8_f(x2[i], g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = f[j] + g[j];
+  }
+}
+
+// out_f32 != null: y = f32((x1 * inv) * w) into out_f32 (the MLP's hf); else bf16 into out.
+__device__ void rms_row(const uint16_t* __restrict__ x, const uint16_t* __restrict__ x2,
+                        const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+                        float* __restrict__ out_f32, int cols, float eps, double* red) {
+  const int n8 = cols >> 3;
+  const uint4* xv = (const uint4*)x;
+  const uint4* x2v = (const uint4*)x2;
+  const uint4* wv = (const uint4*)w;
+  float f[kRegSlots][8];
+  uint4 wr[kRegSlots];
+  double ss = 0.0;
+#pragma unroll
+  for (int r = 0; r < kRegSlots; ++r) {
+    const int i = threadIdx.x + 256 * r;
+    if (i < n8) {
+      row_slice(xv, x2v, i, f[r]);
+      wr[r] = w ? wv[i] : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kRegSlots; ++r)
+    if (threadIdx.x + 256 * r < n8) {
+      double v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = f[r][j];
+      ss += sum_sq_tree(v);
+    }
+  for (int i = threadIdx.x + 256 * kRegSlots; i < n8; i += 256) {
+    float g[8];
+    row_slice(xv, x2v, i, g);
+    double v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = g[j];
+    ss += sum_sq_tree(v);
+  }
+  ss = block_sum_256_d(ss, red);
+  const double inv = inv_rms(ss, cols, (double)eps);
+  auto emit = [&](int i, const float (&g)[8], const uint4 wq) {
+    float wf[8];
+    unpack8_f(wq, wf);
+    double y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      y[j] = (double)g[j] * inv;
+      if (w) y[j] *= (double)wf[j];
+    }
+    if (out_f32) {
+      float4* o = (float4*)(out_f32 + 8 * i);
+      o[0] = make_float4((float)y[0], (float)y[1], (float)y[2], (float)y[3]);
+      o[1] = make_float4((float)y[4], (float)y[5], (float)y[6], (float)y[7]);
+    } else {
+      uint32_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        h[j] = (uint32_t)f64_to_bf16(y[2 * j]) | ((uint32_t)f64_to_bf16(y[2 * j + 1]) << 16);
+      ((uint4*)out)[i] = make_uint4(h[0], h[1], h[2], h[3]);
+    }
+  };
+#pragma unroll
+  for (int r = 0; r < kRegSlots; ++r) {
+    const int i = threadIdx.x + 256 * r;
+    if (i < n8) emit(i, f[r], wr[r]);
+  }
+  for (int i = threadIdx.x + 256 * kRegSlots; i < n8; i += 256) {
+    float g[8];
+    row_slice(xv, x2v, i, g);
+    emit(i, g, w ? wv[i] : make_uint4(0u, 0u, 0u, 0u));
+  }
+}
+
+// rows with cols % 8 == 0 and 16-byte aligned row starts (validated by the launchers)
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ w,
                                                       uint16_t* __restrict__ y, int cols,
                                                       float eps) {
+  __shared__ double red[4];
+  const size_t r = (size_t)blockIdx.x * cols;
+  rms_row(x + r, nullptr, w, y + r, nullptr, cols, eps, red);
+}
+
+// Scalar fallback for rows that are not a whole number of 16-byte slices.
+__global__ __launch_bounds__(256) void rmsnorm_scalar_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ w,
+                                                             uint16_t* __restrict__ y, int cols,
+                                                             float eps) {
   __shared__ double red[4];
   const uint16_t* xr = x + (size_t)blockIdx.x * cols;
   uint16_t* yr = y + (size_t)blockIdx.x * cols;
@@ -56,17 +158,7 @@ __global__ __launch_bounds__(256) void res_rmsnorm_f32_kernel(const uint16_t* __
                                                               float eps) {
   __shared__ double red[4];
   const size_t r = (size_t)blockIdx.x * cols;
-  double ss = 0.0;
-  for (int i = threadIdx.x; i < cols; i += 256) {
-    const double v = bf16_to_f32(cur[r + i]) + bf16_to_f32(a[r + i]);
-    ss = fma(v, v, ss);
-  }
-  ss = block_sum_256_d(ss, red);
-  const double inv = inv_rms(ss, cols, (double)eps);
-  for (int i = threadIdx.x; i < cols; i += 256) {
-    const double v = (double)(bf16_to_f32(cur[r + i]) + bf16_to_f32(a[r + i]));
-    y[r + i] = (float)((v * inv) * (double)bf16_to_f32(w[i]));
-  }
+  rms_row(cur + r, a + r, w, nullptr, y + r, cols, eps, red);
 }
 
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tokens,
@@ -135,7 +227,10 @@ namespace iron {
 
 int rmsnorm_launch(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols,
                    float eps, hipStream_t stream) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream, x, w, y, cols, eps);
+  const bool vec = cols % 8 == 0 && aligned(x, 16) && aligned(y, 16) && (!w || aligned(w, 16));
+  if (vec) hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, stream, x, w, y, cols, eps);
+  else hipLaunchKernelGGL(rmsnorm_scalar_kernel, dim3(rows), dim3(256), 0, stream, x, w, y, cols,
+                          eps);
   return check_launch("rmsnorm");
 }
 
@@ -184,9 +279,7 @@ int iron_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, in
   if (!x || !y) return iron::fail(IRON_ERR_NULL, "iron_rmsnorm: null tensor");
   if (rows <= 0 || cols <= 0)
     return iron::fail(IRON_ERR_SHAPE, "iron_rmsnorm: bad shape rows=%d cols=%d", rows, cols);
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, x, w, y, cols,
-                     eps);
-  return iron::check_launch("iron_rmsnorm");
+  return iron::rmsnorm_launch(x, w, y, rows, cols, eps, (hipStream_t)stream);
 }
 
 int iron_embed(const int32_t* tokens, const uint16_t* emb, uint16_t* x, int B, int D, int vocab,

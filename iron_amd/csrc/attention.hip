@@ -418,8 +418,8 @@ SplitPlan plan_split(int B, int H, int KV, int max_ctx) {
   sp.hb = HG >= 4 ? 4 : HG;
   const int wg_per_split = B * KV * (HG / sp.hb);
   const int target_wgs = 512;
-  int ns = (target_wgs + wg_per_split - 1) / wg_per_split;
   const int max_ns = (max_ctx + kTile - 1) / kTile;
+  int ns = (target_wgs + wg_per_split - 1) / wg_per_split;
   if (ns > max_ns) ns = max_ns;
   if (ns > kMaxSplit) ns = kMaxSplit;
   if (ns < 1) ns = 1;

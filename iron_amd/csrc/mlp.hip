@@ -51,6 +51,10 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
   if (!cur || !cx_or_a || !n_pf || !nxt) return iron::fail(IRON_ERR_NULL, "%s: null tensor", fn);
   if (B <= 0 || D <= 0 || FF <= 0 || D % 16 || FF % 16)
     return iron::fail(IRON_ERR_SHAPE, "%s: bad shape B=%d D=%d FF=%d", fn, B, D, FF);
+  if (!iron::aligned(cur, 16) || !iron::aligned(cx_or_a, 16) || !iron::aligned(n_pf, 16) ||
+      !iron::aligned(nxt, 16))
+    return iron::fail(IRON_ERR_ALIGN, "%s: activations and norm weight must be 16-byte aligned",
+                      fn);
   int st = iron::check_wire(fn, wg, FF, D, G, tile_m_gu, domain);
   if (st) return st;
   st = iron::check_wire(fn, wu, FF, D, G, tile_m_gu, domain);
