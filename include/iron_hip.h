@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 1
+#define IRON_ABI_VERSION 2
 
 enum iron_status {
   IRON_OK = 0,
@@ -39,6 +39,13 @@ enum iron_status {
 
 enum iron_domain { IRON_DOMAIN_SIGNED = 0, IRON_DOMAIN_BIASED = 1 };
 enum iron_weight_kind { IRON_WEIGHT_INT8 = 0, IRON_WEIGHT_BF16 = 1 };
+/* Accumulation of the decode-attention core (scores, softmax, P.V):
+ *   IRON_ACCUM_F64 -- the exact value of the golden, evaluated in fp64 and rounded once to bf16
+ *                     (bit-identical to the fp64 oracle);
+ *   IRON_ACCUM_F32 -- the arithmetic the reference kernel uses: bf16 operands, fp32 dot products,
+ *                     exp2-form softmax and accumulation (within 1 bf16 ulp of the exact value on
+ *                     the parity cases; the contract is rel/abs 1e-2). */
+enum iron_accum { IRON_ACCUM_F64 = 0, IRON_ACCUM_F32 = 1 };
 
 /* ABI version of the loaded library (IRON_ABI_VERSION). No reference counterpart. */
 int iron_abi_version(void);
@@ -144,13 +151,14 @@ int iron_qkv_head(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
                   int Hq, int Hkv, int max_seq, int G, int tile_m, int domain, float eps,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes for iron_decode_attn (fp64 split-K partials; contents need no initialisation). */
+/* Workspace bytes for iron_decode_attn (split-K partials, sized for either accumulation mode;
+ * contents need no initialisation). */
 size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx);
 
 /* GQA decode attention, one query token per sequence:
  *   o[b][h] = softmax_j(q[b][h] . K[b][h*KV/H][j] * scale) . V[b][h*KV/H][j],  j < ctx_len[b]
- * fp64 scores/softmax/accumulation (the exp2-form golden of decode_attn.cc:117-311 in exact
- * arithmetic), rounded once to bf16 output; a sequence
+ * with the scores / softmax / accumulation of `acc` (enum iron_accum: exact fp64, or the fp32
+ * exp2 form of decode_attn.cc:117-311), rounded once to bf16 output; a sequence
  * with ctx_len 0 yields zeros (decode_attn.cc:300-311). q/o: [B][H][D] bf16; K/V addressed as in
  * iron_qkv_head. ctx_len: device int32 [B] (or NULL: every sequence uses ctx_const).
  * Replaces DecodeAttention (iron/operators/decode_attn/op.py:20-181; golden
@@ -158,7 +166,8 @@ size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx);
 int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                      long long kv_sb, long long kv_sh, long long kv_st, const int32_t* ctx_len,
                      int ctx_const, uint16_t* out, int B, int H, int KV, int D, int max_ctx,
-                     float scale, void* workspace, size_t workspace_bytes, void* stream);
+                     float scale, int acc, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /* Workspace bytes for iron_qkv_attn (raw QKV staging + split-K partials). */
 size_t iron_qkv_attn_workspace(int B, int D, int Hq, int Hkv, int HD, int max_seq);
@@ -166,7 +175,8 @@ size_t iron_qkv_attn_workspace(int B, int D, int Hq, int Hkv, int HD, int max_se
 /* Fused QKV head + decode attention for one decode step, per batch row b (ctx = pos[b] + 1):
  *   q, k, v  exactly as iron_qkv_head computes them (the k and v rows are appended to the caches
  *            at pos[b]; q is consumed in registers and not written out)
- *   out[b]   exactly as iron_decode_attn computes it over positions 0..pos[b] with ctx_len = pos+1
+ *   out[b]   exactly as iron_decode_attn computes it (same `acc`) over positions 0..pos[b] with
+ *            ctx_len = pos + 1
  * i.e. the composition of iron_qkv_head and iron_decode_attn with the per-head epilogue moved
  * into the attention kernel (two launches plus the split merge instead of four). out: [B][Hq][HD].
  * ang holds one angle row per batch row ([B][HD], the position's row; no table lookup).
@@ -178,7 +188,7 @@ int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
                   uint16_t* k_cache, uint16_t* v_cache, long long kv_sb, long long kv_sh,
                   long long kv_st, const int32_t* pos, uint16_t* out, int B, int D, int HD, int Hq,
                   int Hkv, int max_seq, int G, int tile_m, int domain, float eps, float scale,
-                  void* workspace, size_t workspace_bytes, void* stream);
+                  int acc, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Causal prefill attention (GQA) on MFMA:
  *   o[b][h][i] = sum_{j <= i} softmax_j(q[b][h][i] . k[b][h*KV/H][j] * scale) v[b][h*KV/H][j]

@@ -16,6 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
+ABI_VERSION = 2          # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2
@@ -28,6 +29,16 @@ IRON_DOMAIN_SIGNED = 0
 IRON_DOMAIN_BIASED = 1
 IRON_WEIGHT_INT8 = 0
 IRON_WEIGHT_BF16 = 1
+IRON_ACCUM_F64 = 0
+IRON_ACCUM_F32 = 1
+ACCUM = {"f64": IRON_ACCUM_F64, "f32": IRON_ACCUM_F32}
+
+
+def accum_mode(name: str) -> int:
+    """Attention accumulation mode (enum iron_accum) from its name, "f64" or "f32"."""
+    if name not in ACCUM:
+        raise ValueError(f"accumulate must be one of {sorted(ACCUM)}, got {name!r}")
+    return ACCUM[name]
 
 _VALUE_ERRORS = {IRON_ERR_NULL, IRON_ERR_SHAPE, IRON_ERR_ALIGN, IRON_ERR_WORKSPACE}
 
@@ -61,13 +72,13 @@ SIGNATURES = {
                                _c_vp]),
     "iron_decode_attn_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "iron_decode_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_ll, _c_ll, _c_ll, _c_vp, _c_int,
-                                  _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_vp,
-                                  _c_sz, _c_vp]),
+                                  _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_int,
+                                  _c_vp, _c_sz, _c_vp]),
     "iron_qkv_attn_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "iron_qkv_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                _c_ll, _c_ll, _c_ll, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
-                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_f, _c_vp, _c_sz,
-                               _c_vp]),
+                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_f, _c_int, _c_vp,
+                               _c_sz, _c_vp]),
     "iron_prefill_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
                                    _c_int, _c_f, _c_vp]),
     "iron_swiglu_mlp_workspace": (_c_sz, [_c_int, _c_int, _c_int]),
@@ -105,8 +116,9 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.iron_abi_version() != 1:
-            raise IronLibraryMissing(f"{path}: ABI version {lib.iron_abi_version()} != 1")
+        if lib.iron_abi_version() != ABI_VERSION:
+            raise IronLibraryMissing(f"{path}: ABI version {lib.iron_abi_version()} != "
+                                     f"{ABI_VERSION} (rebuild the library)")
         _lib = lib
         return lib
 

@@ -15,6 +15,9 @@ Differences from the reference, all deliberate:
   * by default (``fuse_attention=True``) the QKV head and decode attention run as one operator
     (``QKVHeadAttention``) whose attention kernel performs the QK-norm/RoPE/KV-append epilogue;
     ``fuse_attention=False`` keeps the reference's two runlist entries (identical results);
+  * ``attn_accumulate`` selects the attention core's arithmetic: "f64" evaluates it exactly (the
+    whole step is then bit-identical to the fp64 oracle chain), "f32" uses the reference
+    kernel's fp32 arithmetic (decode_attn.cc:117-311);
   * the LM head carries an argmax epilogue, so the token is chosen on the device (the reference
     copies the logits out and runs numpy argmax, qwen3_npu_int8.py:612-621);
   * ``generate()`` runs greedy decoding entirely on the device: each step replays one graph that
@@ -64,11 +67,12 @@ class Qwen3NPU:
                  weights: dict | None = None, seed: int = 0, max_seq_len: int = 512,
                  kv_layout: str = "separate", lm_head: str | None = None,
                  dispatch: str = "auto", context: AIEContext | None = None,
-                 fuse_attention: bool = True):
+                 fuse_attention: bool = True, attn_accumulate: str = "f64"):
         self.cfg = cfg = config or Qwen3Config.qwen3_0_6b()
         self.max_seq_len = max_seq_len
         self.kv_layout = kv_layout
         self.fuse_attention = fuse_attention
+        self.attn_accumulate = attn_accumulate
         self.context = context or AIEContext()
         self.device = self.context.device
         if weights is None:
@@ -91,7 +95,7 @@ class Qwen3NPU:
             num_heads=cfg.n_heads, num_kv_heads=cfg.n_kv_heads, head_dim=cfg.head_dim,
             seq_len_kv=S, use_runtime_seq_len=True,
             kv_layout="separate" if self.kv_layout == "separate" else "combined",
-            kv_token_interleaved=True, context=c)
+            kv_token_interleaved=True, accumulate=self.attn_accumulate, context=c)
         self.mlp_xdna = SwiGLUMLPDataParallelOurs(
             D=cfg.emb_dim, FF=cfg.hidden_dim, group_size=cfg.group_size, epsilon=cfg.eps,
             fuse_o=True, QD=cfg.q_dim, kernel_source=SIGNED_GEMV_KERNEL, context=c)
@@ -104,7 +108,8 @@ class Qwen3NPU:
             D=cfg.emb_dim, HD=cfg.head_dim, Hq=cfg.n_heads, Hkv=cfg.n_kv_heads, max_seq=S,
             num_aie_columns=1, tile_size_input=QKV_TSI, epsilon=cfg.eps,
             group_size=cfg.group_size, kv_layout=self.kv_layout,
-            kernel_source=SIGNED_GEMV_KERNEL, kv_offset_parameter="k_cache_offset", context=c)
+            kernel_source=SIGNED_GEMV_KERNEL, kv_offset_parameter="k_cache_offset",
+            accumulate=self.attn_accumulate, context=c)
         if self.lm_head_kind == "bf16":
             self.lmhead = GEMV(M=cfg.vocab_size, K=cfg.emb_dim, epilogue="argmax", context=c)
         else:

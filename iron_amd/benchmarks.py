@@ -119,8 +119,9 @@ def config2(lib, B):
                     "path": "GEMV" if B <= 4 else "MFMA"})
 
 
-def config3(lib, B, ragged):
-    """GQA decode attention, 16 Q / 8 KV x 128, contiguous [B, 8, L, 128] caches."""
+def config3(lib, B, ragged, acc="f64"):
+    """GQA decode attention, 16 Q / 8 KV x 128, contiguous [B, 8, L, 128] caches; ``acc`` is the
+    accumulation mode ("f64" exact, "f32" the reference kernel's arithmetic)."""
     H, KV, D, L = 16, 8, 128, 4096
     g = torch.Generator().manual_seed(3)
     ctx = (torch.randint(512, L + 1, (B,), generator=g) if ragged
@@ -140,15 +141,16 @@ def config3(lib, B, ragged):
         for i in range(n):
             _lib.check(lib.iron_decode_attn(q.data_ptr(), ks[i].data_ptr(), vs[i].data_ptr(),
                                             KV * L * D, L * D, D, c.data_ptr(), 0, o.data_ptr(), B,
-                                            H, KV, D, L, scale, ws.data_ptr(), wsz, _st()))
+                                            H, KV, D, L, scale, _lib.accum_mode(acc),
+                                            ws.data_ptr(), wsz, _st()))
 
     nbytes = KV * D * 2 * 2 * int(ctx.sum()) + 2 * 2 * B * H * D
     return _result(_time_graph(run, n), nbytes,
                    {"shape": f"B={B} L={'U[512,4096]' if ragged else L}", "copies": n,
-                    "context_sum": int(ctx.sum())})
+                    "context_sum": int(ctx.sum()), "accumulate": acc})
 
 
-def config5_decode(lib, steps: int = 3):
+def config5_decode(lib, steps: int = 3, acc: str = "f64"):
     """Qwen3-8B layer stack (36 layers, D=4096, 32 Q / 8 KV x 128, FF=12288, int8 G=32) decode
     at B=16 with every sequence at context 8192: per step, each layer runs the fused QKV head +
     attention (raw QKV on MFMA) and the MLP with the output projection (three MFMA GEMMs)."""
@@ -174,6 +176,7 @@ def config5_decode(lib, steps: int = 3):
     wm = lib.iron_swiglu_mlp_workspace(B, D, FF)
     wsm = torch.zeros(wm, dtype=torch.uint8, device=DEV)
     eps, scale = ctypes.c_float(1e-6), ctypes.c_float(HD ** -0.5)
+    mode = _lib.accum_mode(acc)
 
     def step():
         for ly in layers:
@@ -181,8 +184,8 @@ def config5_decode(lib, steps: int = 3):
                                          nh.data_ptr(), nh.data_ptr(), ang.data_ptr(),
                                          ly["k"].data_ptr(), ly["v"].data_ptr(), Hkv * L * HD,
                                          L * HD, HD, pos.data_ptr(), attn.data_ptr(), B, D, HD,
-                                         Hq, Hkv, L, G, 16, 0, eps, scale, wsq.data_ptr(), wq,
-                                         _st()))
+                                         Hq, Hkv, L, G, 16, 0, eps, scale, mode, wsq.data_ptr(),
+                                         wq, _st()))
             _lib.check(lib.iron_swiglu_mlp(x.data_ptr(), attn.data_ptr(), nw.data_ptr(),
                                            ly["o"].data_ptr(), ly["g"].data_ptr(),
                                            ly["u"].data_ptr(), ly["d"].data_ptr(), x.data_ptr(),
@@ -197,7 +200,7 @@ def config5_decode(lib, steps: int = 3):
     return {"ms_per_step": round(med / 1e3, 3), "tokens_per_s": round(B / (med * 1e-6), 1),
             "bytes_per_step": int(nbytes), "GB_s": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "shape": "Qwen3-8B int8 G=32, 36 layers, B=16, context 8192"}
+            "shape": "Qwen3-8B int8 G=32, 36 layers, B=16, context 8192", "accumulate": acc}
 
 
 def config5_prefill(lib):
@@ -227,11 +230,14 @@ def run_all(include_c5: bool = True) -> dict:
     lib = _lib.load()
     out = {"c1_qkv_gemv": config1(lib),
            "c2_mlp_b1": config2(lib, 1), "c2_mlp_b8": config2(lib, 8),
-           "c3_attn_b1": config3(lib, 1, False), "c3_attn_b8_ragged": config3(lib, 8, True)}
+           "c3_attn_b1": config3(lib, 1, False), "c3_attn_b8_ragged": config3(lib, 8, True),
+           "c3_attn_b1_f32": config3(lib, 1, False, "f32"),
+           "c3_attn_b8_ragged_f32": config3(lib, 8, True, "f32")}
     torch.cuda.empty_cache()
     if include_c5:
         out["c5_prefill_mha"] = config5_prefill(lib)
         out["c5_decode_b16"] = config5_decode(lib)
+        out["c5_decode_b16_f32"] = config5_decode(lib, acc="f32")
         torch.cuda.empty_cache()
     return out
 

@@ -35,6 +35,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kTile = 64;  // 4 waves x 4 rows x 4 unrolled groups
+constexpr int kMaxSplit = 256;  // the merge kernels hold one split weight per thread pair
 
 struct AttnParams {
   const uint16_t* q;       // [B][H][D] (plain mode)
@@ -56,7 +57,8 @@ struct AttnParams {
   int H, KV, HG, HB;       // heads, kv heads, GQA group, heads per workgroup
   int chunk, nsplit;
   double scale;
-  double* part;            // [B][H][nsplit][D + 2]: o (unnormalised), m, l
+  float scale2;            // scale * log2(e) (fp32 kernels: scores in the exp2 domain)
+  void* part;              // [B][H][nsplit][D + 2] fp64 (or fp32): o (unnormalised), m, l
 };
 
 template <int N>
@@ -120,57 +122,122 @@ IRON_DEV void norm_rope8(const uint4 xr, const uint4 wr, const uint4 a0, const u
   }
 }
 
-template <int HB, bool FUSED>
-__global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
-  const int split = blockIdx.x, b = blockIdx.z;
-  const int groups = p.HG / HB;
-  const int kv = blockIdx.y / groups, hg = blockIdx.y % groups;
-  const int h0 = kv * p.HG + hg * HB;  // first query head of this workgroup
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row = lane >> 4, dl = lane & 15;
-  const int t_begin = split * p.chunk;
-  const int t_lim = min(p.max_ctx, t_begin + p.chunk);
+// Workgroup coordinates: grid (split, kv * head_groups, b), 256 threads.
+struct AttnCoords {
+  int b, kv, hg, h0, wave, row, dl, t_begin, t_lim;
+};
 
-  const uint16_t* kbase = p.k + (size_t)b * p.sb + (size_t)kv * p.sh + dl * 8;
-  const uint16_t* vbase = p.v + (size_t)b * p.sb + (size_t)kv * p.sh + dl * 8;
-  uint4 kr[4], vr[4];
-  // Rows past `bound` (> t0) are clamped to bound - 1: every load is issued unconditionally, so
-  // the compiler's wait counts stay exact; those rows are masked where they are used.
-  auto load_tile = [&](int t0, int bound) {
+template <int HB>
+IRON_DEV AttnCoords attn_coords(const AttnParams& p) {
+  AttnCoords c;
+  const int groups = p.HG / HB;
+  c.b = blockIdx.z;
+  c.kv = blockIdx.y / groups;
+  c.hg = blockIdx.y % groups;
+  c.h0 = c.kv * p.HG + c.hg * HB;  // first query head of this workgroup
+  c.wave = threadIdx.x >> 6;
+  c.row = (threadIdx.x & 63) >> 4;
+  c.dl = threadIdx.x & 15;
+  c.t_begin = blockIdx.x * p.chunk;
+  c.t_lim = min(p.max_ctx, c.t_begin + p.chunk);
+  return c;
+}
+
+// One 64-token K/V tile: lane (wave, row, dl) loads rows t0 + 16u + 4 wave + row, dims 8 dl..+8.
+// Rows past `bound` (> t0) are clamped to bound - 1: every load is issued unconditionally, so
+// the compiler's wait counts stay exact; those rows are masked where they are used.
+IRON_DEV void load_kv_tile(const AttnParams& p, const AttnCoords& c, int t0, int bound,
+                           uint4 (&kr)[4], uint4 (&vr)[4]) {
+  const size_t base = (size_t)c.b * p.sb + (size_t)c.kv * p.sh + c.dl * 8;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      int t = t0 + u * 16 + wave * 4 + row;
-      t = t < bound ? t : bound - 1;
-      kr[u] = *(const uint4*)(kbase + (size_t)t * p.st);
-      vr[u] = *(const uint4*)(vbase + (size_t)t * p.st);
-    }
-  };
-  // Issue order: the position / context length and the query-side rows, then (B == 1) the
-  // first K/V tile. Loads complete in issue order, so the query-side work below waits only for
-  // the first group while the tile is still in flight.
-  uint4 xq[HB];
-  int ctx, pos = -1;
-  uint4 nq, nk, xk, xv, a0, a1;
+  for (int u = 0; u < 4; ++u) {
+    int t = t0 + u * 16 + c.wave * 4 + c.row;
+    t = t < bound ? t : bound - 1;
+    kr[u] = *(const uint4*)(p.k + base + (size_t)t * p.st);
+    vr[u] = *(const uint4*)(p.v + base + (size_t)t * p.st);
+  }
+}
+
+// The query-side loads, issued before any K/V tile. Fused mode: the raw q row this wave rotates
+// (xq[0]), the current token's raw K and V rows, the two norm weights and the angle
+// row (e = {n_qn, n_kn, raw k, raw v, angles lo, angles hi}); plain mode: the q rows. Returns the
+// (unclamped) context length; `pos` is the current token's position (fused) or -1.
+template <int HB, bool FUSED>
+IRON_DEV int load_query_side(const AttnParams& p, const AttnCoords& c, uint4 (&xq)[HB],
+                             uint4 (&e)[6], int& pos) {
+  const int dl = c.dl;
   if constexpr (FUSED) {
-    pos = p.pos[b];
-    const uint16_t* rawb = p.raw + (size_t)b * (p.H + 2 * p.KV) * kD;
-#pragma unroll
-    for (int h = 0; h < HB; ++h) xq[h] = *(const uint4*)(rawb + (size_t)(h0 + h) * kD + dl * 8);
-    xk = *(const uint4*)(rawb + (size_t)(p.H + kv) * kD + dl * 8);
-    xv = *(const uint4*)(rawb + (size_t)(p.H + p.KV + kv) * kD + dl * 8);
-    nq = *(const uint4*)(p.n_qn + dl * 8);
-    nk = *(const uint4*)(p.n_kn + dl * 8);
-    const uint16_t* arow = p.ang + (size_t)b * kD + 16 * (dl & 7);
-    a0 = *(const uint4*)arow;
-    a1 = *(const uint4*)(arow + 8);
-    ctx = pos + 1;
+    pos = p.pos[c.b];
+    const uint16_t* rawb = p.raw + (size_t)c.b * (p.H + 2 * p.KV) * kD;
+    // wave h < HB rotates query head h0 + h: each wave loads only that row (into xq[0])
+    const int hw = c.wave < HB ? c.wave : HB - 1;
+    xq[0] = *(const uint4*)(rawb + (size_t)(c.h0 + hw) * kD + dl * 8);
+    e[2] = *(const uint4*)(rawb + (size_t)(p.H + c.kv) * kD + dl * 8);
+    e[3] = *(const uint4*)(rawb + (size_t)(p.H + p.KV + c.kv) * kD + dl * 8);
+    e[0] = *(const uint4*)(p.n_qn + dl * 8);
+    e[1] = *(const uint4*)(p.n_kn + dl * 8);
+    const uint16_t* arow = p.ang + (size_t)c.b * kD + 16 * (dl & 7);
+    e[4] = *(const uint4*)arow;
+    e[5] = *(const uint4*)(arow + 8);
+    return pos + 1;
   } else {
 #pragma unroll
     for (int h = 0; h < HB; ++h)
-      xq[h] = *(const uint4*)(p.q + ((size_t)b * p.H + h0 + h) * kD + dl * 8);
-    ctx = p.ctx_len ? p.ctx_len[b] : p.ctx_const;
+      xq[h] = *(const uint4*)(p.q + ((size_t)c.b * p.H + c.h0 + h) * kD + dl * 8);
+    pos = -1;
+    return p.ctx_len ? p.ctx_len[c.b] : p.ctx_const;
   }
-  if (p.spec) load_tile(t_begin, t_lim);
+}
+
+// Fused mode: the per-head epilogues run in parallel -- wave h < HB rotates query head h into
+// s_q[h], wave HB % 4 (wave 0 when HB == 4, after its query head) builds the current token's K
+// row into s_new (with its V row) and, in one workgroup per (b, kv head), into the caches. Ends
+// with a barrier. Returns whether the current token lies in this workgroup's split
+// (workgroup-uniform).
+template <int HB>
+IRON_DEV bool rotate_query_side(const AttnParams& p, const AttnCoords& c, const uint4 (&xq)[HB],
+                                const uint4 (&e)[6], int pos, uint4 (&s_q)[HB][16],
+                                uint4 (&s_new)[2][16]) {
+  const bool pos_ok = pos >= 0 && pos < p.max_ctx;
+  const bool has_new = pos_ok && pos >= c.t_begin && pos < c.t_lim;
+  if (c.wave < HB) {
+    double qn[8];
+    norm_rope8(xq[0], e[0], e[4], e[5], c.dl, p.eps, qn);
+    if (c.row == 0) s_q[c.wave][c.dl] = pack8_bf16(qn);
+  }
+  if (has_new && c.wave == HB % 4) {
+    double kn[8];
+    norm_rope8(e[2], e[1], e[4], e[5], c.dl, p.eps, kn);
+    const uint4 kp = pack8_bf16(kn);
+    if (c.row == 0) {
+      s_new[0][c.dl] = kp;
+      s_new[1][c.dl] = e[3];
+      if (c.hg == 0) {  // one writer per (b, kv head)
+        const size_t at = (size_t)c.b * p.sb + (size_t)c.kv * p.sh + (size_t)pos * p.st + c.dl * 8;
+        *(uint4*)(p.k + at) = kp;
+        *(uint4*)(p.v + at) = e[3];
+      }
+    }
+  }
+  __syncthreads();
+  return has_new;
+}
+
+template <int HB, bool FUSED>
+__global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
+  const AttnCoords c = attn_coords<HB>(p);
+  const int split = blockIdx.x, b = c.b, h0 = c.h0;
+  const int wave = c.wave, lane = threadIdx.x & 63, row = c.row, dl = c.dl;
+  const int t_begin = c.t_begin, t_lim = c.t_lim;
+
+  uint4 kr[4], vr[4];
+  // Issue order: the position / context length and the query-side rows, then (B == 1) the
+  // first K/V tile. Loads complete in issue order, so the query-side work below waits only for
+  // the first group while the tile is still in flight.
+  uint4 xq[HB], e[6];
+  int pos;
+  int ctx = load_query_side<HB, FUSED>(p, c, xq, e, pos);
+  if (p.spec) load_kv_tile(p, c, t_begin, t_lim, kr, vr);
   ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
   const int t_end = min(ctx, t_lim);
 
@@ -179,33 +246,7 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   __shared__ uint4 s_q[HB][16];    // the rotated query rows (fused mode)
   bool has_new = false;
   if constexpr (FUSED) {
-    const bool pos_ok = pos >= 0 && pos < p.max_ctx;
-    has_new = pos_ok && pos >= t_begin && pos < t_lim;  // workgroup-uniform
-    // the per-head epilogues run in parallel: wave h < HB rotates query head h, wave HB % 4
-    // (wave 0 when HB == 4, after its query head) builds the current token's K row
-    if (wave < HB) {
-      uint4 mine = xq[0];
-#pragma unroll
-      for (int h = 1; h < HB; ++h)
-        if (wave == h) mine = xq[h];
-      double qn[8];
-      norm_rope8(mine, nq, a0, a1, dl, p.eps, qn);
-      if (row == 0) s_q[wave][dl] = pack8_bf16(qn);
-    }
-    if (has_new && wave == HB % 4) {
-      double kn[8];
-      norm_rope8(xk, nk, a0, a1, dl, p.eps, kn);
-      const uint4 kp = pack8_bf16(kn);
-      if (row == 0) {
-        s_new[0][dl] = kp;
-        s_new[1][dl] = xv;
-        if (hg == 0) {  // one writer per (b, kv head)
-          *(uint4*)(p.k + (size_t)b * p.sb + (size_t)kv * p.sh + (size_t)pos * p.st + dl * 8) = kp;
-          *(uint4*)(p.v + (size_t)b * p.sb + (size_t)kv * p.sh + (size_t)pos * p.st + dl * 8) = xv;
-        }
-      }
-    }
-    __syncthreads();
+    has_new = rotate_query_side<HB>(p, c, xq, e, pos, s_q, s_new);
 #pragma unroll
     for (int h = 0; h < HB; ++h) unpack8d(s_q[h][dl], qf[h]);
   } else {
@@ -225,7 +266,7 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   __shared__ double s_mx[2][4][HB];
   int it = 0;
   for (int t0 = t_begin; t0 < t_end; t0 += kTile, ++it) {
-    if (!(p.spec && t0 == t_begin)) load_tile(t0, t_end);
+    if (!(p.spec && t0 == t_begin)) load_kv_tile(p, c, t0, t_end, kr, vr);
     bool tv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -347,7 +388,7 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
     if (p.nsplit == 1) {
       p.out[((size_t)b * p.H + hq) * kD + od] = f64_to_bf16(L > 0.0 ? O / L : 0.0);
     } else {
-      double* part = p.part + (((size_t)b * p.H + hq) * p.nsplit + split) * (kD + 2);
+      double* part = (double*)p.part + (((size_t)b * p.H + hq) * p.nsplit + split) * (kD + 2);
       part[od] = O;
       if (od == 0) {
         part[kD] = M;
@@ -357,15 +398,262 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// fp32-accumulation variant: the arithmetic the reference kernel specifies (bf16 inputs, fp32
+// scores / softmax / accumulation, decode_attn.cc:117-311) rather than the exact value.
+//   * q . k_j: v_dot2_f32_bf16 on packed bf16 pairs (the products are exact in fp32), summed over
+//     the 16 lanes of a row with DPP; s_j = (q . k_j) * scale * log2(e), probabilities exp2(s - m)
+//     (v_exp_f32), o accumulated with fp32 FMAs, one rounding of o / l to bf16.
+//   * each wavefront keeps its own running maximum (no workgroup barrier per tile); the four
+//     wavefronts' sums are rescaled to the common maximum once, at the end.
+//   * the next tile's K/V rows are loaded while the current tile is processed.
+// The fused query-side epilogue (QK RMSNorm, RoPE, cache append) is the exact one above, so the
+// KV cache holds the same rows in both variants.
+// ---------------------------------------------------------------------------------------------
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+
+IRON_DEV float dot8_bf16(const uint4 a, const uint4 b) {
+  float s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.x),
+                                            __builtin_bit_cast(bf16x2_t, b.x), 0.0f, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.y),
+                                      __builtin_bit_cast(bf16x2_t, b.y), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.z),
+                                      __builtin_bit_cast(bf16x2_t, b.z), s, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.w),
+                                         __builtin_bit_cast(bf16x2_t, b.w), s, false);
+}
+
+template <int N, int HB>
+IRON_DEV void share_one_f(float ev, float (&pe)[4][HB]) {
+  if constexpr (N < 4 * HB) pe[N / HB][N % HB] = dpp_f<0x150 + N>(ev);  // row_newbcast:N
+}
+
+template <int HB, int... Ns>
+IRON_DEV void share_all_f(float ev, float (&pe)[4][HB], std::integer_sequence<int, Ns...>) {
+  (share_one_f<Ns, HB>(ev, pe), ...);
+}
+
+IRON_DEV float exp2_f(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int HB, bool FUSED>
+__global__ __launch_bounds__(256) void decode_attn_f32_kernel(AttnParams p) {
+  const AttnCoords c = attn_coords<HB>(p);
+  const int split = blockIdx.x, b = c.b;
+  const int wave = c.wave, lane = threadIdx.x & 63, row = c.row, dl = c.dl;
+  const int t_begin = c.t_begin, t_lim = c.t_lim;
+
+  uint4 kr[4], vr[4];
+  uint4 xq[HB], e[6];
+  int pos;
+  int ctx = load_query_side<HB, FUSED>(p, c, xq, e, pos);
+  if (p.spec) load_kv_tile(p, c, t_begin, t_lim, kr, vr);
+  ctx = ctx < 0 ? 0 : (ctx > p.max_ctx ? p.max_ctx : ctx);
+  const int t_end = min(ctx, t_lim);
+  if (!p.spec && t_begin < t_end) load_kv_tile(p, c, t_begin, t_end, kr, vr);
+
+  uint4 qp[HB];                    // packed bf16 query rows (dims 8 dl..+8)
+  __shared__ uint4 s_new[2][16];
+  __shared__ uint4 s_q[HB][16];
+  bool has_new = false;
+  if constexpr (FUSED) {
+    has_new = rotate_query_side<HB>(p, c, xq, e, pos, s_q, s_new);
+#pragma unroll
+    for (int h = 0; h < HB; ++h) qp[h] = s_q[h][dl];
+  } else {
+#pragma unroll
+    for (int h = 0; h < HB; ++h) qp[h] = xq[h];
+  }
+
+  float m[HB], l[HB], o[HB][8];
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[h][j] = 0.0f;
+  }
+
+  for (int t0 = t_begin; t0 < t_end; t0 += kTile) {
+    // prefetch the next tile (past the context every row clamps to the last valid row, which
+    // the current tile has just brought into the cache)
+    uint4 kn[4], vn[4];
+    load_kv_tile(p, c, t0 + kTile, t_end, kn, vn);
+    bool tv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = t0 + u * 16 + wave * 4 + row;
+      tv[u] = t < t_end;
+      if constexpr (FUSED) {
+        if (has_new && t == pos) {
+          kr[u] = s_new[0][dl];
+          vr[u] = s_new[1][dl];
+        }
+      }
+      if (!tv[u]) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // rows past the context may hold NaNs
+    }
+    // scores in the exp2 domain, identical in every lane of the row
+    float s[4][HB];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int h = 0; h < HB; ++h) {
+        const float a = row16_sum(dot8_bf16(qp[h], kr[u])) * p.scale2;
+        s[u][h] = tv[u] ? a : -INFINITY;
+      }
+    // wavefront running maximum per head
+    float mn[HB];
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      float v = fmaxf(fmaxf(s[0][h], s[1][h]), fmaxf(s[2][h], s[3][h]));
+      v = fmaxf(v, __shfl_xor(v, 16));
+      v = fmaxf(v, __shfl_xor(v, 32));
+      mn[h] = fmaxf(m[h], v);
+    }
+    // lane dl < 4*HB evaluates exponential (u, h) = (dl / HB, dl % HB); a masked token (or a
+    // wavefront with no valid token yet) contributes 0
+    float sv = -INFINITY, mv = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int h = 0; h < HB; ++h)
+        if (dl == u * HB + h) {
+          sv = s[u][h];
+          mv = mn[h];
+        }
+    const float ev = sv == -INFINITY ? 0.0f : exp2_f(sv - mv);
+    float pe[4][HB];
+    share_all_f<HB>(ev, pe, std::make_integer_sequence<int, 16>{});
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      const float cf = m[h] == mn[h] ? 1.0f : exp2_f(m[h] - mn[h]);
+      l[h] = l[h] * cf + ((pe[0][h] + pe[1][h]) + (pe[2][h] + pe[3][h]));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[h][j] *= cf;
+      m[h] = mn[h];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t d[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float v0 = bf16lo_to_f32(d[jj]), v1 = bf16hi_to_f32(d[jj]);
+#pragma unroll
+        for (int h = 0; h < HB; ++h) {
+          o[h][2 * jj] = fmaf(pe[u][h], v0, o[h][2 * jj]);
+          o[h][2 * jj + 1] = fmaf(pe[u][h], v1, o[h][2 * jj + 1]);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      kr[u] = kn[u];
+      vr[u] = vn[u];
+    }
+  }
+
+  // 16 token rows: the 4 rows of a wavefront share its maximum; wavefronts rescale to the common
+  // maximum M with f_w = exp2(m_w - M)
+  __shared__ float s_o[16][HB][kD];
+  __shared__ float s_l[16][HB];
+  __shared__ float s_m[4][HB];
+  const int rr = wave * 4 + row;
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    *(float4*)&s_o[rr][h][dl * 8] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+    *(float4*)&s_o[rr][h][dl * 8 + 4] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+    if (dl == 0) s_l[rr][h] = l[h];
+    if (lane == 0) s_m[wave][h] = m[h];
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < HB * kD; t += 256) {
+    const int oh = t / kD, od = t % kD;
+    float mw[4], f[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mw[w] = s_m[w][oh];
+    const float M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) f[w] = mw[w] == -INFINITY ? 0.0f : exp2_f(mw[w] - M);
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float ow = (s_o[4 * w][oh][od] + s_o[4 * w + 1][oh][od]) +
+                       (s_o[4 * w + 2][oh][od] + s_o[4 * w + 3][oh][od]);
+      const float lw = (s_l[4 * w][oh] + s_l[4 * w + 1][oh]) +
+                       (s_l[4 * w + 2][oh] + s_l[4 * w + 3][oh]);
+      O = fmaf(f[w], ow, O);
+      L = fmaf(f[w], lw, L);
+    }
+    const int hq = c.h0 + oh;
+    if (p.nsplit == 1) {
+      p.out[((size_t)b * p.H + hq) * kD + od] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
+    } else {
+      float* part = (float*)p.part + (((size_t)b * p.H + hq) * p.nsplit + split) * (kD + 2);
+      part[od] = O;
+      if (od == 0) {
+        part[kD] = M;
+        part[kD + 1] = L;
+      }
+    }
+  }
+}
+
+// fp32 split merge, grid (H, B), 128 threads (one per head dim): the same combination as the
+// fp64 merge below with exp2 weights.
+__global__ __launch_bounds__(128) void attn_merge_f32_kernel(AttnParams p) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int ns = p.nsplit;
+  const float* base = (const float*)p.part + ((size_t)b * p.H + h) * ns * (kD + 2);
+  constexpr int kRegF = 64;
+  float ov[kRegF];
+#pragma unroll
+  for (int s = 0; s < kRegF; ++s) ov[s] = s < ns ? base[(size_t)s * (kD + 2) + d] : 0.0f;
+  float ms[2], ls[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int s = d + 128 * i;
+    ms[i] = s < ns ? base[(size_t)s * (kD + 2) + kD] : -INFINITY;
+    ls[i] = s < ns ? base[(size_t)s * (kD + 2) + kD + 1] : 0.0f;
+  }
+  __shared__ float s_f[kMaxSplit];
+  __shared__ float s_red[2][2];
+  float mloc = row16_max(fmaxf(ms[0], ms[1]));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+  if ((d & 63) == 0) s_red[0][d >> 6] = mloc;
+  __syncthreads();
+  const float M = fmaxf(s_red[0][0], s_red[0][1]);
+  float lloc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int s = d + 128 * i;
+    if (s < ns) {
+      const float f = (M == -INFINITY || ms[i] == -INFINITY) ? 0.0f : exp2_f(ms[i] - M);
+      s_f[s] = f;
+      lloc += f * ls[i];
+    }
+  }
+  lloc = wave_sum(lloc);
+  if ((d & 63) == 0) s_red[1][d >> 6] = lloc;
+  __syncthreads();
+  const float L = s_red[1][0] + s_red[1][1];
+  float Oa[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < kRegF; ++s)
+    if (s < ns) Oa[s & 3] = fmaf(s_f[s], ov[s], Oa[s & 3]);
+  float O0 = Oa[0] + Oa[2], O1 = Oa[1] + Oa[3];
+  for (int s = kRegF; s < ns; ++s) O0 = fmaf(s_f[s], base[(size_t)s * (kD + 2) + d], O0);
+  const float O = O0 + O1;
+  p.out[((size_t)b * p.H + h) * kD + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
+}
+
 // grid (H, B), 128 threads: o = sum_s f_s O_s / sum_s f_s L_s, f_s = e^(m_s - max m). Every
 // partial of the first kReg splits is loaded before the first reduction.
 constexpr int kReg = 64;
-constexpr int kMaxSplit = 256;
 
 __global__ __launch_bounds__(128) void attn_merge_kernel(AttnParams p) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int ns = p.nsplit;
-  const double* base = p.part + ((size_t)b * p.H + h) * ns * (kD + 2);
+  const double* base = (const double*)p.part + ((size_t)b * p.H + h) * ns * (kD + 2);
   double ov[kReg];
 #pragma unroll
   for (int s = 0; s < kReg; ++s) ov[s] = s < ns ? base[(size_t)s * (kD + 2) + d] : 0.0;
@@ -453,8 +741,12 @@ int check_attn_shape(const char* fn, int B, int H, int KV, int D, int max_ctx) {
 
 // Launches the split kernel (and the merge when the context is split). `p` carries the inputs;
 // the split plan, partial buffer and head blocking are filled in here.
-int launch_attention(AttnParams p, bool fused, int B, void* part_ws, size_t part_bytes,
+int launch_attention(AttnParams p, bool fused, int acc, int B, void* part_ws, size_t part_bytes,
                      hipStream_t s, const char* fn) {
+  if (acc != IRON_ACCUM_F64 && acc != IRON_ACCUM_F32)
+    return iron::fail(IRON_ERR_SHAPE, "%s: unknown accumulation mode %d", fn, acc);
+  const bool f32 = acc == IRON_ACCUM_F32;
+  p.scale2 = (float)(p.scale * 1.4426950408889634);
   const SplitPlan sp = plan_split(B, p.H, p.KV, p.max_ctx);
   p.HG = p.H / p.KV;
   p.HB = sp.hb;
@@ -467,12 +759,16 @@ int launch_attention(AttnParams p, bool fused, int B, void* part_ws, size_t part
       return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, part_bytes, need);
     if (!iron::aligned(part_ws, 256))
       return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
-    p.part = (double*)part_ws;
+    p.part = part_ws;
   }
   dim3 grid(sp.nsplit, p.KV * (p.HG / sp.hb), B);
 #define IRON_ATTN_LAUNCH(HBV)                                                                  \
   do {                                                                                         \
-    if (fused)                                                                                 \
+    if (f32 && fused)                                                                          \
+      hipLaunchKernelGGL((decode_attn_f32_kernel<HBV, true>), grid, dim3(256), 0, s, p);       \
+    else if (f32)                                                                              \
+      hipLaunchKernelGGL((decode_attn_f32_kernel<HBV, false>), grid, dim3(256), 0, s, p);      \
+    else if (fused)                                                                            \
       hipLaunchKernelGGL((decode_attn_kernel<HBV, true>), grid, dim3(256), 0, s, p);           \
     else                                                                                       \
       hipLaunchKernelGGL((decode_attn_kernel<HBV, false>), grid, dim3(256), 0, s, p);          \
@@ -485,7 +781,10 @@ int launch_attention(AttnParams p, bool fused, int B, void* part_ws, size_t part
 #undef IRON_ATTN_LAUNCH
   int st = iron::check_launch(fn);
   if (st || sp.nsplit == 1) return st;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(p.H, B), dim3(128), 0, s, p);
+  if (f32)
+    hipLaunchKernelGGL(attn_merge_f32_kernel, dim3(p.H, B), dim3(128), 0, s, p);
+  else
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(p.H, B), dim3(128), 0, s, p);
   return iron::check_launch(fn);
 }
 
@@ -502,7 +801,8 @@ size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx) {
 int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                      long long kv_sb, long long kv_sh, long long kv_st, const int32_t* ctx_len,
                      int ctx_const, uint16_t* out, int B, int H, int KV, int D, int max_ctx,
-                     float scale, void* workspace, size_t workspace_bytes, void* stream) {
+                     float scale, int acc, void* workspace, size_t workspace_bytes,
+                     void* stream) {
   iron::clear_error();
   const char* fn = "iron_decode_attn";
   if (!q || !k_cache || !v_cache || !out) return iron::fail(IRON_ERR_NULL, "%s: null tensor", fn);
@@ -527,7 +827,8 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
   p.H = H;
   p.KV = KV;
   p.scale = (double)scale;
-  return launch_attention(p, false, B, workspace, workspace_bytes, (hipStream_t)stream, fn);
+  return launch_attention(p, false, acc, B, workspace, workspace_bytes, (hipStream_t)stream,
+                          fn);
 }
 
 size_t iron_qkv_attn_workspace(int B, int D, int Hq, int Hkv, int HD, int max_seq) {
@@ -541,7 +842,7 @@ int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
                   uint16_t* k_cache, uint16_t* v_cache, long long kv_sb, long long kv_sh,
                   long long kv_st, const int32_t* pos, uint16_t* out, int B, int D, int HD, int Hq,
                   int Hkv, int max_seq, int G, int tile_m, int domain, float eps, float scale,
-                  void* workspace, size_t workspace_bytes, void* stream) {
+                  int acc, void* workspace, size_t workspace_bytes, void* stream) {
   iron::clear_error();
   const char* fn = "iron_qkv_attn";
   if (!cur || !n_in || !n_qn || !n_kn || !ang || !k_cache || !v_cache || !pos || !out)
@@ -586,8 +887,8 @@ int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
   p.H = Hq;
   p.KV = Hkv;
   p.scale = (double)scale;
-  return launch_attention(p, true, B, (char*)workspace + raw_bytes, workspace_bytes - raw_bytes, s,
-                          fn);
+  return launch_attention(p, true, acc, B, (char*)workspace + raw_bytes,
+                          workspace_bytes - raw_bytes, s, fn);
 }
 
 }  // extern "C"

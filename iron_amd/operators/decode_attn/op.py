@@ -13,8 +13,10 @@ KV layouts (all head-major, addressed by strides in one kernel):
   * ``kv_layout="combined"``, ``kv_token_interleaved=False``: one (KV, 2*S*D) arg with a K half
     then a V half per head -- the layout of the reference golden (decode_attn/reference.py:41-60).
 New fields: ``batch`` (sequences per call; Q/O become (batch*H, D), K/V (batch*KV, ...), and
-``S_kv_eff`` holds one count per sequence, so ragged batches are one call) and ``scale``
-(default 1/sqrt(D)). The speculative-verify batch mode (``batch_queries``) is not implemented.
+``S_kv_eff`` holds one count per sequence, so ragged batches are one call), ``scale``
+(default 1/sqrt(D)) and ``accumulate``: "f64" evaluates the golden exactly (fp64, one rounding to
+bf16), "f32" uses the reference kernel's own arithmetic (fp32 dot products, exp2 softmax and
+accumulation; decode_attn.cc:117-311). The speculative-verify batch mode (``batch_queries``) is not implemented.
 """
 
 from __future__ import annotations
@@ -45,6 +47,7 @@ class DecodeAttention(MLIROperator):
     kv_layout: str = "combined"
     batch: int = 1
     scale: float | None = None
+    accumulate: str = "f64"
     context: object = field(default=None, repr=False)
 
     _name_aliases: ClassVar[Dict[str, str]] = {
@@ -72,6 +75,7 @@ class DecodeAttention(MLIROperator):
             raise ValueError("num_heads must be a multiple of num_kv_heads")
         if self.batch < 1:
             raise ValueError("batch must be >= 1")
+        _lib.accum_mode(self.accumulate)
         MLIROperator.__init__(self, context=self.context)
 
     @property
@@ -109,6 +113,7 @@ class DecodeAttention(MLIROperator):
         H, KV, D, S, B = self.num_heads, self.num_kv_heads, self.head_dim, self.seq_len_kv, self.batch
         ws = Workspace(lib.iron_decode_attn_workspace(B, H, KV, D, S), self.context.device)
         voff, sb, sh, st = self.kv_strides()
+        acc = _lib.accum_mode(self.accumulate)
         params = params if params is not None else RuntimeParams(self.context.device)
         if self.use_runtime_seq_len and "S_kv_eff" not in params:
             params.define("S_kv_eff", B)
@@ -125,7 +130,7 @@ class DecodeAttention(MLIROperator):
             ctx = params.tensor("S_kv_eff", B) if self.use_runtime_seq_len else None
             _lib.check(lib.iron_decode_attn(
                 q.data_ptr(), kp, vp, sb, sh, st, _lib.ptr(ctx), S, o.data_ptr(), B, H, KV, D, S,
-                float(self.softmax_scale), ws.ptr, ws.nbytes, stream_ptr()), "DecodeAttention")
+                float(self.softmax_scale), acc, ws.ptr, ws.nbytes, stream_ptr()), "DecodeAttention")
 
         call.params = params
         call.workspace = ws

@@ -7,12 +7,14 @@ cache; iron/operators/qkv_head_dp/op_ours.py:31-262) and then ``DecodeAttention`
 RMSNorm, RoPE, KV append) runs inside the attention kernel, so q never goes through memory and the
 step is the QKV GEMV, the attention split kernel and the split merge.
 
-Fields are those of ``QKVHeadDataParallel`` plus ``scale`` (softmax scale, default 1/sqrt(HD)).
+Fields are those of ``QKVHeadDataParallel`` plus ``scale`` (softmax scale, default 1/sqrt(HD)) and
+``accumulate`` (the attention core's arithmetic, "f64" exact or "f32" as DecodeAttention).
 The spec is the QKV head's inputs and caches followed by the attention output:
 ``cur, n_in, Wqkv, n_qn, n_kn, ang, k_cache, v_cache, out`` (``kv_layout="separate"``) or
 ``cur, n_in, Wqkv, n_qn, n_kn, ang, kv_cache, out`` (merged token-interleaved cache). The context
 of row b is ``pos[b] + 1`` where ``pos`` is the position carried by the KV offset parameter. The
-result equals the two-operator composition bit for bit (same kernels' arithmetic and roundings).
+result equals the two-operator composition bit for bit (same kernels' arithmetic and roundings,
+for either accumulation mode).
 """
 
 from __future__ import annotations
@@ -30,8 +32,10 @@ from ..qkv_head_dp.op import QKVHeadDataParallel
 @dataclass
 class QKVHeadAttention(QKVHeadDataParallel):
     scale: float | None = None
+    accumulate: str = "f64"
 
-    _name_aliases: ClassVar[Dict[str, str]] = {**QKVHeadDataParallel._name_aliases, "scale": "sc"}
+    _name_aliases: ClassVar[Dict[str, str]] = {**QKVHeadDataParallel._name_aliases, "scale": "sc",
+                                               "accumulate": "acc"}
 
     @property
     def softmax_scale(self) -> float:
@@ -46,6 +50,7 @@ class QKVHeadAttention(QKVHeadDataParallel):
         if self.angles_from_table:
             raise ValueError("QKVHeadAttention takes the position's angle row per batch row "
                              "(angles_from_table=False)")
+        _lib.accum_mode(self.accumulate)
         super().__post_init__()
 
     def get_callable(self, params: RuntimeParams | None = None):
@@ -55,6 +60,7 @@ class QKVHeadAttention(QKVHeadDataParallel):
                                                    self.max_seq),
                        self.context.device)
         dom = domain_code(self.domain)
+        acc = _lib.accum_mode(self.accumulate)
         voff, sb, sh, st = self.kv_strides()
         params = params if params is not None else RuntimeParams(self.context.device)
         pname = self.kv_offset_parameter or "kv_off"
@@ -73,7 +79,8 @@ class QKVHeadAttention(QKVHeadDataParallel):
                 ang.data_ptr(), kp, vp, sb, sh, st,
                 params.tensor(pname, B).data_ptr(), out.data_ptr(), B, self.D, self.HD, self.Hq,
                 self.Hkv, self.max_seq, self.group_size, self.tile_size_input, dom,
-                float(self.epsilon), float(self.softmax_scale), ws.ptr, ws.nbytes, stream_ptr()),
+                float(self.epsilon), float(self.softmax_scale), acc, ws.ptr, ws.nbytes,
+                stream_ptr()),
                 type(self).__name__)
 
         call.params = params

@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iron_abi_version() == 1
+    assert lib.iron_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_wire_bytes(lib):
@@ -68,19 +68,21 @@ def test_attention_rejects_bad_arguments(lib):
     f = lib.iron_decode_attn
     fake = 1 << 20
     args = lambda **kw: dict(dict(q=fake, k=fake, v=fake, sb=0, sh=0, st=128, ctx=None, cc=1,  # noqa
-                                  o=fake, B=1, H=16, KV=8, D=128, L=64, scale=0.1, ws=None,
-                                  wsb=0), **kw)
+                                  o=fake, B=1, H=16, KV=8, D=128, L=64, scale=0.1, acc=0,
+                                  ws=None, wsb=0), **kw)
 
     def call(**kw):
         a = args(**kw)
         return f(a["q"], a["k"], a["v"], a["sb"], a["sh"], a["st"], a["ctx"], a["cc"], a["o"],
-                 a["B"], a["H"], a["KV"], a["D"], a["L"], a["scale"], a["ws"], a["wsb"], None)
+                 a["B"], a["H"], a["KV"], a["D"], a["L"], a["scale"], a["acc"], a["ws"], a["wsb"],
+                 None)
 
     assert call(q=None) == _lib.IRON_ERR_NULL
     assert call(D=64) == _lib.IRON_ERR_UNSUPPORTED
     assert call(H=12, KV=8) == _lib.IRON_ERR_SHAPE
     assert call(cc=65) == _lib.IRON_ERR_SHAPE
     assert call(st=100) == _lib.IRON_ERR_ALIGN
+    assert call(acc=7) == _lib.IRON_ERR_SHAPE           # unknown accumulation mode
     # a long context needs split-K scratch: missing workspace is reported, not ignored
     assert call(L=4096, cc=4096) == _lib.IRON_ERR_WORKSPACE
     assert lib.iron_decode_attn_workspace(1, 16, 8, 128, 4096) > 0
