@@ -254,9 +254,24 @@ def copy_probe(mib: int = 256, reps: int = 4) -> dict:
 
 
 if __name__ == "__main__":
-    import sys
+    import argparse
 
-    if "--copy-probe" in sys.argv:
+    ap = argparse.ArgumentParser(description="standalone timings of the BASELINE configurations")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run only the byte-counter calibration copy")
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c5_prefill", "c5_decode"],
+                    help="run one configuration (for profiling)")
+    ap.add_argument("--acc", choices=["f64", "f32"], default="f64",
+                    help="attention accumulation for --only c3 / c5_decode")
+    a = ap.parse_args()
+    if a.copy_probe:
         print(json.dumps(copy_probe()), flush=True)
+    elif a.only:
+        lib = _lib.load()
+        one = {"c1": lambda: config1(lib), "c2": lambda: config2(lib, 1),
+               "c3": lambda: config3(lib, 8, True, a.acc),
+               "c5_prefill": lambda: config5_prefill(lib),
+               "c5_decode": lambda: config5_decode(lib, acc=a.acc)}[a.only]
+        print(json.dumps(one()), flush=True)
     else:
         print(json.dumps(run_all()), flush=True)
