@@ -48,10 +48,11 @@ IRON_DEV void row_slice(const uint4* x, const uint4* x2, int i, float (&f)[8]) {
   }
 }
 
-// out_f32 != null: y = f32((x1 * inv) * w) into out_f32 (the MLP's hf); else bf16 into out.
+// plane != 0: y = f32((x1 * inv) * w) as three exact bf16 planes at out, out + plane,
+// out + 2 plane (the MLP's hf for the MFMA path); else bf16(y) into out.
 __device__ void rms_row(const uint16_t* __restrict__ x, const uint16_t* __restrict__ x2,
                         const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
-                        float* __restrict__ out_f32, int cols, float eps, double* red) {
+                        size_t plane, int cols, float eps, double* red) {
   const int n8 = cols >> 3;
   const uint4* xv = (const uint4*)x;
   const uint4* x2v = (const uint4*)x2;
@@ -94,10 +95,19 @@ __device__ void rms_row(const uint16_t* __restrict__ x, const uint16_t* __restri
       y[j] = (double)g[j] * inv;
       if (w) y[j] *= (double)wf[j];
     }
-    if (out_f32) {
-      float4* o = (float4*)(out_f32 + 8 * i);
-      o[0] = make_float4((float)y[0], (float)y[1], (float)y[2], (float)y[3]);
-      o[1] = make_float4((float)y[4], (float)y[5], (float)y[6], (float)y[7]);
+    if (plane) {
+      uint32_t h[3][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint16_t e0[3], e1[3];
+        split3_bf16((float)y[2 * j], e0[0], e0[1], e0[2]);
+        split3_bf16((float)y[2 * j + 1], e1[0], e1[1], e1[2]);
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) h[pl][j] = (uint32_t)e0[pl] | ((uint32_t)e1[pl] << 16);
+      }
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        ((uint4*)(out + pl * plane))[i] = make_uint4(h[pl][0], h[pl][1], h[pl][2], h[pl][3]);
     } else {
       uint32_t h[4];
 #pragma unroll
@@ -125,7 +135,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
                                                       float eps) {
   __shared__ double red[4];
   const size_t r = (size_t)blockIdx.x * cols;
-  rms_row(x + r, nullptr, w, y + r, nullptr, cols, eps, red);
+  rms_row(x + r, nullptr, w, y + r, 0, cols, eps, red);
 }
 
 // Scalar fallback for rows that are not a whole number of 16-byte slices.
@@ -150,15 +160,16 @@ __global__ __launch_bounds__(256) void rmsnorm_scalar_kernel(const uint16_t* __r
 }
 
 // One 256-thread workgroup per row: x1 = f32(cur + a), y = f32((x1 * inv_rms(x1)) * w), the
-// SwiGLU MLP's fp32 hf (swiglu_mlp_dp/reference.py:54-67) for batches on the MFMA path.
-__global__ __launch_bounds__(256) void res_rmsnorm_f32_kernel(const uint16_t* __restrict__ cur,
-                                                              const uint16_t* __restrict__ a,
-                                                              const uint16_t* __restrict__ w,
-                                                              float* __restrict__ y, int cols,
-                                                              float eps) {
+// SwiGLU MLP's fp32 hf (swiglu_mlp_dp/reference.py:54-67) for batches on the MFMA path, written as
+// three exact bf16 planes [3][rows][cols].
+__global__ __launch_bounds__(256) void res_rmsnorm_planes_kernel(const uint16_t* __restrict__ cur,
+                                                                 const uint16_t* __restrict__ a,
+                                                                 const uint16_t* __restrict__ w,
+                                                                 uint16_t* __restrict__ planes,
+                                                                 int rows, int cols, float eps) {
   __shared__ double red[4];
   const size_t r = (size_t)blockIdx.x * cols;
-  rms_row(cur + r, a + r, w, nullptr, y + r, cols, eps, red);
+  rms_row(cur + r, a + r, w, planes + r, (size_t)rows * cols, cols, eps, red);
 }
 
 __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tokens,
@@ -234,11 +245,12 @@ int rmsnorm_launch(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, 
   return check_launch("rmsnorm");
 }
 
-int res_rmsnorm_f32_launch(const uint16_t* cur, const uint16_t* a, const uint16_t* w, float* y,
-                           int rows, int cols, float eps, hipStream_t stream) {
-  hipLaunchKernelGGL(res_rmsnorm_f32_kernel, dim3(rows), dim3(256), 0, stream, cur, a, w, y,
-                     cols, eps);
-  return check_launch("res_rmsnorm_f32");
+int res_rmsnorm_planes_launch(const uint16_t* cur, const uint16_t* a, const uint16_t* w,
+                              uint16_t* planes, int rows, int cols, float eps,
+                              hipStream_t stream) {
+  hipLaunchKernelGGL(res_rmsnorm_planes_kernel, dim3(rows), dim3(256), 0, stream, cur, a, w,
+                     planes, rows, cols, eps);
+  return check_launch("res_rmsnorm_planes");
 }
 
 }  // namespace iron

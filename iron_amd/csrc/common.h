@@ -28,6 +28,18 @@ IRON_DEV uint16_t f32_to_bf16(float f) {
 }
 IRON_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// An fp32 value as three bf16 planes: hi = v truncated to bf16, mid = the remainder truncated,
+// lo = what is left (at most 8 significant bits, so exact). hi + mid + lo == v exactly, so a
+// product of a bf16 with each plane, summed in fp32 or wider, sees the fp32 value.
+IRON_DEV void split3_bf16(float v, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
+  const float h = __uint_as_float(__float_as_uint(v) & 0xffff0000u);
+  const float r = v - h;
+  const float m = __uint_as_float(__float_as_uint(r) & 0xffff0000u);
+  hi = (uint16_t)(__float_as_uint(h) >> 16);
+  mid = (uint16_t)(__float_as_uint(m) >> 16);
+  lo = (uint16_t)(__float_as_uint(r - m) >> 16);
+}
+
 // fp64 -> bf16 goes through fp32 (RNE at each step), the conversion path torch uses for a
 // float64 tensor cast to bfloat16, so device results and the fp64 oracle round identically.
 IRON_DEV uint16_t f64_to_bf16(double d) { return f32_to_bf16((float)d); }

@@ -9,8 +9,8 @@
 // Arithmetic: q is exact in bf16 (|q| <= 127), so one v_mfma_f32_16x16x32_bf16 per 32-wide k
 // step multiplies q by x exactly and sums 32 products in fp32; at the end of each quantization
 // group the fp32 partial is scaled by s (in fp64) and added to an fp64 accumulator. fp32 inputs
-// (the MLP's hf and gh) are split exactly into three bf16 planes (hi + mid + lo), three MFMAs
-// per step. The result is within the fp32 rounding of the per-group sums of the exact value (the
+// (the MLP's hf and gh) arrive as their three exact bf16 planes (hi + mid + lo, written so by
+// their producers), three MFMAs per step. The result is within the fp32 rounding of the per-group sums of the exact value (the
 // parity bar is the north star's rel/abs 1e-2; measured errors are a few fp32 ulps).
 //
 // Mapping: a workgroup (4 wavefronts) owns 64 rows x 16 batch columns over a K range (split-K
@@ -34,7 +34,7 @@ constexpr int kBN = 16;           // batch columns
 constexpr int kWRow = kKS + 16;   // LDS bytes per weight row (padded)
 constexpr int kXRow = kKS + 8;    // LDS bf16 per x row (padded)
 
-// epilogues (iron::GEMM_EPI_*): bf16(acc) | f32(acc) | f32(silu(acc0) * acc1) (dual) |
+// epilogues (iron::GEMM_EPI_*): bf16(acc) | f32(silu(acc0) * acc1) as three bf16 planes (dual) |
 // bf16(f32(r1 + r2) + acc)
 
 struct GemmParams {
@@ -43,13 +43,15 @@ struct GemmParams {
   int M, K, gshift, tile_m;
   FastDiv tdiv;
   uint32_t blk_bytes, xor_mask;
-  const void* x;          // [B][x_stride] bf16, or fp32 when x_f32
-  int x_f32, B, x_stride;
+  const uint16_t* x;      // [B][x_stride] bf16, or [3][B][x_stride] bf16 planes of fp32 values
+  size_t x_plane;         // plane stride (elements) of the planes form, 0 for plain bf16
+  int B, x_stride;
   int splits, ksteps;     // split s covers pipeline steps [s*ksteps, (s+1)*ksteps)
   double* part;           // [2][splits][kBN][M] fp64 partials (splits > 1)
   int epi;
   void* y;
   int y_stride;
+  size_t y_plane;         // plane stride of the planes epilogue
   const uint16_t* r1;
   const uint16_t* r2;
   int r_stride;
@@ -70,8 +72,11 @@ IRON_DEV void store_out(const GemmParams& p, int b, int m, double a0, double a1)
   const size_t o = (size_t)b * p.y_stride + m;
   switch (p.epi) {
     case iron::GEMM_EPI_BF16: ((uint16_t*)p.y)[o] = f64_to_bf16(a0); break;
-    case iron::GEMM_EPI_F32: ((float*)p.y)[o] = (float)a0; break;
-    case iron::GEMM_EPI_SWIGLU_F32: ((float*)p.y)[o] = (float)silu_mul_d(a0, a1); break;
+    case iron::GEMM_EPI_SWIGLU_PLANES: {
+      uint16_t* y = (uint16_t*)p.y;
+      split3_bf16((float)silu_mul_d(a0, a1), y[o], y[o + p.y_plane], y[o + 2 * p.y_plane]);
+      break;
+    }
     default: {
       const size_t ro = (size_t)b * p.r_stride + m;
       float x1 = bf16_to_f32(p.r1[ro]);
@@ -96,34 +101,10 @@ IRON_DEV bf16x8 q8_to_bf16(uint32_t lo, uint32_t hi, uint32_t xm) {
   return r;
 }
 
-// 8 fp32 -> 8 bf16 of one of three planes: hi = the value truncated to bf16, mid = the remainder
-// truncated to bf16, lo = what is left (at most 8 significant bits, so exact in bf16). Every
-// plane value is exact and hi + mid + lo == the fp32 value.
-IRON_DEV uint4 split_plane(const uint4 a, const uint4 b, bool valid, int plane) {
-  const uint32_t f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t h2[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const float v = __uint_as_float(valid ? f[2 * j + t] : 0u);
-      const float hi = __uint_as_float(__float_as_uint(v) & 0xffff0000u);
-      const float r1 = v - hi;
-      const float mid = __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
-      const float lo = r1 - mid;
-      const float pick = plane == 0 ? hi : (plane == 1 ? mid : lo);
-      h2[t] = __float_as_uint(pick) >> 16;
-    }
-    o[j] = h2[0] | (h2[1] << 16);
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
-}
-
-template <bool DUAL, bool XF32>
+template <bool DUAL, bool XPL>
 __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
   constexpr int NM = DUAL ? 2 : 1;
-  constexpr int NX = XF32 ? 3 : 1;   // bf16 planes of x (fp32 x: hi, mid, lo)
+  constexpr int NX = XPL ? 3 : 1;    // bf16 planes of x (fp32 x: hi, mid, lo)
   __shared__ __align__(16) uint8_t s_w[2][NM][kTM][kWRow];
   __shared__ __align__(16) uint16_t s_s[2][NM][kTM][kKS / 32];
   __shared__ __align__(16) uint16_t s_x[2][NX][kBN][kXRow];
@@ -153,8 +134,8 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
   }
   const int xb = tid >> 4, xk = (tid & 15) * 8;  // x tile: batch row, 8-element chunk
   // registers of one pipeline step: the weight quarter-rows of matrix 0 (and 1), their
-  // scales, and x (bf16, or the two halves of 8 fp32)
-  uint4 wa0, wa1, wb0, wb1, rx0, rx1;
+  // scales, and 8 x values of each plane
+  uint4 wa0, wa1, wb0, wb1, rx0, rx1, rx2;
   uint32_t sa, sb;
   const int gpr = kKS / G;  // groups per step (G <= kKS)
   const uint8_t* wsrc0 = wbase[0];
@@ -176,12 +157,10 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
       wb1 = s1_[1];                                                                            \
       sb = ssrc1[gi_];                                                                         \
     }                                                                                          \
-    if (XF32) {                                                                                \
-      const uint4* xr_ = (const uint4*)((const float*)p.x + xrow + k0_ + xk);                  \
-      rx0 = xr_[0];                                                                            \
-      rx1 = xr_[1];                                                                            \
-    } else {                                                                                   \
-      rx0 = *(const uint4*)((const uint16_t*)p.x + xrow + k0_ + xk);                           \
+    rx0 = *(const uint4*)(p.x + xrow + k0_ + xk);                                              \
+    if (XPL) {                                                                                 \
+      rx1 = *(const uint4*)(p.x + p.x_plane + xrow + k0_ + xk);                                \
+      rx2 = *(const uint4*)(p.x + 2 * p.x_plane + xrow + k0_ + xk);                            \
     }                                                                                          \
   } while (0)
 #define GEMM_LSTORE(buf_)                                                                      \
@@ -196,11 +175,10 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
       d1_[1] = wb1;                                                                            \
       if (lpart < kKS / 32) s_s[(buf_)][NM - 1][lrow][lpart] = (uint16_t)sb;                   \
     }                                                                                          \
-    if (XF32) {                                                                                \
-      _Pragma("unroll") for (int pl_ = 0; pl_ < NX; ++pl_)                                     \
-        *(uint4*)&s_x[(buf_)][pl_][xb][xk] = split_plane(rx0, rx1, xb < p.B, pl_);              \
-    } else {                                                                                   \
-      *(uint4*)&s_x[(buf_)][0][xb][xk] = xb < p.B ? rx0 : make_uint4(0u, 0u, 0u, 0u);          \
+    *(uint4*)&s_x[(buf_)][0][xb][xk] = xb < p.B ? rx0 : make_uint4(0u, 0u, 0u, 0u);            \
+    if (XPL) {                                                                                 \
+      *(uint4*)&s_x[(buf_)][NX - 2][xb][xk] = xb < p.B ? rx1 : make_uint4(0u, 0u, 0u, 0u);     \
+      *(uint4*)&s_x[(buf_)][NX - 1][xb][xk] = xb < p.B ? rx2 : make_uint4(0u, 0u, 0u, 0u);     \
     }                                                                                          \
   } while (0)
 
@@ -327,9 +305,9 @@ int gemm_check(const char* fn, int B, int M, int K, int G) {
 }
 
 int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile_m, int domain,
-                   const void* x, bool x_f32, int B, int x_stride, int epi, void* y, int y_stride,
-                   const uint16_t* r1, const uint16_t* r2, int r_stride, void* ws,
-                   size_t ws_bytes, hipStream_t stream, const char* fn) {
+                   const uint16_t* x, size_t x_plane, int B, int x_stride, int epi, void* y,
+                   int y_stride, size_t y_plane, const uint16_t* r1, const uint16_t* r2,
+                   int r_stride, void* ws, size_t ws_bytes, hipStream_t stream, const char* fn) {
   int st = gemm_check(fn, B, M, K, G);
   if (st) return st;
   const bool dual = w1 != nullptr;
@@ -345,7 +323,8 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
   p.blk_bytes = (uint32_t)wire_block_bytes(K, G, tile_m);
   p.xor_mask = domain == IRON_DOMAIN_BIASED ? 0x80808080u : 0u;
   p.x = x;
-  p.x_f32 = x_f32;
+  p.x_plane = x_plane;
+  const bool x_f32 = x_plane != 0;
   p.B = B;
   p.x_stride = x_stride;
   p.splits = pl.splits;
@@ -353,6 +332,7 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
   p.epi = epi;
   p.y = y;
   p.y_stride = y_stride;
+  p.y_plane = y_plane;
   p.r1 = r1;
   p.r2 = r2;
   p.r_stride = r_stride;
@@ -399,8 +379,8 @@ int iron_gemm_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int
   int st = iron::check_wire(fn, wire, M, K, G, tile_m, domain);
   if (st) return st;
   if (!iron::aligned(x, 16)) return iron::fail(IRON_ERR_ALIGN, "%s: x not 16-byte aligned", fn);
-  return iron::gemm_w8_launch(wire, nullptr, M, K, G, tile_m, domain, x, false, B, K,
-                              iron::GEMM_EPI_BF16, y, M, nullptr, nullptr, 0, workspace,
+  return iron::gemm_w8_launch(wire, nullptr, M, K, G, tile_m, domain, x, 0, B, K,
+                              iron::GEMM_EPI_BF16, y, M, 0, nullptr, nullptr, 0, workspace,
                               workspace_bytes, (hipStream_t)stream, fn);
 }
 

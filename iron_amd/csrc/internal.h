@@ -45,19 +45,27 @@ int check_wire(const char* fn, const void* wire, int M, int K, int G, int tile_m
 // Small prologue kernels (api.hip).
 int rmsnorm_launch(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols,
                    float eps, hipStream_t stream);
-int res_rmsnorm_f32_launch(const uint16_t* cur, const uint16_t* a, const uint16_t* w, float* y,
-                           int rows, int cols, float eps, hipStream_t stream);
+// y = RMSNorm(cur + a) * w in fp32, written as its three exact bf16 planes (hi, mid, lo):
+// planes [3][rows][cols], plane stride rows * cols.
+int res_rmsnorm_planes_launch(const uint16_t* cur, const uint16_t* a, const uint16_t* w,
+                              uint16_t* planes, int rows, int cols, float eps,
+                              hipStream_t stream);
 
 // MFMA batched GEMM (gemm_mfma.hip) for decode batches above the GEMV limit.
 constexpr int kGemvMaxBatch = 4;
 constexpr int kGemmMaxBatch = 16;
-enum : int { GEMM_EPI_BF16 = 0, GEMM_EPI_F32 = 1, GEMM_EPI_SWIGLU_F32 = 2, GEMM_EPI_RES_BF16 = 3 };
+// Epilogues: bf16(acc) | silu(acc0) * acc1 in fp32 as three bf16 planes (dual) |
+// bf16(f32(r1 + r2) + acc).
+enum : int { GEMM_EPI_BF16 = 0, GEMM_EPI_SWIGLU_PLANES = 1, GEMM_EPI_RES_BF16 = 2 };
 int gemm_check(const char* fn, int B, int M, int K, int G);
 size_t gemm_workspace_bound(int M, bool dual);
+// x: bf16 [B][x_stride], or (x_plane > 0) an fp32 activation as three exact bf16 planes
+// [3][B][x_stride] with plane stride x_plane elements. y_plane: the plane stride of the planes
+// epilogue's output.
 int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile_m, int domain,
-                   const void* x, bool x_f32, int B, int x_stride, int epi, void* y, int y_stride,
-                   const uint16_t* r1, const uint16_t* r2, int r_stride, void* ws,
-                   size_t ws_bytes, hipStream_t stream, const char* fn);
+                   const uint16_t* x, size_t x_plane, int B, int x_stride, int epi, void* y,
+                   int y_stride, size_t y_plane, const uint16_t* r1, const uint16_t* r2,
+                   int r_stride, void* ws, size_t ws_bytes, hipStream_t stream, const char* fn);
 
 
 // The raw-QKV stage shared by the QKV head and the fused QKV head + attention (qkv.hip).

@@ -105,9 +105,9 @@ int qkv_raw_internal(const void* wqkv, const uint16_t* cur, const uint16_t* n_in
   char* part = (char*)hn + round256((size_t)B * D * 2);
   st = rmsnorm_launch(cur, n_in, hn, B, D, eps, s);
   if (st) return st;
-  return gemm_w8_launch(wqkv, nullptr, M, D, G, tile_m, domain, hn, false, B, D, GEMM_EPI_BF16,
-                        raw, M, nullptr, nullptr, 0, part, ws_bytes - (size_t)(part - (char*)ws),
-                        s, fn);
+  return gemm_w8_launch(wqkv, nullptr, M, D, G, tile_m, domain, hn, 0, B, D, GEMM_EPI_BF16,
+                        raw, M, 0, nullptr, nullptr, 0, part,
+                        ws_bytes - (size_t)(part - (char*)ws), s, fn);
 }
 
 }  // namespace iron
