@@ -26,6 +26,7 @@
 // known (bounded by max_ctx, masked afterwards), which takes the length's load off the critical
 // path; with several sequences the length is read first so that short sequences read nothing
 // beyond their context.
+#include <type_traits>
 #include <utility>
 
 #include "common.h"
@@ -597,103 +598,98 @@ __global__ __launch_bounds__(256) void decode_attn_f32_kernel(AttnParams p) {
   }
 }
 
-// fp32 split merge, grid (H, B), 128 threads (one per head dim): the same combination as the
-// fp64 merge below with exp2 weights.
-__global__ __launch_bounds__(128) void attn_merge_f32_kernel(AttnParams p) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+
+// Split merge, grid (H, B), one wavefront per (head, sequence):
+//   o = sum_s f_s O_s / sum_s f_s L_s,  f_s = e^(m_s - max m)  (exp2 in the fp32 mode, whose
+//   maxima are in the log2 domain)
+// Lane l owns head dims 2l, 2l+1 and the statistics of splits l, l+64, ...; the weights reach the
+// accumulation through readlane (wave-uniform), so no LDS or barrier is involved. Every partial
+// of the first kRegW splits is loaded before the first reduction.
+constexpr int kRegW = 48;
+
+template <bool F32>
+__global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams p) {
+  using T = typename std::conditional<F32, float, double>::type;
+  using T2 = typename std::conditional<F32, float2, double2>::type;
+  const int h = blockIdx.x, b = blockIdx.y, l = threadIdx.x;
   const int ns = p.nsplit;
-  const float* base = (const float*)p.part + ((size_t)b * p.H + h) * ns * (kD + 2);
-  constexpr int kRegF = 64;
-  float ov[kRegF];
+  const T* base = (const T*)p.part + ((size_t)b * p.H + h) * ns * (kD + 2);
+  T2 ov[kRegW];
 #pragma unroll
-  for (int s = 0; s < kRegF; ++s) ov[s] = s < ns ? base[(size_t)s * (kD + 2) + d] : 0.0f;
-  float ms[2], ls[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int s = d + 128 * i;
-    ms[i] = s < ns ? base[(size_t)s * (kD + 2) + kD] : -INFINITY;
-    ls[i] = s < ns ? base[(size_t)s * (kD + 2) + kD + 1] : 0.0f;
+  for (int sp = 0; sp < kRegW; ++sp) {
+    const int sc = sp < ns ? sp : 0;  // clamped: every load is issued
+    ov[sp] = *(const T2*)(base + (size_t)sc * (kD + 2) + 2 * l);
   }
-  __shared__ float s_f[kMaxSplit];
-  __shared__ float s_red[2][2];
-  float mloc = row16_max(fmaxf(ms[0], ms[1]));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-  if ((d & 63) == 0) s_red[0][d >> 6] = mloc;
-  __syncthreads();
-  const float M = fmaxf(s_red[0][0], s_red[0][1]);
-  float lloc = 0.0f;
+  T ms[kMaxSplit / 64], ls[kMaxSplit / 64];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int s = d + 128 * i;
-    if (s < ns) {
-      const float f = (M == -INFINITY || ms[i] == -INFINITY) ? 0.0f : exp2_f(ms[i] - M);
-      s_f[s] = f;
-      lloc += f * ls[i];
+  for (int i = 0; i < kMaxSplit / 64; ++i) {
+    const int sp = l + 64 * i;
+    const int sc = sp < ns ? sp : 0;
+    ms[i] = base[(size_t)sc * (kD + 2) + kD];
+    ls[i] = base[(size_t)sc * (kD + 2) + kD + 1];
+    if (sp >= ns) {
+      ms[i] = -INFINITY;
+      ls[i] = 0;
     }
   }
-  lloc = wave_sum(lloc);
-  if ((d & 63) == 0) s_red[1][d >> 6] = lloc;
-  __syncthreads();
-  const float L = s_red[1][0] + s_red[1][1];
-  float Oa[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  T mloc = ms[0];
 #pragma unroll
-  for (int s = 0; s < kRegF; ++s)
-    if (s < ns) Oa[s & 3] = fmaf(s_f[s], ov[s], Oa[s & 3]);
-  float O0 = Oa[0] + Oa[2], O1 = Oa[1] + Oa[3];
-  for (int s = kRegF; s < ns; ++s) O0 = fmaf(s_f[s], base[(size_t)s * (kD + 2) + d], O0);
-  const float O = O0 + O1;
-  p.out[((size_t)b * p.H + h) * kD + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
-}
-
-// grid (H, B), 128 threads: o = sum_s f_s O_s / sum_s f_s L_s, f_s = e^(m_s - max m). Every
-// partial of the first kReg splits is loaded before the first reduction.
-constexpr int kReg = 64;
-
-__global__ __launch_bounds__(128) void attn_merge_kernel(AttnParams p) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int ns = p.nsplit;
-  const double* base = (const double*)p.part + ((size_t)b * p.H + h) * ns * (kD + 2);
-  double ov[kReg];
-#pragma unroll
-  for (int s = 0; s < kReg; ++s) ov[s] = s < ns ? base[(size_t)s * (kD + 2) + d] : 0.0;
-  double ms[2], ls[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int s = d + 128 * i;
-    ms[i] = s < ns ? base[(size_t)s * (kD + 2) + kD] : -INFINITY;
-    ls[i] = s < ns ? base[(size_t)s * (kD + 2) + kD + 1] : 0.0;
+  for (int i = 1; i < kMaxSplit / 64; ++i) mloc = F32 ? fmaxf(mloc, ms[i]) : fmax(mloc, ms[i]);
+  T M;
+  if constexpr (F32) {
+    M = row16_max(mloc);
+    M = fmaxf(M, __shfl_xor(M, 16));
+    M = fmaxf(M, __shfl_xor(M, 32));
+  } else {
+    M = row16_max_d(mloc);
+    M = fmax(M, __shfl_xor(M, 16));
+    M = fmax(M, __shfl_xor(M, 32));
   }
-  __shared__ double s_f[kMaxSplit];
-  __shared__ double s_red[2][2];
-  double mloc = row16_max_d(fmax(ms[0], ms[1]));
-  mloc = fmax(mloc, __shfl_xor(mloc, 16));
-  mloc = fmax(mloc, __shfl_xor(mloc, 32));
-  if ((d & 63) == 0) s_red[0][d >> 6] = mloc;
-  __syncthreads();
-  const double M = fmax(s_red[0][0], s_red[0][1]);
-  double lloc = 0.0;
+  T f[kMaxSplit / 64];
+  T lloc = 0;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int s = d + 128 * i;
-    if (s < ns) {
-      const double f = (M == -INFINITY || ms[i] == -INFINITY) ? 0.0 : exp(ms[i] - M);
-      s_f[s] = f;
-      lloc += f * ls[i];
+  for (int i = 0; i < kMaxSplit / 64; ++i) {
+    if constexpr (F32) f[i] = (M == -INFINITY || ms[i] == -INFINITY) ? 0.f : exp2_f(ms[i] - M);
+    else f[i] = (M == -INFINITY || ms[i] == -INFINITY) ? 0.0 : exp(ms[i] - M);
+    lloc += f[i] * ls[i];
+  }
+  const T L = F32 ? (T)wave_sum((float)lloc) : (T)wave_sum_d((double)lloc);
+  auto weight = [&](int sp) -> T {  // f of split sp, wave-uniform
+    const int i = sp >> 6, lane = sp & 63;
+    const T v = i == 0 ? f[0] : (i == 1 ? f[1] : (i == 2 ? f[2] : f[3]));
+    if constexpr (F32) {
+      return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+    } else {
+      const int lo = __builtin_amdgcn_readlane(__double2loint(v), lane);
+      const int hi = __builtin_amdgcn_readlane(__double2hiint(v), lane);
+      return __hiloint2double(hi, lo);
     }
-  }
-  lloc = wave_sum_d(lloc);
-  if ((d & 63) == 0) s_red[1][d >> 6] = lloc;
-  __syncthreads();
-  const double L = s_red[1][0] + s_red[1][1];
-  double Oa[4] = {0.0, 0.0, 0.0, 0.0};
+  };
+  T a0[4] = {0, 0, 0, 0}, a1[4] = {0, 0, 0, 0};
 #pragma unroll
-  for (int s = 0; s < kReg; ++s)
-    if (s < ns) Oa[s & 3] = fma(s_f[s], ov[s], Oa[s & 3]);
-  double O0 = Oa[0] + Oa[2], O1 = Oa[1] + Oa[3];
-  for (int s = kReg; s < ns; ++s) O0 = fma(s_f[s], base[(size_t)s * (kD + 2) + d], O0);
-  const double O = O0 + O1;
-  p.out[((size_t)b * p.H + h) * kD + d] = f64_to_bf16(L > 0.0 ? O / L : 0.0);
+  for (int sp = 0; sp < kRegW; ++sp)
+    if (sp < ns) {
+      const T w = weight(sp);
+      a0[sp & 3] = F32 ? fmaf(w, ov[sp].x, a0[sp & 3]) : fma(w, ov[sp].x, a0[sp & 3]);
+      a1[sp & 3] = F32 ? fmaf(w, ov[sp].y, a1[sp & 3]) : fma(w, ov[sp].y, a1[sp & 3]);
+    }
+  for (int sp = kRegW; sp < ns; ++sp) {
+    const T w = weight(sp);
+    const T2 v = *(const T2*)(base + (size_t)sp * (kD + 2) + 2 * l);
+    a0[0] = F32 ? fmaf(w, v.x, a0[0]) : fma(w, v.x, a0[0]);
+    a1[0] = F32 ? fmaf(w, v.y, a1[0]) : fma(w, v.y, a1[0]);
+  }
+  const T o0 = (a0[0] + a0[2]) + (a0[1] + a0[3]);
+  const T o1 = (a1[0] + a1[2]) + (a1[1] + a1[3]);
+  uint16_t r0, r1;
+  if constexpr (F32) {
+    r0 = f32_to_bf16(L > 0.f ? o0 / L : 0.f);
+    r1 = f32_to_bf16(L > 0.f ? o1 / L : 0.f);
+  } else {
+    r0 = f64_to_bf16(L > 0.0 ? o0 / L : 0.0);
+    r1 = f64_to_bf16(L > 0.0 ? o1 / L : 0.0);
+  }
+  *(uint32_t*)(p.out + ((size_t)b * p.H + h) * kD + 2 * l) = (uint32_t)r0 | ((uint32_t)r1 << 16);
 }
 
 struct SplitPlan {
@@ -782,9 +778,9 @@ int launch_attention(AttnParams p, bool fused, int acc, int B, void* part_ws, si
   int st = iron::check_launch(fn);
   if (st || sp.nsplit == 1) return st;
   if (f32)
-    hipLaunchKernelGGL(attn_merge_f32_kernel, dim3(p.H, B), dim3(128), 0, s, p);
+    hipLaunchKernelGGL(attn_merge_kernel<true>, dim3(p.H, B), dim3(64), 0, s, p);
   else
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(p.H, B), dim3(128), 0, s, p);
+    hipLaunchKernelGGL(attn_merge_kernel<false>, dim3(p.H, B), dim3(64), 0, s, p);
   return iron::check_launch(fn);
 }
 
