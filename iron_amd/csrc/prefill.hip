@@ -8,15 +8,16 @@
 // exp2 in fp32, probabilities rounded to bf16 for the P V product (as the reference's AIE kernels
 // do), fp32 accumulation, one division by the row sum and one bf16 rounding of the output.
 //
-// Mapping: a wavefront owns 16 query rows of one head; a workgroup (4 wavefronts) owns 4 heads of
-// one GQA group for the same 16 rows (or, for groups smaller than 4, more query blocks), so the
-// 32-key K/V blocks it stages in LDS (double buffered) serve every wavefront. Per key block a
-// wavefront computes S^T = K Q^T (two 16-key tiles, D/32 v_mfma_f32_16x16x32_bf16 each): lane l
-// then holds the scores of query l%16 for keys (l/16)*4 + i of each tile, which is exactly the
-// A-operand layout of P for the P V product when its 32 k-slots take the keys in the order
-// (tile 0: 4 keys, tile 1: 4 keys) per lane quarter; V is staged transposed so the B operand
-// reads those keys with two 8-byte LDS reads. Row statistics of query q live in the lanes with
-// l%16 == q; the output tiles (rows (l/16)*4 + i) fetch them with cross-lane shuffles.
+// Mapping: a wavefront owns 32 query rows (two 16-row tiles) of one head; a workgroup (4
+// wavefronts) owns 4 heads of one GQA group for the same rows (or, for groups smaller than 4,
+// more query blocks), so the K/V blocks it stages in LDS (16 KiB each: 64 keys at d = 128, 128 at
+// d = 64; double buffered, V transposed) serve every wavefront. Per key block a wavefront computes
+// S^T = K Q^T per 16-key tile (each K operand read serves both query tiles): lane l then holds the
+// scores of query l%16 for keys (l/16)*4 + i of the tile, which is exactly the B-operand layout of
+// P^T for O^T = V^T P^T when a 32-key step takes its keys in the order (tile 2s: 4 keys, tile
+// 2s+1: 4 keys) per lane quarter; the V^T operand reads those keys with two 8-byte LDS reads. In
+// O^T's layout lane l also owns query l%16, so the softmax correction and the final division need
+// no cross-lane exchange. Query blocks run latest (longest) first.
 #include "common.h"
 #include "internal.h"
 
@@ -25,8 +26,6 @@ namespace {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
-constexpr int kQB = 16;   // query rows per wavefront
-constexpr int kKB = 32;   // keys per block
 
 struct PrefillParams {
   const uint16_t* q;   // [B][H][S][D]
@@ -39,173 +38,225 @@ struct PrefillParams {
 
 IRON_DEV bf16x8 as_bf16x8(const uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
-IRON_DEV uint16_t f32_to_bf16_rne(float f) { return f32_to_bf16(f); }
+// Staging of one key block: thread -> keys 4 sg .. 4 sg + 3 (clamped to the sequence), dims
+// dc .. dc + 7. K rows go to LDS as they are; V goes transposed, the 4 keys of one dim in one
+// 8-byte write.
+// The staging registers of one key block (four K and four V slices of 8 dims), as native vectors
+// so that they stay in registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+struct KVRegs {
+  u32x4 k0, k1, k2, k3, v0, v1, v2, v3;
+};
+
+template <int D, int KB>
+IRON_DEV void pf_gload(const uint16_t* kbase, const uint16_t* vbase, int kb, int sg, int dc, int S,
+                       KVRegs& r) {
+  const int k0 = kb * KB + 4 * sg;
+  const size_t o0 = (size_t)min(k0, S - 1) * D + dc, o1 = (size_t)min(k0 + 1, S - 1) * D + dc;
+  const size_t o2 = (size_t)min(k0 + 2, S - 1) * D + dc, o3 = (size_t)min(k0 + 3, S - 1) * D + dc;
+  r.k0 = *(const u32x4*)(kbase + o0);
+  r.v0 = *(const u32x4*)(vbase + o0);
+  r.k1 = *(const u32x4*)(kbase + o1);
+  r.v1 = *(const u32x4*)(vbase + o1);
+  r.k2 = *(const u32x4*)(kbase + o2);
+  r.v2 = *(const u32x4*)(vbase + o2);
+  r.k3 = *(const u32x4*)(kbase + o3);
+  r.v3 = *(const u32x4*)(vbase + o3);
+}
+
+// dims dc + 2w (low halves) and dc + 2w + 1 (high halves) of the 4 keys, one 8-byte write each
+IRON_DEV void pf_vt_pair(uint16_t* lo_row, uint16_t* hi_row, uint32_t a0, uint32_t a1, uint32_t a2,
+                         uint32_t a3) {
+  *(uint2*)lo_row = make_uint2((a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16));
+  *(uint2*)hi_row = make_uint2((a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u));
+}
+
+template <int D, int KB>
+IRON_DEV void pf_lstore(uint16_t (*s_k)[D + 8], uint16_t (*s_vt)[KB + 8], int sg, int dc,
+                        const KVRegs& r) {
+  *(u32x4*)&s_k[4 * sg][dc] = r.k0;
+  *(u32x4*)&s_k[4 * sg + 1][dc] = r.k1;
+  *(u32x4*)&s_k[4 * sg + 2][dc] = r.k2;
+  *(u32x4*)&s_k[4 * sg + 3][dc] = r.k3;
+  const int c = 4 * sg;
+  pf_vt_pair(&s_vt[dc][c], &s_vt[dc + 1][c], r.v0.x, r.v1.x, r.v2.x, r.v3.x);
+  pf_vt_pair(&s_vt[dc + 2][c], &s_vt[dc + 3][c], r.v0.y, r.v1.y, r.v2.y, r.v3.y);
+  pf_vt_pair(&s_vt[dc + 4][c], &s_vt[dc + 5][c], r.v0.z, r.v1.z, r.v2.z, r.v3.z);
+  pf_vt_pair(&s_vt[dc + 6][c], &s_vt[dc + 7][c], r.v0.w, r.v1.w, r.v2.w, r.v3.w);
+}
+
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+// Round-to-nearest-even of two fp32 values to packed bf16 (v_cvt_pk_bf16_f32).
+IRON_DEV uint32_t pack_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
+}
 
 // HW = query heads per workgroup (min(group, 4)); the 4 wavefronts are HW heads x (4 / HW) query
-// blocks.
+// tile pairs. Query tiles are 16 rows; pair i is tiles i and NT - 1 - i (NT = S / 16), so every
+// pair costs the same number of key blocks and the workgroups stay balanced under the causal mask.
 template <int D, int HW>
-__global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillParams p) {
-  constexpr int QBW = 4 / HW;          // query blocks per workgroup
-  constexpr int QT = kQB * QBW;        // query rows per workgroup
-  constexpr int KROW = D + 8;          // padded LDS row of K (bf16)
-  constexpr int VROW = kKB + 8;        // padded LDS row of V^T (bf16)
-  constexpr int ND = D / 16;           // output d tiles
-  __shared__ __align__(16) uint16_t s_k[2][kKB][KROW];
-  __shared__ __align__(16) uint16_t s_vt[2][D][VROW];
+__global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
+  constexpr int KB = 8192 / D;         // keys per block (16 KiB of K)
+  constexpr int NKT = KB / 16;         // 16-key tiles per block
+  constexpr int NKS = KB / 32;         // 32-key P.V steps per block
+  constexpr int NJ = D / 32;           // 32-wide head-dim steps of Q K^T
+  constexpr int ND = D / 16;           // 16-wide head-dim tiles of O
+  constexpr int PW = 4 / HW;           // tile pairs per workgroup
+  __shared__ __align__(16) uint16_t s_k[2][KB][D + 8];
+  __shared__ __align__(16) uint16_t s_vt[2][D][KB + 8];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int quarter = lane >> 4, col = lane & 15;
   const int HG = p.H / p.KV;
   const int kv = blockIdx.y;
   const int b = blockIdx.z / (HG / HW), hsub = blockIdx.z % (HG / HW);
   const int head = kv * HG + hsub * HW + wave % HW;
-  const int qw0 = blockIdx.x * QT + (wave / HW) * kQB;  // this wavefront's first query row
-  const int q_last = blockIdx.x * QT + QT - 1;          // the workgroup's last query row
-  const int nkb = q_last / kKB + 1;                     // key blocks the workgroup needs
   const int S = p.S;
+  const int NT = S / 16, npairs = (NT + 1) / 2;
+  const int pair = blockIdx.x * PW + wave / HW;          // this wavefront's tile pair
+  const bool live = pair < npairs;
+  // tile t's first row (t = 0 light, t = 1 heavy; with an odd tile count the middle tile pairs
+  // with itself and the copy is skipped)
+  const int r0[2] = {16 * pair, 16 * (NT - 1 - pair)};
+  const bool twin = live && r0[0] == r0[1];
+  // key blocks the workgroup needs: up to the heavy tile of its lightest pair
+  const int pmin = blockIdx.x * PW;
+  const int nkb = (16 * (NT - 1 - pmin) + 15) / KB + 1;
 
   const uint16_t* kbase = p.k + ((size_t)b * p.KV + kv) * S * D;
   const uint16_t* vbase = p.v + ((size_t)b * p.KV + kv) * S * D;
 
-  // Q^T operand: lane l holds q row qw0 + l%16, d = 32j + (l/16)*8 .. +8
-  uint4 qf[D / 32];
-  {
-    const uint16_t* qrow = p.q + (((size_t)b * p.H + head) * S + qw0 + (lane & 15)) * D;
+  // Q^T operands: lane l holds query row r0[t] + l%16 (clamped), d = 32 j + (l/16)*8 .. +8
+  uint4 qf[2][NJ];
 #pragma unroll
-    for (int j = 0; j < D / 32; ++j) qf[j] = *(const uint4*)(qrow + 32 * j + (lane >> 4) * 8);
+  for (int t = 0; t < 2; ++t) {
+    const int qr = max(0, min(r0[t] + col, S - 1));  // pairs past the last one read row 0
+    const uint16_t* qrow = p.q + (((size_t)b * p.H + head) * S + qr) * D;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) qf[t][j] = *(const uint4*)(qrow + 32 * j + quarter * 8);
   }
 
-  // staging of one key block: thread -> key tid / (256/32), D/8 columns split over the rest
-  constexpr int TPK = 256 / kKB;        // threads per key row (8)
-  constexpr int EPT = D / TPK;          // elements per thread (16 for D=128, 8 for D=64)
-  const int skey = tid / TPK, scol = (tid % TPK) * EPT;
-  static_assert(EPT == 8 || EPT == 16, "one or two 16-byte chunks per thread");
-  uint4 rk0, rk1, rv0, rv1;
-  const size_t soff = (size_t)skey * D + scol;
-#define PREFILL_GLOAD(kb_)                                                                     \
-  do {                                                                                         \
-    const size_t o_ = (size_t)(kb_) * kKB * D + soff;                                          \
-    rk0 = *(const uint4*)(kbase + o_);                                                         \
-    rv0 = *(const uint4*)(vbase + o_);                                                         \
-    if (EPT == 16) {                                                                           \
-      rk1 = *(const uint4*)(kbase + o_ + 8);                                                   \
-      rv1 = *(const uint4*)(vbase + o_ + 8);                                                   \
-    }                                                                                          \
-  } while (0)
-#define PREFILL_VT(buf_, c_, u_)                                                               \
-  do {                                                                                         \
-    const uint32_t w_[4] = {(u_).x, (u_).y, (u_).z, (u_).w};                                   \
-    _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) {                                         \
-      s_vt[(buf_)][(c_) + 2 * j_][skey] = (uint16_t)(w_[j_] & 0xffffu);                        \
-      s_vt[(buf_)][(c_) + 2 * j_ + 1][skey] = (uint16_t)(w_[j_] >> 16);                        \
-    }                                                                                          \
-  } while (0)
-#define PREFILL_LSTORE(buf_)                                                                   \
-  do {                                                                                         \
-    *(uint4*)&s_k[(buf_)][skey][scol] = rk0;                                                   \
-    PREFILL_VT(buf_, scol, rv0);                                                               \
-    if (EPT == 16) {                                                                           \
-      *(uint4*)&s_k[(buf_)][skey][scol + 8] = rk1;                                             \
-      PREFILL_VT(buf_, scol + 8, rv1);                                                         \
-    }                                                                                          \
-  } while (0)
+  constexpr int TPG = D / 8;  // staging threads per key
+  const int sg = tid / TPG, dc = (tid % TPG) * 8;
+  KVRegs rkv;
 
-  f32x4 o[ND];
+  // O^T accumulators: tile (t, dt) is 16 dims x 16 queries; lane l holds query r0[t] + l%16,
+  // dims 16 dt + (l/16)*4 + i
+  f32x4 o[2][ND];
 #pragma unroll
-  for (int t = 0; t < ND; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, lsum = 0.f;  // statistics of query qw0 + lane%16 (this lane's share)
-  const int qi = qw0 + (lane & 15);
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) o[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};  // this lane's share of query stats
+  const float c = p.scale_log2;
 
-  PREFILL_GLOAD(0);
-  PREFILL_LSTORE(0);
+  pf_gload<D, KB>(kbase, vbase, 0, sg, dc, S, rkv);
+  pf_lstore<D, KB>(s_k[0], s_vt[0], sg, dc, rkv);
   __syncthreads();
   for (int kbi = 0; kbi < nkb; ++kbi) {
     const int buf = kbi & 1;
-    if (kbi + 1 < nkb) PREFILL_GLOAD(kbi + 1);
-    const int kb0 = kbi * kKB;
-    if (kb0 <= qw0 + kQB - 1) {  // this wavefront has unmasked keys in the block
-      // S^T tiles: rows = keys kb0 + 16t + l%16 (A operand from LDS), columns = queries
-      f32x4 st[2];
+    const int kb0 = kbi * KB;
+    if (kbi + 1 < nkb) pf_gload<D, KB>(kbase, vbase, kbi + 1, sg, dc, S, rkv);
+    // tile t takes part while the block starts at or before its last row (wave-uniform)
+    const bool act[2] = {live && !twin && kb0 <= r0[0] + 15, live && kb0 <= r0[1] + 15};
+    f32x4 st[2][NKT];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        st[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < NKT; ++kt) {
+      st[0][kt] = st[1][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < D / 32; ++j) {
-          const bf16x8 a =
-              as_bf16x8(*(const uint4*)&s_k[buf][16 * t + (lane & 15)][32 * j + (lane >> 4) * 8]);
-          st[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[j]), st[t], 0, 0, 0);
-        }
+      for (int j = 0; j < NJ; ++j) {
+        const bf16x8 a = as_bf16x8(*(const uint4*)&s_k[buf][16 * kt + col][32 * j + quarter * 8]);
+        if (act[0])
+          st[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[0][j]), st[0][kt], 0, 0, 0);
+        if (act[1])
+          st[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[1][j]), st[1][kt], 0, 0, 0);
       }
-      // scale (log2 domain), causal mask, block maximum of query qi across the lane quarters
-      float sv[2][4];
+    }
+    bf16x8 pb[2][NKS];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (!act[t]) continue;
+      const int qi = r0[t] + col;
+      const bool diag = kb0 + KB - 1 > r0[t];  // some key may lie past some query: mask
       float mx = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = kb0 + 16 * t + (lane >> 4) * 4 + i;
-          const float v = key <= qi ? st[t][i] * p.scale_log2 : -INFINITY;
-          sv[t][i] = v;
-          mx = fmaxf(mx, v);
+          if (diag && kb0 + 16 * kt + quarter * 4 + i > qi) st[t][kt][i] = -INFINITY;
+          mx = fmaxf(mx, st[t][kt][i]);
         }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mn = fmaxf(m, mx);  // finite: key kb0 <= qw0 <= qi is always valid
-      const float corr = exp2f(m - mn);  // m = -inf on the first block -> 0
-      m = mn;
+      // running maximum in the exp2 domain (scale > 0, so the raw maximum maps to it)
+      const float mn = fmaxf(m[t], mx * c);  // finite: every query has a key in block 0
+      const float corr = __builtin_amdgcn_exp2f(m[t] - mn);  // m = -inf on the first block
+      m[t] = mn;
       float ps = 0.f;
-      bf16x8 pa;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int ks = 0; ks < NKS; ++ks) {
+        uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = exp2f(sv[t][i] - mn);
-          ps += e;
-          pa[4 * t + i] = __builtin_bit_cast(__bf16, f32_to_bf16_rne(e));
+        for (int h = 0; h < 2; ++h) {
+          float e[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            e[i] = __builtin_amdgcn_exp2f(fmaf(st[t][2 * ks + h][i], c, -mn));
+            ps += e[i];
+          }
+          w[2 * h] = pack_bf16(e[0], e[1]);
+          w[2 * h + 1] = pack_bf16(e[2], e[3]);
         }
-      lsum = lsum * corr + ps;
-      // rescale the output rows (l/16)*4 + i with their queries' corrections
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float c = __shfl(corr, (lane >> 4) * 4 + i);
-#pragma unroll
-        for (int t = 0; t < ND; ++t) o[t][i] *= c;
+        pb[t][ks] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
       }
-      // O += P V: B operand = V^T[d][keys (l/16)*4 .. +4 of each tile]
+      lsum[t] = lsum[t] * corr + ps;
 #pragma unroll
-      for (int t = 0; t < ND; ++t) {
-        const uint16_t* vr = &s_vt[buf][16 * t + (lane & 15)][(lane >> 4) * 4];
+      for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[t][dt][i] *= corr;
+    }
+    // O^T += V^T P^T; each V^T operand serves both query tiles
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) {
+        const uint16_t* vr = &s_vt[buf][16 * dt + col][32 * ks + quarter * 4];
         const uint2 v0 = *(const uint2*)vr;
         const uint2 v1 = *(const uint2*)(vr + 16);
-        const bf16x8 bv = as_bf16x8(make_uint4(v0.x, v0.y, v1.x, v1.y));
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, bv, o[t], 0, 0, 0);
+        const bf16x8 a = as_bf16x8(make_uint4(v0.x, v0.y, v1.x, v1.y));
+        if (act[0]) o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][ks], o[0][dt], 0, 0, 0);
+        if (act[1]) o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][ks], o[1][dt], 0, 0, 0);
       }
-    }
-    if (kbi + 1 < nkb) PREFILL_LSTORE(buf ^ 1);
+    if (kbi + 1 < nkb) pf_lstore<D, KB>(s_k[buf ^ 1], s_vt[buf ^ 1], sg, dc, rkv);
     __syncthreads();
   }
 
-#undef PREFILL_GLOAD
-#undef PREFILL_VT
-#undef PREFILL_LSTORE
-  // row sums: every lane quarter holds part of query qi's sum
-  lsum += __shfl_xor(lsum, 16);
-  lsum += __shfl_xor(lsum, 32);
-  uint16_t* obase = p.o + (((size_t)b * p.H + head) * S + qw0) * D;
+  // row sums: the four lane quarters hold disjoint keys of the same query
+  if (!live) return;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (lane >> 4) * 4 + i;
-    const float inv = 1.f / __shfl(lsum, r);
+  for (int t = 0; t < 2; ++t) {
+    if (t == 0 && twin) continue;
+    float l = lsum[t];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = 1.f / l;
+    uint16_t* orow = p.o + (((size_t)b * p.H + head) * S + r0[t] + col) * D;
 #pragma unroll
-    for (int t = 0; t < ND; ++t)
-      obase[(size_t)r * D + 16 * t + (lane & 15)] = f32_to_bf16_rne(o[t][i] * inv);
+    for (int dt = 0; dt < ND; ++dt)
+      *(uint2*)(orow + 16 * dt + quarter * 4) =
+          make_uint2(pack_bf16(o[t][dt][0] * inv, o[t][dt][1] * inv),
+                     pack_bf16(o[t][dt][2] * inv, o[t][dt][3] * inv));
   }
 }
 
 template <int D>
 void launch_d(const PrefillParams& p, int B, int HG, hipStream_t s) {
   const int HW = HG >= 4 ? 4 : HG;
-  const int QT = kQB * (4 / HW);
-  dim3 grid(p.S / QT, p.KV, B * (HG / HW));
+  const int PW = 4 / HW;
+  const int npairs = (p.S / 16 + 1) / 2;
+  dim3 grid((npairs + PW - 1) / PW, p.KV, B * (HG / HW));
   switch (HW) {
     case 1: hipLaunchKernelGGL((prefill_attn_kernel<D, 1>), grid, dim3(256), 0, s, p); break;
     case 2: hipLaunchKernelGGL((prefill_attn_kernel<D, 2>), grid, dim3(256), 0, s, p); break;
