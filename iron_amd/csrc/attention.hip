@@ -599,26 +599,31 @@ __global__ __launch_bounds__(256) void decode_attn_f32_kernel(AttnParams p) {
 }
 
 
-// Split merge, grid (H, B), one wavefront per (head, sequence):
+// Split merge, grid (H, B), 4 wavefronts per (head, sequence):
 //   o = sum_s f_s O_s / sum_s f_s L_s,  f_s = e^(m_s - max m)  (exp2 in the fp32 mode, whose
 //   maxima are in the log2 domain)
-// Lane l owns head dims 2l, 2l+1 and the statistics of splits l, l+64, ...; the weights reach the
-// accumulation through readlane (wave-uniform), so no LDS or barrier is involved. Every partial
-// of the first kRegW splits is loaded before the first reduction.
-constexpr int kRegW = 48;
+// Every wavefront computes the statistics of all splits (lane l holds splits l, l+64, ...), then
+// sums the O partials of its quarter of the splits for head dims 2l, 2l+1, taking the weights by
+// readlane; the four quarter sums add in LDS in a fixed order. All O loads of a quarter (up to
+// kRegW splits) are issued before the first reduction.
+constexpr int kRegW = 16;
 
 template <bool F32>
-__global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
   using T = typename std::conditional<F32, float, double>::type;
   using T2 = typename std::conditional<F32, float2, double2>::type;
-  const int h = blockIdx.x, b = blockIdx.y, l = threadIdx.x;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int ns = p.nsplit;
+  const int per = (ns + 3) >> 2;                // splits per wavefront
+  const int s0 = wave * per, s1 = min(ns, s0 + per);
   const T* base = (const T*)p.part + ((size_t)b * p.H + h) * ns * (kD + 2);
   T2 ov[kRegW];
 #pragma unroll
-  for (int sp = 0; sp < kRegW; ++sp) {
-    const int sc = sp < ns ? sp : 0;  // clamped: every load is issued
-    ov[sp] = *(const T2*)(base + (size_t)sc * (kD + 2) + 2 * l);
+  for (int i = 0; i < kRegW; ++i) {
+    const int sp = s0 + i;
+    const int sc = sp < s1 ? sp : 0;  // clamped: every load is issued
+    ov[i] = *(const T2*)(base + (size_t)sc * (kD + 2) + 2 * l);
   }
   T ms[kMaxSplit / 64], ls[kMaxSplit / 64];
 #pragma unroll
@@ -667,20 +672,25 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(AttnParams p) {
   };
   T a0[4] = {0, 0, 0, 0}, a1[4] = {0, 0, 0, 0};
 #pragma unroll
-  for (int sp = 0; sp < kRegW; ++sp)
-    if (sp < ns) {
-      const T w = weight(sp);
-      a0[sp & 3] = F32 ? fmaf(w, ov[sp].x, a0[sp & 3]) : fma(w, ov[sp].x, a0[sp & 3]);
-      a1[sp & 3] = F32 ? fmaf(w, ov[sp].y, a1[sp & 3]) : fma(w, ov[sp].y, a1[sp & 3]);
+  for (int i = 0; i < kRegW; ++i)
+    if (s0 + i < s1) {
+      const T w = weight(s0 + i);
+      a0[i & 3] = F32 ? fmaf(w, ov[i].x, a0[i & 3]) : fma(w, ov[i].x, a0[i & 3]);
+      a1[i & 3] = F32 ? fmaf(w, ov[i].y, a1[i & 3]) : fma(w, ov[i].y, a1[i & 3]);
     }
-  for (int sp = kRegW; sp < ns; ++sp) {
+  for (int sp = s0 + kRegW; sp < s1; ++sp) {
     const T w = weight(sp);
     const T2 v = *(const T2*)(base + (size_t)sp * (kD + 2) + 2 * l);
     a0[0] = F32 ? fmaf(w, v.x, a0[0]) : fma(w, v.x, a0[0]);
     a1[0] = F32 ? fmaf(w, v.y, a1[0]) : fma(w, v.y, a1[0]);
   }
-  const T o0 = (a0[0] + a0[2]) + (a0[1] + a0[3]);
-  const T o1 = (a1[0] + a1[2]) + (a1[1] + a1[3]);
+  __shared__ T2 s_q[4][64];
+  s_q[wave][l] = T2{(a0[0] + a0[2]) + (a0[1] + a0[3]), (a1[0] + a1[2]) + (a1[1] + a1[3])};
+  __syncthreads();
+  if (wave != 0) return;
+  const T2 q0 = s_q[0][l], q1 = s_q[1][l], q2 = s_q[2][l], q3 = s_q[3][l];
+  const T o0 = (q0.x + q1.x) + (q2.x + q3.x);
+  const T o1 = (q0.y + q1.y) + (q2.y + q3.y);
   uint16_t r0, r1;
   if constexpr (F32) {
     r0 = f32_to_bf16(L > 0.f ? o0 / L : 0.f);
@@ -778,9 +788,9 @@ int launch_attention(AttnParams p, bool fused, int acc, int B, void* part_ws, si
   int st = iron::check_launch(fn);
   if (st || sp.nsplit == 1) return st;
   if (f32)
-    hipLaunchKernelGGL(attn_merge_kernel<true>, dim3(p.H, B), dim3(64), 0, s, p);
+    hipLaunchKernelGGL(attn_merge_kernel<true>, dim3(p.H, B), dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL(attn_merge_kernel<false>, dim3(p.H, B), dim3(64), 0, s, p);
+    hipLaunchKernelGGL(attn_merge_kernel<false>, dim3(p.H, B), dim3(256), 0, s, p);
   return iron::check_launch(fn);
 }
 
