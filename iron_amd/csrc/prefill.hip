@@ -38,9 +38,8 @@ struct PrefillParams {
 
 IRON_DEV bf16x8 as_bf16x8(const uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
-// Staging of one key block: thread -> keys 4 sg .. 4 sg + 3 (clamped to the sequence), dims
-// dc .. dc + 7. K rows go to LDS as they are; V goes transposed, the 4 keys of one dim in one
-// 8-byte write.
+// Staging of one key block (keys clamped to the sequence). K rows go to LDS as they are; V goes
+// transposed, the 4 keys of one dim in one 8-byte write.
 // The staging registers of one key block (four K and four V slices of 8 dims), as native vectors
 // so that they stay in registers.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -48,20 +47,33 @@ struct KVRegs {
   u32x4 k0, k1, k2, k3, v0, v1, v2, v3;
 };
 
+// Staging coordinates: K is copied by thread -> (keys 4 kg .. +4, dims kd .. +8) with the dims
+// fastest across lanes (whole rows per 16 lanes: conflict-free row writes); V by thread -> (keys
+// 4 vg .. +4, dims vd .. +8) with the key groups fastest across lanes, so that the 8-byte V^T
+// writes of a wavefront spread over the LDS banks.
+struct StageIdx {
+  int kg, kd, vg, vd;
+};
+
 template <int D, int KB>
-IRON_DEV void pf_gload(const uint16_t* kbase, const uint16_t* vbase, int kb, int sg, int dc, int S,
-                       KVRegs& r) {
-  const int k0 = kb * KB + 4 * sg;
-  const size_t o0 = (size_t)min(k0, S - 1) * D + dc, o1 = (size_t)min(k0 + 1, S - 1) * D + dc;
-  const size_t o2 = (size_t)min(k0 + 2, S - 1) * D + dc, o3 = (size_t)min(k0 + 3, S - 1) * D + dc;
-  r.k0 = *(const u32x4*)(kbase + o0);
-  r.v0 = *(const u32x4*)(vbase + o0);
-  r.k1 = *(const u32x4*)(kbase + o1);
-  r.v1 = *(const u32x4*)(vbase + o1);
-  r.k2 = *(const u32x4*)(kbase + o2);
-  r.v2 = *(const u32x4*)(vbase + o2);
-  r.k3 = *(const u32x4*)(kbase + o3);
-  r.v3 = *(const u32x4*)(vbase + o3);
+IRON_DEV StageIdx stage_idx(int tid) {
+  constexpr int TPG = D / 8;   // threads per key row
+  constexpr int NG = KB / 4;   // key groups per block
+  return StageIdx{tid / TPG, (tid % TPG) * 8, tid % NG, (tid / NG) * 8};
+}
+
+template <int D, int KB>
+IRON_DEV void pf_gload(const uint16_t* kbase, const uint16_t* vbase, int kb, const StageIdx& x,
+                       int S, KVRegs& r) {
+  const int k0 = kb * KB + 4 * x.kg, v0 = kb * KB + 4 * x.vg;
+  r.k0 = *(const u32x4*)(kbase + (size_t)min(k0, S - 1) * D + x.kd);
+  r.k1 = *(const u32x4*)(kbase + (size_t)min(k0 + 1, S - 1) * D + x.kd);
+  r.k2 = *(const u32x4*)(kbase + (size_t)min(k0 + 2, S - 1) * D + x.kd);
+  r.k3 = *(const u32x4*)(kbase + (size_t)min(k0 + 3, S - 1) * D + x.kd);
+  r.v0 = *(const u32x4*)(vbase + (size_t)min(v0, S - 1) * D + x.vd);
+  r.v1 = *(const u32x4*)(vbase + (size_t)min(v0 + 1, S - 1) * D + x.vd);
+  r.v2 = *(const u32x4*)(vbase + (size_t)min(v0 + 2, S - 1) * D + x.vd);
+  r.v3 = *(const u32x4*)(vbase + (size_t)min(v0 + 3, S - 1) * D + x.vd);
 }
 
 // dims dc + 2w (low halves) and dc + 2w + 1 (high halves) of the 4 keys, one 8-byte write each
@@ -72,13 +84,13 @@ IRON_DEV void pf_vt_pair(uint16_t* lo_row, uint16_t* hi_row, uint32_t a0, uint32
 }
 
 template <int D, int KB>
-IRON_DEV void pf_lstore(uint16_t (*s_k)[D + 8], uint16_t (*s_vt)[KB + 8], int sg, int dc,
+IRON_DEV void pf_lstore(uint16_t (*s_k)[D + 8], uint16_t (*s_vt)[KB + 8], const StageIdx& x,
                         const KVRegs& r) {
-  *(u32x4*)&s_k[4 * sg][dc] = r.k0;
-  *(u32x4*)&s_k[4 * sg + 1][dc] = r.k1;
-  *(u32x4*)&s_k[4 * sg + 2][dc] = r.k2;
-  *(u32x4*)&s_k[4 * sg + 3][dc] = r.k3;
-  const int c = 4 * sg;
+  *(u32x4*)&s_k[4 * x.kg][x.kd] = r.k0;
+  *(u32x4*)&s_k[4 * x.kg + 1][x.kd] = r.k1;
+  *(u32x4*)&s_k[4 * x.kg + 2][x.kd] = r.k2;
+  *(u32x4*)&s_k[4 * x.kg + 3][x.kd] = r.k3;
+  const int c = 4 * x.vg, dc = x.vd;
   pf_vt_pair(&s_vt[dc][c], &s_vt[dc + 1][c], r.v0.x, r.v1.x, r.v2.x, r.v3.x);
   pf_vt_pair(&s_vt[dc + 2][c], &s_vt[dc + 3][c], r.v0.y, r.v1.y, r.v2.y, r.v3.y);
   pf_vt_pair(&s_vt[dc + 4][c], &s_vt[dc + 5][c], r.v0.z, r.v1.z, r.v2.z, r.v3.z);
@@ -138,8 +150,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
     for (int j = 0; j < NJ; ++j) qf[t][j] = *(const uint4*)(qrow + 32 * j + quarter * 8);
   }
 
-  constexpr int TPG = D / 8;  // staging threads per key
-  const int sg = tid / TPG, dc = (tid % TPG) * 8;
+  const StageIdx sx = stage_idx<D, KB>(tid);
   KVRegs rkv;
 
   // O^T accumulators: tile (t, dt) is 16 dims x 16 queries; lane l holds query r0[t] + l%16,
@@ -152,13 +163,13 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};  // this lane's share of query stats
   const float c = p.scale_log2;
 
-  pf_gload<D, KB>(kbase, vbase, 0, sg, dc, S, rkv);
-  pf_lstore<D, KB>(s_k[0], s_vt[0], sg, dc, rkv);
+  pf_gload<D, KB>(kbase, vbase, 0, sx, S, rkv);
+  pf_lstore<D, KB>(s_k[0], s_vt[0], sx, rkv);
   __syncthreads();
   for (int kbi = 0; kbi < nkb; ++kbi) {
     const int buf = kbi & 1;
     const int kb0 = kbi * KB;
-    if (kbi + 1 < nkb) pf_gload<D, KB>(kbase, vbase, kbi + 1, sg, dc, S, rkv);
+    if (kbi + 1 < nkb) pf_gload<D, KB>(kbase, vbase, kbi + 1, sx, S, rkv);
     // tile t takes part while the block starts at or before its last row (wave-uniform)
     const bool act[2] = {live && !twin && kb0 <= r0[0] + 15, live && kb0 <= r0[1] + 15};
     f32x4 st[2][NKT];
@@ -229,7 +240,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
         if (act[0]) o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][ks], o[0][dt], 0, 0, 0);
         if (act[1]) o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][ks], o[1][dt], 0, 0, 0);
       }
-    if (kbi + 1 < nkb) pf_lstore<D, KB>(s_k[buf ^ 1], s_vt[buf ^ 1], sg, dc, rkv);
+    if (kbi + 1 < nkb) pf_lstore<D, KB>(s_k[buf ^ 1], s_vt[buf ^ 1], sx, rkv);
     __syncthreads();
   }
 
