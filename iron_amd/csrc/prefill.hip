@@ -32,7 +32,7 @@ struct PrefillParams {
   const uint16_t* k;   // [B][KV][S][D]
   const uint16_t* v;
   uint16_t* o;         // [B][H][S][D]
-  int H, KV, S;
+  int B, H, KV, S;
   float scale_log2;    // scale * log2(e)
 };
 
@@ -122,19 +122,25 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int quarter = lane >> 4, col = lane & 15;
   const int HG = p.H / p.KV;
-  const int kv = blockIdx.y;
-  const int b = blockIdx.z / (HG / HW), hsub = blockIdx.z % (HG / HW);
+  // 1-D grid, head groups fastest: consecutive workgroups go to consecutive XCDs, so with a
+  // multiple of 8 groups every workgroup of one (sequence, KV head) runs on the same XCD and its
+  // K/V blocks stay in that XCD's L2
+  const int ngroups = p.B * p.KV * (HG / HW);
+  const int grp = blockIdx.x % ngroups, pblk = blockIdx.x / ngroups;
+  const int kv = grp % p.KV;
+  const int bh = grp / p.KV;
+  const int b = bh / (HG / HW), hsub = bh % (HG / HW);
   const int head = kv * HG + hsub * HW + wave % HW;
   const int S = p.S;
   const int NT = S / 16, npairs = (NT + 1) / 2;
-  const int pair = blockIdx.x * PW + wave / HW;          // this wavefront's tile pair
+  const int pair = pblk * PW + wave / HW;                // this wavefront's tile pair
   const bool live = pair < npairs;
   // tile t's first row (t = 0 light, t = 1 heavy; with an odd tile count the middle tile pairs
   // with itself and the copy is skipped)
   const int r0[2] = {16 * pair, 16 * (NT - 1 - pair)};
   const bool twin = live && r0[0] == r0[1];
   // key blocks the workgroup needs: up to the heavy tile of its lightest pair
-  const int pmin = blockIdx.x * PW;
+  const int pmin = pblk * PW;
   const int nkb = (16 * (NT - 1 - pmin) + 15) / KB + 1;
 
   const uint16_t* kbase = p.k + ((size_t)b * p.KV + kv) * S * D;
@@ -267,7 +273,7 @@ void launch_d(const PrefillParams& p, int B, int HG, hipStream_t s) {
   const int HW = HG >= 4 ? 4 : HG;
   const int PW = 4 / HW;
   const int npairs = (p.S / 16 + 1) / 2;
-  dim3 grid((npairs + PW - 1) / PW, p.KV, B * (HG / HW));
+  dim3 grid((unsigned)((npairs + PW - 1) / PW) * B * p.KV * (HG / HW));
   switch (HW) {
     case 1: hipLaunchKernelGGL((prefill_attn_kernel<D, 1>), grid, dim3(256), 0, s, p); break;
     case 2: hipLaunchKernelGGL((prefill_attn_kernel<D, 2>), grid, dim3(256), 0, s, p); break;
@@ -301,6 +307,7 @@ int iron_prefill_attn(const uint16_t* q, const uint16_t* k, const uint16_t* v, u
   p.k = k;
   p.v = v;
   p.o = o;
+  p.B = B;
   p.H = H;
   p.KV = KV;
   p.S = S;
