@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   }
 
   const StageIdx sx = stage_idx<D, KB>(tid);
-  KVRegs rkv;
+  KVRegs ra, rb;  // two register sets: block i + 2 is fetched while block i + 1 waits
 
   // O^T accumulators: tile (t, dt) is 16 dims x 16 queries; lane l holds query r0[t] + l%16,
   // dims 16 dt + (l/16)*4 + i
@@ -169,13 +169,16 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};  // this lane's share of query stats
   const float c = p.scale_log2;
 
-  pf_gload<D, KB>(kbase, vbase, 0, sx, S, rkv);
-  pf_lstore<D, KB>(s_k[0], s_vt[0], sx, rkv);
+  pf_gload<D, KB>(kbase, vbase, 0, sx, S, ra);
+  if (nkb > 1) pf_gload<D, KB>(kbase, vbase, 1, sx, S, rb);
+  pf_lstore<D, KB>(s_k[0], s_vt[0], sx, ra);
   __syncthreads();
-  for (int kbi = 0; kbi < nkb; ++kbi) {
+  // iteration kbi: fetch block kbi + 2 into the set that held block kbi, compute block kbi, then
+  // stage block kbi + 1 (fetched an iteration earlier) into the other LDS buffer
+  auto iteration = [&](int kbi, KVRegs& fetch, KVRegs& stage) {
     const int buf = kbi & 1;
     const int kb0 = kbi * KB;
-    if (kbi + 1 < nkb) pf_gload<D, KB>(kbase, vbase, kbi + 1, sx, S, rkv);
+    if (kbi + 2 < nkb) pf_gload<D, KB>(kbase, vbase, kbi + 2, sx, S, fetch);
     // tile t takes part while the block starts at or before its last row (wave-uniform)
     const bool act[2] = {live && !twin && kb0 <= r0[0] + 15, live && kb0 <= r0[1] + 15};
     f32x4 st[2][NKT];
@@ -246,8 +249,12 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
         if (act[0]) o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][ks], o[0][dt], 0, 0, 0);
         if (act[1]) o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][ks], o[1][dt], 0, 0, 0);
       }
-    if (kbi + 1 < nkb) pf_lstore<D, KB>(s_k[buf ^ 1], s_vt[buf ^ 1], sx, rkv);
+    if (kbi + 1 < nkb) pf_lstore<D, KB>(s_k[buf ^ 1], s_vt[buf ^ 1], sx, stage);
     __syncthreads();
+  };
+  for (int kbi = 0; kbi < nkb; kbi += 2) {
+    iteration(kbi, ra, rb);
+    if (kbi + 1 < nkb) iteration(kbi + 1, rb, ra);
   }
 
   // row sums: the four lane quarters hold disjoint keys of the same query
