@@ -175,6 +175,12 @@ def main():
     }
 
     if not args.no_configs:
+        # the achievable streaming-read rate on this device, the practical ceiling beside the
+        # 8 TB/s nominal peak
+        from iron_amd import benchmarks
+        rc = benchmarks.read_probe()
+        result["roofline"]["achievable_read_GB_s"] = rc["GB_s"]
+        result["roofline"]["frac_of_achievable"] = round(lm_gbs / rc["GB_s"], 4)
         # the other BASELINE configurations, each timed standalone over >= 512 MiB of rotating
         # operands (iron_amd/benchmarks.py); config 5 includes the 36-layer Qwen3-8B B=16 stack
         del model, w

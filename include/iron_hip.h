@@ -224,6 +224,12 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
  * the same multiply-shift sequence the kernels use (test hook; no reference counterpart). */
 uint32_t iron_test_fastdiv(uint32_t n, uint32_t d);
 
+/* Measurement hook (no reference counterpart): streams `bytes` (a multiple of 16, 16-byte aligned)
+ * through 16-byte loads with a grid of `blocks` x 256 threads and writes one xor word per thread
+ * to out[blocks * 256]. Its time is the achievable HBM read rate that the roofline figures are
+ * read against. */
+int iron_stream_read(const void* p, size_t bytes, uint32_t* out, int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -86,6 +86,7 @@ SIGNATURES = {
                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                  _c_int, _c_f, _c_vp, _c_sz, _c_vp]),
     "iron_test_fastdiv": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32]),
+    "iron_stream_read": (_c_int, [_c_vp, _c_sz, _c_vp, _c_int, _c_vp]),
 }
 
 _lock = threading.Lock()

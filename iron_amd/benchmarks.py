@@ -228,7 +228,8 @@ def config5_prefill(lib):
 
 def run_all(include_c5: bool = True) -> dict:
     lib = _lib.load()
-    out = {"c1_qkv_gemv": config1(lib),
+    out = {"read_ceiling": read_probe(),
+           "c1_qkv_gemv": config1(lib),
            "c2_mlp_b1": config2(lib, 1), "c2_mlp_b8": config2(lib, 8),
            "c3_attn_b1": config3(lib, 1, False), "c3_attn_b8_ragged": config3(lib, 8, True),
            "c3_attn_b1_f32": config3(lib, 1, False, "f32"),
@@ -240,6 +241,29 @@ def run_all(include_c5: bool = True) -> dict:
         out["c5_decode_b16_f32"] = config5_decode(lib, acc="f32")
         torch.cuda.empty_cache()
     return out
+
+
+def read_probe(gib: int = 1, reps: int = 5) -> dict:
+    """The achievable HBM read rate: iron_stream_read over a buffer far larger than the caches
+    (grid sizes swept; the best is the ceiling the decode kernels are read against)."""
+    lib = _lib.load()
+    nbytes = gib << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=DEV)
+    out = torch.empty(16384 * 256, dtype=torch.int32, device=DEV)
+    best = 0.0
+    for blocks in (2048, 4096, 8192, 16384):
+        _lib.check(lib.iron_stream_read(buf.data_ptr(), nbytes, out.data_ptr(), blocks, _st()))
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            _lib.check(lib.iron_stream_read(buf.data_ptr(), nbytes, out.data_ptr(), blocks, _st()))
+        e1.record()
+        e1.synchronize()
+        gbs = reps * nbytes / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        best = max(best, gbs)
+    return {"GB_s": round(best, 1), "frac": round(best / HBM_PEAK_GBS, 4),
+            "bytes": nbytes, "kernel": "iron_stream_read (16-byte loads, grid-stride)"}
 
 
 def copy_probe(mib: int = 256, reps: int = 4) -> dict:
@@ -259,6 +283,8 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser(description="standalone timings of the BASELINE configurations")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run only the byte-counter calibration copy")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="run only the achievable-read-bandwidth probe")
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c5_prefill", "c5_decode"],
                     help="run one configuration (for profiling)")
     ap.add_argument("--acc", choices=["f64", "f32"], default="f64",
@@ -266,6 +292,8 @@ if __name__ == "__main__":
     a = ap.parse_args()
     if a.copy_probe:
         print(json.dumps(copy_probe()), flush=True)
+    elif a.read_probe:
+        print(json.dumps(read_probe()), flush=True)
     elif a.only:
         lib = _lib.load()
         one = {"c1": lambda: config1(lib), "c2": lambda: config2(lib, 1),

@@ -232,6 +232,22 @@ __global__ __launch_bounds__(64) void advance_kernel(int32_t* pos, int32_t* ctx,
   }
 }
 
+// Streaming read (the bandwidth reference of iron_stream_read): grid-stride 16-byte loads, four
+// in flight per thread per iteration; every index stays below n16.
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, size_t n16,
+                                                          uint32_t* __restrict__ out) {
+  uint32_t a = 0;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const uint4 v0 = p[i], v1 = p[i + stride], v2 = p[i + 2 * stride], v3 = p[i + 3 * stride];
+    a ^= v0.x ^ v1.y ^ v2.z ^ v3.w;
+  }
+  for (; i < n16; i += stride) a ^= p[i].x;
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = a;
+}
+
+
 }  // namespace
 
 namespace iron {
@@ -283,6 +299,17 @@ const char* iron_last_error(void) { return iron::g_err; }
 uint32_t iron_test_fastdiv(uint32_t n, uint32_t d) {
   if (d == 0) return 0xffffffffu;
   return fastdiv_host(n, make_fastdiv(d));
+}
+
+int iron_stream_read(const void* p, size_t bytes, uint32_t* out, int blocks, void* stream) {
+  iron::clear_error();
+  const char* fn = "iron_stream_read";
+  if (!p || !out) return iron::fail(IRON_ERR_NULL, "%s: null buffer", fn);
+  if (bytes % 16 || !iron::aligned(p, 16) || blocks <= 0)
+    return iron::fail(IRON_ERR_SHAPE, "%s: bytes %zu / blocks %d / alignment", fn, bytes, blocks);
+  hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const uint4*)p, bytes / 16, out);
+  return iron::check_launch(fn);
 }
 
 int iron_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols, float eps,
