@@ -1,7 +1,10 @@
 // Shared device helpers for the gfx950 (MI355X) kernels of the Qwen3 int8 decode path.
 //
 // Conventions used by every kernel in this directory:
-//   * bf16 values travel as uint16_t bit patterns; all arithmetic is fp32.
+//   * bf16 values travel as uint16_t bit patterns. Sums that decide a rounded output are
+//     accumulated in fp64 (exact to within 2^-50 for these magnitudes), so every operator
+//     boundary is the correctly rounded value; the fp32 variants (decode attention with
+//     IRON_ACCUM_F32, prefill, the MFMA group sums) say so where they are defined.
 //   * fp32 -> bf16 is round-to-nearest-even, the rounding the reference applies at every
 //     operator boundary (iron/common/sequence.py:997-999) and inside its kernels
 //     (aie_kernels/aie2p/mv_int8_signed.cc:66 sets conv_even).
