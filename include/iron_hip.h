@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 2
+#define IRON_ABI_VERSION 3
 
 enum iron_status {
   IRON_OK = 0,
@@ -219,6 +219,64 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
                     uint16_t* nxt, uint16_t* a_out, int B, int D, int FF, int QD, int G,
                     int tile_m_o, int tile_m_gu, int tile_m_d, int domain, float eps,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* One decoder layer's device pointers for iron_decode_persistent (a device array of these, one per
+ * layer). Wires as in iron_qkv_attn / iron_swiglu_mlp: wqkv [Hq*HD + 2*Hkv*HD][D], wo [D][Hq*HD],
+ * wg and wu [FF][D], wd [D][FF]; norm weights bf16 (n_in, n_post [D]; n_qn, n_kn [HD]); the
+ * layer's K and V caches for batch 1 ([Hkv][max_seq][HD] through the kv_sh / kv_st strides).
+ * Mirrors the per-layer buffer names of the reference runlist (W_norm1_i, W_qkv_i, W_qn_i, W_kn_i,
+ * W_norm2_i, Wo_i, Wg_i, Wu_i, Wd_i and the layer's caches; qwen3_npu_int8.py:249-281). */
+typedef struct iron_layer_desc {
+  const void* wqkv;
+  const void* wo;
+  const void* wg;
+  const void* wu;
+  const void* wd;
+  const uint16_t* n_in;
+  const uint16_t* n_post;
+  const uint16_t* n_qn;
+  const uint16_t* n_kn;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+} iron_layer_desc;
+
+/* Workspace bytes for iron_decode_persistent (0 if no kernel exists for the shape). The workspace
+ * holds the tagged hand-off words and two control words: uint32 [0] = epoch, [1] = error flags
+ * (nonzero after a hand-off wait timed out). It must be zero-filled once before its first use
+ * and then kept for the lifetime of the decode state. */
+size_t iron_decode_persistent_workspace(int D, int FF, int Hq, int Hkv, int HD);
+
+/* IRON_OK if iron_decode_persistent has a kernel for this shape and the current device can hold
+ * its grid resident (256 CUs, two 256-thread workgroups per CU); else IRON_ERR_UNSUPPORTED. Shapes:
+ * D, FF, Hq, Hkv = (1024, 3072, 16, 8) (Qwen3-0.6B) and (256, 768, 4, 2); HD = 128. */
+int iron_decode_persistent_supported(int D, int FF, int Hq, int Hkv, int HD);
+
+/* Host-only validation of one layer descriptor (a host copy of what the device array holds): wire
+ * geometry and alignment as the standalone entry points check them. */
+int iron_decode_persistent_check_layer(const iron_layer_desc* layer, int D, int FF, int Hq,
+                                       int Hkv, int HD, int G, int tile_qkv, int tile_o,
+                                       int tile_gu, int tile_d, int domain);
+
+/* Whole-token decode of n_layers Qwen3 layers at batch 1 in one persistent kernel:
+ *   x = x_in; for each layer i (layers[i], a device array):
+ *     out = iron_qkv_attn(x, ...)            (QKV head at position *pos, K/V appended, attention
+ *                                              over positions 0..*pos, exact fp64 core)
+ *     x   = iron_swiglu_mlp(x, out, ...)     (fuse_o: Wo, residual, RMSNorm, SwiGLU, down)
+ *   x_out = x.
+ * The results equal those of the per-operator entry points (same arithmetic and roundings).
+ * pos: device int32 [1]; ang: the position's RoPE row (bf16 [HD]); kv_sh / kv_st: head and token
+ * strides of the caches in elements. Launches 512 workgroups that exchange activations through the
+ * workspace: calls on one workspace must be stream-ordered, and the workspace's error word must be
+ * checked (and cleared) by the caller after synchronising. Replaces the per-token runlist dispatch
+ * of Qwen3NPU (iron/applications/qwen3_0.6b/qwen3_npu_int8.py:249-281, 594-621; one dispatch of
+ * iron/common/sequence.py:270-559) for the layers; the final RMSNorm and LM head follow it
+ * (iron_lm_head). */
+int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, int FF, int Hq,
+                           int Hkv, int HD, int max_seq, long long kv_sh, long long kv_st, int G,
+                           int tile_qkv, int tile_o, int tile_gu, int tile_d, int domain,
+                           const uint16_t* x_in, uint16_t* x_out, const int32_t* pos,
+                           const uint16_t* ang, float eps, float scale, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /* Host-only check of the device-side divide used for wire row-blocks: returns n / d computed with
  * the same multiply-shift sequence the kernels use (test hook; no reference counterpart). */

@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
-ABI_VERSION = 2          # IRON_ABI_VERSION of include/iron_hip.h
+ABI_VERSION = 3          # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2
@@ -44,6 +44,14 @@ _VALUE_ERRORS = {IRON_ERR_NULL, IRON_ERR_SHAPE, IRON_ERR_ALIGN, IRON_ERR_WORKSPA
 
 _c_int, _c_ll, _c_f, _c_sz, _c_vp = (ctypes.c_int, ctypes.c_longlong, ctypes.c_float,
                                      ctypes.c_size_t, ctypes.c_void_p)
+
+
+class LayerDesc(ctypes.Structure):
+    """``iron_layer_desc``: one decoder layer's device pointers (include/iron_hip.h)."""
+
+    _fields_ = [(name, _c_vp) for name in ("wqkv", "wo", "wg", "wu", "wd", "n_in", "n_post",
+                                           "n_qn", "n_kn", "k_cache", "v_cache")]
+
 
 # name -> (restype, argtypes). Kept in the order of include/iron_hip.h.
 SIGNATURES = {
@@ -85,6 +93,15 @@ SIGNATURES = {
     "iron_swiglu_mlp": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                  _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                  _c_int, _c_f, _c_vp, _c_sz, _c_vp]),
+    "iron_decode_persistent_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "iron_decode_persistent_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "iron_decode_persistent_check_layer": (_c_int, [ctypes.POINTER(LayerDesc), _c_int, _c_int,
+                                                    _c_int, _c_int, _c_int, _c_int, _c_int,
+                                                    _c_int, _c_int, _c_int, _c_int]),
+    "iron_decode_persistent": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                        _c_int, _c_ll, _c_ll, _c_int, _c_int, _c_int, _c_int,
+                                        _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_f, _c_f,
+                                        _c_vp, _c_sz, _c_vp]),
     "iron_test_fastdiv": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32]),
     "iron_stream_read": (_c_int, [_c_vp, _c_sz, _c_vp, _c_int, _c_vp]),
 }

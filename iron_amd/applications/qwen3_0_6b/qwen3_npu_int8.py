@@ -22,10 +22,18 @@ Differences from the reference, all deliberate:
     copies the logits out and runs numpy argmax, qwen3_npu_int8.py:612-621);
   * ``generate()`` runs greedy decoding entirely on the device: each step replays one graph that
     consumes the previous argmax, gathers its embedding, runs the layers and advances the
-    positions, with no host synchronisation between tokens.
+    positions, with no host synchronisation between tokens;
+  * ``persistent`` runs all layers of a token in ONE kernel (``iron_decode_persistent``) with the
+    same arithmetic as the runlist's operators, followed by the LM head with the final RMSNorm
+    fused into its prologue: the counterpart of the reference's single dispatch per token
+    (sequence.py:270-559). ``None`` (the default) uses it wherever it is available: batch 1, the
+    exact attention core, a shape the kernel is built for, and a device that holds its grid.
 """
 
 from __future__ import annotations
+
+import ctypes
+import math
 
 import numpy as np
 import torch
@@ -67,7 +75,8 @@ class Qwen3NPU:
                  weights: dict | None = None, seed: int = 0, max_seq_len: int = 512,
                  kv_layout: str = "separate", lm_head: str | None = None,
                  dispatch: str = "auto", context: AIEContext | None = None,
-                 fuse_attention: bool = True, attn_accumulate: str = "f64"):
+                 fuse_attention: bool = True, attn_accumulate: str = "f64",
+                 persistent: bool | None = False):
         self.cfg = cfg = config or Qwen3Config.qwen3_0_6b()
         self.max_seq_len = max_seq_len
         self.kv_layout = kv_layout
@@ -85,6 +94,7 @@ class Qwen3NPU:
         self._build_sequence(dispatch)
         self._load_weights(weights)
         self._gen_graph = None
+        self.persistent = self._setup_persistent(persistent)
 
     # ---------------- operators ----------------
     def _build_operators(self):
@@ -188,6 +198,102 @@ class Qwen3NPU:
                                            cfg.rope_theta).to(self.device).reshape(-1)
         torch.cuda.synchronize(self.device)
 
+    # ---------------- persistent whole-token kernel ----------------
+    def persistent_unavailable_reason(self) -> str | None:
+        """Why ``iron_decode_persistent`` cannot run this model (None when it can)."""
+        cfg = self.cfg
+        if self.attn_accumulate != "f64":
+            return "the persistent kernel implements the exact (f64) attention core only"
+        lib = _lib.load()
+        if lib.iron_decode_persistent_supported(cfg.emb_dim, cfg.hidden_dim, cfg.n_heads,
+                                                cfg.n_kv_heads, cfg.head_dim) != _lib.IRON_OK:
+            return lib.iron_last_error().decode(errors="replace")
+        return None
+
+    def _cache_ptrs(self, layer: int):
+        if self.kv_layout == "separate":
+            return (self.fc.get_buffer(f"k_cache_{layer}").torch_view(torch.bfloat16).data_ptr(),
+                    self.fc.get_buffer(f"v_cache_{layer}").torch_view(torch.bfloat16).data_ptr())
+        kv = self.fc.get_buffer(f"kv_cache_{layer}").torch_view(torch.bfloat16).data_ptr()
+        return kv, kv + 2 * self.cfg.head_dim
+
+    def _kv_strides(self):
+        """(head stride, token stride) of a layer's cache in elements (batch 1)."""
+        HD, S = self.cfg.head_dim, self.max_seq_len
+        per_tok = HD * (1 if self.kv_layout == "separate" else 2)
+        return S * per_tok, per_tok
+
+    def _setup_persistent(self, want: bool | None) -> bool:
+        if want is False:
+            return False
+        reason = self.persistent_unavailable_reason()
+        if reason is not None:
+            if want:
+                raise ValueError(f"persistent decode unavailable: {reason}")
+            return False
+        cfg, lib, mlp = self.cfg, _lib.load(), self.mlp_xdna
+        buf = lambda name: self.fc.get_buffer(name).torch_view(torch.uint8).data_ptr()  # noqa: E731
+        descs = (_lib.LayerDesc * cfg.n_layers)()
+        for i in range(cfg.n_layers):
+            k, v = self._cache_ptrs(i)
+            d = descs[i]
+            d.wqkv, d.wo, d.wg, d.wu, d.wd = (buf(f"W_qkv_{i}"), buf(f"Wo_{i}"), buf(f"Wg_{i}"),
+                                              buf(f"Wu_{i}"), buf(f"Wd_{i}"))
+            d.n_in, d.n_post = buf(f"W_norm1_{i}"), buf(f"W_norm2_{i}")
+            d.n_qn, d.n_kn = buf(f"W_qn_{i}"), buf(f"W_kn_{i}")
+            d.k_cache, d.v_cache = k, v
+            _lib.check(lib.iron_decode_persistent_check_layer(
+                ctypes.byref(d), cfg.emb_dim, cfg.hidden_dim, cfg.n_heads, cfg.n_kv_heads,
+                cfg.head_dim, cfg.group_size, QKV_TSI, mlp.tile_rows_o, mlp.tile_rows_gu,
+                mlp.tile_rows_d, _lib.IRON_DOMAIN_SIGNED), f"layer {i}")
+        self._p_layers = torch.frombuffer(bytearray(descs), dtype=torch.uint8).to(self.device)
+        nbytes = lib.iron_decode_persistent_workspace(cfg.emb_dim, cfg.hidden_dim, cfg.n_heads,
+                                                      cfg.n_kv_heads, cfg.head_dim)
+        self._p_ws = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        self._p_xout = torch.zeros(cfg.emb_dim, dtype=torch.bfloat16, device=self.device)
+        torch.cuda.synchronize(self.device)
+        return True
+
+    def _persistent_launches(self):
+        """The token's layers in one kernel, then the LM head with the final RMSNorm fused."""
+        cfg, lib, mlp = self.cfg, _lib.load(), self.mlp_xdna
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        view = lambda name, dt: self.fc.get_buffer(name).torch_view(dt)  # noqa: E731
+        sh, st = self._kv_strides()
+        _lib.check(lib.iron_decode_persistent(
+            self._p_layers.data_ptr(), cfg.n_layers, cfg.emb_dim, cfg.hidden_dim, cfg.n_heads,
+            cfg.n_kv_heads, cfg.head_dim, self.max_seq_len, sh, st, cfg.group_size, QKV_TSI,
+            mlp.tile_rows_o, mlp.tile_rows_gu, mlp.tile_rows_d, _lib.IRON_DOMAIN_SIGNED,
+            view("x", torch.bfloat16).data_ptr(), self._p_xout.data_ptr(),
+            self.fc.params.tensor("k_cache_offset").data_ptr(),
+            view("rope_row", torch.bfloat16).data_ptr(), float(cfg.eps),
+            1.0 / math.sqrt(cfg.head_dim), self._p_ws.data_ptr(), self._p_ws.numel(), stream),
+            "iron_decode_persistent")
+        head = view("W_out_head", torch.uint8).data_ptr()
+        kind, G, tile = ((_lib.IRON_WEIGHT_BF16, 16, 1) if self.lm_head_kind == "bf16"
+                         else (_lib.IRON_WEIGHT_INT8, cfg.group_size, LMHEAD_TSI))
+        _lib.check(lib.iron_lm_head(
+            head, kind, self._p_xout.data_ptr(), view("W_final_norm", torch.bfloat16).data_ptr(),
+            float(cfg.eps), view("logits", torch.bfloat16).data_ptr(),
+            view("argmax_key", torch.int64).data_ptr(), 1, cfg.vocab_size, cfg.emb_dim, G, tile,
+            _lib.IRON_DOMAIN_SIGNED, stream), "iron_lm_head")
+
+    def persistent_errors(self, clear: bool = True) -> int:
+        """The persistent kernel's error word (nonzero: a hand-off wait timed out)."""
+        if not self.persistent:
+            return 0
+        word = self._p_ws[4:8].view(torch.int32)
+        err = int(word.item())
+        if err and clear:
+            word.zero_()
+        return err
+
+    def _persistent_check(self):
+        err = self.persistent_errors()
+        if err:
+            raise RuntimeError(f"iron_decode_persistent: a hand-off wait timed out (flags {err:#x});"
+                               " the token's outputs are invalid")
+
     # ---------------- state helpers ----------------
     def kv_caches(self, layer: int):
         """(K, V) device views of one layer's cache, each (Hkv, max_seq, HD)."""
@@ -233,7 +339,12 @@ class Qwen3NPU:
             torch.as_tensor(x).reshape(-1).to(self.device, torch.bfloat16))
         self.fc.get_buffer("argmax_key").torch_view(torch.int64).zero_()
         self._set_position(seq_pos)
-        self.fc()
+        if self.persistent:
+            self._persistent_launches()
+            torch.cuda.synchronize(self.device)
+            self._persistent_check()
+        else:
+            self.fc()
         key = int(self.fc.get_buffer("argmax_key").torch_view(torch.int64)[0].item())
         return _decode_key(key)
 
@@ -259,7 +370,10 @@ class Qwen3NPU:
         _lib.call("iron_next_token", keys.data_ptr(), gs["tokens"].data_ptr(),
                   self.embed.data_ptr(), x.data_ptr(), gs["log"].data_ptr(), 0,
                   gs["step"].data_ptr(), 1, cfg.emb_dim, cfg.vocab_size, stream)
-        self.fc.run_steps()
+        if self.persistent:
+            self._persistent_launches()
+        else:
+            self.fc.run_steps()
         _lib.call("iron_advance_positions", self.fc.params.tensor("k_cache_offset").data_ptr(),
                   self.fc.params.tensor("S_kv_eff").data_ptr(), self.rope_table.data_ptr(),
                   self.fc.get_buffer("rope_row").torch_view(torch.bfloat16).data_ptr(),
@@ -303,6 +417,7 @@ class Qwen3NPU:
                   gs["log"].data_ptr(), 0, gs["step"].data_ptr(), 1, cfg.emb_dim,
                   cfg.vocab_size, stream)
         torch.cuda.synchronize(self.device)
+        self._persistent_check()
         n = int(gs["step"].item())
         # log[0] is the armed first token; log[1..n-1] are the generated ones
         return gs["log"][1:n].cpu().tolist()

@@ -1,0 +1,224 @@
+// Device building blocks of the exact (fp64) GQA decode-attention core, shared by the split-K
+// kernels (attention.hip) and the persistent whole-token decode kernel (decode_persistent.hip).
+//
+// Reference: DecodeAttention (iron/operators/decode_attn/op.py:20-181), kernels
+// aie_kernels/aie2p/decode_attn.cc:117-311, golden iron/operators/decode_attn/reference.py:26-38;
+// the per-head QKV epilogue follows qkv_head_dp/reference.py:13-33.
+//
+// A workgroup is 256 threads (4 wavefronts). Lane l of wavefront w works on token rows
+// 16u + 4w + l/16 (u = 0..3) of a 64-token tile and on head dims [8 (l % 16), +8), so one
+// 128-bit load per lane reads 4 consecutive K (or V) rows per wavefront instruction, and the HB
+// query heads of a GQA group share every K/V load.
+#pragma once
+#include <utility>
+
+#include "common.h"
+
+namespace iron {
+namespace dev {
+
+constexpr int kAttnD = 128;   // head dim
+constexpr int kAttnTile = 64; // tokens per tile
+
+template <int N>
+IRON_DEV double row_share_d(double v) {
+  // every lane of a 16-lane row receives lane N of that row (row_newbcast)
+  return dpp_d<0x150 + N>(v);
+}
+
+template <int N, int HB>
+IRON_DEV void share_one(double ev, double (&pe)[4][HB]) {
+  if constexpr (N < 4 * HB) pe[N / HB][N % HB] = row_share_d<N>(ev);
+}
+
+template <int HB, int... Ns>
+IRON_DEV void share_all(double ev, double (&pe)[4][HB], std::integer_sequence<int, Ns...>) {
+  (share_one<Ns, HB>(ev, pe), ...);
+}
+
+IRON_DEV void unpack8d(const uint4 v, double (&f)[8]) {
+  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[2 * j] = bf16lo_to_f32(d[j]);
+    f[2 * j + 1] = bf16hi_to_f32(d[j]);
+  }
+}
+
+IRON_DEV uint4 pack8_bf16(const double (&f)[8]) {
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = (uint32_t)f64_to_bf16(f[2 * j]) | ((uint32_t)f64_to_bf16(f[2 * j + 1]) << 16);
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// The QKV head epilogue for one head held by a 16-lane row (lane dl owns dims 8*dl..8*dl+7):
+//   y = bf16(RMSNorm(x) * w), r = bf16(RoPE(y)) with the two-halves rotation
+//   r[i] = y[i] cos_i - y[i+64] sin_i, r[i+64] = y[i+64] cos_i + y[i] sin_i (i < 64).
+// a0/a1: this lane's 8 (cos, sin) bf16 pairs of the interleaved angle row (indices (dl%8)*8..+8).
+// The same operations and roundings as the standalone epilogue kernel (qkv.hip).
+IRON_DEV void norm_rope8(const uint4 xr, const uint4 wr, const uint4 a0, const uint4 a1, int dl,
+                         double eps, double (&out)[8]) {
+  double x[8], w[8];
+  unpack8d(xr, x);
+  unpack8d(wr, w);
+  const double ss = row16_sum_d(sum_sq_tree(x));
+  const double inv = inv_rms(ss, kAttnD, eps);
+  float y[8], yp[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = bf16_to_f32(f64_to_bf16((x[j] * inv) * w[j]));
+  // the partner dims (+-64) live in lane dl ^ 8 of the same row (row_ror:8)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) yp[j] = dpp_f<0x128>(y[j]);
+  const uint32_t ad[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const double c = bf16lo_to_f32(ad[j]), s = bf16hi_to_f32(ad[j]);
+    const double r = dl < 8 ? (double)y[j] * c - (double)yp[j] * s
+                            : (double)y[j] * c + (double)yp[j] * s;
+    out[j] = bf16_to_f32(f64_to_bf16(r));
+  }
+}
+
+// One 64-token tile of the exact (fp64) core. Lane (wave, row, dl) holds the K/V rows
+// t0 + 16u + 4 wave + row (u = 0..3), head dims 8 dl..+8; rows at or past t_end are masked and,
+// with FUSED and has_new, the row at `pos` is replaced by the current token's rows (s_new).
+// Updates the running maximum m, sum l and unnormalised output o of the HB heads; `it` is the
+// tile's index within this workgroup's sequence (0 = the first tile, which starts from zero).
+// s_mx is the workgroup's tile-maximum exchange; the function ends past its one barrier.
+template <int HB, bool FUSED>
+IRON_DEV void attn_tile_f64(uint4 (&kr)[4], uint4 (&vr)[4], int t0, int t_end, bool has_new,
+                            int pos, const uint4 (&s_new)[2][16], const double (&qf)[HB][8],
+                            double scale, int it, double (&m)[HB], double (&l)[HB],
+                            double (&o)[HB][8], double (&s_mx)[2][4][HB], int wave, int lane,
+                            int row, int dl) {
+  bool tv[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = t0 + u * 16 + wave * 4 + row;
+    tv[u] = t < t_end;
+    if constexpr (FUSED) {
+      if (has_new && t == pos) {
+        kr[u] = s_new[0][dl];
+        vr[u] = s_new[1][dl];
+      }
+    }
+    if (!tv[u]) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // rows past the context may hold NaNs
+  }
+  // scores s[u][h], identical in every lane of the row
+  double s[4][HB];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    double kf[8];
+    unpack8d(kr[u], kf);
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      double a = 0.0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a = fma(qf[h][j], kf[j], a);
+      a = row16_sum_d(a) * scale;
+      s[u][h] = tv[u] ? a : -INFINITY;
+    }
+  }
+  // workgroup-wide tile maximum per head
+  double mx[HB];
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    double v = fmax(fmax(s[0][h], s[1][h]), fmax(s[2][h], s[3][h]));
+    v = fmax(v, __shfl_xor(v, 16));
+    v = fmax(v, __shfl_xor(v, 32));
+    mx[h] = v;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < HB; ++h) s_mx[it & 1][wave][h] = mx[h];
+  }
+  __syncthreads();
+  double mn[HB];
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    const double t = fmax(fmax(s_mx[it & 1][0][h], s_mx[it & 1][1][h]),
+                          fmax(s_mx[it & 1][2][h], s_mx[it & 1][3][h]));
+    mn[h] = fmax(m[h], t);
+  }
+  // every tile of the loop holds at least one valid token, so mn is finite here
+  // lane dl < 4*HB evaluates exponential (u, h) = (dl / HB, dl % HB)
+  double arg = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int h = 0; h < HB; ++h)
+      if (dl == u * HB + h) arg = s[u][h] - mn[h];
+  const double ev = arg == -INFINITY ? 0.0 : exp(arg);
+  double pe[4][HB];
+  share_all<HB>(ev, pe, std::make_integer_sequence<int, 16>{});
+  if (it > 0) {  // rescale the running sums (the first tile starts from zero)
+#pragma unroll
+    for (int h = 0; h < HB; ++h) {
+      const double c = m[h] == -INFINITY ? 0.0 : exp(m[h] - mn[h]);
+      l[h] *= c;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[h][j] *= c;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    l[h] += (pe[0][h] + pe[1][h]) + (pe[2][h] + pe[3][h]);
+    m[h] = mn[h];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    double vf[8];
+    unpack8d(vr[u], vf);
+#pragma unroll
+    for (int h = 0; h < HB; ++h)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[h][j] = fma(pe[u][h], vf[j], o[h][j]);
+  }
+}
+
+// The end of the exact core: the 16 token rows of a workgroup (4 per wavefront) hold partial sums
+// under the same offsets m, so they add. For every (head oh, dim od) of the HB heads the
+// workgroup's unnormalised output O, its sum L and maximum M go to emit(oh, od, O, L, M), called
+// once per pair by one thread.
+template <int HB, class Emit>
+IRON_DEV void attn_finish_f64(const double (&m)[HB], const double (&l)[HB],
+                              const double (&o)[HB][8], int wave, int row, int dl, Emit emit) {
+  __shared__ double s_o[16][HB][kAttnD];
+  __shared__ double s_l[16][HB];
+  const int rr = wave * 4 + row;
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+#pragma unroll
+    for (int j = 0; j < 8; j += 2)
+      *(double2*)&s_o[rr][h][dl * 8 + j] = make_double2(o[h][j], o[h][j + 1]);
+    if (dl == 0) s_l[rr][h] = l[h];
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < HB * kAttnD; t += 256) {
+    const int oh = t / kAttnD, od = t % kAttnD;
+    double so[16], sl[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      so[r] = s_o[r][oh][od];
+      sl[r] = s_l[r][oh];
+    }
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int r = 0; r < w; ++r) {
+        so[r] += so[r + w];
+        sl[r] += sl[r + w];
+      }
+    const double O = so[0], L = sl[0];
+    double M = m[0];
+#pragma unroll
+    for (int h = 1; h < HB; ++h)
+      if (oh == h) M = m[h];
+    emit(oh, od, O, L, M);
+  }
+}
+
+}  // namespace dev
+}  // namespace iron

@@ -24,10 +24,11 @@ IRON_DEV float bf16lo_to_f32(uint32_t packed) { return __uint_as_float(packed <<
 IRON_DEV float bf16hi_to_f32(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
 
 IRON_DEV uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  // branch-free (a select, not a divergent branch, keeps the NaN case off the common path)
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x40u;
+  return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? qnan : rne);
 }
 IRON_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
@@ -46,6 +47,37 @@ IRON_DEV void split3_bf16(float v, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
 // fp64 -> bf16 goes through fp32 (RNE at each step), the conversion path torch uses for a
 // float64 tensor cast to bfloat16, so device results and the fp64 oracle round identically.
 IRON_DEV uint16_t f64_to_bf16(double d) { return f32_to_bf16((float)d); }
+
+// ---------------------------------------------------------------------------------------------
+// Loads and stores through the global address space. A pointer the compiler cannot trace to a
+// kernel argument (one read from device memory) is generic, and generic accesses compile to FLAT
+// instructions, whose completion waits the compiler can only place as vmcnt(0). These helpers make
+// the access a global one, counted in order with the other vector memory operations.
+// ---------------------------------------------------------------------------------------------
+template <class T>
+IRON_DEV T ld_global(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+
+template <class T>
+IRON_DEV void st_global(T* p, const T& v) {
+  *(__attribute__((address_space(1))) T*)p = v;
+}
+
+// 16-byte accesses go through a native vector type: HIP's uint4 copies through a generic `this`.
+typedef unsigned int iron_u32x4 __attribute__((ext_vector_type(4)));
+
+template <>
+IRON_DEV uint4 ld_global<uint4>(const uint4* p) {
+  const iron_u32x4 v = *(const __attribute__((address_space(1))) iron_u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <>
+IRON_DEV void st_global<uint4>(uint4* p, const uint4& v) {
+  const iron_u32x4 u = {v.x, v.y, v.z, v.w};
+  *(__attribute__((address_space(1))) iron_u32x4*)p = u;
+}
 
 // ---------------------------------------------------------------------------------------------
 // Wavefront reductions (wave64) with DPP.

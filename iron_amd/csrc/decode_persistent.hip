@@ -1,0 +1,984 @@
+// Persistent whole-token decode for batch 1: one kernel launch runs every layer of a Qwen3 decode
+// step -- per layer the fused QKV head (RMSNorm, QKV GEMV, QK-norm, RoPE, KV append), split-K
+// decode attention and its merge, and the fused MLP (Wo, residual, RMSNorm, gate/up, SiLU*mul,
+// down, residual) -- with the arithmetic of the standalone kernels (exact fp64 accumulation, the
+// reference's bf16 / fp32 boundaries), so its results equal theirs.
+//
+// Reference: the per-token runlist of Qwen3NPU (iron/applications/qwen3_0.6b/qwen3_npu_int8.py:
+// 249-281), which the reference runs as one NPU dispatch (iron/common/sequence.py:270-559); the
+// operators are QKVHeadDataParallelOurs (qkv_head_dp/op_ours.py:31-262), DecodeAttention
+// (decode_attn/op.py:20-181) and SwiGLUMLPDataParallelOurs with fuse_o (swiglu_mlp_dp/
+// op_ours.py:46-582). Goldens: qkv_head_dp/reference.py:13-33, decode_attn/reference.py:26-38,
+// swiglu_mlp_dp/reference.py:8-67.
+//
+// Why one kernel: at batch 1 every operator is a short dependent chain (a 2-26 KiB weight slice
+// per CU, then a reduction), so kernel boundaries and the activation round trip behind each launch
+// dominate the token. Here the grid stays resident and hands activations from phase to phase
+// through device memory, and each phase's weights (or K/V tile) are loaded before its input is
+// awaited, so the weight stream overlaps the hand-off instead of following it.
+//
+// Grid: 256 workgroups of 256 threads, one per CU (the whole register file per wavefront). Each
+// runs the six phases of every layer in order: QKV (A), attention (B), split merge (C), Wo (D),
+// gate/up (E), down (F). A phase first issues its weight (or K/V) loads, then waits for its input
+// words, so the weight stream overlaps the hand-off from the previous phase.
+//
+// Hand-off: every activation word is a 64-bit {tag, payload} pair written with one agent-scope
+// atomic store and read with agent-scope atomic loads; a consumer waits until the tag of each
+// word it needs equals the producing phase's tag (epoch, layer, phase). No counter, fence or
+// cache flush is involved: a 64-bit atomic is seen whole or not at all. The epoch (control word
+// 0 of the workspace) advances once per launch, so words of an earlier token never match.
+// Every wait is bounded: a word that does not arrive within kSpinLimit polls sets control word 1
+// and the workgroup stops; waiting workgroups also stop once they see that word set, so the grid
+// drains within about one spin limit (the caller then reports the error).
+//
+// Buffer reuse is safe because each phase consumes ALL of an earlier phase's words (the RMSNorm
+// of x, the Wo / down inputs, the split merge), so a word is only rewritten after every reader of
+// its previous value has finished.
+#include "attn_core.h"
+#include "common.h"
+#include "gemv_core.h"
+#include "internal.h"
+
+namespace {
+
+using namespace iron::dev;
+
+constexpr int kNT = 256;                     // workgroups (one per CU of an MI355X)
+constexpr int kPhases = 6;                   // phases per layer
+constexpr long long kSpinLimit = 1ll << 18;  // polls of one word before a wait fails (~0.3 s)
+// s_waitcnt immediate: vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding)
+constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);
+
+constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+template <int D_, int FF_, int HQ_, int HKV_>
+struct Shape {
+  static constexpr int D = D_, FF = FF_, HQ = HQ_, HKV = HKV_, HD = kAttnD;
+  static constexpr int QD = HQ * HD, KVD = HKV * HD, MQKV = QD + 2 * KVD;
+  static constexpr int WAVES = kNT * 4;             // wavefronts in the grid
+  static constexpr int HB = HQ / HKV;               // query heads per KV head
+  static constexpr int NS = kNT / HKV;              // attention splits per KV head
+  static constexpr int MERGE_PER = HQ * HD / kNT;   // attention outputs merged per workgroup
+  // rows per wavefront (R*) and 1024-wide chunks per row (C*) of each GEMV phase
+  static constexpr int RA = cdiv(MQKV, WAVES), CA = cdiv(D, 1024);
+  static constexpr int RD = cdiv(D, WAVES), CD = cdiv(QD, 1024);
+  static constexpr int RE = cdiv(FF, WAVES), CE = cdiv(D, 1024);
+  static constexpr int RF = cdiv(D, WAVES), CF = cdiv(FF, 1024);
+  static constexpr int MERGE_WPS = 2 * MERGE_PER + 4;  // words per split: o[PER], m, l as fp64
+  // LDS words of the widest phase input
+  static constexpr int LDS_WORDS =
+      cmax(cmax(D, QD / 2), cmax(FF + 4 * RF, cmax(NS * MERGE_WPS, (HB + 2) * 64)));
+  static constexpr int RMAX = cmax(cmax(RA, RD), RF);
+
+  static_assert(HQ % HKV == 0 && (HB == 1 || HB == 2 || HB == 4), "GQA group must be 1, 2 or 4");
+  static_assert(kNT % HKV == 0 && NS <= 256, "splits per KV head");
+  static_assert(kNT * MERGE_PER == HQ * HD && MERGE_PER >= 2 && MERGE_PER % 2 == 0 &&
+                    HD % MERGE_PER == 0, "merge slices");
+  static_assert(D % 16 == 0 && FF % 16 == 0 && MQKV % 2 == 0, "GEMV widths");
+};
+
+using ShapeQwen3_0_6B = Shape<1024, 3072, 16, 8>;
+using ShapeTiny = Shape<256, 768, 4, 2>;
+
+struct WireGeom {
+  int gshift, tile_m;
+  FastDiv tdiv;
+  uint32_t blk_bytes, xor_mask;
+};
+
+struct PParams {
+  const iron_layer_desc* layers;
+  int n_layers, max_seq;
+  WireGeom g_qkv, g_o, g_gu, g_d;
+  const uint16_t* x_in;   // bf16 [D]: the current token's embedding row
+  uint16_t* x_out;        // bf16 [D]: the last layer's output
+  const int32_t* pos;     // device int32: the current position
+  const uint16_t* ang;    // bf16 [HD]: the position's interleaved (cos, sin) row
+  long long kv_sh, kv_st;
+  float eps;
+  double scale;
+  unsigned long long *X, *RAW, *PART, *ATT, *AO, *GH;  // tagged hand-off buffers
+  uint32_t* ctrl;         // [0] epoch, [1] error flags
+};
+
+IRON_DEV GemvParams gemv_of(const WireGeom& g, const void* w, int M, int K) {
+  GemvParams p = {};
+  p.w = (const uint8_t*)w;
+  p.M = M;
+  p.K = K;
+  p.gshift = g.gshift;
+  p.tile_m = g.tile_m;
+  p.tdiv = g.tdiv;
+  p.blk_bytes = g.blk_bytes;
+  p.xor_mask = g.xor_mask;
+  return p;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Tagged words
+// ---------------------------------------------------------------------------------------------
+IRON_DEV uint32_t phase_tag(uint32_t epoch, int n_layers, int layer, int phase) {
+  const unsigned long long v = (unsigned long long)epoch * (unsigned long long)(kPhases * n_layers) +
+                               (unsigned long long)(kPhases * layer + phase);
+  return (uint32_t)(v % 0xffffffffull) + 1u;  // never 0, the value of a cleared word
+}
+
+IRON_DEV void put_word(unsigned long long* dst, uint32_t payload, uint32_t tag) {
+  __hip_atomic_store(dst, ((unsigned long long)tag << 32) | payload, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+IRON_DEV void put_double(unsigned long long* dst, double v, uint32_t tag) {
+  put_word(dst, (uint32_t)__double2loint(v), tag);
+  put_word(dst + 1, (uint32_t)__double2hiint(v), tag);
+}
+
+IRON_DEV double word_double(uint32_t lo, uint32_t hi) {
+  return __hiloint2double((int)hi, (int)lo);
+}
+
+// Waits for n tagged words and puts their payloads in LDS. Thread t owns slots j = t + 256 k < n;
+// src(j, tag) names slot j's word and the tag it must carry; the payload goes to dst[j]. A thread
+// re-reads its pending words together each round.
+//
+// With n_sent > 0, thread t < n_sent first polls only sent(t, tag), the word its producer writes
+// last, so the full read usually finds every word present on its first pass and the polling
+// traffic of a wide input stays at one word per producer.
+//
+// `issue` runs once in every thread, right after its first poll loads are issued: the caller
+// issues the weight loads of a later phase there. Loads complete in issue order, so the poll's
+// first answer does not wait for them, and they stream while this phase waits for its input.
+//
+// Returns false (workgroup-uniform) if a word did not arrive within kSpinLimit rounds (or another
+// workgroup has already failed), after raising the error flag. Starts and ends with a workgroup
+// barrier.
+template <int NPT, class Src, class Sent, class Issue>
+IRON_DEV bool gather_words(int n, Src src, int n_sent, Sent sent, Issue issue, uint32_t* dst,
+                           uint32_t* err) {
+  __syncthreads();  // the previous phase's LDS reads are done before dst is rewritten
+  // Every load issued so far (this phase's weights, issued a phase or two ago) completes here,
+  // before the poll and the `issue` loads: the compiler then knows those registers are ready and
+  // places no wait on them in this phase's compute, which would otherwise also wait for the
+  // younger `issue` loads (vector loads complete in order).
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  bool issued = false;
+  auto issue_once = [&]() {
+    if (!issued) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue();
+      __builtin_amdgcn_sched_barrier(0);
+      issued = true;
+    }
+  };
+  auto gave_up = [&](long long spins) {
+    return spins >= kSpinLimit ||
+           ((spins & 255) == 255 &&
+            __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u);
+  };
+  bool missing = false;
+  if (n_sent > 0) {
+    const bool has = (int)threadIdx.x < n_sent;
+    uint32_t want = 0;
+    unsigned long long* sp = has ? sent((int)threadIdx.x, want) : nullptr;
+    for (long long spins = 0;; ++spins) {
+      unsigned long long w = 0;
+      if (has) w = __hip_atomic_load(sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      issue_once();
+      missing = has && (uint32_t)(w >> 32) != want;
+      if (!missing || gave_up(spins)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (missing) atomicOr(err, 1u);
+    if (__syncthreads_or(missing ? 1 : 0)) return false;
+  }
+  bool pending[NPT];
+  unsigned long long* ptr[NPT];
+  uint32_t want[NPT];
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    const int j = threadIdx.x + 256 * k;
+    pending[k] = j < n;
+    ptr[k] = pending[k] ? src(j, want[k]) : nullptr;
+  }
+  for (long long spins = 0;; ++spins) {
+    unsigned long long w[NPT];
+#pragma unroll
+    for (int k = 0; k < NPT; ++k)
+      if (pending[k]) w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    issue_once();
+    missing = false;
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+      if (!pending[k]) continue;
+      if ((uint32_t)(w[k] >> 32) == want[k]) {
+        dst[threadIdx.x + 256 * k] = (uint32_t)w[k];
+        pending[k] = false;
+      } else {
+        missing = true;
+      }
+    }
+    if (!missing || gave_up(spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (missing) atomicOr(err, 1u);
+  return __syncthreads_or(missing ? 1 : 0) == 0;
+}
+
+// No sentinel stage.
+struct NoSentinel {
+  IRON_DEV unsigned long long* operator()(int, uint32_t&) const { return nullptr; }
+};
+
+// Plain bf16 pairs (the embedding row written by an earlier kernel) into LDS words [0, n).
+IRON_DEV void copy_words(const uint16_t* src, int n, uint32_t* dst) {
+  __syncthreads();
+  for (int j = threadIdx.x; j < n; j += 256) dst[j] = ((const uint32_t*)src)[j];
+}
+
+// This lane's activation slices from LDS, in the layout load_x_lane produces from global memory:
+// bf16 elements [c*1024 + 16 lane, +16) as two uint4, or fp32 ones as four.
+template <int NCH>
+IRON_DEV void lane_bf16(const uint32_t* s, int K, int lane, uint4 (&xl)[NCH][4]) {
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e = c * 1024 + lane * 16;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) xl[c][u] = make_uint4(0u, 0u, 0u, 0u);
+    if (e < K) {
+      xl[c][0] = ((const uint4*)s)[e / 8];
+      xl[c][1] = ((const uint4*)s)[e / 8 + 1];
+    }
+  }
+}
+
+template <int NCH>
+IRON_DEV void lane_f32(const uint32_t* s, int K, int lane, uint4 (&xl)[NCH][4]) {
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e = c * 1024 + lane * 16;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      xl[c][u] = e < K ? ((const uint4*)s)[e / 4 + u] : make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// A norm weight's slices for this lane (bf16 [K], elements [c*1024 + 16 lane, +16)).
+template <int NCH>
+IRON_DEV void lane_weight(const uint16_t* w, int K, int lane, uint4 (&nw)[NCH][2]) {
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int e = c * 1024 + lane * 16;
+    const int ec = e < K ? e : 0;
+    nw[c][0] = ld_global((const uint4*)(w + ec));
+    nw[c][1] = ld_global((const uint4*)(w + ec + 8));
+  }
+}
+
+// bf16 outputs of R rows per wavefront: the workgroup's 4R consecutive rows go out as tagged
+// pairs (rows 4R wg + 2t, +1). `res` (optional): also written as plain bf16 pairs.
+template <int R>
+IRON_DEV void store_bf16_pairs(const uint16_t (&h)[R], int wg, int M, unsigned long long* dst,
+                               uint32_t tag, uint16_t* s_out, uint16_t* plain) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane < R) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (lane == r) s_out[wave * R + r] = h[r];
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < 2 * R) {
+    const int row = wg * 4 * R + 2 * t;
+    if (row < M) {
+      const uint32_t pair = (uint32_t)s_out[2 * t] | ((uint32_t)s_out[2 * t + 1] << 16);
+      put_word(dst + row / 2, pair, tag);
+      if (plain) ((uint32_t*)plain)[row / 2] = pair;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Register-resident prefetches: the weight slices (or first K/V tile) a phase multiplies, loaded
+// one or two phases before the phase runs.
+// ---------------------------------------------------------------------------------------------
+template <int R, int NCH>
+struct W8 {
+  uint4 w[R][NCH];
+  uint32_t sc[R][NCH];
+};
+
+template <class S>
+IRON_DEV int row0_of(int wg, int R) {
+  return (wg * 4 + (int)(threadIdx.x >> 6)) * R;
+}
+
+template <class S>
+IRON_DEV void prefetch_qkv(const PParams& p, const iron_layer_desc& L, int wg,
+                           W8<S::RA, S::CA>& W, uint4 (&nw)[S::CA][2]) {
+  const GemvParams g = gemv_of(p.g_qkv, L.wqkv, S::MQKV, S::D);
+  fetch_w8<S::RA, S::CA>(g, g.w, row0_of<S>(wg, S::RA), threadIdx.x & 63, W.w, W.sc);
+  lane_weight<S::CA>(L.n_in, S::D, threadIdx.x & 63, nw);
+}
+
+// The first K/V tile of this workgroup's split and the QKV epilogue's constants.
+struct KVPrefetch {
+  uint4 kr[4], vr[4];
+  uint4 nq, nk, a0, a1;
+};
+
+template <class S>
+IRON_DEV void load_kv_rows(const PParams& p, const iron_layer_desc& L, int kv, int t0, int ctx,
+                           uint4 (&kr)[4], uint4 (&vr)[4]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, row = lane >> 4, dl = lane & 15;
+  const size_t base = (size_t)kv * p.kv_sh + dl * 8;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    int t = t0 + u * 16 + wave * 4 + row;
+    t = t < ctx ? t : ctx - 1;  // rows past the context are masked where they are used
+    kr[u] = ld_global((const uint4*)(L.k_cache + base + (size_t)t * p.kv_st));
+    vr[u] = ld_global((const uint4*)(L.v_cache + base + (size_t)t * p.kv_st));
+  }
+}
+
+IRON_DEV int context_of(const PParams& p, int pos) {
+  const int ctx = pos + 1;
+  return ctx < 0 ? 0 : (ctx > p.max_seq ? p.max_seq : ctx);
+}
+
+template <class S>
+IRON_DEV void prefetch_attn(const PParams& p, const iron_layer_desc& L, int wg, int pos,
+                            KVPrefetch& kv) {
+  const int head = wg / S::NS, split = wg % S::NS, dl = threadIdx.x & 15;
+  const int ctx = context_of(p, pos);
+  if (split * kAttnTile < ctx) load_kv_rows<S>(p, L, head, split * kAttnTile, ctx, kv.kr, kv.vr);
+  kv.nq = ld_global((const uint4*)(L.n_qn + dl * 8));
+  kv.nk = ld_global((const uint4*)(L.n_kn + dl * 8));
+  const uint16_t* arow = p.ang + 16 * (dl & 7);
+  kv.a0 = ld_global((const uint4*)arow);
+  kv.a1 = ld_global((const uint4*)(arow + 8));
+}
+
+template <class S>
+IRON_DEV void prefetch_wo(const PParams& p, const iron_layer_desc& L, int wg, W8<S::RD, S::CD>& W) {
+  const GemvParams g = gemv_of(p.g_o, L.wo, S::D, S::QD);
+  fetch_w8<S::RD, S::CD>(g, g.w, row0_of<S>(wg, S::RD), threadIdx.x & 63, W.w, W.sc);
+}
+
+template <class S>
+IRON_DEV void prefetch_gateup(const PParams& p, const iron_layer_desc& L, int wg,
+                              W8<S::RE, S::CE>& Wg, W8<S::RE, S::CE>& Wu,
+                              uint4 (&nw)[S::CE][2]) {
+  const GemvParams g = gemv_of(p.g_gu, L.wg, S::FF, S::D);
+  const int row0 = row0_of<S>(wg, S::RE), lane = threadIdx.x & 63;
+  fetch_w8<S::RE, S::CE>(g, (const uint8_t*)L.wg, row0, lane, Wg.w, Wg.sc);
+  fetch_w8<S::RE, S::CE>(g, (const uint8_t*)L.wu, row0, lane, Wu.w, Wu.sc);
+  lane_weight<S::CE>(L.n_post, S::D, lane, nw);
+}
+
+template <class S>
+IRON_DEV void prefetch_down(const PParams& p, const iron_layer_desc& L, int wg,
+                            W8<S::RF, S::CF>& W) {
+  const GemvParams g = gemv_of(p.g_d, L.wd, S::D, S::FF);
+  fetch_w8<S::RF, S::CF>(g, g.w, row0_of<S>(wg, S::RF), threadIdx.x & 63, W.w, W.sc);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Phase A: raw = bf16(Wqkv . bf16(RMSNorm(x) * n_in))                [MQKV rows x D]
+// ---------------------------------------------------------------------------------------------
+template <class S, class Issue>
+IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s_in,
+                        uint16_t* s_out, const W8<S::RA, S::CA>& W,
+                        const uint4 (&nwl)[S::CA][2], Issue issue) {
+  constexpr int R = S::RA, NCH = S::CA;
+  const int lane = threadIdx.x & 63;
+  const int row0 = row0_of<S>(wg, R);
+  GemvParams g = gemv_of(p.g_qkv, nullptr, S::MQKV, S::D);
+  g.pro = PRO_RMS_BF16;
+  g.eps = p.eps;
+  if (l == 0) {
+    copy_words(p.x_in, S::D / 2, s_in);
+    issue();
+    __syncthreads();
+  } else {
+    const uint32_t tx = phase_tag(ep, p.n_layers, l - 1, 5);
+    auto src = [&](int j, uint32_t& t) { t = tx; return p.X + j; };
+    if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src, 0, NoSentinel(), issue, s_in,
+                                           p.ctrl + 1))
+      return false;
+  }
+  uint4 xl[NCH][4], x2l[NCH][2] = {};
+  lane_bf16<NCH>(s_in, S::D, lane, xl);
+  float xf[NCH][16];
+  prologue_lane<NCH, 16>(g, lane, xl, x2l, nwl, xf);
+  double acc[R][1];
+  dot_w8_lane<R, NCH>(g, W.w, W.sc, xf, row0, lane, acc);
+  uint16_t h[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) h[r] = f64_to_bf16(acc[r][0]);
+  store_bf16_pairs<R>(h, wg, S::MQKV, p.RAW, phase_tag(ep, p.n_layers, l, 0), s_out, nullptr);
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Phase B: the QKV epilogue and the exact attention core over this split's tiles. Workgroup
+// (kv, split) handles 64-token tiles split, split + NS, ... of KV head kv and writes its partial
+// (o unnormalised, m, l) of the HB query heads as tagged fp64 words.
+// ---------------------------------------------------------------------------------------------
+template <class S, class Issue>
+IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int wg, uint32_t ep,
+                         int pos, uint32_t* s_in, KVPrefetch& kv, Issue issue) {
+  constexpr int HB = S::HB, NS = S::NS;
+  const int head = wg / NS, split = wg % NS;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, row = lane >> 4, dl = lane & 15;
+  const bool pos_ok = pos >= 0 && pos < p.max_seq;
+  const int ctx = context_of(p, pos);
+  const int ntile = (ctx + kAttnTile - 1) / kAttnTile;
+
+  // the raw q rows of heads head*HB.., and the raw k and v rows of KV head `head`
+  {
+    constexpr int n = (HB + 2) * 64;
+    const uint32_t tr = phase_tag(ep, p.n_layers, l, 0);
+    auto src = [&](int j, uint32_t& t) {
+      t = tr;
+      const int seg = j >> 6, off = j & 63;
+      const int base = seg < HB ? (head * HB + seg) * 64
+                                : (seg == HB ? (S::QD + head * S::HD) / 2
+                                             : (S::QD + S::KVD + head * S::HD) / 2);
+      return p.RAW + base + off;
+    };
+    if (!gather_words<cdiv(n, 256)>(n, src, 0, NoSentinel(), issue, s_in, p.ctrl + 1))
+      return false;
+  }
+  const uint4* s_raw = (const uint4*)s_in;  // segment seg: 16 uint4 (128 bf16)
+
+  // QK RMSNorm + RoPE: wave h < HB rotates query head h; wave HB % 4 builds the current token's
+  // K row (V unchanged) when this split owns its tile, and appends both to the caches
+  __shared__ uint4 s_q[HB][16];
+  __shared__ uint4 s_new[2][16];
+  const bool has_new = pos_ok && (pos / kAttnTile) % NS == split;
+  if (wave < HB) {
+    double qn[8];
+    norm_rope8(s_raw[wave * 16 + dl], kv.nq, kv.a0, kv.a1, dl, (double)p.eps, qn);
+    if (row == 0) s_q[wave][dl] = pack8_bf16(qn);
+  }
+  if (has_new && wave == HB % 4) {
+    double kn[8];
+    norm_rope8(s_raw[HB * 16 + dl], kv.nk, kv.a0, kv.a1, dl, (double)p.eps, kn);
+    const uint4 kp = pack8_bf16(kn);
+    const uint4 vp = s_raw[(HB + 1) * 16 + dl];
+    if (row == 0) {
+      s_new[0][dl] = kp;
+      s_new[1][dl] = vp;
+      const size_t at = (size_t)head * p.kv_sh + (size_t)pos * p.kv_st + dl * 8;
+      st_global((uint4*)(L.k_cache + at), kp);
+      st_global((uint4*)(L.v_cache + at), vp);
+    }
+  }
+  __syncthreads();
+
+  double qf[HB][8];
+#pragma unroll
+  for (int h = 0; h < HB; ++h) unpack8d(s_q[h][dl], qf[h]);
+  double m[HB], lsum[HB], o[HB][8];
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    m[h] = -INFINITY;
+    lsum[h] = 0.0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[h][j] = 0.0;
+  }
+  __shared__ double s_mx[2][4][HB];
+  int it = 0;
+  for (int tile = split; tile < ntile; tile += NS, ++it) {
+    if (it > 0) load_kv_rows<S>(p, L, head, tile * kAttnTile, ctx, kv.kr, kv.vr);
+    attn_tile_f64<HB, true>(kv.kr, kv.vr, tile * kAttnTile, ctx, has_new, pos, s_new, qf,
+                            p.scale, it, m, lsum, o, s_mx, wave, lane, row, dl);
+  }
+  const uint32_t tp = phase_tag(ep, p.n_layers, l, 1);
+  attn_finish_f64<HB>(m, lsum, o, wave, row, dl,
+                      [&](int oh, int od, double O, double Ls, double M) {
+    unsigned long long* part =
+        p.PART + ((size_t)(head * HB + oh) * NS + split) * (2 * (kAttnD + 2));
+    put_double(part + 2 * od, O, tp);
+    if (od == 0) {
+      put_double(part + 2 * kAttnD, M, tp);
+      put_double(part + 2 * (kAttnD + 1), Ls, tp);
+    }
+  });
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Phase C: merge the NS splits of MERGE_PER attention outputs (one head, consecutive dims):
+// o = sum_s f_s O_s / sum_s f_s L_s with f_s = e^(m_s - max m), evaluated in fp64.
+// ---------------------------------------------------------------------------------------------
+template <class S, class Issue>
+IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s_in,
+                          Issue issue) {
+  constexpr int PER = S::MERGE_PER, NS = S::NS, WPS = S::MERGE_WPS;
+  const int o0 = wg * PER, h = o0 / kAttnD, d0 = o0 % kAttnD;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  {
+    constexpr int n = NS * WPS;
+    const uint32_t tp = phase_tag(ep, p.n_layers, l, 1);
+    auto part_of = [&](int s) { return p.PART + ((size_t)h * NS + s) * (2 * (kAttnD + 2)); };
+    auto src = [&](int j, uint32_t& t) {
+      t = tp;
+      const int s = j / WPS, k = j % WPS;
+      unsigned long long* part = part_of(s);
+      return k < 2 * PER ? part + 2 * d0 + k : part + 2 * kAttnD + (k - 2 * PER);
+    };
+    // a split's partial ends with the high word of its sum l
+    auto sent = [&](int s, uint32_t& t) { t = tp; return part_of(s) + 2 * (kAttnD + 1) + 1; };
+    if (!gather_words<cdiv(n, 256)>(n, src, NS, sent, issue, s_in, p.ctrl + 1)) return false;
+  }
+  // thread t < NS holds split t
+  const int t = threadIdx.x;
+  double ms = -INFINITY, ls = 0.0, os[PER];
+#pragma unroll
+  for (int d = 0; d < PER; ++d) os[d] = 0.0;
+  if (t < NS) {
+    const uint32_t* w = s_in + t * WPS;
+#pragma unroll
+    for (int d = 0; d < PER; ++d) os[d] = word_double(w[2 * d], w[2 * d + 1]);
+    ms = word_double(w[2 * PER], w[2 * PER + 1]);
+    ls = word_double(w[2 * PER + 2], w[2 * PER + 3]);
+  }
+  __shared__ double s_red[4][PER + 1];
+  double mx = row16_max_d(ms);
+  mx = fmax(mx, __shfl_xor(mx, 16));
+  mx = fmax(mx, __shfl_xor(mx, 32));
+  if (lane == 0) s_red[wave][0] = mx;
+  __syncthreads();
+  const double M = fmax(fmax(s_red[0][0], s_red[1][0]), fmax(s_red[2][0], s_red[3][0]));
+  __syncthreads();
+  const double f = (M == -INFINITY || ms == -INFINITY) ? 0.0 : exp(ms - M);
+  double v[PER + 1];
+  v[0] = f * ls;
+#pragma unroll
+  for (int d = 0; d < PER; ++d) v[d + 1] = f * os[d];
+#pragma unroll
+  for (int k = 0; k <= PER; ++k) v[k] = wave_sum_d(v[k]);
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k <= PER; ++k) s_red[wave][k] = v[k];
+  }
+  __syncthreads();
+  if (t < PER / 2) {
+    auto total = [&](int k) {
+      return (s_red[0][k] + s_red[1][k]) + (s_red[2][k] + s_red[3][k]);
+    };
+    const double Lt = total(0);
+    const double O0 = total(1 + 2 * t), O1 = total(2 + 2 * t);
+    const uint16_t r0 = f64_to_bf16(Lt > 0.0 ? O0 / Lt : 0.0);
+    const uint16_t r1 = f64_to_bf16(Lt > 0.0 ? O1 / Lt : 0.0);
+    put_word(p.ATT + (h * kAttnD + d0) / 2 + t, (uint32_t)r0 | ((uint32_t)r1 << 16),
+             phase_tag(ep, p.n_layers, l, 2));
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Phase D: a = bf16(Wo . attn)                                        [D rows x QD]
+// ---------------------------------------------------------------------------------------------
+template <class S, class Issue>
+IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s_in,
+                       uint16_t* s_out, const W8<S::RD, S::CD>& W, Issue issue) {
+  constexpr int R = S::RD, NCH = S::CD;
+  const int lane = threadIdx.x & 63;
+  const int row0 = row0_of<S>(wg, R);
+  GemvParams g = gemv_of(p.g_o, nullptr, S::D, S::QD);
+  g.pro = PRO_BF16;
+  {
+    const uint32_t ta = phase_tag(ep, p.n_layers, l, 2);
+    auto src = [&](int j, uint32_t& t) { t = ta; return p.ATT + j; };
+    if (!gather_words<cdiv(S::QD / 2, 256)>(S::QD / 2, src, 0, NoSentinel(), issue, s_in,
+                                            p.ctrl + 1))
+      return false;
+  }
+  uint4 xl[NCH][4], x2l[NCH][2] = {}, nwl[NCH][2] = {};
+  lane_bf16<NCH>(s_in, S::QD, lane, xl);
+  float xf[NCH][16];
+  prologue_lane<NCH, 16>(g, lane, xl, x2l, nwl, xf);
+  double acc[R][1];
+  dot_w8_lane<R, NCH>(g, W.w, W.sc, xf, row0, lane, acc);
+  uint16_t h[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) h[r] = f64_to_bf16(acc[r][0]);
+  store_bf16_pairs<R>(h, wg, S::D, p.AO, phase_tag(ep, p.n_layers, l, 3), s_out, nullptr);
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Phase E: x1 = f32(x + a); hf = f32(RMSNorm(x1) * n_post);
+//          gh = f32(silu(Wg . hf) * (Wu . hf))                        [FF rows x D, two matrices]
+// ---------------------------------------------------------------------------------------------
+template <class S, class Issue>
+IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s_in,
+                           float* s_gh, const W8<S::RE, S::CE>& Wg, const W8<S::RE, S::CE>& Wu,
+                           const uint4 (&nwl)[S::CE][2], Issue issue) {
+  constexpr int R = S::RE, NCH = S::CE;
+  const int lane = threadIdx.x & 63;
+  const int row0 = row0_of<S>(wg, R);
+  GemvParams g = gemv_of(p.g_gu, nullptr, S::FF, S::D);
+  g.pro = PRO_RES_RMS_F32;
+  g.eps = p.eps;
+  g.x2 = (const uint16_t*)p.AO;  // marks the residual term (read from LDS here)
+  {
+    // words [0, D/2): x; [D/2, D): a
+    constexpr int half = S::D / 2;
+    const uint32_t tx = phase_tag(ep, p.n_layers, l - 1, 5), ta = phase_tag(ep, p.n_layers, l, 3);
+    if (l == 0) {
+      copy_words(p.x_in, half, s_in);
+      auto src = [&](int j, uint32_t& t) { t = ta; return p.AO + j; };
+      if (!gather_words<cdiv(half, 256)>(half, src, 0, NoSentinel(), issue, s_in + half,
+                                         p.ctrl + 1))
+        return false;
+    } else {
+      auto src = [&](int j, uint32_t& t) {
+        t = j < half ? tx : ta;
+        return j < half ? p.X + j : p.AO + (j - half);
+      };
+      if (!gather_words<cdiv(S::D, 256)>(S::D, src, 0, NoSentinel(), issue, s_in, p.ctrl + 1))
+        return false;
+    }
+  }
+  uint4 xl[NCH][4], al[NCH][4], x2l[NCH][2];
+  lane_bf16<NCH>(s_in, S::D, lane, xl);
+  lane_bf16<NCH>(s_in + S::D / 2, S::D, lane, al);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    x2l[c][0] = al[c][0];
+    x2l[c][1] = al[c][1];
+  }
+  float xf[NCH][16];
+  prologue_lane<NCH, 16>(g, lane, xl, x2l, nwl, xf);
+  double acc[R][1], acc2[R][1];
+  dot_w8_lane<R, NCH>(g, Wg.w, Wg.sc, xf, row0, lane, acc);
+  dot_w8_lane<R, NCH>(g, Wu.w, Wu.sc, xf, row0, lane, acc2);
+  // the workgroup's 4R gh values leave together from wave 0 (the down phase polls the last one
+  // as the sentinel of the group)
+  const int wave = threadIdx.x >> 6;
+  if (lane < R) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (lane == r) s_gh[wave * R + r] = (float)silu_mul(acc[r][0], acc2[r][0]);
+  }
+  __syncthreads();
+  const int t = threadIdx.x, row = wg * 4 * R + t;
+  if (t < 4 * R && row < S::FF)
+    put_word(p.GH + row, __float_as_uint(s_gh[t]), phase_tag(ep, p.n_layers, l, 4));
+  return true;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Phase F: x' = bf16(f32(x + a) + Wd . gh)                            [D rows x FF]
+// ---------------------------------------------------------------------------------------------
+template <class S, class Issue>
+IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s_in,
+                         uint16_t* s_out, const W8<S::RF, S::CF>& W, Issue issue) {
+  constexpr int R = S::RF, NCH = S::CF;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row0 = row0_of<S>(wg, R);
+  GemvParams g = gemv_of(p.g_d, nullptr, S::D, S::FF);
+  g.pro = PRO_F32;
+  // LDS words [0, FF): gh; then a and x of this workgroup's 4R rows, 2R words each
+  constexpr int nres = 2 * R;
+  const int wrow = wg * nres;  // first word (row pair) of this workgroup's rows
+  {
+    const uint32_t tg = phase_tag(ep, p.n_layers, l, 4), ta = phase_tag(ep, p.n_layers, l, 3);
+    const uint32_t tx = phase_tag(ep, p.n_layers, l - 1, 5);
+    auto src = [&](int j, uint32_t& t) {
+      if (j < S::FF) {
+        t = tg;
+        return p.GH + j;
+      }
+      const int k = j - S::FF;
+      const int word = wrow + (k % nres);
+      const int wc = word < S::D / 2 ? word : 0;  // rows past D are never stored
+      t = k < nres ? ta : tx;
+      return (k < nres ? p.AO : p.X) + wc;
+    };
+    // gate/up workgroup q writes rows [4 RE q, 4 RE (q + 1)); its last row is the sentinel
+    constexpr int rows_e = 4 * S::RE;
+    constexpr int n_sent = cdiv(S::FF, rows_e) < kNT ? cdiv(S::FF, rows_e) : kNT;
+    auto sent = [&](int q, uint32_t& t) {
+      t = tg;
+      const int last = q * rows_e + rows_e - 1;
+      return p.GH + (last < S::FF ? last : S::FF - 1);
+    };
+    if (l == 0) {
+      // x is the embedding row, written by an earlier kernel
+      if (!gather_words<cdiv(S::FF + nres, 256)>(S::FF + nres, src, n_sent, sent, issue, s_in,
+                                                  p.ctrl + 1))
+        return false;
+      if (threadIdx.x < nres) {
+        const int word = wrow + threadIdx.x;
+        s_in[S::FF + nres + threadIdx.x] =
+            ((const uint32_t*)p.x_in)[word < S::D / 2 ? word : 0];
+      }
+      __syncthreads();
+    } else if (!gather_words<cdiv(S::FF + 2 * nres, 256)>(S::FF + 2 * nres, src, n_sent, sent,
+                                                             issue, s_in, p.ctrl + 1)) {
+      return false;
+    }
+  }
+  uint4 xl[NCH][4], x2l[NCH][2] = {}, nwl[NCH][2] = {};
+  lane_f32<NCH>(s_in, S::FF, lane, xl);
+  float xf[NCH][16];
+  prologue_lane<NCH, 16>(g, lane, xl, x2l, nwl, xf);
+  double acc[R][1];
+  dot_w8_lane<R, NCH>(g, W.w, W.sc, xf, row0, lane, acc);
+  const uint16_t* s_res = (const uint16_t*)(s_in + S::FF);  // a rows, then x rows (4R each)
+  uint16_t h[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int k = wave * R + r;  // row within the workgroup
+    const float x1 = bf16_to_f32(s_res[4 * R + k]) + bf16_to_f32(s_res[k]);
+    h[r] = f64_to_bf16((double)x1 + acc[r][0]);
+  }
+  store_bf16_pairs<R>(h, wg, S::D, p.X, phase_tag(ep, p.n_layers, l, 5), s_out,
+                      l == p.n_layers - 1 ? p.x_out : nullptr);
+  return true;
+}
+
+// Each phase's weights are issued from an earlier phase's wait (gather_words' `issue` hook):
+//   A waits -> B's first K/V tile;  B waits -> D's Wo;  C waits -> E's Wg/Wu;
+//   D waits -> F's Wd;  E waits -> the next layer's Wqkv.
+template <class S>
+__global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
+  __shared__ uint32_t s_in[S::LDS_WORDS];
+  __shared__ uint16_t s_out[4 * S::RMAX];
+  __shared__ float s_gh[4 * S::RE];
+  const int wg = blockIdx.x;
+  const uint32_t ep = p.ctrl[0];
+  const int pos = *p.pos;
+  W8<S::RA, S::CA> wqkv;
+  uint4 n_in[S::CA][2];
+  prefetch_qkv<S>(p, p.layers[0], wg, wqkv, n_in);
+  for (int l = 0; l < p.n_layers; ++l) {
+    const iron_layer_desc L = p.layers[l];
+    KVPrefetch kv;
+    W8<S::RD, S::CD> wo;
+    W8<S::RE, S::CE> wgate, wup;
+    uint4 n_post[S::CE][2];
+    W8<S::RF, S::CF> wdown;
+    const bool ok =
+        phase_qkv<S>(p, l, wg, ep, s_in, s_out, wqkv, n_in,
+                     [&]() { prefetch_attn<S>(p, L, wg, pos, kv); }) &&
+        phase_attn<S>(p, L, l, wg, ep, pos, s_in, kv, [&]() { prefetch_wo<S>(p, L, wg, wo); }) &&
+        phase_merge<S>(p, l, wg, ep, s_in,
+                       [&]() { prefetch_gateup<S>(p, L, wg, wgate, wup, n_post); }) &&
+        phase_wo<S>(p, l, wg, ep, s_in, s_out, wo, [&]() { prefetch_down<S>(p, L, wg, wdown); }) &&
+        phase_gateup<S>(p, l, wg, ep, s_in, s_gh, wgate, wup, n_post, [&]() {
+          if (l + 1 < p.n_layers) prefetch_qkv<S>(p, p.layers[l + 1], wg, wqkv, n_in);
+        }) &&
+        phase_down<S>(p, l, wg, ep, s_in, s_out, wdown, []() {});
+    if (!ok) break;
+  }
+  // Advance the epoch for the next launch. Workgroup 0 finishes only after every workgroup has
+  // contributed to the last layer, so every workgroup has read `ep` by now.
+  if (wg == 0 && threadIdx.x == 0) p.ctrl[0] = ep + 1u;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------------------------
+size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+struct Layout {
+  size_t ctrl, X, RAW, PART, ATT, AO, GH, total;
+};
+
+template <class S>
+Layout layout_of() {
+  Layout lo;
+  size_t off = 0;
+  auto take = [&](size_t words) {
+    const size_t at = off;
+    off += round256(words * 8);
+    return at;
+  };
+  lo.ctrl = take(32);
+  lo.X = take(S::D / 2);
+  lo.RAW = take(S::MQKV / 2);
+  lo.PART = take((size_t)S::HQ * S::NS * (S::HD + 2) * 2);
+  lo.ATT = take(S::QD / 2);
+  lo.AO = take(S::D / 2);
+  lo.GH = take(S::FF);
+  lo.total = off;
+  return lo;
+}
+
+enum ShapeId { SHAPE_NONE = 0, SHAPE_0_6B = 1, SHAPE_TINY = 2 };
+
+ShapeId shape_id(int D, int FF, int Hq, int Hkv, int HD) {
+  if (HD != kAttnD) return SHAPE_NONE;
+  if (D == ShapeQwen3_0_6B::D && FF == ShapeQwen3_0_6B::FF && Hq == ShapeQwen3_0_6B::HQ &&
+      Hkv == ShapeQwen3_0_6B::HKV)
+    return SHAPE_0_6B;
+  if (D == ShapeTiny::D && FF == ShapeTiny::FF && Hq == ShapeTiny::HQ && Hkv == ShapeTiny::HKV)
+    return SHAPE_TINY;
+  return SHAPE_NONE;
+}
+
+Layout layout_for(ShapeId id) {
+  return id == SHAPE_0_6B ? layout_of<ShapeQwen3_0_6B>() : layout_of<ShapeTiny>();
+}
+
+// The grid must be resident at once: kNT workgroups, one per CU of a kNT-CU device. Checked once
+// per device and shape.
+int device_check(ShapeId id, const char* fn) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return iron::fail(IRON_ERR_HIP, "%s: no current HIP device", fn);
+  static int cache[64][3];  // 0 unknown, 1 ok, -1 unsupported
+  if (dev < 0 || dev >= 64) return iron::fail(IRON_ERR_UNSUPPORTED, "%s: device %d", fn, dev);
+  int& c = cache[dev][id];
+  if (c == 0) {
+    int ncu = 0, nb = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return iron::fail(IRON_ERR_HIP, "%s: cannot query the CU count", fn);
+    hipError_t e = id == SHAPE_0_6B
+        ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &nb, decode_persistent_kernel<ShapeQwen3_0_6B>, 256, 0)
+        : hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_persistent_kernel<ShapeTiny>,
+                                                       256, 0);
+    if (e != hipSuccess) return iron::fail(IRON_ERR_HIP, "%s: occupancy query failed", fn);
+    c = (ncu == kNT && nb >= 1) ? 1 : -1;
+    if (c < 0)
+      return iron::fail(IRON_ERR_UNSUPPORTED,
+                        "%s: needs %d CUs holding a workgroup each (device has %d CUs, %d per CU)",
+                        fn, kNT, ncu, nb);
+  }
+  return c > 0 ? IRON_OK
+               : iron::fail(IRON_ERR_UNSUPPORTED, "%s: grid cannot be resident on device %d", fn,
+                            dev);
+}
+
+WireGeom geom(int K, int G, int tile_m, int domain) {
+  WireGeom g;
+  g.gshift = iron::ilog2(G);
+  g.tile_m = tile_m;
+  g.tdiv = make_fastdiv((uint32_t)tile_m);
+  g.blk_bytes = (uint32_t)iron::wire_block_bytes(K, G, tile_m);
+  g.xor_mask = domain == IRON_DOMAIN_BIASED ? 0x80808080u : 0u;
+  return g;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t iron_decode_persistent_workspace(int D, int FF, int Hq, int Hkv, int HD) {
+  const ShapeId id = shape_id(D, FF, Hq, Hkv, HD);
+  return id == SHAPE_NONE ? 0 : layout_for(id).total;
+}
+
+int iron_decode_persistent_supported(int D, int FF, int Hq, int Hkv, int HD) {
+  iron::clear_error();
+  const char* fn = "iron_decode_persistent_supported";
+  const ShapeId id = shape_id(D, FF, Hq, Hkv, HD);
+  if (id == SHAPE_NONE)
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: no persistent kernel for D=%d FF=%d Hq=%d "
+                      "Hkv=%d HD=%d", fn, D, FF, Hq, Hkv, HD);
+  return device_check(id, fn);
+}
+
+int iron_decode_persistent_check_layer(const iron_layer_desc* layer, int D, int FF, int Hq,
+                                       int Hkv, int HD, int G, int tile_qkv, int tile_o,
+                                       int tile_gu, int tile_d, int domain) {
+  iron::clear_error();
+  const char* fn = "iron_decode_persistent_check_layer";
+  if (!layer) return iron::fail(IRON_ERR_NULL, "%s: null descriptor", fn);
+  if (shape_id(D, FF, Hq, Hkv, HD) == SHAPE_NONE)
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: unsupported shape", fn);
+  const int QD = Hq * HD, MQKV = QD + 2 * Hkv * HD;
+  int st;
+  if ((st = iron::check_wire(fn, layer->wqkv, MQKV, D, G, tile_qkv, domain)) ||
+      (st = iron::check_wire(fn, layer->wo, D, QD, G, tile_o, domain)) ||
+      (st = iron::check_wire(fn, layer->wg, FF, D, G, tile_gu, domain)) ||
+      (st = iron::check_wire(fn, layer->wu, FF, D, G, tile_gu, domain)) ||
+      (st = iron::check_wire(fn, layer->wd, D, FF, G, tile_d, domain)))
+    return st;
+  if (!layer->n_in || !layer->n_post || !layer->n_qn || !layer->n_kn || !layer->k_cache ||
+      !layer->v_cache)
+    return iron::fail(IRON_ERR_NULL, "%s: null norm weight or cache", fn);
+  if (!iron::aligned(layer->n_in, 16) || !iron::aligned(layer->n_post, 16) ||
+      !iron::aligned(layer->n_qn, 16) || !iron::aligned(layer->n_kn, 16) ||
+      !iron::aligned(layer->k_cache, 16) || !iron::aligned(layer->v_cache, 16))
+    return iron::fail(IRON_ERR_ALIGN, "%s: norm weights and caches must be 16-byte aligned", fn);
+  return IRON_OK;
+}
+
+int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, int FF, int Hq,
+                           int Hkv, int HD, int max_seq, long long kv_sh, long long kv_st, int G,
+                           int tile_qkv, int tile_o, int tile_gu, int tile_d, int domain,
+                           const uint16_t* x_in, uint16_t* x_out, const int32_t* pos,
+                           const uint16_t* ang, float eps, float scale, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  iron::clear_error();
+  const char* fn = "iron_decode_persistent";
+  if (!layers || !x_in || !x_out || !pos || !ang)
+    return iron::fail(IRON_ERR_NULL, "%s: null pointer", fn);
+  const ShapeId id = shape_id(D, FF, Hq, Hkv, HD);
+  if (id == SHAPE_NONE)
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: no persistent kernel for D=%d FF=%d Hq=%d Hkv=%d "
+                      "HD=%d", fn, D, FF, Hq, Hkv, HD);
+  if (n_layers <= 0 || max_seq <= 0)
+    return iron::fail(IRON_ERR_SHAPE, "%s: n_layers=%d max_seq=%d", fn, n_layers, max_seq);
+  if (kv_st % 8 || kv_sh % 8 || kv_st < HD || kv_sh < (long long)max_seq * kv_st / 2)
+    return iron::fail(IRON_ERR_SHAPE, "%s: KV strides sh=%lld st=%lld", fn, kv_sh, kv_st);
+  const int QD = Hq * HD, MQKV = QD + 2 * Hkv * HD;
+  if (!iron::is_pow2(G) || G < 16 || D % G || FF % G || QD % G)
+    return iron::fail(IRON_ERR_SHAPE, "%s: group size %d", fn, G);
+  if (tile_qkv <= 0 || MQKV % tile_qkv || tile_o <= 0 || D % tile_o || tile_gu <= 0 ||
+      FF % tile_gu || tile_d <= 0 || D % tile_d)
+    return iron::fail(IRON_ERR_SHAPE, "%s: row-block heights must divide the row counts", fn);
+  if (domain != IRON_DOMAIN_SIGNED && domain != IRON_DOMAIN_BIASED)
+    return iron::fail(IRON_ERR_SHAPE, "%s: unknown payload domain %d", fn, domain);
+  if (!iron::aligned(x_in, 16) || !iron::aligned(x_out, 16) || !iron::aligned(ang, 16))
+    return iron::fail(IRON_ERR_ALIGN, "%s: x_in, x_out and ang must be 16-byte aligned", fn);
+  const Layout lo = layout_for(id);
+  if (!workspace || workspace_bytes < lo.total)
+    return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes,
+                      lo.total);
+  if (!iron::aligned(workspace, 256))
+    return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
+  int st = device_check(id, fn);
+  if (st) return st;
+  PParams p = {};
+  p.layers = layers;
+  p.n_layers = n_layers;
+  p.max_seq = max_seq;
+  p.g_qkv = geom(D, G, tile_qkv, domain);
+  p.g_o = geom(QD, G, tile_o, domain);
+  p.g_gu = geom(D, G, tile_gu, domain);
+  p.g_d = geom(FF, G, tile_d, domain);
+  p.x_in = x_in;
+  p.x_out = x_out;
+  p.pos = pos;
+  p.ang = ang;
+  p.kv_sh = kv_sh;
+  p.kv_st = kv_st;
+  p.eps = eps;
+  p.scale = (double)scale;
+  char* base = (char*)workspace;
+  p.ctrl = (uint32_t*)(base + lo.ctrl);
+  p.X = (unsigned long long*)(base + lo.X);
+  p.RAW = (unsigned long long*)(base + lo.RAW);
+  p.PART = (unsigned long long*)(base + lo.PART);
+  p.ATT = (unsigned long long*)(base + lo.ATT);
+  p.AO = (unsigned long long*)(base + lo.AO);
+  p.GH = (unsigned long long*)(base + lo.GH);
+  hipStream_t s = (hipStream_t)stream;
+  if (id == SHAPE_0_6B)
+    hipLaunchKernelGGL(decode_persistent_kernel<ShapeQwen3_0_6B>, dim3(kNT), dim3(256), 0, s,
+                       p);
+  else
+    hipLaunchKernelGGL(decode_persistent_kernel<ShapeTiny>, dim3(kNT), dim3(256), 0, s, p);
+  return iron::check_launch(fn);
+}
+
+}  // extern "C"

@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iron_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.iron_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_wire_bytes(lib):
@@ -111,3 +111,47 @@ def test_mlp_and_qkv_reject_bad_arguments(lib):
     rc = lib.iron_qkv_head(fake, fake, fake, fake, fake, fake, 0, fake, fake, fake, 0, 0, 0,
                            fake, 1, 1024, 128, 16, 8, 512, 32, 4, 0, 1e-6, fake, 16, None)
     assert rc == _lib.IRON_ERR_WORKSPACE
+
+
+def test_persistent_decode_rejects_bad_arguments(lib):
+    """Validation of iron_decode_persistent runs before any HIP call."""
+    f = lib.iron_decode_persistent
+    fake = 1 << 20
+    ws = lib.iron_decode_persistent_workspace(1024, 3072, 16, 8, 128)
+    assert ws > 0 and ws % 256 == 0
+    assert lib.iron_decode_persistent_workspace(1024, 3072, 16, 8, 64) == 0
+    assert lib.iron_decode_persistent_workspace(2048, 6144, 16, 8, 128) == 0
+
+    def call(**kw):
+        a = dict(layers=fake, n=28, D=1024, FF=3072, Hq=16, Hkv=8, HD=128, S=4096,
+                 sh=4096 * 128, st=128, G=32, tq=4, to=4, tgu=12, td=4, dom=0, x=fake, xo=fake,
+                 pos=fake, ang=fake, ws=fake, wsb=ws)
+        a.update(kw)
+        return f(a["layers"], a["n"], a["D"], a["FF"], a["Hq"], a["Hkv"], a["HD"], a["S"],
+                 a["sh"], a["st"], a["G"], a["tq"], a["to"], a["tgu"], a["td"], a["dom"], a["x"],
+                 a["xo"], a["pos"], a["ang"], 1e-6, 0.088, a["ws"], a["wsb"], None)
+
+    assert call(layers=None) == _lib.IRON_ERR_NULL
+    assert call(FF=4096) == _lib.IRON_ERR_UNSUPPORTED       # no kernel for that shape
+    assert b"no persistent kernel" in lib.iron_last_error()
+    assert call(n=0) == _lib.IRON_ERR_SHAPE
+    assert call(st=100) == _lib.IRON_ERR_SHAPE              # token stride not 16-byte rows
+    assert call(G=48) == _lib.IRON_ERR_SHAPE
+    assert call(tgu=7) == _lib.IRON_ERR_SHAPE               # row blocks must divide FF
+    assert call(dom=5) == _lib.IRON_ERR_SHAPE
+    assert call(ang=fake + 2) == _lib.IRON_ERR_ALIGN
+    assert call(wsb=ws - 8) == _lib.IRON_ERR_WORKSPACE
+    assert call(ws=fake + 64) == _lib.IRON_ERR_ALIGN
+
+
+def test_persistent_layer_check(lib):
+    fake = 1 << 20
+    d = _lib.LayerDesc(*([fake] * 11))
+    args = (1024, 3072, 16, 8, 128, 32, 4, 4, 12, 4, 0)
+    assert lib.iron_decode_persistent_check_layer(ctypes.byref(d), *args) == _lib.IRON_OK
+    d.wd = fake + 8
+    assert lib.iron_decode_persistent_check_layer(ctypes.byref(d), *args) == _lib.IRON_ERR_ALIGN
+    d.wd = fake
+    d.n_kn = None
+    assert lib.iron_decode_persistent_check_layer(ctypes.byref(d), *args) == _lib.IRON_ERR_NULL
+    assert lib.iron_decode_persistent_check_layer(None, *args) == _lib.IRON_ERR_NULL

@@ -1,0 +1,121 @@
+"""The persistent whole-token decode kernel (iron_decode_persistent) on the GPU.
+
+The kernel runs every layer of a token with the arithmetic of the per-operator entry points
+(iron_qkv_attn + iron_swiglu_mlp, exact fp64 accumulation), so its results must be identical:
+
+* tiny model: logits bit-identical to the exact CPU oracle chain (oracle/qwen3.py) at every step,
+  for the separate and the reference's interleaved KV layouts, bf16 and int8 LM heads;
+* the same model through the runlist (one HIP graph of per-operator kernels) and through the
+  persistent kernel: identical logits, tokens and KV-cache rows;
+* Qwen3-0.6B architecture (BASELINE config 4 shape) with the KV cache prefilled past 2048
+  positions, so every split of the attention phase walks more than one tile: the device greedy
+  loop (graph-captured persistent launches) gives the same tokens and caches as the runlist path.
+"""
+
+import pytest
+import torch
+
+from iron_amd.applications.qwen3_0_6b.qwen3_npu_int8 import Qwen3NPU
+from iron_amd.applications.qwen3_0_6b.weights import (Qwen3Config, random_qwen3_weights,
+                                                       synthetic_kv)
+from oracle.qwen3 import Qwen3CpuChain
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16)
+
+
+@pytest.mark.parametrize("kv_layout,lm_head", [("separate", "bf16"), ("interleaved", "int8")])
+def test_persistent_tiny_matches_cpu_chain(kv_layout, lm_head):
+    _say(f"persistent tiny kv_layout={kv_layout} lm_head={lm_head}")
+    cfg = Qwen3Config.tiny()
+    w = random_qwen3_weights(cfg, seed=5, lm_head=lm_head)
+    S = 128
+    model = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, kv_layout=kv_layout, persistent=True)
+    assert model.persistent
+    chain = Qwen3CpuChain(cfg, w, S)
+    tok = 3
+    for pos in range(8):
+        g = model.step_token(tok, pos)
+        lg = model.logits()
+        lc = chain.step(tok, pos)
+        assert torch.equal(_bits(lg), _bits(lc)), f"logits differ from the oracle @{pos}"
+        assert g == Qwen3CpuChain.argmax(lc)
+        tok = g
+    assert model.persistent_errors() == 0
+
+
+def test_persistent_matches_runlist_tiny_prefilled():
+    """Prefilled context (several tiles, several splits) through both execution paths."""
+    _say("persistent vs runlist, tiny, prefilled KV")
+    cfg = Qwen3Config.tiny()
+    w = random_qwen3_weights(cfg, seed=17)
+    S, P0 = 512, 300
+    k0, v0 = synthetic_kv(cfg, P0, seed=3)
+    runs = []
+    for persistent in (False, True):
+        m = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, persistent=persistent)
+        m.load_kv(k0, v0)
+        toks, logits = [], []
+        tok = 41
+        for pos in range(P0, P0 + 6):
+            tok = m.step_token(tok, pos)
+            toks.append(tok)
+            logits.append(m.logits())
+        caches = [tuple(c[:, : P0 + 6].cpu() for c in m.kv_caches(i)) for i in range(cfg.n_layers)]
+        runs.append((toks, torch.stack(logits), caches))
+    (ta, la, ca), (tb, lb, cb) = runs
+    assert ta == tb
+    assert torch.equal(_bits(la), _bits(lb))
+    for i in range(cfg.n_layers):
+        assert torch.equal(_bits(ca[i][0]), _bits(cb[i][0])), f"K cache of layer {i} differs"
+        assert torch.equal(_bits(ca[i][1]), _bits(cb[i][1])), f"V cache of layer {i} differs"
+
+
+def test_persistent_epoch_advances_per_token():
+    _say("persistent epoch / error words")
+    cfg = Qwen3Config.tiny()
+    m = Qwen3NPU(config=cfg, weights=random_qwen3_weights(cfg, seed=8), max_seq_len=64,
+                 persistent=True)
+    ctrl = lambda: m._p_ws[:8].view(torch.int32).cpu().tolist()  # noqa: E731
+    e0, err0 = ctrl()
+    tok = 1
+    for pos in range(3):
+        tok = m.step_token(tok, pos)
+    e1, err1 = ctrl()
+    assert e1 == e0 + 3 and err0 == 0 and err1 == 0
+
+
+@pytest.mark.slow
+def test_persistent_qwen3_0_6b_matches_runlist():
+    cfg = Qwen3Config.qwen3_0_6b()
+    P0, n_prompt, n_new = 2100, 8, 24
+    S = (P0 + n_prompt + n_new + 63) // 64 * 64
+    _say(f"qwen3-0.6b persistent vs runlist: KV {P0}, prompt {n_prompt}, {n_new} tokens")
+    w = random_qwen3_weights(cfg, seed=2024, device="cuda")
+    k0, v0 = synthetic_kv(cfg, P0, seed=7)
+    prompt = torch.randint(0, cfg.vocab_size, (n_prompt,),
+                           generator=torch.Generator().manual_seed(64)).tolist()
+    runs = []
+    for persistent in (False, True):
+        _say(f"qwen3-0.6b persistent={persistent}")
+        m = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, persistent=persistent)
+        assert m.persistent == persistent
+        m.load_kv(k0, v0)
+        toks = m.generate(prompt, n_new, start_pos=P0)
+        end = P0 + n_prompt + n_new - 1
+        caches = [tuple(c[:, P0:end].cpu() for c in m.kv_caches(i)) for i in (0, 13, 27)]
+        runs.append((toks, m.logits(), caches))
+        del m
+        torch.cuda.empty_cache()
+    (ta, la, ca), (tb, lb, cb) = runs
+    assert ta == tb, "greedy tokens differ between the runlist and the persistent kernel"
+    assert torch.equal(_bits(la), _bits(lb))
+    for a, b in zip(ca, cb):
+        assert torch.equal(_bits(a[0]), _bits(b[0])) and torch.equal(_bits(a[1]), _bits(b[1]))
