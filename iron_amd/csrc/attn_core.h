@@ -26,14 +26,27 @@ IRON_DEV double row_share_d(double v) {
   return dpp_d<0x150 + N>(v);
 }
 
-template <int N, int HB>
-IRON_DEV void share_one(double ev, double (&pe)[4][HB]) {
-  if constexpr (N < 4 * HB) pe[N / HB][N % HB] = row_share_d<N>(ev);
+template <int N, int HB, int U>
+IRON_DEV void share_one(double ev, double (&pe)[U][HB]) {
+  if constexpr (N < U * HB) pe[N / HB][N % HB] = row_share_d<N>(ev);
 }
 
-template <int HB, int... Ns>
-IRON_DEV void share_all(double ev, double (&pe)[4][HB], std::integer_sequence<int, Ns...>) {
-  (share_one<Ns, HB>(ev, pe), ...);
+template <int HB, int U, int... Ns>
+IRON_DEV void share_all(double ev, double (&pe)[U][HB], std::integer_sequence<int, Ns...>) {
+  (share_one<Ns, HB, U>(ev, pe), ...);
+}
+
+// Sum of a tile's U exponentials of head h, as a balanced pairwise tree ((0+1)+(2+3) for U = 4).
+template <int U, int HB>
+IRON_DEV double tile_sum(const double (&pe)[U][HB], int h) {
+  if constexpr (U == 4) {
+    return (pe[0][h] + pe[1][h]) + (pe[2][h] + pe[3][h]);
+  } else {
+    double t = (pe[0][h] + pe[1][h]) + (pe[2][h] + pe[3][h]);
+#pragma unroll
+    for (int u = 4; u < U; ++u) t += pe[u][h];
+    return t;
+  }
 }
 
 IRON_DEV void unpack8d(const uint4 v, double (&f)[8]) {
@@ -87,15 +100,16 @@ IRON_DEV void norm_rope8(const uint4 xr, const uint4 wr, const uint4 a0, const u
 // Updates the running maximum m, sum l and unnormalised output o of the HB heads; `it` is the
 // tile's index within this workgroup's sequence (0 = the first tile, which starts from zero).
 // s_mx is the workgroup's tile-maximum exchange; the function ends past its one barrier.
-template <int HB, bool FUSED>
-IRON_DEV void attn_tile_f64(uint4 (&kr)[4], uint4 (&vr)[4], int t0, int t_end, bool has_new,
+template <int HB, bool FUSED, int U = 4>
+IRON_DEV void attn_tile_f64(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, bool has_new,
                             int pos, const uint4 (&s_new)[2][16], const double (&qf)[HB][8],
                             double scale, int it, double (&m)[HB], double (&l)[HB],
                             double (&o)[HB][8], double (&s_mx)[2][4][HB], int wave, int lane,
                             int row, int dl) {
-  bool tv[4];
+  static_assert(U * HB <= 16, "one exponential per lane of a 16-lane row");
+  bool tv[U];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < U; ++u) {
     const int t = t0 + u * 16 + wave * 4 + row;
     tv[u] = t < t_end;
     if constexpr (FUSED) {
@@ -107,9 +121,9 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[4], uint4 (&vr)[4], int t0, int t_end, b
     if (!tv[u]) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // rows past the context may hold NaNs
   }
   // scores s[u][h], identical in every lane of the row
-  double s[4][HB];
+  double s[U][HB];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < U; ++u) {
     double kf[8];
     unpack8d(kr[u], kf);
 #pragma unroll
@@ -125,7 +139,9 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[4], uint4 (&vr)[4], int t0, int t_end, b
   double mx[HB];
 #pragma unroll
   for (int h = 0; h < HB; ++h) {
-    double v = fmax(fmax(s[0][h], s[1][h]), fmax(s[2][h], s[3][h]));
+    double v = s[0][h];
+#pragma unroll
+    for (int u = 1; u < U; ++u) v = fmax(v, s[u][h]);
     v = fmax(v, __shfl_xor(v, 16));
     v = fmax(v, __shfl_xor(v, 32));
     mx[h] = v;
@@ -143,16 +159,16 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[4], uint4 (&vr)[4], int t0, int t_end, b
     mn[h] = fmax(m[h], t);
   }
   // every tile of the loop holds at least one valid token, so mn is finite here
-  // lane dl < 4*HB evaluates exponential (u, h) = (dl / HB, dl % HB)
+  // lane dl < U*HB evaluates exponential (u, h) = (dl / HB, dl % HB)
   double arg = -INFINITY;
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int h = 0; h < HB; ++h)
       if (dl == u * HB + h) arg = s[u][h] - mn[h];
   const double ev = arg == -INFINITY ? 0.0 : exp(arg);
-  double pe[4][HB];
-  share_all<HB>(ev, pe, std::make_integer_sequence<int, 16>{});
+  double pe[U][HB];
+  share_all<HB, U>(ev, pe, std::make_integer_sequence<int, 16>{});
   if (it > 0) {  // rescale the running sums (the first tile starts from zero)
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
@@ -164,11 +180,11 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[4], uint4 (&vr)[4], int t0, int t_end, b
   }
 #pragma unroll
   for (int h = 0; h < HB; ++h) {
-    l[h] += (pe[0][h] + pe[1][h]) + (pe[2][h] + pe[3][h]);
+    l[h] += tile_sum<U>(pe, h);
     m[h] = mn[h];
   }
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < U; ++u) {
     double vf[8];
     unpack8d(vr[u], vf);
 #pragma unroll

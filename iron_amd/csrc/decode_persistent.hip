@@ -50,6 +50,12 @@ constexpr long long kSpinLimit = 1ll << 18;  // polls of one word before a wait 
 constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);
 
 constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// Attention tile: 16 * kRows tokens (4 wavefronts x 4 lane rows x kRows). Each split covers a
+// contiguous ceil(ctx / NS) tokens, so up to 80 * NS tokens (2560 for the 0.6B shape) every split
+// finishes in one tile.
+constexpr int kRows = 5;
+constexpr int kTileTokens = 16 * kRows;
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 template <int D_, int FF_, int HQ_, int HKV_>
@@ -75,6 +81,8 @@ struct Shape {
   static_assert(kNT % HKV == 0 && NS <= 256, "splits per KV head");
   static_assert(kNT * MERGE_PER == HQ * HD && MERGE_PER >= 2 && MERGE_PER % 2 == 0 &&
                     HD % MERGE_PER == 0, "merge slices");
+  static_assert(NS * MERGE_PER == 256 && (NS == 32 || NS == 64 || NS == 128),
+                "one merge thread per (split, dim)");
   static_assert(D % 16 == 0 && FF % 16 == 0 && MQKV % 2 == 0, "GEMV widths");
 };
 
@@ -143,8 +151,12 @@ IRON_DEV double word_double(uint32_t lo, uint32_t hi) {
 // re-reads its pending words together each round.
 //
 // With n_sent > 0, thread t < n_sent first polls only sent(t, tag), the word its producer writes
-// last, so the full read usually finds every word present on its first pass and the polling
-// traffic of a wide input stays at one word per producer.
+// last, so the polling traffic of a wide input stays at one word per producer. Once every
+// sentinel is in, the words are normally all written, and the first pass of the full read uses
+// ordinary cached loads: the 32 workgroups of an XCD then share one fetch of each line through
+// that XCD's L2 instead of each reading it from memory. A cached copy can be stale (a line kept
+// from an earlier token); its tag then does not match, and that word is re-read by the coherent
+// polls of the following passes.
 //
 // `issue` runs once in every thread, right after its first poll loads are issued: the caller
 // issues the weight loads of a later phase there. Loads complete in issue order, so the poll's
@@ -203,9 +215,17 @@ IRON_DEV bool gather_words(int n, Src src, int n_sent, Sent sent, Issue issue, u
   }
   for (long long spins = 0;; ++spins) {
     unsigned long long w[NPT];
+    if (n_sent > 0 && spins == 0) {
 #pragma unroll
-    for (int k = 0; k < NPT; ++k)
-      if (pending[k]) w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int k = 0; k < NPT; ++k)
+        if (pending[k])
+          w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+#pragma unroll
+      for (int k = 0; k < NPT; ++k)
+        if (pending[k])
+          w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     issue_once();
     missing = false;
 #pragma unroll
@@ -298,6 +318,37 @@ IRON_DEV void store_bf16_pairs(const uint16_t (&h)[R], int wg, int M, unsigned l
   }
 }
 
+// Max / sum over the G consecutive threads of a group (G = 32 or 64 within a wavefront, G = 128
+// over two wavefronts through LDS); every thread of the group receives the result. All 256 threads
+// call it together. Sums add in a fixed tree order.
+template <int G>
+IRON_DEV double group_max(double v, double (&s_red)[4][2]) {
+#pragma unroll
+  for (int k = 1; k < (G < 64 ? G : 64); k <<= 1) v = fmax(v, __shfl_xor(v, k));
+  if constexpr (G > 64) {
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_red[wave][0] = v;
+    __syncthreads();
+    v = fmax(s_red[wave & ~1][0], s_red[wave | 1][0]);
+  }
+  return v;
+}
+
+template <int G>
+IRON_DEV double group_sum(double v, double (&s_red)[4][2]) {
+#pragma unroll
+  for (int k = 1; k < (G < 64 ? G : 64); k <<= 1) v += __shfl_xor(v, k);
+  if constexpr (G > 64) {
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_red[wave][1] = v;
+    __syncthreads();
+    v = s_red[wave & ~1][1] + s_red[wave | 1][1];
+  }
+  return v;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Register-resident prefetches: the weight slices (or first K/V tile) a phase multiplies, loaded
 // one or two phases before the phase runs.
@@ -323,19 +374,21 @@ IRON_DEV void prefetch_qkv(const PParams& p, const iron_layer_desc& L, int wg,
 
 // The first K/V tile of this workgroup's split and the QKV epilogue's constants.
 struct KVPrefetch {
-  uint4 kr[4], vr[4];
+  uint4 kr[kRows], vr[kRows];
   uint4 nq, nk, a0, a1;
 };
 
-template <class S>
-IRON_DEV void load_kv_rows(const PParams& p, const iron_layer_desc& L, int kv, int t0, int ctx,
-                           uint4 (&kr)[4], uint4 (&vr)[4]) {
+// Rows t0 + 16u + 4 wave + lane/16 of a tile; rows at or past `bound` repeat row bound - 1 (and
+// row 0 when bound is 0: the cache always has it), so every load is issued unconditionally.
+IRON_DEV void load_kv_rows(const PParams& p, const iron_layer_desc& L, int kv, int t0, int bound,
+                           uint4 (&kr)[kRows], uint4 (&vr)[kRows]) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, row = lane >> 4, dl = lane & 15;
   const size_t base = (size_t)kv * p.kv_sh + dl * 8;
+  const int last = bound > 0 ? bound - 1 : 0;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < kRows; ++u) {
     int t = t0 + u * 16 + wave * 4 + row;
-    t = t < ctx ? t : ctx - 1;  // rows past the context are masked where they are used
+    t = t <= last ? t : last;  // rows past the split are masked where they are used
     kr[u] = ld_global((const uint4*)(L.k_cache + base + (size_t)t * p.kv_st));
     vr[u] = ld_global((const uint4*)(L.v_cache + base + (size_t)t * p.kv_st));
   }
@@ -346,12 +399,25 @@ IRON_DEV int context_of(const PParams& p, int pos) {
   return ctx < 0 ? 0 : (ctx > p.max_seq ? p.max_seq : ctx);
 }
 
+// Split s of NS covers positions [s * chunk, min(ctx, (s + 1) * chunk)).
+struct SplitRange {
+  int begin, end;
+};
+
+template <class S>
+IRON_DEV SplitRange split_range(int ctx, int split) {
+  const int chunk = (ctx + S::NS - 1) / S::NS;
+  const int b = split * chunk;
+  const int e = b + chunk < ctx ? b + chunk : ctx;
+  return {b < ctx ? b : ctx, e};
+}
+
 template <class S>
 IRON_DEV void prefetch_attn(const PParams& p, const iron_layer_desc& L, int wg, int pos,
                             KVPrefetch& kv) {
   const int head = wg / S::NS, split = wg % S::NS, dl = threadIdx.x & 15;
-  const int ctx = context_of(p, pos);
-  if (split * kAttnTile < ctx) load_kv_rows<S>(p, L, head, split * kAttnTile, ctx, kv.kr, kv.vr);
+  const SplitRange r = split_range<S>(context_of(p, pos), split);
+  load_kv_rows(p, L, head, r.begin, r.end, kv.kr, kv.vr);
   kv.nq = ld_global((const uint4*)(L.n_qn + dl * 8));
   kv.nk = ld_global((const uint4*)(L.n_kn + dl * 8));
   const uint16_t* arow = p.ang + 16 * (dl & 7);
@@ -421,8 +487,8 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Phase B: the QKV epilogue and the exact attention core over this split's tiles. Workgroup
-// (kv, split) handles 64-token tiles split, split + NS, ... of KV head kv and writes its partial
+// Phase B: the QKV epilogue and the exact attention core over this split's positions. Workgroup
+// (kv, split) handles a contiguous 1/NS of the context of KV head kv and writes its partial
 // (o unnormalised, m, l) of the HB query heads as tagged fp64 words.
 // ---------------------------------------------------------------------------------------------
 template <class S, class Issue>
@@ -432,8 +498,7 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
   const int head = wg / NS, split = wg % NS;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, row = lane >> 4, dl = lane & 15;
   const bool pos_ok = pos >= 0 && pos < p.max_seq;
-  const int ctx = context_of(p, pos);
-  const int ntile = (ctx + kAttnTile - 1) / kAttnTile;
+  const SplitRange range = split_range<S>(context_of(p, pos), split);
 
   // the raw q rows of heads head*HB.., and the raw k and v rows of KV head `head`
   {
@@ -456,7 +521,7 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
   // K row (V unchanged) when this split owns its tile, and appends both to the caches
   __shared__ uint4 s_q[HB][16];
   __shared__ uint4 s_new[2][16];
-  const bool has_new = pos_ok && (pos / kAttnTile) % NS == split;
+  const bool has_new = pos_ok && pos >= range.begin && pos < range.end;
   if (wave < HB) {
     double qn[8];
     norm_rope8(s_raw[wave * 16 + dl], kv.nq, kv.a0, kv.a1, dl, (double)p.eps, qn);
@@ -490,10 +555,10 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
   }
   __shared__ double s_mx[2][4][HB];
   int it = 0;
-  for (int tile = split; tile < ntile; tile += NS, ++it) {
-    if (it > 0) load_kv_rows<S>(p, L, head, tile * kAttnTile, ctx, kv.kr, kv.vr);
-    attn_tile_f64<HB, true>(kv.kr, kv.vr, tile * kAttnTile, ctx, has_new, pos, s_new, qf,
-                            p.scale, it, m, lsum, o, s_mx, wave, lane, row, dl);
+  for (int t0 = range.begin; t0 < range.end; t0 += kTileTokens, ++it) {
+    if (it > 0) load_kv_rows(p, L, head, t0, range.end, kv.kr, kv.vr);
+    attn_tile_f64<HB, true, kRows>(kv.kr, kv.vr, t0, range.end, has_new, pos, s_new, qf,
+                                   p.scale, it, m, lsum, o, s_mx, wave, lane, row, dl);
   }
   const uint32_t tp = phase_tag(ep, p.n_layers, l, 1);
   attn_finish_f64<HB>(m, lsum, o, wave, row, dl,
@@ -533,49 +598,27 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
     auto sent = [&](int s, uint32_t& t) { t = tp; return part_of(s) + 2 * (kAttnD + 1) + 1; };
     if (!gather_words<cdiv(n, 256)>(n, src, NS, sent, issue, s_in, p.ctrl + 1)) return false;
   }
-  // thread t < NS holds split t
-  const int t = threadIdx.x;
-  double ms = -INFINITY, ls = 0.0, os[PER];
-#pragma unroll
-  for (int d = 0; d < PER; ++d) os[d] = 0.0;
-  if (t < NS) {
-    const uint32_t* w = s_in + t * WPS;
-#pragma unroll
-    for (int d = 0; d < PER; ++d) os[d] = word_double(w[2 * d], w[2 * d + 1]);
-    ms = word_double(w[2 * PER], w[2 * PER + 1]);
-    ls = word_double(w[2 * PER + 2], w[2 * PER + 3]);
-  }
-  __shared__ double s_red[4][PER + 1];
-  double mx = row16_max_d(ms);
-  mx = fmax(mx, __shfl_xor(mx, 16));
-  mx = fmax(mx, __shfl_xor(mx, 32));
-  if (lane == 0) s_red[wave][0] = mx;
-  __syncthreads();
-  const double M = fmax(fmax(s_red[0][0], s_red[1][0]), fmax(s_red[2][0], s_red[3][0]));
-  __syncthreads();
+  // thread (split sp, dim d): sp = t % NS, d = t / NS holds o_sp[d0 + d], m_sp and l_sp; the
+  // max and the two sums run over the NS threads of one d (a wavefront, or two for NS = 128)
+  const int t = threadIdx.x, sp = t % NS, d = t / NS;
+  const uint32_t* w = s_in + sp * WPS;
+  const double os = word_double(w[2 * d], w[2 * d + 1]);
+  const double ms = word_double(w[2 * PER], w[2 * PER + 1]);
+  const double ls = word_double(w[2 * PER + 2], w[2 * PER + 3]);
+  __shared__ double s_red[4][2];
+  const double M = group_max<NS>(ms, s_red);
   const double f = (M == -INFINITY || ms == -INFINITY) ? 0.0 : exp(ms - M);
-  double v[PER + 1];
-  v[0] = f * ls;
-#pragma unroll
-  for (int d = 0; d < PER; ++d) v[d + 1] = f * os[d];
-#pragma unroll
-  for (int k = 0; k <= PER; ++k) v[k] = wave_sum_d(v[k]);
-  if (lane == 0) {
-#pragma unroll
-    for (int k = 0; k <= PER; ++k) s_red[wave][k] = v[k];
-  }
+  const double Lt = group_sum<NS>(f * ls, s_red);
+  const double O = group_sum<NS>(f * os, s_red);
+  __shared__ uint16_t s_o16[PER];
+  if (sp == 0) s_o16[d] = f64_to_bf16(Lt > 0.0 ? O / Lt : 0.0);
   __syncthreads();
-  if (t < PER / 2) {
-    auto total = [&](int k) {
-      return (s_red[0][k] + s_red[1][k]) + (s_red[2][k] + s_red[3][k]);
-    };
-    const double Lt = total(0);
-    const double O0 = total(1 + 2 * t), O1 = total(2 + 2 * t);
-    const uint16_t r0 = f64_to_bf16(Lt > 0.0 ? O0 / Lt : 0.0);
-    const uint16_t r1 = f64_to_bf16(Lt > 0.0 ? O1 / Lt : 0.0);
-    put_word(p.ATT + (h * kAttnD + d0) / 2 + t, (uint32_t)r0 | ((uint32_t)r1 << 16),
+  if (t < PER / 2)
+    put_word(p.ATT + (h * kAttnD + d0) / 2 + t,
+             (uint32_t)s_o16[2 * t] | ((uint32_t)s_o16[2 * t + 1] << 16),
              phase_tag(ep, p.n_layers, l, 2));
-  }
+  (void)wave;
+  (void)lane;
   return true;
 }
 
@@ -660,11 +703,14 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
   // the workgroup's 4R gh values leave together from wave 0 (the down phase polls the last one
   // as the sentinel of the group)
   const int wave = threadIdx.x >> 6;
-  if (lane < R) {
+  double g_r = acc[0][0], u_r = acc2[0][0];  // lane r < R takes row r (one SiLU per lane)
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (lane == r) s_gh[wave * R + r] = (float)silu_mul(acc[r][0], acc2[r][0]);
+  for (int r = 1; r < R; ++r) {
+    g_r = lane == r ? acc[r][0] : g_r;
+    u_r = lane == r ? acc2[r][0] : u_r;
   }
+  const float gh = (float)silu_mul(g_r, u_r);
+  if (lane < R) s_gh[wave * R + lane] = gh;
   __syncthreads();
   const int t = threadIdx.x, row = wg * 4 * R + t;
   if (t < 4 * R && row < S::FF)

@@ -238,13 +238,9 @@ IRON_DEV void dot_w8_lane(const GemvParams& p, const uint4 (&w)[R][NCH],
 // SiLU(g) * u in fp64 with the golden's numerically stable sigmoid
 // (iron/operators/swiglu_mlp_dp/reference.py:28-33).
 IRON_DEV double silu_mul(double g, double u) {
-  double sig;
-  if (g >= 0.0) {
-    sig = 1.0 / (1.0 + exp(-g));
-  } else {
-    const double e = exp(g);
-    sig = e / (1.0 + e);
-  }
+  // one exponential of -|g| serves both branches of the stable form (no divergent branch)
+  const double e = exp(-fabs(g));
+  const double sig = g >= 0.0 ? 1.0 / (1.0 + e) : e / (1.0 + e);
   return (g * sig) * u;
 }
 
