@@ -36,6 +36,9 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE 152040.19 KiB x 2.0 + WRITE_SIZE 310.56 KiB x 1.0, the factors being what the same
 # counters read for a plain 256 MiB device copy (profiles/decode_qwen3_0_6b_hbm_traffic.md).
 LM_HEAD_BF16_TRAFFIC = 311_696_320
+# HBM bytes per launch of the persistent layers kernel (all 28 layers), same method; None until
+# measured for the current kernel.
+PERSISTENT_TRAFFIC = None
 
 
 def parse():
@@ -49,6 +52,9 @@ def parse():
                     help="skip the standalone measurements of BASELINE configs 1, 2, 3 and 5")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--lm-head", default="bf16", choices=["bf16", "int8"])
+    ap.add_argument("--decode", default="auto", choices=["auto", "persistent", "runlist"],
+                    help="auto: the persistent whole-token kernel where available, else the "
+                         "per-operator runlist graph")
     return ap.parse_args()
 
 
@@ -75,7 +81,10 @@ def main():
     w_cpu = None if args.no_cpu_baseline else weights_to(w, "cpu")
     k0, v0 = synthetic_kv(cfg, P0, seed=7)
     print(f"[bench] weights ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
-    model = Qwen3NPU(config=cfg, weights=w, max_seq_len=S)
+    persistent = {"auto": None, "persistent": True, "runlist": False}[args.decode]
+    model = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, persistent=persistent)
+    print(f"[bench] decode path: {'persistent kernel' if model.persistent else 'runlist graph'}",
+          file=sys.stderr, flush=True)
     model.load_kv(k0, v0)
     gen = torch.Generator().manual_seed(64)
     prompt = torch.randint(0, cfg.vocab_size, (n_prompt,), generator=gen).tolist()
@@ -113,36 +122,35 @@ def main():
         kv_per_pos + cfg.vocab_size * 2
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # ---- dominant single launch: the LM head GEMV, HIP events on the stream it runs on.
-    # Timed inside whole decode steps (the 28 layers stream ~700 MB through HBM before it, as in
-    # the step graph), not back to back: repeated launches alone would find part of the 311 MB
-    # head still in the 256 MB last-level cache and overstate the rate. The rest of the step is
-    # one graph replay, so the host has enqueued the head and its events long before the GPU
-    # reaches them and the event pair brackets the kernel alone.
-    lm_fn = model.fc._fns[id(model.lmhead)]
-    lm_views = [v for f, v in model.fc._plan if f is lm_fn][0]
-    stream = torch.cuda.current_stream()
-    body = torch.cuda.CUDAGraph()
-    side = torch.cuda.Stream()
-    side.wait_stream(stream)
-    with torch.cuda.graph(body, stream=side):
-        for fn, views in model.fc._plan:
-            if fn is not lm_fn:
-                fn(*views)
-    stream.wait_stream(side)
-    n_rep = 32
-    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for _ in range(n_rep)]
-    for e0, e1 in pairs:
-        body.replay()
-        e0.record(stream)
-        lm_fn(*lm_views)
-        e1.record(stream)
-    torch.cuda.synchronize()
-    lm_us = sum(e0.elapsed_time(e1) for e0, e1 in pairs) * 1e3 / n_rep
-    del body
+    if model.persistent:
+        layers_us, lm_us = time_persistent(model)
+    else:
+        layers_us, lm_us = None, time_runlist_lm_head(model)
     lm_bytes = wb["lm_head"] + cfg.emb_dim * 2 + cfg.vocab_size * 2
     lm_gbs = lm_bytes / (lm_us * 1e-6) / 1e9
+    lm_roofline = {"bound": "hbm", "kernel": "lm_head GEMV (bf16 [151936x1024], RMSNorm prologue, "
+                                             "argmax epilogue)" if args.lm_head == "bf16" else
+                   "lm_head GEMV (int8 G=32, argmax epilogue)",
+                   "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                   "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
+                   "traffic": LM_HEAD_BF16_TRAFFIC if args.lm_head == "bf16" else None,
+                   "bytes_per_launch": lm_bytes, "avg_launch_us": round(lm_us, 2)}
+    if model.persistent:
+        # the persistent kernel is the step's dominant launch (all 28 layers); its algorithmic
+        # bytes: every layer's weights once, the KV cache read at the timed context, the K/V
+        # rows appended, the embedding row in and the hidden state out
+        ctx = start + 1
+        layer_bytes = wb["layers"] + kv_per_pos * ctx + kv_per_pos + 2 * cfg.emb_dim * 2
+        layer_gbs = layer_bytes / (layers_us * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "kernel": "decode_persistent_kernel (28 layers: QKV, "
+                                              "attention, merge, Wo, gate/up, down)",
+                    "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+                    "traffic": PERSISTENT_TRAFFIC,
+                    "bytes_per_launch": int(layer_bytes), "avg_launch_us": round(layers_us, 2),
+                    "context": ctx}
+    else:
+        roofline = lm_roofline
 
     result = {
         "metric": "decode tokens/s (Qwen3 int8 shapes); achieved HBM GB/s as % of peak",
@@ -162,13 +170,9 @@ def main():
                                f"{start + args.steps}",
                    "global_batch": 1, "seq_len": start + args.steps, "parallelism": "none",
                    "layers": cfg.n_layers, "group_size": cfg.group_size},
-        "roofline": {"bound": "hbm", "kernel": "lm_head GEMV (bf16 [151936x1024], argmax "
-                                                "epilogue)" if args.lm_head == "bf16" else
-                     "lm_head GEMV (int8 G=32, argmax epilogue)",
-                     "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": LM_HEAD_BF16_TRAFFIC if args.lm_head == "bf16" else None,
-                     "bytes_per_launch": lm_bytes, "avg_launch_us": round(lm_us, 2)},
+        "decode_path": "persistent" if model.persistent else "runlist",
+        "roofline": roofline,
+        "lm_head": lm_roofline,
         "step_roofline": {"bytes_per_step": int(step_bytes), "achieved": round(step_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
@@ -179,8 +183,9 @@ def main():
         # 8 TB/s nominal peak
         from iron_amd import benchmarks
         rc = benchmarks.read_probe()
-        result["roofline"]["achievable_read_GB_s"] = rc["GB_s"]
-        result["roofline"]["frac_of_achievable"] = round(lm_gbs / rc["GB_s"], 4)
+        for r in (result["roofline"], result["lm_head"]):
+            r["achievable_read_GB_s"] = rc["GB_s"]
+            r["frac_of_achievable"] = round(r["achieved"] / rc["GB_s"], 4)
         # the other BASELINE configurations, each timed standalone over >= 512 MiB of rotating
         # operands (iron_amd/benchmarks.py); config 5 includes the 36-layer Qwen3-8B B=16 stack
         del model, w
@@ -192,6 +197,62 @@ def main():
         result["cpu_baseline"] = cpu_baseline(cfg, w_cpu, (k0, v0), prompt, tokens, start, S,
                                               args.cpu_sample_steps)
     print(json.dumps(result), flush=True)
+
+
+def time_persistent(model, n_rep: int = 24):
+    """Average duration of the persistent layers kernel and of the LM head, from HIP events on the
+    stream both run on. The events bracket each launch alone; consecutive repetitions recompute
+    the same position (the KV row is rewritten with the same values). The 468 MB of layer weights
+    exceed the 256 MB last-level cache, so every launch streams them from HBM."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_rep)]
+    model.persistent_layers_launch()
+    model.lm_head_launch()
+    for e0, e1, e2 in ev:
+        e0.record(stream)
+        model.persistent_layers_launch()
+        e1.record(stream)
+        model.lm_head_launch()
+        e2.record(stream)
+    torch.cuda.synchronize()
+    if model.persistent_errors():
+        raise RuntimeError("persistent kernel reported a hand-off timeout while timing")
+    layers_us = sum(e0.elapsed_time(e1) for e0, e1, _ in ev) * 1e3 / n_rep
+    lm_us = sum(e1.elapsed_time(e2) for _, e1, e2 in ev) * 1e3 / n_rep
+    return layers_us, lm_us
+
+
+def time_runlist_lm_head(model, n_rep: int = 32):
+    """The runlist path's LM head, timed inside whole decode steps with HIP events on its stream.
+
+    The rest of the step is one graph replay before each launch (the 28 layers stream ~700 MB
+    through HBM first, as in the step graph); back-to-back launches alone would find part of the
+    311 MB head still in the 256 MB last-level cache and overstate the rate."""
+    import torch
+
+    lm_fn = model.fc._fns[id(model.lmhead)]
+    lm_views = [v for f, v in model.fc._plan if f is lm_fn][0]
+    stream = torch.cuda.current_stream()
+    body = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.graph(body, stream=side):
+        for fn, views in model.fc._plan:
+            if fn is not lm_fn:
+                fn(*views)
+    stream.wait_stream(side)
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(n_rep)]
+    for e0, e1 in pairs:
+        body.replay()
+        e0.record(stream)
+        lm_fn(*lm_views)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    del body
+    return sum(e0.elapsed_time(e1) for e0, e1 in pairs) * 1e3 / n_rep
 
 
 def cpu_baseline(cfg, w, kv0, prompt, gpu_tokens, start, S, n_sample):

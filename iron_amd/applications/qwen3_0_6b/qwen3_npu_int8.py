@@ -76,7 +76,7 @@ class Qwen3NPU:
                  kv_layout: str = "separate", lm_head: str | None = None,
                  dispatch: str = "auto", context: AIEContext | None = None,
                  fuse_attention: bool = True, attn_accumulate: str = "f64",
-                 persistent: bool | None = False):
+                 persistent: bool | None = None):
         self.cfg = cfg = config or Qwen3Config.qwen3_0_6b()
         self.max_seq_len = max_seq_len
         self.kv_layout = kv_layout
@@ -256,6 +256,11 @@ class Qwen3NPU:
 
     def _persistent_launches(self):
         """The token's layers in one kernel, then the LM head with the final RMSNorm fused."""
+        self.persistent_layers_launch()
+        self.lm_head_launch()
+
+    def persistent_layers_launch(self):
+        """Launch iron_decode_persistent for the current position on the current stream."""
         cfg, lib, mlp = self.cfg, _lib.load(), self.mlp_xdna
         stream = torch.cuda.current_stream(self.device).cuda_stream
         view = lambda name, dt: self.fc.get_buffer(name).torch_view(dt)  # noqa: E731
@@ -269,6 +274,12 @@ class Qwen3NPU:
             view("rope_row", torch.bfloat16).data_ptr(), float(cfg.eps),
             1.0 / math.sqrt(cfg.head_dim), self._p_ws.data_ptr(), self._p_ws.numel(), stream),
             "iron_decode_persistent")
+
+    def lm_head_launch(self):
+        """Final RMSNorm + LM head + argmax key over the persistent kernel's output."""
+        cfg, lib = self.cfg, _lib.load()
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        view = lambda name, dt: self.fc.get_buffer(name).torch_view(dt)  # noqa: E731
         head = view("W_out_head", torch.uint8).data_ptr()
         kind, G, tile = ((_lib.IRON_WEIGHT_BF16, 16, 1) if self.lm_head_kind == "bf16"
                          else (_lib.IRON_WEIGHT_INT8, cfg.group_size, LMHEAD_TSI))

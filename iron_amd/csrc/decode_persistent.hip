@@ -56,6 +56,10 @@ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 // finishes in one tile.
 constexpr int kRows = 5;
 constexpr int kTileTokens = 16 * kRows;
+
+// gh, the widest hand-off, is read with cached loads (see gather_words); layers rotate over
+// kGhBuffers copies so that a line an XCD's L2 kept from the previous layer is never the one read.
+constexpr int kGhBuffers = 4;
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 template <int D_, int FF_, int HQ_, int HKV_>
@@ -107,6 +111,7 @@ struct PParams {
   float eps;
   double scale;
   unsigned long long *X, *RAW, *PART, *ATT, *AO, *GH;  // tagged hand-off buffers
+  int gh_stride;          // words between the kGhBuffers copies of gh
   uint32_t* ctrl;         // [0] epoch, [1] error flags
 };
 
@@ -301,6 +306,21 @@ template <int R>
 IRON_DEV void store_bf16_pairs(const uint16_t (&h)[R], int wg, int M, unsigned long long* dst,
                                uint32_t tag, uint16_t* s_out, uint16_t* plain) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if constexpr (R % 2 == 0) {
+    // a wavefront's rows pair up within it: lane k < R/2 stores rows 2k, 2k+1 (every lane holds
+    // every row's value)
+    const int row0 = (wg * 4 + wave) * R;
+    uint32_t pair = 0u;
+#pragma unroll
+    for (int k = 0; k < R / 2; ++k)
+      if (lane == k) pair = (uint32_t)h[2 * k] | ((uint32_t)h[2 * k + 1] << 16);
+    const int row = row0 + 2 * lane;
+    if (lane < R / 2 && row < M) {
+      put_word(dst + row / 2, pair, tag);
+      if (plain) ((uint32_t*)plain)[row / 2] = pair;
+    }
+    return;
+  }
   if (lane < R) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -594,9 +614,8 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
       unsigned long long* part = part_of(s);
       return k < 2 * PER ? part + 2 * d0 + k : part + 2 * kAttnD + (k - 2 * PER);
     };
-    // a split's partial ends with the high word of its sum l
-    auto sent = [&](int s, uint32_t& t) { t = tp; return part_of(s) + 2 * (kAttnD + 1) + 1; };
-    if (!gather_words<cdiv(n, 256)>(n, src, NS, sent, issue, s_in, p.ctrl + 1)) return false;
+    if (!gather_words<cdiv(n, 256)>(n, src, 0, NoSentinel(), issue, s_in, p.ctrl + 1))
+      return false;
   }
   // thread (split sp, dim d): sp = t % NS, d = t / NS holds o_sp[d0 + d], m_sp and l_sp; the
   // max and the two sums run over the NS threads of one d (a wavefront, or two for NS = 128)
@@ -714,7 +733,8 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
   __syncthreads();
   const int t = threadIdx.x, row = wg * 4 * R + t;
   if (t < 4 * R && row < S::FF)
-    put_word(p.GH + row, __float_as_uint(s_gh[t]), phase_tag(ep, p.n_layers, l, 4));
+    put_word(p.GH + (l % kGhBuffers) * p.gh_stride + row, __float_as_uint(s_gh[t]),
+             phase_tag(ep, p.n_layers, l, 4));
   return true;
 }
 
@@ -731,6 +751,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   g.pro = PRO_F32;
   // LDS words [0, FF): gh; then a and x of this workgroup's 4R rows, 2R words each
   constexpr int nres = 2 * R;
+  unsigned long long* const gh = p.GH + (l % kGhBuffers) * p.gh_stride;
   const int wrow = wg * nres;  // first word (row pair) of this workgroup's rows
   {
     const uint32_t tg = phase_tag(ep, p.n_layers, l, 4), ta = phase_tag(ep, p.n_layers, l, 3);
@@ -738,7 +759,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
     auto src = [&](int j, uint32_t& t) {
       if (j < S::FF) {
         t = tg;
-        return p.GH + j;
+        return gh + j;
       }
       const int k = j - S::FF;
       const int word = wrow + (k % nres);
@@ -752,7 +773,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
     auto sent = [&](int q, uint32_t& t) {
       t = tg;
       const int last = q * rows_e + rows_e - 1;
-      return p.GH + (last < S::FF ? last : S::FF - 1);
+      return gh + (last < S::FF ? last : S::FF - 1);
     };
     if (l == 0) {
       // x is the embedding row, written by an earlier kernel
@@ -852,7 +873,7 @@ Layout layout_of() {
   lo.PART = take((size_t)S::HQ * S::NS * (S::HD + 2) * 2);
   lo.ATT = take(S::QD / 2);
   lo.AO = take(S::D / 2);
-  lo.GH = take(S::FF);
+  lo.GH = take((size_t)kGhBuffers * S::FF);
   lo.total = off;
   return lo;
 }
@@ -1018,6 +1039,7 @@ int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, i
   p.ATT = (unsigned long long*)(base + lo.ATT);
   p.AO = (unsigned long long*)(base + lo.AO);
   p.GH = (unsigned long long*)(base + lo.GH);
+  p.gh_stride = id == SHAPE_0_6B ? ShapeQwen3_0_6B::FF : ShapeTiny::FF;
   hipStream_t s = (hipStream_t)stream;
   if (id == SHAPE_0_6B)
     hipLaunchKernelGGL(decode_persistent_kernel<ShapeQwen3_0_6B>, dim3(kNT), dim3(256), 0, s,

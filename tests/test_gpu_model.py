@@ -38,7 +38,7 @@ def test_tiny_model_matches_cpu_chain(kv_layout, lm_head):
     cfg = Qwen3Config.tiny()
     w = random_qwen3_weights(cfg, seed=5, lm_head=lm_head)
     S = 128
-    model = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, kv_layout=kv_layout)
+    model = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, kv_layout=kv_layout, persistent=False)
     chain = Qwen3CpuChain(cfg, w, S)                       # exact (fp64) oracle
     literal = Qwen3CpuChain(cfg, w, S, dt=torch.float32)   # the golden as written (fp32)
     tok = 3
@@ -60,7 +60,7 @@ def test_dispatch_modes_bit_identical(tiny):
     cfg, w = tiny
     outs = []
     for dispatch in ("fused", "separate"):
-        m = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, dispatch=dispatch)
+        m = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, dispatch=dispatch, persistent=False)
         toks, logits = [], []
         tok = 11
         for pos in range(5):
@@ -72,14 +72,15 @@ def test_dispatch_modes_bit_identical(tiny):
     assert torch.equal(outs[0][1].view(torch.int16), outs[1][1].view(torch.int16))
 
 
-def test_device_generate_matches_host_loop(tiny):
-    _say("device generate vs host loop")
+@pytest.mark.parametrize("persistent", [False, True])
+def test_device_generate_matches_host_loop(tiny, persistent):
+    _say(f"device generate vs host loop (persistent={persistent})")
     cfg, w = tiny
     prompt = [7, 19, 23, 5]
     n_new = 20
-    a = Qwen3NPU(config=cfg, weights=w, max_seq_len=64)
+    a = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, persistent=persistent)
     dev_tokens = a.generate(prompt, n_new)
-    b = Qwen3NPU(config=cfg, weights=w, max_seq_len=64)
+    b = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, persistent=persistent)
     pos = 0
     for t in prompt[:-1]:
         b.step_token(t, pos)
