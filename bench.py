@@ -6,14 +6,17 @@ random-init weights, every linear layer int8 with per-group-32 bf16 scales, bf16
 tied LM head / norms; the KV cache is prefilled to 2048 positions (1984 seeded synthetic
 positions + a 64-token seeded prompt run through the decode path), then greedy decoding at B=1.
 A step is one decode token: one HIP-graph replay that consumes the previous argmax on the device,
-runs the 28 layers, the final norm and the LM head (argmax fused). ``--warmup`` steps run first,
+runs the 28 layers (by default as one persistent kernel, ``--decode runlist`` for the
+per-operator graph), the final norm and the LM head (argmax fused). ``--warmup`` steps run first,
 then the position is rewound and ``--steps`` steps are timed between two device
 synchronisations (positions 2048 .. 2048+steps-1).
 
 The JSON line also carries:
-  roofline      -- the LM-head GEMV (the largest single launch: the 311 MB bf16 head) timed with
-                   HIP events on the stream it runs on, against the 8 TB/s HBM peak; plus the
-                   whole-step algorithmic bytes / step time in ``step_roofline``;
+  roofline      -- the step's dominant launch (the persistent layers kernel; the LM head on the
+                   runlist path) timed with HIP events on the stream it runs on, against the
+                   8 TB/s HBM peak, with its measured HBM traffic; ``lm_head`` the same for the
+                   311 MB bf16 head; the whole-step algorithmic bytes / step time in
+                   ``step_roofline``;
   cpu_baseline  -- the CPU oracle chain (the reference's per-op goldens composed with bf16 op
                    boundaries, oracle/qwen3.py) on the host cores, teacher-forced on the GPU's
                    tokens for a bounded sample, with the greedy agreement on that sample.
@@ -36,9 +39,9 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE 152040.19 KiB x 2.0 + WRITE_SIZE 310.56 KiB x 1.0, the factors being what the same
 # counters read for a plain 256 MiB device copy (profiles/decode_qwen3_0_6b_hbm_traffic.md).
 LM_HEAD_BF16_TRAFFIC = 311_696_320
-# HBM bytes per launch of the persistent layers kernel (all 28 layers), same method; None until
-# measured for the current kernel.
-PERSISTENT_TRAFFIC = None
+# HBM bytes per launch of the persistent layers kernel (all 28 layers), same method:
+# FETCH_SIZE 386166.31 KiB x 2.0 + WRITE_SIZE 61496.03 KiB x 1.0 at context 2048..2057.
+PERSISTENT_TRAFFIC = 853_840_544
 
 
 def parse():
