@@ -44,7 +44,7 @@ namespace {
 using namespace iron::dev;
 
 constexpr int kNT = 256;                     // workgroups (one per CU of an MI355X)
-constexpr int kPhases = 6;                   // phases per layer
+constexpr int kPhases = 7;                   // tag slots per layer: six phases + the input row
 constexpr long long kSpinLimit = 1ll << 18;  // polls of one word before a wait fails (~0.3 s)
 // s_waitcnt immediate: vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding)
 constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);
@@ -59,7 +59,10 @@ constexpr int kTileTokens = 16 * kRows;
 
 // gh, the widest hand-off, is read with cached loads (see gather_words); layers rotate over
 // kGhBuffers copies so that a line an XCD's L2 kept from the previous layer is never the one read.
+// Each gate/up workgroup's words fill one 128-byte block of kGhBlock words (one cache line, one
+// store instruction), so seeing its last word means the whole line has been written.
 constexpr int kGhBuffers = 4;
+constexpr int kGhBlock = 16;
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 template <int D_, int FF_, int HQ_, int HKV_>
@@ -80,6 +83,9 @@ struct Shape {
   static constexpr int LDS_WORDS =
       cmax(cmax(D, QD / 2), cmax(FF + 4 * RF, cmax(NS * MERGE_WPS, (HB + 2) * 64)));
   static constexpr int RMAX = cmax(cmax(RA, RD), RF);
+  static constexpr int GH_ROWS = 4 * RE;               // gh rows one workgroup produces
+  static constexpr int GH_PROD = cdiv(FF, GH_ROWS);    // gate/up workgroups with rows
+  static constexpr int GH_WORDS = GH_PROD * kGhBlock;  // one gh copy, blocked per producer
 
   static_assert(HQ % HKV == 0 && (HB == 1 || HB == 2 || HB == 4), "GQA group must be 1, 2 or 4");
   static_assert(kNT % HKV == 0 && NS <= 256, "splits per KV head");
@@ -88,6 +94,7 @@ struct Shape {
   static_assert(NS * MERGE_PER == 256 && (NS == 32 || NS == 64 || NS == 128),
                 "one merge thread per (split, dim)");
   static_assert(D % 16 == 0 && FF % 16 == 0 && MQKV % 2 == 0, "GEMV widths");
+  static_assert(GH_ROWS <= kGhBlock && GH_PROD <= kNT, "gh blocks");
 };
 
 using ShapeQwen3_0_6B = Shape<1024, 3072, 16, 8>;
@@ -111,7 +118,6 @@ struct PParams {
   float eps;
   double scale;
   unsigned long long *X, *RAW, *PART, *ATT, *AO, *GH;  // tagged hand-off buffers
-  int gh_stride;          // words between the kGhBuffers copies of gh
   uint32_t* ctrl;         // [0] epoch, [1] error flags
 };
 
@@ -137,6 +143,12 @@ IRON_DEV uint32_t phase_tag(uint32_t epoch, int n_layers, int layer, int phase) 
   return (uint32_t)(v % 0xffffffffull) + 1u;  // never 0, the value of a cleared word
 }
 
+// The tag x carries into layer l: the previous layer's down phase, or for layer 0 the embedding
+// row the grid publishes at its start (slot 6 of layer 0, used by nothing else).
+IRON_DEV uint32_t x_tag(uint32_t epoch, int n_layers, int layer) {
+  return layer == 0 ? phase_tag(epoch, n_layers, 0, 6) : phase_tag(epoch, n_layers, layer - 1, 5);
+}
+
 IRON_DEV void put_word(unsigned long long* dst, uint32_t payload, uint32_t tag) {
   __hip_atomic_store(dst, ((unsigned long long)tag << 32) | payload, __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -157,8 +169,8 @@ IRON_DEV double word_double(uint32_t lo, uint32_t hi) {
 //
 // With n_sent > 0, thread t < n_sent first polls only sent(t, tag), the word its producer writes
 // last, so the polling traffic of a wide input stays at one word per producer. Once every
-// sentinel is in, the words are normally all written, and the first pass of the full read uses
-// ordinary cached loads: the 32 workgroups of an XCD then share one fetch of each line through
+// sentinel is in, those producers' words (slots below n_cached) are normally all written, and
+// the first pass of the full read takes them with ordinary cached loads: the 32 workgroups of an XCD then share one fetch of each line through
 // that XCD's L2 instead of each reading it from memory. A cached copy can be stale (a line kept
 // from an earlier token); its tag then does not match, and that word is re-read by the coherent
 // polls of the following passes.
@@ -172,7 +184,7 @@ IRON_DEV double word_double(uint32_t lo, uint32_t hi) {
 // barrier.
 template <int NPT, class Src, class Sent, class Issue>
 IRON_DEV bool gather_words(int n, Src src, int n_sent, Sent sent, Issue issue, uint32_t* dst,
-                           uint32_t* err) {
+                           uint32_t* err, int n_cached = 0) {
   __syncthreads();  // the previous phase's LDS reads are done before dst is rewritten
   // Every load issued so far (this phase's weights, issued a phase or two ago) completes here,
   // before the poll and the `issue` loads: the compiler then knows those registers are ready and
@@ -201,13 +213,15 @@ IRON_DEV bool gather_words(int n, Src src, int n_sent, Sent sent, Issue issue, u
     for (long long spins = 0;; ++spins) {
       unsigned long long w = 0;
       if (has) w = __hip_atomic_load(sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      issue_once();
       missing = has && (uint32_t)(w >> 32) != want;
       if (!missing || gave_up(spins)) break;
       __builtin_amdgcn_s_sleep(1);
     }
     if (missing) atomicOr(err, 1u);
-    if (__syncthreads_or(missing ? 1 : 0)) return false;
+    if (__syncthreads_or(missing ? 1 : 0)) {
+      issue_once();
+      return false;
+    }
   }
   bool pending[NPT];
   unsigned long long* ptr[NPT];
@@ -221,17 +235,22 @@ IRON_DEV bool gather_words(int n, Src src, int n_sent, Sent sent, Issue issue, u
   for (long long spins = 0;; ++spins) {
     unsigned long long w[NPT];
     if (n_sent > 0 && spins == 0) {
+      // slots below n_cached (the producers the sentinels vouch for) through the L2; the rest
+      // coherently
 #pragma unroll
-      for (int k = 0; k < NPT; ++k)
-        if (pending[k])
-          w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      for (int k = 0; k < NPT; ++k) {
+        if (!pending[k]) continue;
+        if ((int)threadIdx.x + 256 * k < n_cached)
+          w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+        else
+          w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     } else {
 #pragma unroll
       for (int k = 0; k < NPT; ++k)
         if (pending[k])
           w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    issue_once();
     missing = false;
 #pragma unroll
     for (int k = 0; k < NPT; ++k) {
@@ -247,19 +266,15 @@ IRON_DEV bool gather_words(int n, Src src, int n_sent, Sent sent, Issue issue, u
     __builtin_amdgcn_s_sleep(1);
   }
   if (missing) atomicOr(err, 1u);
-  return __syncthreads_or(missing ? 1 : 0) == 0;
+  const bool ok = __syncthreads_or(missing ? 1 : 0) == 0;
+  issue_once();
+  return ok;
 }
 
 // No sentinel stage.
 struct NoSentinel {
   IRON_DEV unsigned long long* operator()(int, uint32_t&) const { return nullptr; }
 };
-
-// Plain bf16 pairs (the embedding row written by an earlier kernel) into LDS words [0, n).
-IRON_DEV void copy_words(const uint16_t* src, int n, uint32_t* dst) {
-  __syncthreads();
-  for (int j = threadIdx.x; j < n; j += 256) dst[j] = ((const uint32_t*)src)[j];
-}
 
 // This lane's activation slices from LDS, in the layout load_x_lane produces from global memory:
 // bf16 elements [c*1024 + 16 lane, +16) as two uint4, or fp32 ones as four.
@@ -482,12 +497,8 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
   GemvParams g = gemv_of(p.g_qkv, nullptr, S::MQKV, S::D);
   g.pro = PRO_RMS_BF16;
   g.eps = p.eps;
-  if (l == 0) {
-    copy_words(p.x_in, S::D / 2, s_in);
-    issue();
-    __syncthreads();
-  } else {
-    const uint32_t tx = phase_tag(ep, p.n_layers, l - 1, 5);
+  {
+    const uint32_t tx = x_tag(ep, p.n_layers, l);
     auto src = [&](int j, uint32_t& t) { t = tx; return p.X + j; };
     if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src, 0, NoSentinel(), issue, s_in,
                                            p.ctrl + 1))
@@ -690,21 +701,13 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
   {
     // words [0, D/2): x; [D/2, D): a
     constexpr int half = S::D / 2;
-    const uint32_t tx = phase_tag(ep, p.n_layers, l - 1, 5), ta = phase_tag(ep, p.n_layers, l, 3);
-    if (l == 0) {
-      copy_words(p.x_in, half, s_in);
-      auto src = [&](int j, uint32_t& t) { t = ta; return p.AO + j; };
-      if (!gather_words<cdiv(half, 256)>(half, src, 0, NoSentinel(), issue, s_in + half,
-                                         p.ctrl + 1))
-        return false;
-    } else {
-      auto src = [&](int j, uint32_t& t) {
-        t = j < half ? tx : ta;
-        return j < half ? p.X + j : p.AO + (j - half);
-      };
-      if (!gather_words<cdiv(S::D, 256)>(S::D, src, 0, NoSentinel(), issue, s_in, p.ctrl + 1))
-        return false;
-    }
+    const uint32_t tx = x_tag(ep, p.n_layers, l), ta = phase_tag(ep, p.n_layers, l, 3);
+    auto src = [&](int j, uint32_t& t) {
+      t = j < half ? tx : ta;
+      return j < half ? p.X + j : p.AO + (j - half);
+    };
+    if (!gather_words<cdiv(S::D, 256)>(S::D, src, 0, NoSentinel(), issue, s_in, p.ctrl + 1))
+      return false;
   }
   uint4 xl[NCH][4], al[NCH][4], x2l[NCH][2];
   lane_bf16<NCH>(s_in, S::D, lane, xl);
@@ -731,9 +734,9 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
   const float gh = (float)silu_mul(g_r, u_r);
   if (lane < R) s_gh[wave * R + lane] = gh;
   __syncthreads();
-  const int t = threadIdx.x, row = wg * 4 * R + t;
-  if (t < 4 * R && row < S::FF)
-    put_word(p.GH + (l % kGhBuffers) * p.gh_stride + row, __float_as_uint(s_gh[t]),
+  const int t = threadIdx.x, row = wg * S::GH_ROWS + t;
+  if (t < S::GH_ROWS && row < S::FF)
+    put_word(p.GH + (l % kGhBuffers) * S::GH_WORDS + wg * kGhBlock + t, __float_as_uint(s_gh[t]),
              phase_tag(ep, p.n_layers, l, 4));
   return true;
 }
@@ -751,15 +754,15 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   g.pro = PRO_F32;
   // LDS words [0, FF): gh; then a and x of this workgroup's 4R rows, 2R words each
   constexpr int nres = 2 * R;
-  unsigned long long* const gh = p.GH + (l % kGhBuffers) * p.gh_stride;
+  unsigned long long* const gh = p.GH + (l % kGhBuffers) * S::GH_WORDS;
   const int wrow = wg * nres;  // first word (row pair) of this workgroup's rows
   {
     const uint32_t tg = phase_tag(ep, p.n_layers, l, 4), ta = phase_tag(ep, p.n_layers, l, 3);
-    const uint32_t tx = phase_tag(ep, p.n_layers, l - 1, 5);
+    const uint32_t tx = x_tag(ep, p.n_layers, l);
     auto src = [&](int j, uint32_t& t) {
       if (j < S::FF) {
         t = tg;
-        return gh + j;
+        return gh + (j / S::GH_ROWS) * kGhBlock + j % S::GH_ROWS;
       }
       const int k = j - S::FF;
       const int word = wrow + (k % nres);
@@ -767,29 +770,17 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
       t = k < nres ? ta : tx;
       return (k < nres ? p.AO : p.X) + wc;
     };
-    // gate/up workgroup q writes rows [4 RE q, 4 RE (q + 1)); its last row is the sentinel
-    constexpr int rows_e = 4 * S::RE;
-    constexpr int n_sent = cdiv(S::FF, rows_e) < kNT ? cdiv(S::FF, rows_e) : kNT;
+    // gate/up workgroup q writes rows [GH_ROWS q, GH_ROWS (q + 1)) into block q; its last row
+    // is the sentinel
+    constexpr int n_sent = S::GH_PROD;
     auto sent = [&](int q, uint32_t& t) {
       t = tg;
-      const int last = q * rows_e + rows_e - 1;
-      return gh + (last < S::FF ? last : S::FF - 1);
+      const int rows = S::FF - q * S::GH_ROWS < S::GH_ROWS ? S::FF - q * S::GH_ROWS : S::GH_ROWS;
+      return gh + q * kGhBlock + rows - 1;
     };
-    if (l == 0) {
-      // x is the embedding row, written by an earlier kernel
-      if (!gather_words<cdiv(S::FF + nres, 256)>(S::FF + nres, src, n_sent, sent, issue, s_in,
-                                                  p.ctrl + 1))
-        return false;
-      if (threadIdx.x < nres) {
-        const int word = wrow + threadIdx.x;
-        s_in[S::FF + nres + threadIdx.x] =
-            ((const uint32_t*)p.x_in)[word < S::D / 2 ? word : 0];
-      }
-      __syncthreads();
-    } else if (!gather_words<cdiv(S::FF + 2 * nres, 256)>(S::FF + 2 * nres, src, n_sent, sent,
-                                                             issue, s_in, p.ctrl + 1)) {
+    if (!gather_words<cdiv(S::FF + 2 * nres, 256)>(S::FF + 2 * nres, src, n_sent, sent, issue,
+                                                    s_in, p.ctrl + 1, S::FF))
       return false;
-    }
   }
   uint4 xl[NCH][4], x2l[NCH][2] = {}, nwl[NCH][2] = {};
   lane_f32<NCH>(s_in, S::FF, lane, xl);
@@ -824,6 +815,10 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
   W8<S::RA, S::CA> wqkv;
   uint4 n_in[S::CA][2];
   prefetch_qkv<S>(p, p.layers[0], wg, wqkv, n_in);
+  // the embedding row enters the hand-off like any layer's output (x's tag of layer 0)
+  if (threadIdx.x < 64)
+    for (int j = wg * 64 + threadIdx.x; j < S::D / 2; j += kNT * 64)
+      put_word(p.X + j, ((const uint32_t*)p.x_in)[j], x_tag(ep, p.n_layers, 0));
   for (int l = 0; l < p.n_layers; ++l) {
     const iron_layer_desc L = p.layers[l];
     KVPrefetch kv;
@@ -873,7 +868,7 @@ Layout layout_of() {
   lo.PART = take((size_t)S::HQ * S::NS * (S::HD + 2) * 2);
   lo.ATT = take(S::QD / 2);
   lo.AO = take(S::D / 2);
-  lo.GH = take((size_t)kGhBuffers * S::FF);
+  lo.GH = take((size_t)kGhBuffers * S::GH_WORDS);
   lo.total = off;
   return lo;
 }
@@ -1039,7 +1034,6 @@ int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, i
   p.ATT = (unsigned long long*)(base + lo.ATT);
   p.AO = (unsigned long long*)(base + lo.AO);
   p.GH = (unsigned long long*)(base + lo.GH);
-  p.gh_stride = id == SHAPE_0_6B ? ShapeQwen3_0_6B::FF : ShapeTiny::FF;
   hipStream_t s = (hipStream_t)stream;
   if (id == SHAPE_0_6B)
     hipLaunchKernelGGL(decode_persistent_kernel<ShapeQwen3_0_6B>, dim3(kNT), dim3(256), 0, s,
