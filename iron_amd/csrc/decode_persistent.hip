@@ -57,8 +57,10 @@ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 constexpr int kRows = 5;
 constexpr int kTileTokens = 16 * kRows;
 
-// gh, the widest hand-off, is read with cached loads (see gather_words); layers rotate over
-// kGhBuffers copies so that a line an XCD's L2 kept from the previous layer is never the one read.
+// gh, the widest hand-off, is read with cached loads (see gather_blocks); layers rotate over
+// kGhBuffers copies, so a line an XCD's L2 kept from the previous layer is never the one read (a
+// stale copy would carry an old tag and be re-read coherently). One copy per layer measured no
+// better than four.
 // Each gate/up workgroup's words fill one 128-byte block of kGhBlock words (one cache line, one
 // store instruction), so seeing its last word means the whole line has been written.
 constexpr int kGhBuffers = 4;
@@ -87,7 +89,7 @@ struct Shape {
   static constexpr int GH_PROD = cdiv(FF, GH_ROWS);    // gate/up workgroups with rows
   static constexpr int GH_WORDS = GH_PROD * kGhBlock;  // one gh copy, blocked per producer
 
-  static_assert(HQ % HKV == 0 && (HB == 1 || HB == 2 || HB == 4), "GQA group must be 1, 2 or 4");
+  static_assert(HQ % HKV == 0 && HB == 2, "the attention phase handles GQA pairs");
   static_assert(kNT % HKV == 0 && NS <= 256, "splits per KV head");
   static_assert(kNT * MERGE_PER == HQ * HD && MERGE_PER >= 2 && MERGE_PER % 2 == 0 &&
                     HD % MERGE_PER == 0, "merge slices");
@@ -167,62 +169,43 @@ IRON_DEV double word_double(uint32_t lo, uint32_t hi) {
 // src(j, tag) names slot j's word and the tag it must carry; the payload goes to dst[j]. A thread
 // re-reads its pending words together each round.
 //
-// With n_sent > 0, thread t < n_sent first polls only sent(t, tag), the word its producer writes
-// last, so the polling traffic of a wide input stays at one word per producer. Once every
-// sentinel is in, those producers' words (slots below n_cached) are normally all written, and
-// the first pass of the full read takes them with ordinary cached loads: the 32 workgroups of an XCD then share one fetch of each line through
-// that XCD's L2 instead of each reading it from memory. A cached copy can be stale (a line kept
-// from an earlier token); its tag then does not match, and that word is re-read by the coherent
-// polls of the following passes.
-//
-// `issue` runs once in every thread, right after its first poll loads are issued: the caller
-// issues the weight loads of a later phase there. Loads complete in issue order, so the poll's
-// first answer does not wait for them, and they stream while this phase waits for its input.
+// `issue` runs once in every thread when the wait is over (also when it failed): the caller
+// issues the weight loads of a later phase there, and they stream during this phase's compute
+// and the next phase's wait. Issued earlier, they would sit ahead of the later poll loads, which
+// complete in issue order behind them.
 //
 // Returns false (workgroup-uniform) if a word did not arrive within kSpinLimit rounds (or another
 // workgroup has already failed), after raising the error flag. Starts and ends with a workgroup
 // barrier.
-template <int NPT, class Src, class Sent, class Issue>
-IRON_DEV bool gather_words(int n, Src src, int n_sent, Sent sent, Issue issue, uint32_t* dst,
-                           uint32_t* err, int n_cached = 0) {
-  __syncthreads();  // the previous phase's LDS reads are done before dst is rewritten
+IRON_DEV void retire_loads() {
   // Every load issued so far (this phase's weights, issued a phase or two ago) completes here,
   // before the poll and the `issue` loads: the compiler then knows those registers are ready and
   // places no wait on them in this phase's compute, which would otherwise also wait for the
   // younger `issue` loads (vector loads complete in order).
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  bool issued = false;
-  auto issue_once = [&]() {
-    if (!issued) {
-      __builtin_amdgcn_sched_barrier(0);
-      issue();
-      __builtin_amdgcn_sched_barrier(0);
-      issued = true;
-    }
-  };
-  auto gave_up = [&](long long spins) {
-    return spins >= kSpinLimit ||
-           ((spins & 255) == 255 &&
-            __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u);
-  };
-  bool missing = false;
-  if (n_sent > 0) {
-    const bool has = (int)threadIdx.x < n_sent;
-    uint32_t want = 0;
-    unsigned long long* sp = has ? sent((int)threadIdx.x, want) : nullptr;
-    for (long long spins = 0;; ++spins) {
-      unsigned long long w = 0;
-      if (has) w = __hip_atomic_load(sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      missing = has && (uint32_t)(w >> 32) != want;
-      if (!missing || gave_up(spins)) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (missing) atomicOr(err, 1u);
-    if (__syncthreads_or(missing ? 1 : 0)) {
-      issue_once();
-      return false;
-    }
-  }
+}
+
+IRON_DEV bool gave_up(long long spins, uint32_t* err) {
+  return spins >= kSpinLimit ||
+         ((spins & 255) == 255 &&
+          __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u);
+}
+
+IRON_DEV unsigned long long poll_word(unsigned long long* w) {
+  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <class Issue>
+IRON_DEV void issue_fenced(Issue issue) {
+  __builtin_amdgcn_sched_barrier(0);
+  issue();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int NPT, class Src, class Issue>
+IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t* err) {
+  __syncthreads();  // the previous phase's LDS reads are done before dst is rewritten
+  retire_loads();
   bool pending[NPT];
   unsigned long long* ptr[NPT];
   uint32_t want[NPT];
@@ -232,25 +215,12 @@ IRON_DEV bool gather_words(int n, Src src, int n_sent, Sent sent, Issue issue, u
     pending[k] = j < n;
     ptr[k] = pending[k] ? src(j, want[k]) : nullptr;
   }
+  bool missing = false;
   for (long long spins = 0;; ++spins) {
     unsigned long long w[NPT];
-    if (n_sent > 0 && spins == 0) {
-      // slots below n_cached (the producers the sentinels vouch for) through the L2; the rest
-      // coherently
 #pragma unroll
-      for (int k = 0; k < NPT; ++k) {
-        if (!pending[k]) continue;
-        if ((int)threadIdx.x + 256 * k < n_cached)
-          w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
-        else
-          w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < NPT; ++k)
-        if (pending[k])
-          w[k] = __hip_atomic_load(ptr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    for (int k = 0; k < NPT; ++k)
+      if (pending[k]) w[k] = poll_word(ptr[k]);
     missing = false;
 #pragma unroll
     for (int k = 0; k < NPT; ++k) {
@@ -262,19 +232,81 @@ IRON_DEV bool gather_words(int n, Src src, int n_sent, Sent sent, Issue issue, u
         missing = true;
       }
     }
-    if (!missing || gave_up(spins)) break;
+    if (!missing || gave_up(spins, err)) break;
     __builtin_amdgcn_s_sleep(1);
   }
   if (missing) atomicOr(err, 1u);
   const bool ok = __syncthreads_or(missing ? 1 : 0) == 0;
-  issue_once();
+  issue_fenced(issue);
   return ok;
 }
 
-// No sentinel stage.
-struct NoSentinel {
-  IRON_DEV unsigned long long* operator()(int, uint32_t&) const { return nullptr; }
-};
+// Waits for a wide input published in per-producer blocks, plus n_ext single words, and puts the
+// payloads in LDS. Block q (q < n_blk) is `rows` <= ROWS words at blk(q, rows); its producer writes
+// them with one store instruction, the last word (the sentinel) included, and they go to
+// dst[ROWS q + r]. Thread q polls only block q's sentinel, which keeps the polling traffic at one
+// word per producer; once the sentinel is in, the same thread reads the block's other words (they
+// are normally in by then; any whose tag is still old is read again next round). So a block from
+// an early producer is read while slower producers are still computing, and only the last
+// block's read follows the last sentinel. Extra word i < n_ext (ext(i, tag)) goes to
+// dst[ROWS n_blk + i] and is polled by thread i. Same contract as gather_words otherwise, with
+// one tag for the blocks.
+template <int ROWS, class Blk, class Ext, class Issue>
+IRON_DEV bool gather_blocks(int n_blk, Blk blk, uint32_t tag, int n_ext, Ext ext, Issue issue,
+                            uint32_t* dst, uint32_t* err) {
+  static_assert(ROWS >= 1 && ROWS <= 32, "block words");
+  __syncthreads();
+  retire_loads();
+  const int t = threadIdx.x;
+  int rows = 0;
+  unsigned long long* bp = t < n_blk ? blk(t, rows) : nullptr;
+  bool sent_in = t >= n_blk;
+  uint32_t body = t < n_blk ? (1u << (rows - 1)) - 1u : 0u;  // block words still to read
+  uint32_t ewant = 0;
+  bool ext_pending = t < n_ext;
+  unsigned long long* ep = ext_pending ? ext(t, ewant) : nullptr;
+  uint32_t* bdst = dst + ROWS * t;
+  bool missing = false, first = true;
+  for (long long spins = 0;; ++spins) {
+    unsigned long long ws = 0, we = 0;
+    if (!sent_in) ws = poll_word(bp + rows - 1);
+    if (ext_pending) we = poll_word(ep);
+    if (!sent_in && (uint32_t)(ws >> 32) == tag) {
+      sent_in = true;
+      bdst[rows - 1] = (uint32_t)ws;
+    }
+    if (ext_pending && (uint32_t)(we >> 32) == ewant) {
+      ext_pending = false;
+      dst[ROWS * n_blk + t] = (uint32_t)we;
+    }
+    if (sent_in && body != 0u) {
+      // the first read of a block goes through the L2, so the workgroups of an XCD share one
+      // fetch of its line; a copy that is stale there (an old tag) is read again coherently
+      unsigned long long wb[ROWS - 1 > 0 ? ROWS - 1 : 1];
+#pragma unroll
+      for (int r = 0; r < ROWS - 1; ++r) {
+        if (!((body >> r) & 1u)) continue;
+        wb[r] = first ? __hip_atomic_load(bp + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT)
+                      : poll_word(bp + r);
+      }
+      first = false;
+#pragma unroll
+      for (int r = 0; r < ROWS - 1; ++r) {
+        if (((body >> r) & 1u) && (uint32_t)(wb[r] >> 32) == tag) {
+          bdst[r] = (uint32_t)wb[r];
+          body &= ~(1u << r);
+        }
+      }
+    }
+    missing = !sent_in || body != 0u || ext_pending;
+    if (!missing || gave_up(spins, err)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (missing) atomicOr(err, 1u);
+  const bool ok = __syncthreads_or(missing ? 1 : 0) == 0;
+  issue_fenced(issue);
+  return ok;
+}
 
 // This lane's activation slices from LDS, in the layout load_x_lane produces from global memory:
 // bf16 elements [c*1024 + 16 lane, +16) as two uint4, or fp32 ones as four.
@@ -408,9 +440,11 @@ IRON_DEV void prefetch_qkv(const PParams& p, const iron_layer_desc& L, int wg,
 }
 
 // The first K/V tile of this workgroup's split and the QKV epilogue's constants.
+// nq / nk: the q / k norm weights of dims lane and lane + 64 (bf16 pair, low half first); cs: the
+// (cos, sin) bf16 pair of rotary index lane.
 struct KVPrefetch {
   uint4 kr[kRows], vr[kRows];
-  uint4 nq, nk, a0, a1;
+  uint32_t nq, nk, cs;
 };
 
 // Rows t0 + 16u + 4 wave + lane/16 of a tile; rows at or past `bound` repeat row bound - 1 (and
@@ -450,14 +484,12 @@ IRON_DEV SplitRange split_range(int ctx, int split) {
 template <class S>
 IRON_DEV void prefetch_attn(const PParams& p, const iron_layer_desc& L, int wg, int pos,
                             KVPrefetch& kv) {
-  const int head = wg / S::NS, split = wg % S::NS, dl = threadIdx.x & 15;
+  const int head = wg / S::NS, split = wg % S::NS, lane = threadIdx.x & 63;
   const SplitRange r = split_range<S>(context_of(p, pos), split);
   load_kv_rows(p, L, head, r.begin, r.end, kv.kr, kv.vr);
-  kv.nq = ld_global((const uint4*)(L.n_qn + dl * 8));
-  kv.nk = ld_global((const uint4*)(L.n_kn + dl * 8));
-  const uint16_t* arow = p.ang + 16 * (dl & 7);
-  kv.a0 = ld_global((const uint4*)arow);
-  kv.a1 = ld_global((const uint4*)(arow + 8));
+  kv.nq = (uint32_t)ld_global(L.n_qn + lane) | ((uint32_t)ld_global(L.n_qn + lane + 64) << 16);
+  kv.nk = (uint32_t)ld_global(L.n_kn + lane) | ((uint32_t)ld_global(L.n_kn + lane + 64) << 16);
+  kv.cs = ld_global((const uint32_t*)p.ang + lane);
 }
 
 template <class S>
@@ -500,7 +532,7 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
   {
     const uint32_t tx = x_tag(ep, p.n_layers, l);
     auto src = [&](int j, uint32_t& t) { t = tx; return p.X + j; };
-    if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src, 0, NoSentinel(), issue, s_in,
+    if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src, issue, s_in,
                                            p.ctrl + 1))
       return false;
   }
@@ -515,6 +547,131 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
   for (int r = 0; r < R; ++r) h[r] = f64_to_bf16(acc[r][0]);
   store_bf16_pairs<R>(h, wg, S::MQKV, p.RAW, phase_tag(ep, p.n_layers, l, 0), s_out, nullptr);
   return true;
+}
+
+// The QKV head epilogue (qkv_head_dp/reference.py:13-33) for one head by one wavefront:
+//   y = bf16(RMSNorm(x) * w), r = bf16(RoPE(y)), r[i] = y[i] c_i - y[i+64] s_i,
+//   r[i+64] = y[i+64] c_i + y[i] s_i (i < 64).
+// Lane a owns dims a and a + 64, the two halves of one rotation, so no lane exchange is needed.
+// The operations and roundings are those of norm_rope8 and of the epilogue kernel in qkv.hip; the
+// sum of squares is exact in fp64, so its order does not matter.
+IRON_DEV void norm_rope_pair(const uint16_t* raw, uint32_t w2, uint32_t cs, int lane, double eps,
+                             uint16_t* out) {
+  const double x0 = bf16_to_f32(raw[lane]), x1 = bf16_to_f32(raw[lane + 64]);
+  const double inv = inv_rms(wave_sum_d(x0 * x0 + x1 * x1), kAttnD, eps);
+  const double y0 = round_bf16((float)((x0 * inv) * (double)bf16lo_to_f32(w2)));
+  const double y1 = round_bf16((float)((x1 * inv) * (double)bf16hi_to_f32(w2)));
+  const double c = bf16lo_to_f32(cs), s = bf16hi_to_f32(cs);
+  out[lane] = f64_to_bf16(y0 * c - y1 * s);
+  out[lane + 64] = f64_to_bf16(y1 * c + y0 * s);
+}
+
+// One tile of kTileTokens positions of the exact (fp64) core for a GQA pair (two query heads).
+// Lane (wave, row, dl) holds K/V rows t0 + tt, tt = 16u + 4 wave + row, head dims 8 dl..+8; rows
+// at or past t_end are masked, and the row at `pos` is the current token's (s_new) when has_new
+// (this split then ends at pos).
+//  1. each lane's 8-dim partial products go to LDS ([head][token][dl]);
+//  2. lane (wave, row, i) of a reducing row sums the 16 partials of one (token, head) pair:
+//     token 32 wave + 16 (row / 2) + i, head row % 2 -- 160 pairs on wavefronts 0..2 -- and the
+//     pair maxima give the tile maximum per head (a row maximum, then rows r and r ^ 2, then
+//     the four wavefronts through LDS);
+//  3. the pair lanes write e^(s - m) to LDS, and every lane reads back the U probabilities of its
+//     rows for the P.V products.
+// The q.k sums are exact in fp64 (bf16 products), so summing them by a tree over lanes gives the
+// values of a sequential sum; the exponential and the P.V order are those of attn_tile_f64.
+// Updates the running maximum m, sum l and unnormalised output o of the two heads; `it` is the
+// tile's index within this workgroup's sequence (0 = the first tile, which starts from zero).
+template <int U>
+IRON_DEV void attn_tile_pairs(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, bool has_new,
+                              int pos, const uint4 (&s_new)[2][16], const double (&qf)[2][8],
+                              double scale, int it, double (&m)[2], double (&l)[2],
+                              double (&o)[2][8], int wave, int lane, int row, int dl) {
+  constexpr int NT = 16 * U;
+  static_assert(NT <= 96, "three wavefronts of pair lanes");
+  // row stride 18 doubles: 16 consecutive tokens of one head fall in distinct LDS bank groups
+  __shared__ __align__(16) double s_ps[2][NT][18];
+  __shared__ __align__(16) double s_p[NT][2];
+  __shared__ double s_mx[4][2];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int tt = u * 16 + wave * 4 + row;
+    // rows past the split repeat its last row (load_kv_rows); when that row is the current
+    // token's, the cache still holds stale data there, so all of them take the new rows: every
+    // masked V row is then finite, and its zero probability adds exact zeros
+    if (has_new && t0 + tt >= pos) {
+      kr[u] = s_new[0][dl];
+      vr[u] = s_new[1][dl];
+    }
+    double kf[8];
+    unpack8d(kr[u], kf);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      double a = 0.0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a = fma(qf[h][j], kf[j], a);
+      s_ps[h][tt][dl] = a;
+    }
+  }
+  __syncthreads();
+  const int ph = row & 1, pt = wave * 32 + (row >> 1) * 16 + dl;
+  double s = -INFINITY;
+  if (pt < NT) {
+    double v[16];
+#pragma unroll
+    for (int k = 0; k < 16; k += 2) {
+      const double2 d = *(const double2*)&s_ps[ph][pt][k];
+      v[k] = d.x;
+      v[k + 1] = d.y;
+    }
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int k = 0; k < w; ++k) v[k] += v[k + w];
+    if (t0 + pt < t_end) s = v[0] * scale;
+  }
+  double wm = row16_max_d(s);
+  wm = fmax(wm, __shfl_xor(wm, 32));
+  if ((lane & 47) == 0) s_mx[wave][ph] = wm;  // lanes 0 and 16: heads 0 and 1
+  __syncthreads();
+  double mn[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const double t = fmax(fmax(s_mx[0][h], s_mx[1][h]), fmax(s_mx[2][h], s_mx[3][h]));
+    mn[h] = fmax(m[h], t);
+  }
+  // every tile of the loop holds at least one valid token, so mn is finite here
+  if (pt < NT) s_p[pt][ph] = s == -INFINITY ? 0.0 : exp(s - (ph ? mn[1] : mn[0]));
+  __syncthreads();
+  double pe[U][2];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const double2 d = *(const double2*)&s_p[u * 16 + wave * 4 + row][0];
+    pe[u][0] = d.x;
+    pe[u][1] = d.y;
+  }
+  if (it > 0) {  // rescale the running sums (the first tile starts from zero)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const double c = m[h] == -INFINITY ? 0.0 : exp(m[h] - mn[h]);
+      l[h] *= c;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[h][j] *= c;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    l[h] += tile_sum<U>(pe, h);
+    m[h] = mn[h];
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    double vf[8];
+    unpack8d(vr[u], vf);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[h][j] = fma(pe[u][h], vf[j], o[h][j]);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -543,39 +700,32 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
                                              : (S::QD + S::KVD + head * S::HD) / 2);
       return p.RAW + base + off;
     };
-    if (!gather_words<cdiv(n, 256)>(n, src, 0, NoSentinel(), issue, s_in, p.ctrl + 1))
+    if (!gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1))
       return false;
   }
-  const uint4* s_raw = (const uint4*)s_in;  // segment seg: 16 uint4 (128 bf16)
+  const uint16_t* s_raw = (const uint16_t*)s_in;  // segment seg: 128 bf16
 
   // QK RMSNorm + RoPE: wave h < HB rotates query head h; wave HB % 4 builds the current token's
   // K row (V unchanged) when this split owns its tile, and appends both to the caches
-  __shared__ uint4 s_q[HB][16];
+  __shared__ __align__(16) uint16_t s_q[HB][kAttnD];
   __shared__ uint4 s_new[2][16];
   const bool has_new = pos_ok && pos >= range.begin && pos < range.end;
-  if (wave < HB) {
-    double qn[8];
-    norm_rope8(s_raw[wave * 16 + dl], kv.nq, kv.a0, kv.a1, dl, (double)p.eps, qn);
-    if (row == 0) s_q[wave][dl] = pack8_bf16(qn);
-  }
-  if (has_new && wave == HB % 4) {
-    double kn[8];
-    norm_rope8(s_raw[HB * 16 + dl], kv.nk, kv.a0, kv.a1, dl, (double)p.eps, kn);
-    const uint4 kp = pack8_bf16(kn);
-    const uint4 vp = s_raw[(HB + 1) * 16 + dl];
-    if (row == 0) {
-      s_new[0][dl] = kp;
-      s_new[1][dl] = vp;
-      const size_t at = (size_t)head * p.kv_sh + (size_t)pos * p.kv_st + dl * 8;
-      st_global((uint4*)(L.k_cache + at), kp);
-      st_global((uint4*)(L.v_cache + at), vp);
-    }
+  const bool new_wave = has_new && wave == HB % 4;
+  if (wave < HB) norm_rope_pair(s_raw + wave * kAttnD, kv.nq, kv.cs, lane, (double)p.eps, s_q[wave]);
+  if (new_wave) {
+    norm_rope_pair(s_raw + HB * kAttnD, kv.nk, kv.cs, lane, (double)p.eps, (uint16_t*)s_new[0]);
+    if (lane < 16) s_new[1][lane] = ((const uint4*)s_raw)[(HB + 1) * 16 + lane];
   }
   __syncthreads();
+  if (new_wave && lane < 16) {
+    const size_t at = (size_t)head * p.kv_sh + (size_t)pos * p.kv_st + lane * 8;
+    st_global((uint4*)(L.k_cache + at), s_new[0][lane]);
+    st_global((uint4*)(L.v_cache + at), s_new[1][lane]);
+  }
 
   double qf[HB][8];
 #pragma unroll
-  for (int h = 0; h < HB; ++h) unpack8d(s_q[h][dl], qf[h]);
+  for (int h = 0; h < HB; ++h) unpack8d(((const uint4*)s_q[h])[dl], qf[h]);
   double m[HB], lsum[HB], o[HB][8];
 #pragma unroll
   for (int h = 0; h < HB; ++h) {
@@ -584,12 +734,11 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[h][j] = 0.0;
   }
-  __shared__ double s_mx[2][4][HB];
   int it = 0;
   for (int t0 = range.begin; t0 < range.end; t0 += kTileTokens, ++it) {
     if (it > 0) load_kv_rows(p, L, head, t0, range.end, kv.kr, kv.vr);
-    attn_tile_f64<HB, true, kRows>(kv.kr, kv.vr, t0, range.end, has_new, pos, s_new, qf,
-                                   p.scale, it, m, lsum, o, s_mx, wave, lane, row, dl);
+    attn_tile_pairs<kRows>(kv.kr, kv.vr, t0, range.end, has_new, pos, s_new, qf, p.scale, it, m,
+                           lsum, o, wave, lane, row, dl);
   }
   const uint32_t tp = phase_tag(ep, p.n_layers, l, 1);
   attn_finish_f64<HB>(m, lsum, o, wave, row, dl,
@@ -625,7 +774,7 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
       unsigned long long* part = part_of(s);
       return k < 2 * PER ? part + 2 * d0 + k : part + 2 * kAttnD + (k - 2 * PER);
     };
-    if (!gather_words<cdiv(n, 256)>(n, src, 0, NoSentinel(), issue, s_in, p.ctrl + 1))
+    if (!gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1))
       return false;
   }
   // thread (split sp, dim d): sp = t % NS, d = t / NS holds o_sp[d0 + d], m_sp and l_sp; the
@@ -666,7 +815,7 @@ IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s
   {
     const uint32_t ta = phase_tag(ep, p.n_layers, l, 2);
     auto src = [&](int j, uint32_t& t) { t = ta; return p.ATT + j; };
-    if (!gather_words<cdiv(S::QD / 2, 256)>(S::QD / 2, src, 0, NoSentinel(), issue, s_in,
+    if (!gather_words<cdiv(S::QD / 2, 256)>(S::QD / 2, src, issue, s_in,
                                             p.ctrl + 1))
       return false;
   }
@@ -706,7 +855,7 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
       t = j < half ? tx : ta;
       return j < half ? p.X + j : p.AO + (j - half);
     };
-    if (!gather_words<cdiv(S::D, 256)>(S::D, src, 0, NoSentinel(), issue, s_in, p.ctrl + 1))
+    if (!gather_words<cdiv(S::D, 256)>(S::D, src, issue, s_in, p.ctrl + 1))
       return false;
   }
   uint4 xl[NCH][4], al[NCH][4], x2l[NCH][2];
@@ -759,27 +908,20 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   {
     const uint32_t tg = phase_tag(ep, p.n_layers, l, 4), ta = phase_tag(ep, p.n_layers, l, 3);
     const uint32_t tx = x_tag(ep, p.n_layers, l);
-    auto src = [&](int j, uint32_t& t) {
-      if (j < S::FF) {
-        t = tg;
-        return gh + (j / S::GH_ROWS) * kGhBlock + j % S::GH_ROWS;
-      }
-      const int k = j - S::FF;
+    // gate/up workgroup q writes rows [GH_ROWS q, GH_ROWS (q + 1)) into block q, the last one
+    // (the sentinel) included, with one store instruction
+    static_assert(S::GH_ROWS * S::GH_PROD == S::FF, "whole gh blocks");
+    auto blk = [&](int q, int& rows) {
+      rows = S::FF - q * S::GH_ROWS < S::GH_ROWS ? S::FF - q * S::GH_ROWS : S::GH_ROWS;
+      return gh + q * kGhBlock;
+    };
+    auto ext = [&](int k, uint32_t& t) {
       const int word = wrow + (k % nres);
       const int wc = word < S::D / 2 ? word : 0;  // rows past D are never stored
       t = k < nres ? ta : tx;
       return (k < nres ? p.AO : p.X) + wc;
     };
-    // gate/up workgroup q writes rows [GH_ROWS q, GH_ROWS (q + 1)) into block q; its last row
-    // is the sentinel
-    constexpr int n_sent = S::GH_PROD;
-    auto sent = [&](int q, uint32_t& t) {
-      t = tg;
-      const int rows = S::FF - q * S::GH_ROWS < S::GH_ROWS ? S::FF - q * S::GH_ROWS : S::GH_ROWS;
-      return gh + q * kGhBlock + rows - 1;
-    };
-    if (!gather_words<cdiv(S::FF + 2 * nres, 256)>(S::FF + 2 * nres, src, n_sent, sent, issue,
-                                                    s_in, p.ctrl + 1, S::FF))
+    if (!gather_blocks<S::GH_ROWS>(S::GH_PROD, blk, tg, 2 * nres, ext, issue, s_in, p.ctrl + 1))
       return false;
   }
   uint4 xl[NCH][4], x2l[NCH][2] = {}, nwl[NCH][2] = {};
