@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 3
+#define IRON_ABI_VERSION 4
 
 enum iron_status {
   IRON_OK = 0,
@@ -281,6 +281,14 @@ int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, i
 /* Host-only check of the device-side divide used for wire row-blocks: returns n / d computed with
  * the same multiply-shift sequence the kernels use (test hook; no reference counterpart). */
 uint32_t iron_test_fastdiv(uint32_t n, uint32_t d);
+
+/* Device check of the bf16 rounding every kernel uses (test hook; no reference counterpart). The
+ * caller zero-fills out[0] and out[2] and sets out[1] = 0xffffffff; after the stream synchronises,
+ * out[0] = number of fp32 bit patterns whose hardware round-to-nearest-even bf16 differs from the
+ * integer form (NaN inputs: a non-NaN result), out[1] = the smallest such pattern, out[2] = the
+ * bf16 of the fp64 value 1 + 2^-8 + 2^-40, which is 0x3f80 when fp64 values round to fp32 and
+ * then to bf16 (as torch does), 0x3f81 if they were rounded once. */
+int iron_test_bf16_round(uint32_t* out, void* stream);
 
 /* Measurement hook (no reference counterpart): streams `bytes` (a multiple of 16, 16-byte aligned)
  * through 16-byte loads with a grid of `blocks` x 256 threads and writes one xor word per thread

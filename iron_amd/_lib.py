@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
-ABI_VERSION = 3          # IRON_ABI_VERSION of include/iron_hip.h
+ABI_VERSION = 4          # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2
@@ -103,6 +103,7 @@ SIGNATURES = {
                                         _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_f, _c_f,
                                         _c_vp, _c_sz, _c_vp]),
     "iron_test_fastdiv": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32]),
+    "iron_test_bf16_round": (_c_int, [_c_vp, _c_vp]),
     "iron_stream_read": (_c_int, [_c_vp, _c_sz, _c_vp, _c_int, _c_vp]),
 }
 

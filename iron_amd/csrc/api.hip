@@ -247,6 +247,31 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
   out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = a;
 }
 
+// Exhaustive check of the hardware bf16 rounding: thread i covers fp32 bit patterns
+// [i * per, (i + 1) * per). out[0] counts patterns whose f32_to_bf16 differs from
+// f32_to_bf16_rne (NaNs: a result that is not a NaN), out[1] is the smallest such pattern, and
+// out[2] is f64_to_bf16(1 + 2^-8 + 2^-40): 0x3f80 when it rounds twice (fp64 -> fp32 -> bf16) as
+// required, 0x3f81 if the two roundings were fused into one.
+__global__ __launch_bounds__(256) void bf16_round_check_kernel(uint32_t per, uint32_t* out) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t bad = 0, first = 0xffffffffu;
+  for (uint32_t k = 0; k < per; ++k) {
+    const uint32_t u = i * per + k;
+    const float f = __uint_as_float(u);
+    const uint32_t hw = f32_to_bf16(f), sw = f32_to_bf16_rne(f);
+    const bool nan_in = (u & 0x7fffffffu) > 0x7f800000u;
+    const bool ok = nan_in ? ((hw & 0x7fffu) > 0x7f80u) : hw == sw;
+    if (!ok) {
+      ++bad;
+      first = u < first ? u : first;
+    }
+  }
+  if (bad) {
+    atomicAdd(out, bad);
+    atomicMin(out + 1, first);
+  }
+  if (i == 0) out[2] = f64_to_bf16(1.0 + 0x1p-8 + 0x1p-40);
+}
 
 }  // namespace
 
@@ -299,6 +324,15 @@ const char* iron_last_error(void) { return iron::g_err; }
 uint32_t iron_test_fastdiv(uint32_t n, uint32_t d) {
   if (d == 0) return 0xffffffffu;
   return fastdiv_host(n, make_fastdiv(d));
+}
+
+int iron_test_bf16_round(uint32_t* out, void* stream) {
+  iron::clear_error();
+  if (!out) return iron::fail(IRON_ERR_NULL, "iron_test_bf16_round: null buffer");
+  // 2^20 threads x 4096 patterns = every fp32 bit pattern; out[0..2] start as 0, ~0, 0
+  hipLaunchKernelGGL(bf16_round_check_kernel, dim3(4096), dim3(256), 0, (hipStream_t)stream,
+                     4096u, out);
+  return iron::check_launch("iron_test_bf16_round");
 }
 
 int iron_stream_read(const void* p, size_t bytes, uint32_t* out, int blocks, void* stream) {

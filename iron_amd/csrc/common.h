@@ -23,8 +23,19 @@ IRON_DEV float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 IRON_DEV float bf16lo_to_f32(uint32_t packed) { return __uint_as_float(packed << 16); }
 IRON_DEV float bf16hi_to_f32(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
 
+// fp32 -> bf16 with round to nearest, ties to even: one gfx950 instruction (v_cvt_pk_bf16_f32). A
+// NaN stays a NaN. iron_test_bf16_round checks it against f32_to_bf16_rne on every fp32 value.
+// The empty asm pins the fp32 operand: for an fp32 value just rounded from fp64 the compiler would
+// otherwise fuse the two roundings into one from fp64 (round to odd, then to even), which
+// differs from rounding twice, the torch semantics every caller relies on.
 IRON_DEV uint16_t f32_to_bf16(float f) {
-  // branch-free (a select, not a divergent branch, keeps the NaN case off the common path)
+  asm("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// The same rounding in integer arithmetic (NaN -> the quiet NaN with the input's sign and top
+// payload bits): the reference form the hardware conversion is checked against.
+IRON_DEV uint16_t f32_to_bf16_rne(float f) {
   const uint32_t u = __float_as_uint(f);
   const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
   const uint32_t qnan = (u >> 16) | 0x40u;

@@ -233,7 +233,6 @@ IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t*
       }
     }
     if (!missing || gave_up(spins, err)) break;
-    __builtin_amdgcn_s_sleep(1);
   }
   if (missing) atomicOr(err, 1u);
   const bool ok = __syncthreads_or(missing ? 1 : 0) == 0;
@@ -300,7 +299,6 @@ IRON_DEV bool gather_blocks(int n_blk, Blk blk, uint32_t tag, int n_ext, Ext ext
     }
     missing = !sent_in || body != 0u || ext_pending;
     if (!missing || gave_up(spins, err)) break;
-    __builtin_amdgcn_s_sleep(1);
   }
   if (missing) atomicOr(err, 1u);
   const bool ok = __syncthreads_or(missing ? 1 : 0) == 0;
@@ -674,6 +672,43 @@ IRON_DEV void attn_tile_pairs(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end,
   }
 }
 
+// The end of the exact core for a GQA pair (attn_finish_f64 with HB = 2): the 16 token rows of
+// the workgroup (4 per wavefront) hold partial sums under the same offsets m, so they add, as a
+// tree over rows. The rows go through LDS with the four 16-byte chunks of each lane's dims
+// 8 dl..+8 XOR-permuted by dl / 4, so the 16 lanes of a row write 16 distinct bank groups.
+// Thread (oh, od) emits head oh, dim od: emit(oh, od, O, L, M).
+template <class Emit>
+IRON_DEV void attn_finish_pairs(const double (&m)[2], const double (&l)[2],
+                                const double (&o)[2][8], int wave, int row, int dl, Emit emit) {
+  __shared__ __align__(16) double s_o[16][2][kAttnD];
+  __shared__ double s_l[16][2];
+  const int rr = wave * 4 + row, sw = (dl >> 2) & 3;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp)
+      *(double2*)&s_o[rr][h][8 * dl + 2 * (jp ^ sw)] = make_double2(o[h][2 * jp], o[h][2 * jp + 1]);
+    if (dl == 0) s_l[rr][h] = l[h];
+  }
+  __syncthreads();
+  const int oh = threadIdx.x >> 7, od = threadIdx.x & 127, d8 = od >> 3;
+  const int at = 8 * d8 + 2 * (((od >> 1) & 3) ^ ((d8 >> 2) & 3)) + (od & 1);
+  double so[16], sl[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    so[r] = s_o[r][oh][at];
+    sl[r] = s_l[r][oh];
+  }
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int r = 0; r < w; ++r) {
+      so[r] += so[r + w];
+      sl[r] += sl[r + w];
+    }
+  emit(oh, od, so[0], sl[0], oh ? m[1] : m[0]);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Phase B: the QKV epilogue and the exact attention core over this split's positions. Workgroup
 // (kv, split) handles a contiguous 1/NS of the context of KV head kv and writes its partial
@@ -741,8 +776,8 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
                            lsum, o, wave, lane, row, dl);
   }
   const uint32_t tp = phase_tag(ep, p.n_layers, l, 1);
-  attn_finish_f64<HB>(m, lsum, o, wave, row, dl,
-                      [&](int oh, int od, double O, double Ls, double M) {
+  attn_finish_pairs(m, lsum, o, wave, row, dl,
+                    [&](int oh, int od, double O, double Ls, double M) {
     unsigned long long* part =
         p.PART + ((size_t)(head * HB + oh) * NS + split) * (2 * (kAttnD + 2));
     put_double(part + 2 * od, O, tp);

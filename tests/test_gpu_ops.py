@@ -411,3 +411,22 @@ def test_lm_head_argmax(kind, lib):
     # device argmax == first index of the max of the bf16 logits
     assert int(tokens.item()) == int(torch.argmax(got.float()))
     assert int(keys.item()) == 0  # consumed and reset
+
+
+def test_bf16_rounding_exhaustive(lib):
+    """Every kernel rounds fp32 -> bf16 with the gfx950 conversion instruction: it must equal the
+    integer round-to-nearest-even (the oracle's f32_to_bf16_rne) on all 2^32 fp32 bit patterns, and
+    fp64 values must round twice (fp64 -> fp32 -> bf16, as torch and the oracle do)."""
+    from iron_amd import _lib
+
+    _say("bf16 rounding: all 2^32 fp32 patterns")
+    out = torch.tensor([0, -1, 0], dtype=torch.int32, device=DEV)
+    _lib.call("iron_test_bf16_round", out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    bad, first, dbl = (int(v) & 0xFFFFFFFF for v in out.cpu().tolist())
+    assert bad == 0, f"{bad} fp32 patterns round differently, first {first:#010x}"
+    # 1 + 2^-8 + 2^-40: fp32 drops 2^-40, the bf16 tie then goes to even (1.0); one rounding from
+    # fp64 would go up to 1 + 2^-7
+    x = torch.tensor([1.0 + 2.0 ** -8 + 2.0 ** -40], dtype=torch.float64)
+    want = int(x.float().to(torch.bfloat16).view(torch.int16).item()) & 0xFFFF
+    assert want == 0x3F80 and dbl == want
