@@ -91,12 +91,15 @@ IRON_DEV void st_global<uint4>(uint4* p, const uint4& v) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Wavefront reductions (wave64) with DPP.
+// Wavefront reductions (wave64) with DPP. The moves leave the destination of lanes they do not
+// write undefined (no old value, which would cost a move per 32 bits): every control used here
+// writes every lane, except the row_bcast steps of wave_sum*, whose unwritten rows (0 and 2,
+// then 0 and 1) are never read again -- the total is taken from lane 63.
 // ---------------------------------------------------------------------------------------------
 template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
 IRON_DEV float dpp_f(float v) {
-  return __int_as_float(
-      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, ROW_MASK, BANK_MASK,
+                                                 false));
 }
 
 // Sum over each 16-lane row; every lane of the row receives the row's sum.
@@ -125,8 +128,8 @@ IRON_DEV float row16_max(float v) {
 }
 
 IRON_DEV float wave_max(float v) {
-  // Masked rows of the bcast steps read `old` = 0, which would clamp negative maxima, so the
-  // cross-row steps use xor-shuffles instead.
+  // every lane receives the maximum, so the cross-row steps are xor-shuffles (a row_bcast step
+  // leaves rows unwritten)
   v = row16_max(v);
   v = fmaxf(v, __shfl_xor(v, 16));
   v = fmaxf(v, __shfl_xor(v, 32));
@@ -136,8 +139,8 @@ IRON_DEV float wave_max(float v) {
 // ---- fp64 variants: DPP moves 32 bits, so a double is moved as two halves.
 template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
 IRON_DEV double dpp_d(double v) {
-  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, ROW_MASK, BANK_MASK, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, ROW_MASK, BANK_MASK, false);
+  const int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, ROW_MASK, BANK_MASK, false);
+  const int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, ROW_MASK, BANK_MASK, false);
   return __hiloint2double(hi, lo);
 }
 
