@@ -65,12 +65,13 @@ constexpr int kTileTokens = 16 * kRows;
 // store instruction), so seeing its last word means the whole line has been written.
 constexpr int kGhBuffers = 4;
 // Every hand-off buffer that many workgroups poll (x, raw qkv, the attention output, a, gh) is
-// written in kCopies copies kCopyWords words (64 KiB) apart, and the workgroups of XCD c (wg % 8)
+// written in kCopies copies kCopyWords words (32 KiB) apart, and the workgroups of XCD c (wg % 8)
 // read copy c. One copy concentrates every workgroup's polls on the one or two memory channels
 // that hold a few KiB; spread over copies, a poll's round trip is shorter (measured: 0.4 us per
-// layer for the attention output alone).
+// layer for the attention output alone, 53 us per token for all five). 4 or 16 copies, or copies
+// 16 or 64 KiB apart, measured slower; copies not 256-byte aligned, much slower.
 constexpr int kCopies = 8;
-constexpr size_t kCopyWords = 8192;
+constexpr size_t kCopyWords = 4096;
 constexpr int kGhBlock = 16;
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
