@@ -91,11 +91,12 @@ struct Shape {
   static constexpr int MERGE_WPS = 2 * MERGE_PER + 4;  // words per split: o[PER], m, l as fp64
   // LDS words of the widest phase input
   static constexpr int LDS_WORDS =
-      cmax(cmax(D, QD / 2), cmax(FF + 4 * RF, cmax(NS * MERGE_WPS, (HB + 2) * 64)));
+      cmax(cmax(D, QD / 2), cmax(FF, cmax(NS * MERGE_WPS, (HB + 2) * 64)));
   static constexpr int RMAX = cmax(cmax(RA, RD), RF);
   static constexpr int GH_ROWS = 4 * RE;               // gh rows one workgroup produces
   static constexpr int GH_PROD = cdiv(FF, GH_ROWS);    // gate/up workgroups with rows
   static constexpr int GH_WORDS = GH_PROD * kGhBlock;  // one gh buffer, blocked per producer
+  static constexpr int XW = 2 * RF;  // words of x (and of a) one down (Wo) workgroup writes
   // words between the replicated copies of the kGhBuffers gh buffers (a multiple of kCopyWords)
   static constexpr size_t GH_COPY =
       (((size_t)kGhBuffers * GH_WORDS + kCopyWords - 1) / kCopyWords) * kCopyWords;
@@ -108,6 +109,7 @@ struct Shape {
                 "one merge thread per (split, dim)");
   static_assert(D % 16 == 0 && FF % 16 == 0 && MQKV % 2 == 0, "GEMV widths");
   static_assert(GH_ROWS <= kGhBlock && GH_PROD <= kNT, "gh blocks");
+  static_assert(RD == RF, "the Wo and down phases own the same rows");
   static_assert(D / 2 <= (int)kCopyWords && MQKV / 2 <= (int)kCopyWords &&
                     QD / 2 <= (int)kCopyWords, "hand-off copies");
 };
@@ -331,6 +333,11 @@ IRON_DEV bool gather_blocks(int n_blk, Blk blk, uint32_t tag, int n_ext, Ext ext
   return ok;
 }
 
+// No extra words for gather_blocks.
+struct NoExt {
+  IRON_DEV unsigned long long* operator()(int, uint32_t&) const { return nullptr; }
+};
+
 // This lane's activation slices from LDS, in the layout load_x_lane produces from global memory:
 // bf16 elements [c*1024 + 16 lane, +16) as two uint4, or fp32 ones as four.
 template <int NCH>
@@ -407,6 +414,16 @@ IRON_DEV void store_bf16_pairs(const uint16_t (&h)[R], int wg, int M, unsigned l
       if (plain) ((uint32_t*)plain)[row / 2] = pair;
     }
   }
+}
+
+// The 2R words store_bf16_pairs (odd R) just published for this workgroup, kept in LDS for a later
+// phase of the same workgroup: word t = rows 2t, 2t+1 of its 4R rows. It reads s_out after the
+// store's barrier, so it needs no barrier of its own.
+template <int R>
+IRON_DEV void keep_own_words(const uint16_t* s_out, uint32_t* own) {
+  static_assert(R % 2 == 1, "the odd-R store stages its rows in s_out");
+  const int t = threadIdx.x;
+  if (t < 2 * R) own[t] = (uint32_t)s_out[2 * t] | ((uint32_t)s_out[2 * t + 1] << 16);
 }
 
 // Max / sum over the G consecutive threads of a group (G = 32 or 64 within a wavefront, G = 128
@@ -870,7 +887,8 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
 // ---------------------------------------------------------------------------------------------
 template <class S, class Issue>
 IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s_in,
-                       uint16_t* s_out, const W8<S::RD, S::CD>& W, Issue issue) {
+                       uint16_t* s_out, uint32_t* s_own, const W8<S::RD, S::CD>& W,
+                       Issue issue) {
   constexpr int R = S::RD, NCH = S::CD;
   const int lane = threadIdx.x & 63;
   const int row0 = row0_of<S>(wg, R);
@@ -894,6 +912,7 @@ IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s
 #pragma unroll
   for (int r = 0; r < R; ++r) h[r] = f64_to_bf16(acc[r][0]);
   store_bf16_pairs<R>(h, wg, S::D, p.AO, phase_tag(ep, p.n_layers, l, 3), s_out, nullptr);
+  keep_own_words<R>(s_out, s_own);  // the down phase's residual a
   return true;
 }
 
@@ -962,20 +981,18 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
 // ---------------------------------------------------------------------------------------------
 template <class S, class Issue>
 IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s_in,
-                         uint16_t* s_out, const W8<S::RF, S::CF>& W, Issue issue) {
+                         uint16_t* s_out, uint32_t* s_own, const W8<S::RF, S::CF>& W,
+                         Issue issue) {
   constexpr int R = S::RF, NCH = S::CF;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row0 = row0_of<S>(wg, R);
   GemvParams g = gemv_of(p.g_d, nullptr, S::D, S::FF);
   g.pro = PRO_F32;
-  // LDS words [0, FF): gh; then a and x of this workgroup's 4R rows, 2R words each
-  constexpr int nres = 2 * R;
+  // LDS words [0, FF): gh; the residual (a and x of this workgroup's 4R rows) is in s_own
   unsigned long long* const gh =
       copy_for(p.GH, S::GH_COPY, wg) + (l % kGhBuffers) * S::GH_WORDS;
-  const int wrow = wg * nres;  // first word (row pair) of this workgroup's rows
   {
-    const uint32_t tg = phase_tag(ep, p.n_layers, l, 4), ta = phase_tag(ep, p.n_layers, l, 3);
-    const uint32_t tx = x_tag(ep, p.n_layers, l);
+    const uint32_t tg = phase_tag(ep, p.n_layers, l, 4);
     // gate/up workgroup q writes rows [GH_ROWS q, GH_ROWS (q + 1)) into block q, the last one
     // (the sentinel) included, with one store instruction
     static_assert(S::GH_ROWS * S::GH_PROD == S::FF, "whole gh blocks");
@@ -983,13 +1000,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
       rows = S::FF - q * S::GH_ROWS < S::GH_ROWS ? S::FF - q * S::GH_ROWS : S::GH_ROWS;
       return gh + q * kGhBlock;
     };
-    auto ext = [&](int k, uint32_t& t) {
-      const int word = wrow + (k % nres);
-      const int wc = word < S::D / 2 ? word : 0;  // rows past D are never stored
-      t = k < nres ? ta : tx;
-      return copy_for(k < nres ? p.AO : p.X, kCopyWords, wg) + wc;
-    };
-    if (!gather_blocks<S::GH_ROWS>(S::GH_PROD, blk, tg, 2 * nres, ext, issue, s_in, p.ctrl + 1))
+    if (!gather_blocks<S::GH_ROWS>(S::GH_PROD, blk, tg, 0, NoExt(), issue, s_in, p.ctrl + 1))
       return false;
   }
   uint4 xl[NCH][4], x2l[NCH][2] = {}, nwl[NCH][2] = {};
@@ -998,7 +1009,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   prologue_lane<NCH, 16>(g, lane, xl, x2l, nwl, xf);
   double acc[R][1];
   dot_w8_lane<R, NCH>(g, W.w, W.sc, xf, row0, lane, acc);
-  const uint16_t* s_res = (const uint16_t*)(s_in + S::FF);  // a rows, then x rows (4R each)
+  const uint16_t* s_res = (const uint16_t*)s_own;  // a rows, then x rows (4R each)
   uint16_t h[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -1008,6 +1019,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   }
   store_bf16_pairs<R>(h, wg, S::D, p.X, phase_tag(ep, p.n_layers, l, 5), s_out,
                       l == p.n_layers - 1 ? p.x_out : nullptr);
+  keep_own_words<R>(s_out, s_own + S::XW);  // the next layer's residual x (its reads are done)
   return true;
 }
 
@@ -1019,6 +1031,10 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
   __shared__ uint32_t s_in[S::LDS_WORDS];
   __shared__ uint16_t s_out[4 * S::RMAX];
   __shared__ float s_gh[4 * S::RE];
+  // this workgroup's own rows of a (words [0, XW), from its Wo phase) and of the layer input x
+  // (words [XW, 2 XW), from its previous down phase): the residual of its down phase, kept here
+  // rather than polled back from the hand-off buffers
+  __shared__ uint32_t s_own[2 * S::XW];
   const int wg = blockIdx.x;
   const uint32_t ep = p.ctrl[0];
   const int pos = *p.pos;
@@ -1030,6 +1046,10 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
     for (int j = wg * 64 + threadIdx.x; j < S::D / 2; j += kNT * 64)
       put_word_copies(p.X + j, kCopyWords, ((const uint32_t*)p.x_in)[j],
                       x_tag(ep, p.n_layers, 0));
+  if (threadIdx.x < S::XW) {
+    const int word = wg * S::XW + threadIdx.x;
+    s_own[S::XW + threadIdx.x] = word < S::D / 2 ? ((const uint32_t*)p.x_in)[word] : 0u;
+  }
   for (int l = 0; l < p.n_layers; ++l) {
     const iron_layer_desc L = p.layers[l];
     KVPrefetch kv;
@@ -1043,11 +1063,12 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
         phase_attn<S>(p, L, l, wg, ep, pos, s_in, kv, [&]() { prefetch_wo<S>(p, L, wg, wo); }) &&
         phase_merge<S>(p, l, wg, ep, s_in,
                        [&]() { prefetch_gateup<S>(p, L, wg, wgate, wup, n_post); }) &&
-        phase_wo<S>(p, l, wg, ep, s_in, s_out, wo, [&]() { prefetch_down<S>(p, L, wg, wdown); }) &&
+        phase_wo<S>(p, l, wg, ep, s_in, s_out, s_own, wo,
+                    [&]() { prefetch_down<S>(p, L, wg, wdown); }) &&
         phase_gateup<S>(p, l, wg, ep, s_in, s_gh, wgate, wup, n_post, [&]() {
           if (l + 1 < p.n_layers) prefetch_qkv<S>(p, p.layers[l + 1], wg, wqkv, n_in);
         }) &&
-        phase_down<S>(p, l, wg, ep, s_in, s_out, wdown, []() {});
+        phase_down<S>(p, l, wg, ep, s_in, s_out, s_own, wdown, []() {});
     if (!ok) break;
   }
   // Advance the epoch for the next launch. Workgroup 0 finishes only after every workgroup has
