@@ -40,8 +40,8 @@ HBM_PEAK_GBS = 8000.0
 # counters read for a plain 256 MiB device copy (profiles/decode_qwen3_0_6b_hbm_traffic.md).
 LM_HEAD_BF16_TRAFFIC = 311_696_320
 # HBM bytes per launch of the persistent layers kernel (all 28 layers), same method:
-# FETCH_SIZE 386849.72 KiB x 2.0 + WRITE_SIZE 61500.03 KiB x 1.0 at context 2048..2057.
-PERSISTENT_TRAFFIC = 855_244_256
+# FETCH_SIZE 387119.80 KiB x 2.0 + WRITE_SIZE 77208.03 KiB x 1.0 at context 2048..2057.
+PERSISTENT_TRAFFIC = 871_882_380
 
 
 def parse():
