@@ -557,6 +557,31 @@ IRON_DEV void prefetch_down(const PParams& p, const iron_layer_desc& L, int wg,
   fetch_w8<S::RF, S::CF>(g, g.w, row0_of<S>(wg, S::RF), threadIdx.x & 63, W.w, W.sc);
 }
 
+// Wavefront totals of R rows of per-lane partials, in exactly wave_sum_d's order (a balanced tree
+// over the 64 lanes in lane order, so bit-identical to it) with the work shared: the partials go
+// through this wavefront's LDS rows s[R][64]; lane j of group r (lanes 8r..8r+7) adds lanes
+// 8j..8j+7 of row r (the tree's first three levels), and the group combines its eight sums with
+// three DPP steps (the last three). R separate wave_sum_d calls cost ~22 instructions a row.
+// Returns row (lane / 8)'s total in every lane of that group; lanes from 8R on return garbage.
+template <int R>
+IRON_DEV double rows_sum_d(const double (&v)[R], double (*s)[64]) {
+  static_assert(R >= 1 && R <= 8, "one 8-lane group per row");
+  const int lane = threadIdx.x & 63, grp = lane >> 3, j = lane & 7;
+#pragma unroll
+  for (int r = 0; r < R; ++r) s[r][lane] = v[r];
+  // one wavefront's LDS accesses complete in order: its reads below see its writes
+  double t = 0.0;
+  if (grp < R) {
+    const double2* q = (const double2*)&s[grp][8 * j];
+    const double2 a = q[0], b = q[1], c = q[2], d = q[3];
+    t = ((a.x + a.y) + (b.x + b.y)) + ((c.x + c.y) + (d.x + d.y));
+  }
+  t += dpp_d<0xb1>(t);   // quad_perm [1,0,3,2]: lane groups 2i, 2i+1 (16-lane rows)
+  t += dpp_d<0x4e>(t);   // quad_perm [2,3,0,1]: rows 0+1, 2+3
+  t += dpp_d<0x141>(t);  // row_half_mirror: (0+1) + (2+3)
+  return t;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Phase A: raw = bf16(Wqkv . bf16(RMSNorm(x) * n_in))                [MQKV rows x D]
 // ---------------------------------------------------------------------------------------------
@@ -583,11 +608,27 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
   float xf[NCH][16];
   prologue_lane<NCH, 16>(g, lane, xl, x2l, nwl, xf);
   double acc[R][1];
-  dot_w8_lane<R, NCH>(g, W.w, W.sc, xf, row0, lane, acc);
-  uint16_t h[R];
+  const uint32_t tag = phase_tag(ep, p.n_layers, l, 0);
+  if constexpr (R % 2 == 0 && R <= 8) {
+    // a wavefront's rows pair up within it
+    dot_w8_lane<R, NCH, false>(g, W.w, W.sc, xf, row0, lane, acc);
+    __shared__ double s_rows[4][R][64];
+    double v[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) h[r] = f64_to_bf16(acc[r][0]);
-  store_bf16_pairs<R>(h, wg, S::MQKV, p.RAW, phase_tag(ep, p.n_layers, l, 0), s_out, nullptr);
+    for (int r = 0; r < R; ++r) v[r] = acc[r][0];
+    // row r's total is in lanes 8r..8r+7; lane 16k pairs rows 2k and 2k+1 (row_ror:8)
+    const uint32_t hb = f64_to_bf16(rows_sum_d<R>(v, s_rows[threadIdx.x >> 6]));
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hb, 0x128, 0xf, 0xf, false);
+    const int k = lane >> 4, row = row0 + 2 * k;
+    if ((lane & 15) == 0 && k < R / 2 && row < S::MQKV)
+      put_word_copies(p.RAW + row / 2, kCopyWords, (hb & 0xffffu) | (hi << 16), tag);
+  } else {
+    dot_w8_lane<R, NCH>(g, W.w, W.sc, xf, row0, lane, acc);
+    uint16_t h[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) h[r] = f64_to_bf16(acc[r][0]);
+    store_bf16_pairs<R>(h, wg, S::MQKV, p.RAW, tag, s_out, nullptr);
+  }
   return true;
 }
 
@@ -955,19 +996,23 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
   float xf[NCH][16];
   prologue_lane<NCH, 16>(g, lane, xl, x2l, nwl, xf);
   double acc[R][1], acc2[R][1];
-  dot_w8_lane<R, NCH>(g, Wg.w, Wg.sc, xf, row0, lane, acc);
-  dot_w8_lane<R, NCH>(g, Wu.w, Wu.sc, xf, row0, lane, acc2);
+  dot_w8_lane<R, NCH, false>(g, Wg.w, Wg.sc, xf, row0, lane, acc);
+  dot_w8_lane<R, NCH, false>(g, Wu.w, Wu.sc, xf, row0, lane, acc2);
   // the workgroup's 4R gh values leave together from wave 0 (the down phase polls the last one
   // as the sentinel of the group)
   const int wave = threadIdx.x >> 6;
-  double g_r = acc[0][0], u_r = acc2[0][0];  // lane r < R takes row r (one SiLU per lane)
+  static_assert(2 * R <= 8, "gate and up rows of a wavefront in 8-lane groups");
+  __shared__ double s_rows[4][2 * R][64];
+  double v[2 * R];  // gate row r in group 2r, up row r in group 2r + 1 (the same 16-lane row)
 #pragma unroll
-  for (int r = 1; r < R; ++r) {
-    g_r = lane == r ? acc[r][0] : g_r;
-    u_r = lane == r ? acc2[r][0] : u_r;
+  for (int r = 0; r < R; ++r) {
+    v[2 * r] = acc[r][0];
+    v[2 * r + 1] = acc2[r][0];
   }
-  const float gh = (float)silu_mul(g_r, u_r);
-  if (lane < R) s_gh[wave * R + lane] = gh;
+  const double tot = rows_sum_d<2 * R>(v, s_rows[wave]);
+  const double u_r = dpp_d<0x128>(tot);  // row_ror:8: lane 16r gets up row r
+  const float gh = (float)silu_mul(tot, u_r);  // lane 16r: SiLU(gate r) * up r
+  if ((lane & 15) == 0 && (lane >> 4) < R) s_gh[wave * R + (lane >> 4)] = gh;
   __syncthreads();
   const int t = threadIdx.x, row = wg * S::GH_ROWS + t;
   if (t < S::GH_ROWS && row < S::FF)

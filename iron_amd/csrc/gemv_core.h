@@ -204,7 +204,9 @@ IRON_DEV void prologue_lane(const GemvParams& p, int lane, const uint4 (&xl)[NCH
   }
 }
 
-template <int R, int NCH>
+// With REDUCE, acc[r] ends as row r's total in every lane (wave_sum_d); without, as this lane's
+// partial, for a caller that reduces several rows together.
+template <int R, int NCH, bool REDUCE = true>
 IRON_DEV void dot_w8_lane(const GemvParams& p, const uint4 (&w)[R][NCH],
                           const uint32_t (&sc)[R][NCH], const float (&xf)[NCH][16], int row0,
                           int lane, double (&acc)[R][1]) {
@@ -231,8 +233,10 @@ IRON_DEV void dot_w8_lane(const GemvParams& p, const uint4 (&w)[R][NCH],
                       acc[r][0]);
     }
   }
+  if constexpr (REDUCE) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r][0] = wave_sum_d(acc[r][0]);
+    for (int r = 0; r < R; ++r) acc[r][0] = wave_sum_d(acc[r][0]);
+  }
 }
 
 // SiLU(g) * u in fp64 with the golden's numerically stable sigmoid
