@@ -291,9 +291,9 @@ uint32_t iron_test_fastdiv(uint32_t n, uint32_t d);
 int iron_test_bf16_round(uint32_t* out, void* stream);
 
 /* Measurement hook (no reference counterpart): streams `bytes` (a multiple of 16, 16-byte aligned)
- * through 16-byte loads with a grid of `blocks` x 256 threads and writes one xor word per thread
- * to out[blocks * 256]. Its time is the achievable HBM read rate that the roofline figures are
- * read against. */
+ * through 16-byte loads, workgroup b of `blocks` (x 256 threads) reading the b-th contiguous
+ * 1/blocks of the buffer, and writes one xor word per thread to out[blocks * 256]. Its time is
+ * the achievable HBM read rate that the roofline figures are read against. */
 int iron_stream_read(const void* p, size_t bytes, uint32_t* out, int blocks, void* stream);
 
 #ifdef __cplusplus
