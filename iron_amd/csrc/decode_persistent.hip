@@ -429,8 +429,25 @@ IRON_DEV void keep_own_words(const uint16_t* s_out, uint32_t* own) {
 // Max / sum over the G consecutive threads of a group (G = 32 or 64 within a wavefront, G = 128
 // over two wavefronts through LDS); every thread of the group receives the result. All 256 threads
 // call it together. Sums add in a fixed tree order.
+// Lane n's value, in every lane.
+IRON_DEV double readlane_d(double v, int n) {
+  return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), n),
+                          __builtin_amdgcn_readlane(__double2loint(v), n));
+}
+
+// Maximum / sum over groups of G consecutive lanes, in every lane of the group. G = 32: the four
+// 16-lane DPP steps, then the two rows of each half-wavefront through readlane -- the same
+// pairings as an xor butterfly (lane l with l ^ 1, 2, 4, 8, 16), so the same values, without
+// the LDS round trip of a cross-lane shuffle per step. Other G: xor shuffles, and for G > 64 the
+// wavefronts through LDS.
 template <int G>
 IRON_DEV double group_max(double v, double (&s_red)[4][2]) {
+  if constexpr (G == 32) {
+    v = row16_max_d(v);
+    const double a = fmax(readlane_d(v, 0), readlane_d(v, 16));
+    const double b = fmax(readlane_d(v, 32), readlane_d(v, 48));
+    return (threadIdx.x & 32) ? b : a;
+  }
 #pragma unroll
   for (int k = 1; k < (G < 64 ? G : 64); k <<= 1) v = fmax(v, __shfl_xor(v, k));
   if constexpr (G > 64) {
@@ -445,6 +462,12 @@ IRON_DEV double group_max(double v, double (&s_red)[4][2]) {
 
 template <int G>
 IRON_DEV double group_sum(double v, double (&s_red)[4][2]) {
+  if constexpr (G == 32) {
+    v = row16_sum_d(v);
+    const double a = readlane_d(v, 0) + readlane_d(v, 16);
+    const double b = readlane_d(v, 32) + readlane_d(v, 48);
+    return (threadIdx.x & 32) ? b : a;
+  }
 #pragma unroll
   for (int k = 1; k < (G < 64 ? G : 64); k <<= 1) v += __shfl_xor(v, k);
   if constexpr (G > 64) {
