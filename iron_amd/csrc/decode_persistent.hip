@@ -212,6 +212,17 @@ IRON_DEV void retire_loads() {
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 }
 
+// True in every thread if `flag` is set in any thread of the workgroup: one barrier (where
+// __syncthreads_or takes three). The flags are rewritten only after the next wait's opening
+// barrier, which every wavefront reaches after reading these.
+IRON_DEV bool workgroup_any(bool flag) {
+  __shared__ uint32_t s_flag[4];
+  const bool w = __ballot(flag) != 0ull;
+  if ((threadIdx.x & 63) == 0) s_flag[threadIdx.x >> 6] = w ? 1u : 0u;
+  __syncthreads();
+  return (s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3]) != 0u;
+}
+
 IRON_DEV bool gave_up(long long spins, uint32_t* err) {
   return spins >= kSpinLimit ||
          ((spins & 255) == 255 &&
@@ -262,7 +273,7 @@ IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t*
     if (!missing || gave_up(spins, err)) break;
   }
   if (missing) atomicOr(err, 1u);
-  const bool ok = __syncthreads_or(missing ? 1 : 0) == 0;
+  const bool ok = !workgroup_any(missing);
   issue_fenced(issue);
   return ok;
 }
@@ -328,7 +339,7 @@ IRON_DEV bool gather_blocks(int n_blk, Blk blk, uint32_t tag, int n_ext, Ext ext
     if (!missing || gave_up(spins, err)) break;
   }
   if (missing) atomicOr(err, 1u);
-  const bool ok = __syncthreads_or(missing ? 1 : 0) == 0;
+  const bool ok = !workgroup_any(missing);
   issue_fenced(issue);
   return ok;
 }
@@ -735,9 +746,11 @@ IRON_DEV void attn_tile_pairs(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end,
       for (int k = 0; k < w; ++k) v[k] += v[k + w];
     if (t0 + pt < t_end) s = v[0] * scale;
   }
-  double wm = row16_max_d(s);
-  wm = fmax(wm, __shfl_xor(wm, 32));
-  if ((lane & 47) == 0) s_mx[wave][ph] = wm;  // lanes 0 and 16: heads 0 and 1
+  // row maxima; rows r and r + 2 hold the same head (readlane: no LDS shuffle)
+  const double wm = row16_max_d(s);
+  const double m0 = fmax(readlane_d(wm, 0), readlane_d(wm, 32));
+  const double m1 = fmax(readlane_d(wm, 16), readlane_d(wm, 48));
+  if ((lane & 47) == 0) s_mx[wave][ph] = ph ? m1 : m0;  // lanes 0 and 16: heads 0 and 1
   __syncthreads();
   double mn[2];
 #pragma unroll
