@@ -653,9 +653,14 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
     // row r's total is in lanes 8r..8r+7; lane 16k pairs rows 2k and 2k+1 (row_ror:8)
     const uint32_t hb = f64_to_bf16(rows_sum_d<R>(v, s_rows[threadIdx.x >> 6]));
     const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)hb, 0x128, 0xf, 0xf, false);
-    const int k = lane >> 4, row = row0 + 2 * k;
-    if ((lane & 15) == 0 && k < R / 2 && row < S::MQKV)
-      put_word_copies(p.RAW + row / 2, kCopyWords, (hb & 0xffffu) | (hi << 16), tag);
+    const int k = lane >> 4, wave = threadIdx.x >> 6;
+    // the workgroup's 4R rows leave as 2R consecutive words from one store instruction
+    __shared__ uint32_t s_pairs[4 * R / 2];
+    if ((lane & 15) == 0 && k < R / 2) s_pairs[wave * (R / 2) + k] = (hb & 0xffffu) | (hi << 16);
+    __syncthreads();
+    const int t = threadIdx.x, row = wg * 4 * R + 2 * t;
+    if (t < 2 * R && row < S::MQKV)
+      put_word_copies(p.RAW + row / 2, kCopyWords, s_pairs[t], tag);
   } else {
     dot_w8_lane<R, NCH>(g, W.w, W.sc, xf, row0, lane, acc);
     uint16_t h[R];
