@@ -223,6 +223,13 @@ IRON_DEV bool workgroup_any(bool flag) {
   return (s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3]) != 0u;
 }
 
+// A wait's first poll is issued ~0.27 us after the phase starts (s_sleep counts 64 clocks). Its
+// producers are other workgroups finishing the same previous phase, so an immediate poll almost
+// never finds the words; it only adds to the poll traffic that lengthens every hand-off's round
+// trip. Measured per step: sleep 4 / 6 / 8 / 10 / 12 / 16 / 32 units -> -6 / -10 / -18 / -21 /
+// -18 / -5 / +47 us against no sleep.
+IRON_DEV void first_poll_delay() { __builtin_amdgcn_s_sleep(10); }
+
 IRON_DEV bool gave_up(long long spins, uint32_t* err) {
   return spins >= kSpinLimit ||
          ((spins & 255) == 255 &&
@@ -244,6 +251,7 @@ template <int NPT, class Src, class Issue>
 IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t* err) {
   __syncthreads();  // the previous phase's LDS reads are done before dst is rewritten
   retire_loads();
+  first_poll_delay();
   bool pending[NPT];
   unsigned long long* ptr[NPT];
   uint32_t want[NPT];
@@ -294,6 +302,7 @@ IRON_DEV bool gather_blocks(int n_blk, Blk blk, uint32_t tag, int n_ext, Ext ext
   static_assert(ROWS >= 1 && ROWS <= 32, "block words");
   __syncthreads();
   retire_loads();
+  first_poll_delay();
   const int t = threadIdx.x;
   int rows = 0;
   unsigned long long* bp = t < n_blk ? blk(t, rows) : nullptr;
