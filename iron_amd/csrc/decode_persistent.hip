@@ -228,7 +228,9 @@ IRON_DEV bool workgroup_any(bool flag) {
 // never finds the words; it only adds to the poll traffic that lengthens every hand-off's round
 // trip. Measured per step: sleep 4 / 6 / 8 / 10 / 12 / 16 / 32 units -> -6 / -10 / -18 / -21 /
 // -18 / -5 / +47 us against no sleep.
-IRON_DEV void first_poll_delay() { __builtin_amdgcn_s_sleep(10); }
+constexpr int kFirstPollDelay = 10;
+template <int UNITS>
+IRON_DEV void first_poll_delay() { __builtin_amdgcn_s_sleep(UNITS); }
 
 IRON_DEV bool gave_up(long long spins, uint32_t* err) {
   return spins >= kSpinLimit ||
@@ -247,11 +249,11 @@ IRON_DEV void issue_fenced(Issue issue) {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int NPT, class Src, class Issue>
+template <int NPT, int DELAY = kFirstPollDelay, class Src, class Issue>
 IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t* err) {
   __syncthreads();  // the previous phase's LDS reads are done before dst is rewritten
   retire_loads();
-  first_poll_delay();
+  first_poll_delay<DELAY>();
   bool pending[NPT];
   unsigned long long* ptr[NPT];
   uint32_t want[NPT];
@@ -296,13 +298,13 @@ IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t*
 // block's read follows the last sentinel. Extra word i < n_ext (ext(i, tag)) goes to
 // dst[ROWS n_blk + i] and is polled by thread i. Same contract as gather_words otherwise, with
 // one tag for the blocks.
-template <int ROWS, class Blk, class Ext, class Issue>
+template <int ROWS, int DELAY = kFirstPollDelay, class Blk, class Ext, class Issue>
 IRON_DEV bool gather_blocks(int n_blk, Blk blk, uint32_t tag, int n_ext, Ext ext, Issue issue,
                             uint32_t* dst, uint32_t* err) {
   static_assert(ROWS >= 1 && ROWS <= 32, "block words");
   __syncthreads();
   retire_loads();
-  first_poll_delay();
+  first_poll_delay<DELAY>();
   const int t = threadIdx.x;
   int rows = 0;
   unsigned long long* bp = t < n_blk ? blk(t, rows) : nullptr;
@@ -1095,7 +1097,10 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
       rows = S::FF - q * S::GH_ROWS < S::GH_ROWS ? S::FF - q * S::GH_ROWS : S::GH_ROWS;
       return gh + q * kGhBlock;
     };
-    if (!gather_blocks<S::GH_ROWS>(S::GH_PROD, blk, tg, 0, NoExt(), issue, s_in, p.ctrl + 1))
+    // gh's producers finish last in the layer and its hand-off is the longest: a later first
+    // poll measured best here (24 units: -7 to -17 us per step against 10; 32 and 40 worse)
+    if (!gather_blocks<S::GH_ROWS, 24>(S::GH_PROD, blk, tg, 0, NoExt(), issue, s_in,
+                                       p.ctrl + 1))
       return false;
   }
   uint4 xl[NCH][4], x2l[NCH][2] = {}, nwl[NCH][2] = {};
