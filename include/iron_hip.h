@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 4
+#define IRON_ABI_VERSION 5
 
 enum iron_status {
   IRON_OK = 0,
@@ -277,6 +277,34 @@ int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, i
                            const uint16_t* x_in, uint16_t* x_out, const int32_t* pos,
                            const uint16_t* ang, float eps, float scale, void* workspace,
                            size_t workspace_bytes, void* stream);
+
+/* Device state of a greedy decode loop run by iron_decode_persistent_gen. */
+typedef struct iron_decode_gen {
+  unsigned long long* keys;   /* [1] the previous iron_lm_head's argmax key; reset to 0 */
+  const uint16_t* emb;        /* bf16 [vocab][D] embedding table (16-byte aligned) */
+  int32_t* tokens;            /* [1] receives the decoded token */
+  int32_t* token_log;         /* [log_len] token by step, or NULL */
+  int32_t* step;              /* [1] step counter, incremented (needed with token_log) */
+  int32_t* ctx;               /* [1] receives the new position + 1, or NULL */
+  const uint16_t* rope_table; /* bf16 [max_seq][HD] RoPE rows, or NULL */
+  int vocab, log_len;
+} iron_decode_gen;
+
+/* iron_decode_persistent with the greedy loop's per-token work folded in:
+ *   token = the index of gen->keys[0] (0 for a zero key, clamped to [0, vocab)); x_in is
+ *   emb[token]; the layers run as in iron_decode_persistent; then keys[0] = 0, tokens[0] = token,
+ *   token_log[*step] = token (when *step < log_len), *step += 1, *pos += 1, ctx[0] = *pos + 1 and
+ *   ang = rope_table[*pos] (when *pos < max_seq).
+ * The results equal iron_next_token (emb, log) + iron_decode_persistent + iron_advance_positions
+ * (delta 1), the per-token loop of the reference decode (qwen3_npu_int8.py:594-621) in one
+ * launch. */
+int iron_decode_persistent_gen(const iron_layer_desc* layers, int n_layers, int D, int FF,
+                               int Hq, int Hkv, int HD, int max_seq, long long kv_sh,
+                               long long kv_st, int G, int tile_qkv, int tile_o, int tile_gu,
+                               int tile_d, int domain, const iron_decode_gen* gen,
+                               uint16_t* x_out, int32_t* pos, uint16_t* ang, float eps,
+                               float scale, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 /* Host-only check of the device-side divide used for wire row-blocks: returns n / d computed with
  * the same multiply-shift sequence the kernels use (test hook; no reference counterpart). */

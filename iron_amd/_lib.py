@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
-ABI_VERSION = 4          # IRON_ABI_VERSION of include/iron_hip.h
+ABI_VERSION = 5          # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2
@@ -51,6 +51,14 @@ class LayerDesc(ctypes.Structure):
 
     _fields_ = [(name, _c_vp) for name in ("wqkv", "wo", "wg", "wu", "wd", "n_in", "n_post",
                                            "n_qn", "n_kn", "k_cache", "v_cache")]
+
+
+class DecodeGen(ctypes.Structure):
+    """``iron_decode_gen``: device state of the greedy loop (include/iron_hip.h)."""
+
+    _fields_ = [(name, _c_vp) for name in ("keys", "emb", "tokens", "token_log", "step", "ctx",
+                                           "rope_table")] + [("vocab", _c_int),
+                                                             ("log_len", _c_int)]
 
 
 # name -> (restype, argtypes). Kept in the order of include/iron_hip.h.
@@ -102,6 +110,11 @@ SIGNATURES = {
                                         _c_int, _c_ll, _c_ll, _c_int, _c_int, _c_int, _c_int,
                                         _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_f, _c_f,
                                         _c_vp, _c_sz, _c_vp]),
+    "iron_decode_persistent_gen": (_c_int, [_c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                            _c_int, _c_int, _c_ll, _c_ll, _c_int, _c_int, _c_int,
+                                            _c_int, _c_int, _c_int, ctypes.POINTER(DecodeGen),
+                                            _c_vp, _c_vp, _c_vp, _c_f, _c_f, _c_vp, _c_sz,
+                                            _c_vp]),
     "iron_test_fastdiv": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32]),
     "iron_test_bf16_round": (_c_int, [_c_vp, _c_vp]),
     "iron_stream_read": (_c_int, [_c_vp, _c_sz, _c_vp, _c_int, _c_vp]),

@@ -275,6 +275,29 @@ class Qwen3NPU:
             1.0 / math.sqrt(cfg.head_dim), self._p_ws.data_ptr(), self._p_ws.numel(), stream),
             "iron_decode_persistent")
 
+    def persistent_gen_launch(self, keys, gs):
+        """Launch iron_decode_persistent_gen: one greedy step's layers plus its token decode,
+        embedding gather, token log and position advance."""
+        cfg, lib, mlp = self.cfg, _lib.load(), self.mlp_xdna
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        view = lambda name, dt: self.fc.get_buffer(name).torch_view(dt)  # noqa: E731
+        sh, st = self._kv_strides()
+        gen = _lib.DecodeGen(keys=keys.data_ptr(), emb=self.embed.data_ptr(),
+                             tokens=gs["tokens"].data_ptr(), token_log=gs["log"].data_ptr(),
+                             step=gs["step"].data_ptr(),
+                             ctx=self.fc.params.tensor("S_kv_eff").data_ptr(),
+                             rope_table=self.rope_table.data_ptr(), vocab=cfg.vocab_size,
+                             log_len=gs["log"].numel())
+        _lib.check(lib.iron_decode_persistent_gen(
+            self._p_layers.data_ptr(), cfg.n_layers, cfg.emb_dim, cfg.hidden_dim, cfg.n_heads,
+            cfg.n_kv_heads, cfg.head_dim, self.max_seq_len, sh, st, cfg.group_size, QKV_TSI,
+            mlp.tile_rows_o, mlp.tile_rows_gu, mlp.tile_rows_d, _lib.IRON_DOMAIN_SIGNED,
+            ctypes.byref(gen), self._p_xout.data_ptr(),
+            self.fc.params.tensor("k_cache_offset").data_ptr(),
+            view("rope_row", torch.bfloat16).data_ptr(), float(cfg.eps),
+            1.0 / math.sqrt(cfg.head_dim), self._p_ws.data_ptr(), self._p_ws.numel(), stream),
+            "iron_decode_persistent_gen")
+
     def lm_head_launch(self):
         """Final RMSNorm + LM head + argmax key over the persistent kernel's output."""
         cfg, lib = self.cfg, _lib.load()
@@ -377,14 +400,16 @@ class Qwen3NPU:
         cfg, gs = self.cfg, self._gen_state()
         stream = torch.cuda.current_stream(self.device).cuda_stream
         keys = self.fc.get_buffer("argmax_key").torch_view(torch.int64)
+        if self.persistent:
+            # token decode, embedding, log and position advance inside the layers' kernel
+            self.persistent_gen_launch(keys, gs)
+            self.lm_head_launch()
+            return
         x = self.fc.get_buffer("x").torch_view(torch.bfloat16)
         _lib.call("iron_next_token", keys.data_ptr(), gs["tokens"].data_ptr(),
                   self.embed.data_ptr(), x.data_ptr(), gs["log"].data_ptr(), 0,
                   gs["step"].data_ptr(), 1, cfg.emb_dim, cfg.vocab_size, stream)
-        if self.persistent:
-            self._persistent_launches()
-        else:
-            self.fc.run_steps()
+        self.fc.run_steps()
         _lib.call("iron_advance_positions", self.fc.params.tensor("k_cache_offset").data_ptr(),
                   self.fc.params.tensor("S_kv_eff").data_ptr(), self.rope_table.data_ptr(),
                   self.fc.get_buffer("rope_row").torch_view(torch.bfloat16).data_ptr(),

@@ -136,6 +136,13 @@ struct PParams {
   double scale;
   unsigned long long *X, *RAW, *PART, *ATT, *AO, *GH;  // tagged hand-off buffers
   uint32_t* ctrl;         // [0] epoch, [1] error flags
+  // device-resident greedy loop (iron_decode_persistent_gen); key is null otherwise
+  unsigned long long* key;     // argmax key of the previous token: read first, reset last
+  const uint16_t* emb;         // bf16 [vocab][D] embedding table
+  int vocab, log_len;
+  int32_t *token, *token_log, *step, *pos_next, *ctx;
+  const uint16_t* rope_table;  // bf16 [max_seq][HD] RoPE rows
+  uint16_t* ang_next;          // the buffer `ang` points to, given the next position's row
 };
 
 IRON_DEV GemvParams gemv_of(const WireGeom& g, const void* w, int M, int K) {
@@ -1141,14 +1148,24 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
   W8<S::RA, S::CA> wqkv;
   uint4 n_in[S::CA][2];
   prefetch_qkv<S>(p, p.layers[0], wg, wqkv, n_in);
+  // the greedy loop's input: the embedding row of the token the previous LM head chose (key =
+  // (order(max) << 32) | ~index; a zero key is token 0)
+  const uint16_t* x_in = p.x_in;
+  int32_t tok = 0;
+  if (p.key) {
+    const unsigned long long k = *p.key;
+    tok = k ? (int32_t)(~(uint32_t)(k & 0xffffffffull)) : 0;
+    tok = tok < 0 ? 0 : (tok >= p.vocab ? p.vocab - 1 : tok);
+    x_in = p.emb + (size_t)tok * S::D;
+  }
   // the embedding row enters the hand-off like any layer's output (x's tag of layer 0)
   if (threadIdx.x < 64)
     for (int j = wg * 64 + threadIdx.x; j < S::D / 2; j += kNT * 64)
-      put_word_copies(p.X + j, kCopyWords, ((const uint32_t*)p.x_in)[j],
+      put_word_copies(p.X + j, kCopyWords, ((const uint32_t*)x_in)[j],
                       x_tag(ep, p.n_layers, 0));
   if (threadIdx.x < S::XW) {
     const int word = wg * S::XW + threadIdx.x;
-    s_own[S::XW + threadIdx.x] = word < S::D / 2 ? ((const uint32_t*)p.x_in)[word] : 0u;
+    s_own[S::XW + threadIdx.x] = word < S::D / 2 ? ((const uint32_t*)x_in)[word] : 0u;
   }
   for (int l = 0; l < p.n_layers; ++l) {
     const iron_layer_desc L = p.layers[l];
@@ -1172,8 +1189,27 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
     if (!ok) break;
   }
   // Advance the epoch for the next launch. Workgroup 0 finishes only after every workgroup has
-  // contributed to the last layer, so every workgroup has read `ep` by now.
-  if (wg == 0 && threadIdx.x == 0) p.ctrl[0] = ep + 1u;
+  // contributed to the last layer, so every workgroup has read `ep`, the key, the position and
+  // (in its attention phase) the RoPE row by now: the greedy loop's state advances here too.
+  if (wg != 0) return;
+  if (p.key) {
+    const int next = pos + 1;
+    if (threadIdx.x == 0) {
+      *p.key = 0ull;
+      *p.token = tok;
+      if (p.token_log) {
+        const int32_t s = *p.step;
+        if (s >= 0 && s < p.log_len) p.token_log[s] = tok;
+        *p.step = s + 1;
+      }
+      *p.pos_next = next;
+      if (p.ctx) *p.ctx = next + 1;
+    }
+    if (p.rope_table && next < p.max_seq && threadIdx.x < S::HD / 8)
+      ((uint4*)p.ang_next)[threadIdx.x] =
+          ((const uint4*)(p.rope_table + (size_t)next * S::HD))[threadIdx.x];
+  }
+  if (threadIdx.x == 0) p.ctrl[0] = ep + 1u;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1306,16 +1342,29 @@ int iron_decode_persistent_check_layer(const iron_layer_desc* layer, int D, int 
   return IRON_OK;
 }
 
-int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, int FF, int Hq,
-                           int Hkv, int HD, int max_seq, long long kv_sh, long long kv_st, int G,
-                           int tile_qkv, int tile_o, int tile_gu, int tile_d, int domain,
-                           const uint16_t* x_in, uint16_t* x_out, const int32_t* pos,
-                           const uint16_t* ang, float eps, float scale, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// Both entry points: `gen` null takes the input row from x_in; otherwise from the embedding row
+// of gen->keys[0]'s token, and the loop's state advances at the end (pos is then written).
+static int decode_persistent(const char* fn, const iron_decode_gen* gen,
+                             const iron_layer_desc* layers, int n_layers, int D, int FF, int Hq,
+                             int Hkv, int HD, int max_seq, long long kv_sh, long long kv_st,
+                             int G, int tile_qkv, int tile_o, int tile_gu, int tile_d, int domain,
+                             const uint16_t* x_in, uint16_t* x_out, int32_t* pos,
+                             uint16_t* ang, float eps, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream) {
   iron::clear_error();
-  const char* fn = "iron_decode_persistent";
-  if (!layers || !x_in || !x_out || !pos || !ang)
+  if (!layers || (!gen && !x_in) || !x_out || !pos || !ang)
     return iron::fail(IRON_ERR_NULL, "%s: null pointer", fn);
+  if (gen) {
+    if (!gen->keys || !gen->emb || !gen->tokens)
+      return iron::fail(IRON_ERR_NULL, "%s: null keys, embedding table or tokens", fn);
+    if (gen->vocab <= 0) return iron::fail(IRON_ERR_SHAPE, "%s: vocab=%d", fn, gen->vocab);
+    if (gen->token_log && (!gen->step || gen->log_len <= 0))
+      return iron::fail(IRON_ERR_NULL, "%s: token_log needs a step counter and a length", fn);
+    if (!iron::aligned(gen->emb, 16) || (gen->rope_table && !iron::aligned(gen->rope_table, 16)))
+      return iron::fail(IRON_ERR_ALIGN, "%s: emb and rope_table must be 16-byte aligned", fn);
+  }
   const ShapeId id = shape_id(D, FF, Hq, Hkv, HD);
   if (id == SHAPE_NONE)
     return iron::fail(IRON_ERR_UNSUPPORTED, "%s: no persistent kernel for D=%d FF=%d Hq=%d Hkv=%d "
@@ -1332,7 +1381,7 @@ int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, i
     return iron::fail(IRON_ERR_SHAPE, "%s: row-block heights must divide the row counts", fn);
   if (domain != IRON_DOMAIN_SIGNED && domain != IRON_DOMAIN_BIASED)
     return iron::fail(IRON_ERR_SHAPE, "%s: unknown payload domain %d", fn, domain);
-  if (!iron::aligned(x_in, 16) || !iron::aligned(x_out, 16) || !iron::aligned(ang, 16))
+  if ((x_in && !iron::aligned(x_in, 16)) || !iron::aligned(x_out, 16) || !iron::aligned(ang, 16))
     return iron::fail(IRON_ERR_ALIGN, "%s: x_in, x_out and ang must be 16-byte aligned", fn);
   const Layout lo = layout_for(id);
   if (!workspace || workspace_bytes < lo.total)
@@ -1366,6 +1415,19 @@ int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, i
   p.ATT = (unsigned long long*)(base + lo.ATT);
   p.AO = (unsigned long long*)(base + lo.AO);
   p.GH = (unsigned long long*)(base + lo.GH);
+  if (gen) {
+    p.key = gen->keys;
+    p.emb = gen->emb;
+    p.vocab = gen->vocab;
+    p.log_len = gen->log_len;
+    p.token = gen->tokens;
+    p.token_log = gen->token_log;
+    p.step = gen->step;
+    p.pos_next = pos;
+    p.ctx = gen->ctx;
+    p.rope_table = gen->rope_table;
+    p.ang_next = ang;
+  }
   hipStream_t s = (hipStream_t)stream;
   if (id == SHAPE_0_6B)
     hipLaunchKernelGGL(decode_persistent_kernel<ShapeQwen3_0_6B>, dim3(kNT), dim3(256), 0, s,
@@ -1373,6 +1435,37 @@ int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, i
   else
     hipLaunchKernelGGL(decode_persistent_kernel<ShapeTiny>, dim3(kNT), dim3(256), 0, s, p);
   return iron::check_launch(fn);
+}
+
+extern "C" {
+
+int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, int FF, int Hq,
+                           int Hkv, int HD, int max_seq, long long kv_sh, long long kv_st, int G,
+                           int tile_qkv, int tile_o, int tile_gu, int tile_d, int domain,
+                           const uint16_t* x_in, uint16_t* x_out, const int32_t* pos,
+                           const uint16_t* ang, float eps, float scale, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  // without `gen` the kernel only reads pos and ang
+  return decode_persistent("iron_decode_persistent", nullptr, layers, n_layers, D, FF, Hq, Hkv,
+                           HD, max_seq, kv_sh, kv_st, G, tile_qkv, tile_o, tile_gu, tile_d,
+                           domain, x_in, x_out, const_cast<int32_t*>(pos),
+                           const_cast<uint16_t*>(ang), eps, scale, workspace, workspace_bytes,
+                           stream);
+}
+
+int iron_decode_persistent_gen(const iron_layer_desc* layers, int n_layers, int D, int FF,
+                               int Hq, int Hkv, int HD, int max_seq, long long kv_sh,
+                               long long kv_st, int G, int tile_qkv, int tile_o, int tile_gu,
+                               int tile_d, int domain, const iron_decode_gen* gen,
+                               uint16_t* x_out, int32_t* pos, uint16_t* ang, float eps,
+                               float scale, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  iron::clear_error();
+  if (!gen) return iron::fail(IRON_ERR_NULL, "iron_decode_persistent_gen: null gen");
+  return decode_persistent("iron_decode_persistent_gen", gen, layers, n_layers, D, FF, Hq, Hkv,
+                           HD, max_seq, kv_sh, kv_st, G, tile_qkv, tile_o, tile_gu, tile_d,
+                           domain, nullptr, x_out, pos, ang, eps, scale, workspace,
+                           workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iron_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.iron_abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_wire_bytes(lib):
@@ -142,6 +142,38 @@ def test_persistent_decode_rejects_bad_arguments(lib):
     assert call(ang=fake + 2) == _lib.IRON_ERR_ALIGN
     assert call(wsb=ws - 8) == _lib.IRON_ERR_WORKSPACE
     assert call(ws=fake + 64) == _lib.IRON_ERR_ALIGN
+
+
+def test_persistent_gen_validation(lib):
+    """The greedy-loop variant's own argument checks (host-only; nothing is launched)."""
+    f = lib.iron_decode_persistent_gen
+    fake = 1 << 20
+    ws = lib.iron_decode_persistent_workspace(1024, 3072, 16, 8, 128)
+
+    def call(gen, **kw):
+        a = dict(ang=fake, wsb=ws)
+        a.update(kw)
+        g = ctypes.byref(gen) if gen is not None else None
+        return f(fake, 28, 1024, 3072, 16, 8, 128, 4096, 4096 * 128, 128, 32, 4, 4, 12, 4, 0, g,
+                 fake, fake, a["ang"], 1e-6, 0.088, fake, a["wsb"], None)
+
+    def gen(**kw):
+        a = dict(keys=fake, emb=fake, tokens=fake, token_log=fake, step=fake, ctx=fake,
+                 rope_table=fake, vocab=151936, log_len=4097)
+        a.update(kw)
+        return _lib.DecodeGen(**a)
+
+    assert call(None) == _lib.IRON_ERR_NULL
+    assert b"null gen" in lib.iron_last_error()
+    assert call(gen(keys=None)) == _lib.IRON_ERR_NULL
+    assert call(gen(emb=None)) == _lib.IRON_ERR_NULL
+    assert call(gen(vocab=0)) == _lib.IRON_ERR_SHAPE
+    assert call(gen(step=None)) == _lib.IRON_ERR_NULL      # a log needs a step counter
+    assert call(gen(log_len=0)) == _lib.IRON_ERR_NULL
+    assert call(gen(emb=fake + 2)) == _lib.IRON_ERR_ALIGN
+    assert call(gen(rope_table=fake + 2)) == _lib.IRON_ERR_ALIGN
+    assert call(gen(), ang=fake + 2) == _lib.IRON_ERR_ALIGN
+    assert call(gen(), wsb=ws - 8) == _lib.IRON_ERR_WORKSPACE
 
 
 def test_persistent_layer_check(lib):

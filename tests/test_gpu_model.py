@@ -80,6 +80,12 @@ def test_device_generate_matches_host_loop(tiny, persistent):
     n_new = 20
     a = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, persistent=persistent)
     dev_tokens = a.generate(prompt, n_new)
+    # the loop's state advanced once per step: position, context length, RoPE row
+    end, HD = len(prompt) - 1 + n_new, cfg.head_dim
+    assert int(a.fc.params.tensor("k_cache_offset")[0]) == end
+    assert int(a.fc.params.tensor("S_kv_eff")[0]) == end + 1
+    row = a.fc.get_buffer("rope_row").torch_view(torch.bfloat16)[:HD]
+    assert torch.equal(row.view(torch.int16), a.rope_table[end * HD:(end + 1) * HD].view(torch.int16))
     b = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, persistent=persistent)
     pos = 0
     for t in prompt[:-1]:
