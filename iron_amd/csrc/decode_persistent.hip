@@ -1022,7 +1022,8 @@ IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s
 // ---------------------------------------------------------------------------------------------
 template <class S, class Issue>
 IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s_in,
-                           float* s_gh, const W8<S::RE, S::CE>& Wg, const W8<S::RE, S::CE>& Wu,
+                           const uint32_t* s_x, float* s_gh, const W8<S::RE, S::CE>& Wg,
+                           const W8<S::RE, S::CE>& Wu,
                            const uint4 (&nwl)[S::CE][2], Issue issue) {
   constexpr int R = S::RE, NCH = S::CE;
   const int lane = threadIdx.x & 63;
@@ -1032,21 +1033,19 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
   g.eps = p.eps;
   g.x2 = (const uint16_t*)p.AO;  // marks the residual term (read from LDS here)
   {
-    // words [0, D/2): x; [D/2, D): a
-    constexpr int half = S::D / 2;
-    const uint32_t tx = x_tag(ep, p.n_layers, l), ta = phase_tag(ep, p.n_layers, l, 3);
-    unsigned long long* const xs = copy_for(p.X, kCopyWords, wg);
+    // a only: the layer input x is still in s_x from this workgroup's QKV phase
+    const uint32_t ta = phase_tag(ep, p.n_layers, l, 3);
     unsigned long long* const as = copy_for(p.AO, kCopyWords, wg);
     auto src = [&](int j, uint32_t& t) {
-      t = j < half ? tx : ta;
-      return j < half ? xs + j : as + (j - half);
+      t = ta;
+      return as + j;
     };
-    if (!gather_words<cdiv(S::D, 256)>(S::D, src, issue, s_in, p.ctrl + 1))
+    if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src, issue, s_in, p.ctrl + 1))
       return false;
   }
   uint4 xl[NCH][4], al[NCH][4], x2l[NCH][2];
-  lane_bf16<NCH>(s_in, S::D, lane, xl);
-  lane_bf16<NCH>(s_in + S::D / 2, S::D, lane, al);
+  lane_bf16<NCH>(s_x, S::D, lane, xl);
+  lane_bf16<NCH>(s_in, S::D, lane, al);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     x2l[c][0] = al[c][0];
@@ -1142,6 +1141,8 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
   // (words [XW, 2 XW), from its previous down phase): the residual of its down phase, kept here
   // rather than polled back from the hand-off buffers
   __shared__ uint32_t s_own[2 * S::XW];
+  // the layer input x as the QKV phase gathered it; the gate/up phase reads it back from here
+  __shared__ uint32_t s_x[S::D / 2];
   const int wg = blockIdx.x;
   const uint32_t ep = p.ctrl[0];
   const int pos = *p.pos;
@@ -1175,14 +1176,14 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
     uint4 n_post[S::CE][2];
     W8<S::RF, S::CF> wdown;
     const bool ok =
-        phase_qkv<S>(p, l, wg, ep, s_in, s_out, wqkv, n_in,
+        phase_qkv<S>(p, l, wg, ep, s_x, s_out, wqkv, n_in,
                      [&]() { prefetch_attn<S>(p, L, wg, pos, kv); }) &&
         phase_attn<S>(p, L, l, wg, ep, pos, s_in, kv, [&]() { prefetch_wo<S>(p, L, wg, wo); }) &&
         phase_merge<S>(p, l, wg, ep, s_in,
                        [&]() { prefetch_gateup<S>(p, L, wg, wgate, wup, n_post); }) &&
         phase_wo<S>(p, l, wg, ep, s_in, s_out, s_own, wo,
                     [&]() { prefetch_down<S>(p, L, wg, wdown); }) &&
-        phase_gateup<S>(p, l, wg, ep, s_in, s_gh, wgate, wup, n_post, [&]() {
+        phase_gateup<S>(p, l, wg, ep, s_in, s_x, s_gh, wgate, wup, n_post, [&]() {
           if (l + 1 < p.n_layers) prefetch_qkv<S>(p, p.layers[l + 1], wg, wqkv, n_in);
         }) &&
         phase_down<S>(p, l, wg, ep, s_in, s_out, s_own, wdown, []() {});
