@@ -9,7 +9,9 @@ The kernel runs every layer of a token with the arithmetic of the per-operator e
   persistent kernel: identical logits, tokens and KV-cache rows;
 * Qwen3-0.6B architecture (BASELINE config 4 shape) with the KV cache prefilled past 2048
   positions, so every split of the attention phase walks more than one tile: the device greedy
-  loop (graph-captured persistent launches) gives the same tokens and caches as the runlist path.
+  loop (graph-captured persistent launches) gives the same tokens and caches as the runlist path;
+* the generation entry point (iron_decode_persistent_gen) keeps its token log within its length
+  while the step counter, position and context length advance every token.
 """
 
 import pytest
@@ -49,6 +51,37 @@ def test_persistent_tiny_matches_cpu_chain(kv_layout, lm_head):
         assert g == Qwen3CpuChain.argmax(lc)
         tok = g
     assert model.persistent_errors() == 0
+
+
+def test_persistent_gen_short_log():
+    """iron_decode_persistent_gen called step by step: a token log shorter than the run keeps its
+    first entries and is never written past its length, the step counter and the position still
+    advance every token, and the tokens equal the device greedy loop's."""
+    _say("persistent generation entry point, 6 steps into a 3-entry token log")
+    from iron_amd.applications.qwen3_0_6b.qwen3_npu_int8 import _decode_key
+
+    cfg = Qwen3Config.tiny()
+    w = random_qwen3_weights(cfg, seed=5)
+    S, n = 64, 6
+    want = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, persistent=True).generate([3], n)
+    m = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, persistent=True)
+    m.start_generation(3, 0)
+    gs = m._gen_state()
+    log = torch.full((8,), -7, dtype=torch.int32, device="cuda")
+    keys = m.fc.get_buffer("argmax_key").torch_view(torch.int64)
+    short = {"tokens": gs["tokens"], "log": log[:3], "step": gs["step"]}
+    for _ in range(n):
+        m.persistent_gen_launch(keys, short)
+        m.lm_head_launch()
+    torch.cuda.synchronize()
+    assert m.persistent_errors() == 0
+    assert int(gs["step"].item()) == n
+    # step s logs the token it consumed: the armed 3, then the generated ones
+    assert log.cpu().tolist() == [3] + want[:2] + [-7] * 5
+    assert int(gs["tokens"].item()) == want[n - 2]
+    assert _decode_key(int(keys[0].item())) == want[n - 1]
+    assert int(m.fc.params.tensor("k_cache_offset")[0]) == n
+    assert int(m.fc.params.tensor("S_kv_eff")[0]) == n + 1
 
 
 def test_persistent_matches_runlist_tiny_prefilled():
