@@ -75,6 +75,10 @@ constexpr int kGhBuffers = 4;
 constexpr int kCopies = 8;
 constexpr size_t kCopyWords = 4096;
 constexpr int kGhBlock = 32;
+// Word j of the x and a hand-off buffers: 16 words (one 128-byte line) per 256 bytes, which
+// spreads each copy's polled lines over twice the memory channels.
+IRON_DEV constexpr size_t spread_word(int j) { return (size_t)(j >> 4) * 32 + (j & 15); }
+
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 template <int D_, int FF_, int HQ_, int HKV_>
@@ -112,6 +116,7 @@ struct Shape {
   static_assert(D % 16 == 0 && FF % 16 == 0 && MQKV % 2 == 0, "GEMV widths");
   static_assert(GH_ROWS <= kGhBlock && GH_PROD <= kNT, "gh blocks");
   static_assert(RD == RF, "the Wo and down phases own the same rows");
+  static_assert(spread_word(D / 2 - 1) < kCopyWords, "spread x and a words in one copy");
   static_assert(D / 2 <= (int)kCopyWords && MQKV / 2 <= (int)kCopyWords &&
                     QD / 2 <= (int)kCopyWords, "hand-off copies");
 };
@@ -409,8 +414,9 @@ IRON_DEV void lane_weight(const uint16_t* w, int K, int lane, uint4 (&nw)[NCH][2
 }
 
 // bf16 outputs of R rows per wavefront: the workgroup's 4R consecutive rows go out as tagged
-// pairs (rows 4R wg + 2t, +1). `res` (optional): also written as plain bf16 pairs.
-template <int R>
+// pairs (rows 4R wg + 2t, +1), at word spread_word(row / 2) when SPREAD. `plain` (optional):
+// also written as plain bf16 pairs.
+template <int R, bool SPREAD = false>
 IRON_DEV void store_bf16_pairs(const uint16_t (&h)[R], int wg, int M, unsigned long long* dst,
                                uint32_t tag, uint16_t* s_out, uint16_t* plain) {
   // dst: copy 0 of a replicated buffer (put_word_copies)
@@ -425,7 +431,8 @@ IRON_DEV void store_bf16_pairs(const uint16_t (&h)[R], int wg, int M, unsigned l
       if (lane == k) pair = (uint32_t)h[2 * k] | ((uint32_t)h[2 * k + 1] << 16);
     const int row = row0 + 2 * lane;
     if (lane < R / 2 && row < M) {
-      put_word_copies(dst + row / 2, kCopyWords, pair, tag);
+      put_word_copies(dst + (SPREAD ? spread_word(row / 2) : (size_t)(row / 2)), kCopyWords,
+                      pair, tag);
       if (plain) ((uint32_t*)plain)[row / 2] = pair;
     }
     return;
@@ -441,7 +448,8 @@ IRON_DEV void store_bf16_pairs(const uint16_t (&h)[R], int wg, int M, unsigned l
     const int row = wg * 4 * R + 2 * t;
     if (row < M) {
       const uint32_t pair = (uint32_t)s_out[2 * t] | ((uint32_t)s_out[2 * t + 1] << 16);
-      put_word_copies(dst + row / 2, kCopyWords, pair, tag);
+      put_word_copies(dst + (SPREAD ? spread_word(row / 2) : (size_t)(row / 2)), kCopyWords,
+                      pair, tag);
       if (plain) ((uint32_t*)plain)[row / 2] = pair;
     }
   }
@@ -652,7 +660,7 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
   {
     const uint32_t tx = x_tag(ep, p.n_layers, l);
     unsigned long long* const xs = copy_for(p.X, kCopyWords, wg);
-    auto src = [&](int j, uint32_t& t) { t = tx; return xs + j; };
+    auto src = [&](int j, uint32_t& t) { t = tx; return xs + spread_word(j); };
     if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src, issue, s_in,
                                            p.ctrl + 1))
       return false;
@@ -1013,7 +1021,7 @@ IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s
   uint16_t h[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) h[r] = f64_to_bf16(acc[r][0]);
-  store_bf16_pairs<R>(h, wg, S::D, p.AO, phase_tag(ep, p.n_layers, l, 3), s_out, nullptr);
+  store_bf16_pairs<R, true>(h, wg, S::D, p.AO, phase_tag(ep, p.n_layers, l, 3), s_out, nullptr);
   keep_own_words<R>(s_out, s_own);  // the down phase's residual a
   return true;
 }
@@ -1040,7 +1048,7 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
     unsigned long long* const as = copy_for(p.AO, kCopyWords, wg);
     auto src = [&](int j, uint32_t& t) {
       t = ta;
-      return as + j;
+      return as + spread_word(j);
     };
     if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src, issue, s_in, p.ctrl + 1))
       return false;
@@ -1125,7 +1133,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
     const float x1 = bf16_to_f32(s_res[4 * R + k]) + bf16_to_f32(s_res[k]);
     h[r] = f64_to_bf16((double)x1 + acc[r][0]);
   }
-  store_bf16_pairs<R>(h, wg, S::D, p.X, phase_tag(ep, p.n_layers, l, 5), s_out,
+  store_bf16_pairs<R, true>(h, wg, S::D, p.X, phase_tag(ep, p.n_layers, l, 5), s_out,
                       l == p.n_layers - 1 ? p.x_out : nullptr);
   keep_own_words<R>(s_out, s_own + S::XW);  // the next layer's residual x (its reads are done)
   return true;
@@ -1164,7 +1172,7 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
   // the embedding row enters the hand-off like any layer's output (x's tag of layer 0)
   if (threadIdx.x < 64)
     for (int j = wg * 64 + threadIdx.x; j < S::D / 2; j += kNT * 64)
-      put_word_copies(p.X + j, kCopyWords, ((const uint32_t*)x_in)[j],
+      put_word_copies(p.X + spread_word(j), kCopyWords, ((const uint32_t*)x_in)[j],
                       x_tag(ep, p.n_layers, 0));
   if (threadIdx.x < S::XW) {
     const int word = wg * S::XW + threadIdx.x;
