@@ -75,8 +75,8 @@ constexpr int kGhBuffers = 4;
 constexpr int kCopies = 8;
 constexpr size_t kCopyWords = 4096;
 constexpr int kGhBlock = 32;
-// Word j of the x and a hand-off buffers: 16 words (one 128-byte line) per 256 bytes, which
-// spreads each copy's polled lines over twice the memory channels.
+// Word j of the x, a and attention-output hand-off buffers: 16 words (one 128-byte line) per
+// 256 bytes, which spreads each copy's polled lines over twice the memory channels.
 IRON_DEV constexpr size_t spread_word(int j) { return (size_t)(j >> 4) * 32 + (j & 15); }
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
@@ -116,7 +116,8 @@ struct Shape {
   static_assert(D % 16 == 0 && FF % 16 == 0 && MQKV % 2 == 0, "GEMV widths");
   static_assert(GH_ROWS <= kGhBlock && GH_PROD <= kNT, "gh blocks");
   static_assert(RD == RF, "the Wo and down phases own the same rows");
-  static_assert(spread_word(D / 2 - 1) < kCopyWords, "spread x and a words in one copy");
+  static_assert(spread_word(D / 2 - 1) < kCopyWords && spread_word(QD / 2 - 1) < kCopyWords,
+                "spread x, a and attention-output words in one copy");
   static_assert(D / 2 <= (int)kCopyWords && MQKV / 2 <= (int)kCopyWords &&
                     QD / 2 <= (int)kCopyWords, "hand-off copies");
 };
@@ -984,9 +985,9 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
   if (sp == 0) s_o16[d] = f64_to_bf16(Lt > 0.0 ? O / Lt : 0.0);
   __syncthreads();
   if (t < PER / 2)
-    put_word_copies(p.ATT + (h * kAttnD + d0) / 2 + t, kCopyWords,
-             (uint32_t)s_o16[2 * t] | ((uint32_t)s_o16[2 * t + 1] << 16),
-             phase_tag(ep, p.n_layers, l, 2));
+    put_word_copies(p.ATT + spread_word((h * kAttnD + d0) / 2 + t), kCopyWords,
+                    (uint32_t)s_o16[2 * t] | ((uint32_t)s_o16[2 * t + 1] << 16),
+                    phase_tag(ep, p.n_layers, l, 2));
   (void)wave;
   (void)lane;
   return true;
@@ -1007,7 +1008,7 @@ IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s
   {
     const uint32_t ta = phase_tag(ep, p.n_layers, l, 2);
     unsigned long long* const att = copy_for(p.ATT, kCopyWords, wg);
-    auto src = [&](int j, uint32_t& t) { t = ta; return att + j; };
+    auto src = [&](int j, uint32_t& t) { t = ta; return att + spread_word(j); };
     if (!gather_words<cdiv(S::QD / 2, 256)>(S::QD / 2, src, issue, s_in,
                                             p.ctrl + 1))
       return false;
