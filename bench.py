@@ -36,12 +36,12 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the bf16 LM-head GEMV from two rocprofv3 --pmc passes over this bench:
-# FETCH_SIZE 152066.38 KiB x 2.0 + WRITE_SIZE 361.28 KiB x 1.0, the factors being what the same
+# FETCH_SIZE 152066.19 KiB x 2.0 + WRITE_SIZE 362.28 KiB x 1.0, the factors being what the same
 # counters read for a plain 256 MiB device copy (profiles/decode_qwen3_0_6b_hbm_traffic.md).
-LM_HEAD_BF16_TRAFFIC = 311_801_888
+LM_HEAD_BF16_TRAFFIC = 311_802_528
 # HBM bytes per launch of the persistent layers kernel (all 28 layers), same method:
-# FETCH_SIZE 382703.44 KiB x 2.0 + WRITE_SIZE 73624.03 KiB x 1.0 at context 2048..2057.
-PERSISTENT_TRAFFIC = 859_167_648
+# FETCH_SIZE 382599.72 KiB x 2.0 + WRITE_SIZE 73624.03 KiB x 1.0 at context 2048..2057.
+PERSISTENT_TRAFFIC = 858_955_232
 
 
 def parse():
