@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 5
+#define IRON_ABI_VERSION 6
 
 enum iron_status {
   IRON_OK = 0,
@@ -106,12 +106,13 @@ int iron_lm_head(const void* w, int w_kind, const uint16_t* x, const uint16_t* n
 /* Decode the token id from an argmax key written by iron_lm_head, on the device:
  * tokens[b] = index of keys[b]; then keys[b] = 0 (ready for the next iron_lm_head).
  * If `emb` != NULL also gathers x[b][:] = emb[tokens[b]][:] (bf16 [vocab][D]) and, when
- * `token_log` != NULL, appends tokens[b] to token_log[b * log_stride + *step] and increments
- * *step (device int32). Replaces the host argmax + embedding lookup of the reference decode
- * loop (qwen3_npu_int8.py:612-621; check_cosine_int8.py:41-52). */
+ * `token_log` != NULL, writes tokens[b] to token_log[b * log_stride + *step] if *step < log_len
+ * (a row of the log holds log_len entries) and increments *step (device int32) either way.
+ * Replaces the host argmax + embedding lookup of the reference decode loop
+ * (qwen3_npu_int8.py:612-621; check_cosine_int8.py:41-52). */
 int iron_next_token(unsigned long long* keys, int32_t* tokens, const uint16_t* emb, uint16_t* x,
-                    int32_t* token_log, int log_stride, int32_t* step, int B, int D, int vocab,
-                    void* stream);
+                    int32_t* token_log, int log_stride, int log_len, int32_t* step, int B, int D,
+                    int vocab, void* stream);
 
 /* Embedding gather x[b][:] = emb[tokens[b]][:] (tokens device int32 [B]). */
 int iron_embed(const int32_t* tokens, const uint16_t* emb, uint16_t* x, int B, int D, int vocab,
@@ -168,6 +169,27 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
                      int ctx_const, uint16_t* out, int B, int H, int KV, int D, int max_ctx,
                      float scale, int acc, void* workspace, size_t workspace_bytes,
                      void* stream);
+
+/* Workspace bytes for iron_decode_attn_verify (split-K partials, fp32; 256 when none are needed;
+ * 0 for an invalid shape). */
+size_t iron_decode_attn_verify_workspace(int n_new, int H, int KV, int D, int max_ctx);
+
+/* Batch / verify decode attention (speculative-decode verify): n_new new tokens at positions
+ * base .. base + n_new - 1 query ONE KV cache (K/V addressed as in iron_qkv_head, batch 1):
+ *   o[t][h] = softmax_j(q[t][h] . K[h*KV/H][j] * scale) . V[h*KV/H][j],
+ *             j < min(base + t + 1, max_ctx) when causal, j < max_ctx otherwise.
+ * q/o: [n_new][H][D] bf16, token-major (row t * H + h). base: device int32 (the S_kv_base runtime
+ * parameter), or NULL to use base_const. Arithmetic of the reference kernel: bf16 operands, fp32
+ * scores and exp2-form online softmax, probabilities rounded to bf16 for P.V, fp32 accumulation
+ * (MFMA); each staged 64-key K/V block serves up to 64 query rows (64 / (H/KV) tokens).
+ * n_new <= 4096. Replaces DecodeAttention's batch mode (iron/operators/decode_attn/op.py:40-48;
+ * design.py:243-276, per-query bound S_kv_base + g*M + m + 1; causal=False attends the whole
+ * cache). */
+int iron_decode_attn_verify(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                            long long kv_sh, long long kv_st, const int32_t* base,
+                            int base_const, int causal, uint16_t* out, int n_new, int H, int KV,
+                            int D, int max_ctx, float scale, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /* Workspace bytes for iron_qkv_attn (raw QKV staging + split-K partials). */
 size_t iron_qkv_attn_workspace(int B, int D, int Hq, int Hkv, int HD, int max_seq);
@@ -247,7 +269,7 @@ typedef struct iron_layer_desc {
 size_t iron_decode_persistent_workspace(int D, int FF, int Hq, int Hkv, int HD);
 
 /* IRON_OK if iron_decode_persistent has a kernel for this shape and the current device can hold
- * its grid resident (256 CUs, two 256-thread workgroups per CU); else IRON_ERR_UNSUPPORTED. Shapes:
+ * its grid resident (256 CUs, one 256-thread workgroup per CU); else IRON_ERR_UNSUPPORTED. Shapes:
  * D, FF, Hq, Hkv = (1024, 3072, 16, 8) (Qwen3-0.6B) and (256, 768, 4, 2); HD = 128. */
 int iron_decode_persistent_supported(int D, int FF, int Hq, int Hkv, int HD);
 
@@ -265,8 +287,8 @@ int iron_decode_persistent_check_layer(const iron_layer_desc* layer, int D, int 
  *   x_out = x.
  * The results equal those of the per-operator entry points (same arithmetic and roundings).
  * pos: device int32 [1]; ang: the position's RoPE row (bf16 [HD]); kv_sh / kv_st: head and token
- * strides of the caches in elements. Launches 512 workgroups that exchange activations through the
- * workspace: calls on one workspace must be stream-ordered, and the workspace's error word must be
+ * strides of the caches in elements. Launches 256 workgroups (one per CU) that exchange activations
+ * through the workspace: calls on one workspace must be stream-ordered, and the workspace's error word must be
  * checked (and cleared) by the caller after synchronising. Replaces the per-token runlist dispatch
  * of Qwen3NPU (iron/applications/qwen3_0.6b/qwen3_npu_int8.py:249-281, 594-621; one dispatch of
  * iron/common/sequence.py:270-559) for the layers; the final RMSNorm and LM head follow it

@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
-ABI_VERSION = 5          # IRON_ABI_VERSION of include/iron_hip.h
+ABI_VERSION = 6          # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2
@@ -76,8 +76,8 @@ SIGNATURES = {
     "iron_rmsnorm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_f, _c_vp]),
     "iron_lm_head": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_int, _c_int,
                               _c_int, _c_int, _c_int, _c_int, _c_vp]),
-    "iron_next_token": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_vp, _c_int,
-                                 _c_int, _c_int, _c_vp]),
+    "iron_next_token": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp,
+                                 _c_int, _c_int, _c_int, _c_vp]),
     "iron_embed": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
     "iron_advance_positions": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int,
                                         _c_int, _c_vp]),
@@ -90,6 +90,10 @@ SIGNATURES = {
     "iron_decode_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_ll, _c_ll, _c_ll, _c_vp, _c_int,
                                   _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_int,
                                   _c_vp, _c_sz, _c_vp]),
+    "iron_decode_attn_verify_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "iron_decode_attn_verify": (_c_int, [_c_vp, _c_vp, _c_vp, _c_ll, _c_ll, _c_vp, _c_int,
+                                         _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                         _c_f, _c_vp, _c_sz, _c_vp]),
     "iron_qkv_attn_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "iron_qkv_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                _c_ll, _c_ll, _c_ll, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,

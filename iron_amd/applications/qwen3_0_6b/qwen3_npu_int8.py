@@ -94,7 +94,19 @@ class Qwen3NPU:
         self._build_sequence(dispatch)
         self._load_weights(weights)
         self._gen_graph = None
+        self._gen_pos = None
+        if self._dispatch_name(dispatch) in ("reference", "compare"):
+            # per-step goldens run over the runlist entries (reference: on CPU buffers), so the
+            # whole-token kernel, which bypasses the runlist, is not used
+            if persistent:
+                raise ValueError(f"persistent decode runs no per-step goldens (dispatch="
+                                 f"{self._dispatch_name(dispatch)!r})")
+            persistent = False
         self.persistent = self._setup_persistent(persistent)
+
+    @staticmethod
+    def _dispatch_name(dispatch) -> str:
+        return dispatch if isinstance(dispatch, str) else getattr(dispatch, "name", "")
 
     # ---------------- operators ----------------
     def _build_operators(self):
@@ -408,7 +420,8 @@ class Qwen3NPU:
         x = self.fc.get_buffer("x").torch_view(torch.bfloat16)
         _lib.call("iron_next_token", keys.data_ptr(), gs["tokens"].data_ptr(),
                   self.embed.data_ptr(), x.data_ptr(), gs["log"].data_ptr(), 0,
-                  gs["step"].data_ptr(), 1, cfg.emb_dim, cfg.vocab_size, stream)
+                  gs["log"].numel(), gs["step"].data_ptr(), 1, cfg.emb_dim, cfg.vocab_size,
+                  stream)
         self.fc.run_steps()
         _lib.call("iron_advance_positions", self.fc.params.tensor("k_cache_offset").data_ptr(),
                   self.fc.params.tensor("S_kv_eff").data_ptr(), self.rope_table.data_ptr(),
@@ -433,16 +446,28 @@ class Qwen3NPU:
         if self._gen_graph is None:
             self._capture_gen_graph()
         gs = self._gen_state()
+        if not 0 <= start_pos < self.max_seq_len:
+            raise ValueError(f"start position {start_pos} outside [0, {self.max_seq_len})")
         gs["step"].zero_()
+        self._gen_pos = start_pos
         self._set_position(start_pos)
         self.fc.get_buffer("argmax_key").torch_view(torch.int64)[:1].fill_(
             _encode_token(first_token))
         torch.cuda.synchronize(self.device)
 
     def decode_steps(self, n: int):
-        """Replay the per-token graph n times (no host synchronisation)."""
+        """Replay the per-token graph n times (no host synchronisation).
+
+        Step i consumes the token at position start_pos + i, so every step's position must stay
+        below max_seq_len (the KV caches and the token log are sized by it)."""
+        if self._gen_graph is None or self._gen_pos is None:
+            raise RuntimeError("decode_steps() before start_generation()")
+        if self._gen_pos + n > self.max_seq_len:
+            raise ValueError(f"{n} steps from position {self._gen_pos} pass max_seq_len "
+                             f"{self.max_seq_len}")
         for _ in range(n):
             self._gen_graph.replay()
+        self._gen_pos += n
 
     def finish_generation(self) -> list[int]:
         """Tokens produced since start_generation (the last one decoded from the final key)."""
@@ -450,8 +475,8 @@ class Qwen3NPU:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         keys = self.fc.get_buffer("argmax_key").torch_view(torch.int64)
         _lib.call("iron_next_token", keys.data_ptr(), gs["tokens"].data_ptr(), None, None,
-                  gs["log"].data_ptr(), 0, gs["step"].data_ptr(), 1, cfg.emb_dim,
-                  cfg.vocab_size, stream)
+                  gs["log"].data_ptr(), 0, gs["log"].numel(), gs["step"].data_ptr(), 1,
+                  cfg.emb_dim, cfg.vocab_size, stream)
         torch.cuda.synchronize(self.device)
         self._persistent_check()
         n = int(gs["step"].item())
@@ -462,6 +487,12 @@ class Qwen3NPU:
         """Greedy decode: prefill ``prompt_ids`` token by token from ``start_pos``, then produce
         ``n_new`` tokens on the device. Returns the generated token ids."""
         prompt_ids = list(prompt_ids)
+        if not prompt_ids:
+            raise ValueError("generate() needs at least one prompt token")
+        last = start_pos + len(prompt_ids) - 1 + n_new
+        if start_pos < 0 or last > self.max_seq_len:
+            raise ValueError(f"{len(prompt_ids)} prompt + {n_new} new tokens from position "
+                             f"{start_pos} need max_seq_len >= {last} (it is {self.max_seq_len})")
         pos = start_pos
         for tok in prompt_ids[:-1]:
             self.step_token(tok, pos)

@@ -29,7 +29,8 @@ _REFERENCE_PROVIDER: Callable[..., Any] | None = None
 
 
 def register_reference_provider(provider: Callable[..., Any] | None) -> None:
-    """Install ``provider(op, *inputs) -> output`` as the source of ``op.reference()``."""
+    """Install ``provider(op, *inputs, **context) -> output`` as the source of
+    ``op.reference()`` (``context``: ``params`` and ``last`` inside a sequence)."""
     global _REFERENCE_PROVIDER
     _REFERENCE_PROVIDER = provider
 
@@ -149,15 +150,16 @@ class MLIROperator(AIEOperatorBase):
     def design_key(self) -> str | None:
         return None
 
-    def reference(self, *inputs):
-        """Golden output for ``inputs`` from the registered reference provider."""
+    def reference(self, *inputs, **context):
+        """Golden output for ``inputs`` from the registered reference provider. A sequence adds
+        ``params`` (runtime-parameter values) and, for an ``inout`` last argument, ``last``."""
         provider = reference_provider()
         if provider is None:
             raise RuntimeError(
                 f"{type(self).__name__}.reference(): no reference provider registered; the CPU "
                 "goldens live in the test oracle (register_reference_provider)"
             )
-        return provider(self, *inputs)
+        return provider(self, *inputs, **context)
 
 
 class CompositeOperator(AIEOperatorBase):

@@ -105,9 +105,8 @@ class OperatorSequence(AIEOperatorBase):
         dispatch = self._coerce_dispatch(dispatch)
         if not all(isinstance(op, MLIROperator) and all(isinstance(b, str) for b in bufs)
                    for op, *bufs in runlist):
-            raise TypeError(
-                "runlist entries must be (MLIROperator, *str) tuples; "
-                "each operator must be an MLIROperator and each buffer name must be a str")
+            raise TypeError("OperatorSequence: every runlist entry is an operator (an "
+                            "MLIROperator) followed by its buffer names (strings)")
         super().__init__(context)
         self.runlist = runlist
         self.name = name + "_shared" if share_designs else name
@@ -127,7 +126,8 @@ class OperatorSequence(AIEOperatorBase):
             return dispatch
         if isinstance(dispatch, str) and dispatch in _DISPATCH_ALIASES:
             return _DISPATCH_ALIASES[dispatch]()
-        raise TypeError("selected dispatch mode not supported")
+        raise TypeError(f"OperatorSequence: unknown dispatch {dispatch!r} (one of "
+                        f"{sorted(_DISPATCH_ALIASES)} or a SequenceDispatch)")
 
     def unique_operators(self):
         seen = {}
@@ -143,29 +143,28 @@ class OperatorSequence(AIEOperatorBase):
         for op, *bufs in self.runlist:
             specs = op.get_arg_spec()
             if len(specs) != len(bufs):
-                raise ValueError(
-                    f"Number of buffers ({len(bufs)}) must match operator argument "
-                    f"specification ({len(specs)}) for operator {op!r}")
+                raise ValueError(f"{op!r} declares {len(specs)} arguments but its runlist "
+                                 f"entry names {len(bufs)} buffers")
             for buf, spec in zip(bufs, specs):
                 if "[" in buf and buf.endswith("]"):
                     base = buf[: buf.index("[")]
                     start, end = map(int, buf[buf.index("[") + 1: -1].split(":"))
                     if base not in args and base not in self.explicit_buffer_sizes:
-                        raise ValueError(f"Sliced buffer '{buf}' requires explicit size for base "
-                                         f"buffer '{base}' in buffer_sizes parameter")
+                        raise ValueError(f"slice {buf!r}: its parent {base!r} needs a size in "
+                                         "buffer_sizes")
                     sliced[buf] = (base, start, end, spec)
                 elif buf not in args:
                     args[buf] = spec
                 elif args[buf].nbytes != spec.nbytes:
-                    raise ValueError(f"Buffer '{buf}' has conflicting sizes between operators: "
-                                     f"{args[buf].shape} vs {spec.shape}")
+                    raise ValueError(f"buffer {buf!r} is declared with two sizes "
+                                     f"({args[buf].shape} and {spec.shape}) by different steps")
         names = set(args) | set(sliced)
         for a in self.input_args:
             if a not in names and a not in self.explicit_buffer_sizes:
-                raise ValueError(f"Input argument {a} not found in runlist buffers")
+                raise ValueError(f"input_args names {a!r}, which no runlist step uses")
         for a in self.output_args:
             if a not in names and a not in self.explicit_buffer_sizes:
-                raise ValueError(f"Output argument {a} not found in runlist buffers")
+                raise ValueError(f"output_args names {a!r}, which no runlist step uses")
         layout, slice_info = {}, {}
         self._specs = args
 
@@ -206,9 +205,8 @@ class OperatorSequence(AIEOperatorBase):
         return super().compile(dry_run)
 
     def get_arg_spec(self):
-        raise NotImplementedError(
-            "OperatorSequence does not expose a unified arg spec; "
-            "use get_layout_for_buffer() to inspect individual buffer layouts")
+        raise NotImplementedError("a sequence has per-buffer layouts, not one argument list: "
+                                  "see get_layout_for_buffer()")
 
     def get_callable(self):
         if self.subbuffer_layout is None:
@@ -262,8 +260,8 @@ class SequenceCallable:
         for step_op, *names in self.op.runlist:
             specs = step_op.get_arg_spec()
             if len(specs) != len(names):
-                raise ValueError(f"Operator {step_op!r} arg-spec count {len(specs)} does not "
-                                 f"match runlist buffer count {len(names)}")
+                raise ValueError(f"{step_op!r} declares {len(specs)} arguments but its runlist "
+                                 f"entry names {len(names)} buffers")
             yield step_op, names, specs
 
     def __call__(self):
@@ -353,7 +351,13 @@ class SequenceHipCallable(SequenceCallable):
 
 
 class SequenceReferenceCallable(SequenceCallable):
-    """CPU evaluation through each operator's ``reference()`` (needs a golden provider)."""
+    """CPU evaluation through each operator's ``reference()`` (needs a golden provider).
+
+    A step's inputs are copies of its buffers; its ``out`` / ``inout`` arguments other than the
+    last are passed as the buffers themselves, so a golden that updates them (a KV-cache append,
+    the logits beside an argmax key) leaves its effect for later steps. The runtime parameters
+    (positions, context lengths, converted as the device callables convert them) go to the golden
+    as ``params``, and an ``inout`` last argument's pre-step value as ``last``."""
 
     def _allocate_buffers(self):
         in_sz, out_sz, scratch_sz = self.op.buffer_sizes
@@ -363,6 +367,11 @@ class SequenceReferenceCallable(SequenceCallable):
         for n, sz in zip(self.op.independent_order, self.op.independent_sizes):
             self._arenas[n] = torch.zeros(max(sz, 2), dtype=torch.uint8)
         self.params = _HostParams()
+        for step_op in self.op.unique_operators():
+            pname = getattr(step_op, "kv_offset_parameter", None)
+            conv = getattr(step_op, "offset_to_position", None)
+            if pname and conv is not None:
+                self.params.define(pname, convert=conv)
 
     def get_buffer(self, buffer_name) -> DeviceBuffer:
         if buffer_name not in self._buffer_cache:
@@ -374,27 +383,52 @@ class SequenceReferenceCallable(SequenceCallable):
     def sync_independent_buffers(self):
         pass
 
+    def _view(self, name, spec):
+        return self.get_buffer(name).torch_view(spec.dtype)[: spec.numel].reshape(spec.shape)
+
     def _run(self):
         for step_op, names, specs in self._iter_steps():
             *in_names, out_name = names
             *in_specs, out_spec = specs
-            inputs = [self.get_buffer(n).torch_view(s.dtype)[: s.numel].reshape(s.shape).clone()
-                      for n, s in zip(in_names, in_specs)]
-            out = step_op.reference(*inputs)
+            inputs = [self._view(n, s) if s.direction in ("out", "inout")
+                      else self._view(n, s).clone() for n, s in zip(in_names, in_specs)]
+            kw = {"params": self.params.snapshot()}
+            if out_spec.direction == "inout":
+                kw["last"] = self._view(out_name, out_spec).clone()
+            out = step_op.reference(*inputs, **kw)
             dst = self.get_buffer(out_name).torch_view(out_spec.dtype)
             flat = out.reshape(-1).to(out_spec.dtype)
             dst[: flat.numel()].copy_(flat)
 
 
 class _HostParams:
+    """Runtime parameters of the reference dispatch (host values, same conversions)."""
+
     def __init__(self):
         self.values = {}
+        self._convert = {}
+
+    def define(self, name, n=1, convert=None):
+        if convert is not None:
+            self._convert[name] = convert
 
     def write(self, name, value):
-        self.values[name] = np.asarray(value)
+        conv = self._convert.get(name)
+        if conv is not None:
+            value = conv(value)
+        self.values[name] = np.atleast_1d(np.asarray(value, dtype=np.int64))
+
+    def read(self, name):
+        return self.values[name]
+
+    def snapshot(self) -> dict:
+        return dict(self.values)
 
     def sync(self):
         pass
+
+    def __contains__(self, name):
+        return name in self.values
 
 
 class SequenceCompareCallable(SequenceHipCallable):
@@ -412,15 +446,27 @@ class SequenceCompareCallable(SequenceHipCallable):
         for idx, ((fn, views), (step_op, names, specs)) in enumerate(
                 zip(self._plan, self._iter_steps())):
             cpu_inputs = [v.reshape(s.shape).cpu().clone() for v, s in zip(views[:-1], specs[:-1])]
+            kw = {"params": self.params.snapshot()}
+            if specs[-1].direction == "inout":
+                kw["last"] = views[-1].reshape(specs[-1].shape).cpu().clone()
             fn(*views)
             torch.cuda.synchronize(self.device)
-            dev_out = views[-1].reshape(-1).float().cpu()
-            ref = step_op.reference(*cpu_inputs).reshape(-1).float()
-            n = min(ref.numel(), dev_out.numel())
-            diff = (dev_out[:n] - ref[:n]).abs()
-            max_abs = float(diff.max()) if n else 0.0
-            max_rel = float((diff / (ref[:n].abs() + 1e-6)).max()) if n else 0.0
-            fail = (max_abs > self.abs_tol) and (max_rel > self.rel_tol)
+            ref = step_op.reference(*cpu_inputs, **kw).reshape(-1)
+            if specs[-1].dtype.is_floating_point:
+                dev_out = views[-1].reshape(-1).float().cpu()
+                ref = ref.float()
+                n = min(ref.numel(), dev_out.numel())
+                diff = (dev_out[:n] - ref[:n]).abs()
+                max_abs = float(diff.max()) if n else 0.0
+                max_rel = float((diff / (ref[:n].abs() + 1e-6)).max()) if n else 0.0
+                fail = (max_abs > self.abs_tol) and (max_rel > self.rel_tol)
+            else:
+                # integer outputs (argmax keys) must match exactly
+                dev_out = views[-1].reshape(-1).cpu().to(torch.int64)
+                ref = ref.to(torch.int64)
+                n = min(ref.numel(), dev_out.numel())
+                fail = not torch.equal(dev_out[:n], ref[:n])
+                max_abs = max_rel = float(fail)
             stats = {"step": idx, "op": type(step_op).__name__, "output": names[-1],
                      "max_abs": max_abs, "max_rel": max_rel, "mismatch": fail}
             logger.log(logging.ERROR if fail else logging.INFO,

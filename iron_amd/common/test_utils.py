@@ -25,19 +25,6 @@ torch_dtype_map = {
 }
 
 
-def nearly_equal(a: float, b: float, rel_tol: float = 128 * np.finfo(np.float32).eps,
-                 abs_tol: float = np.finfo(np.float32).tiny) -> bool:
-    if np.finfo(np.float32).eps > rel_tol:
-        raise ValueError(f"rel_tol {rel_tol!r} must be >= machine epsilon")
-    if rel_tol >= 1.0:
-        raise ValueError(f"rel_tol {rel_tol!r} must be < 1.0")
-    if a == b:
-        return True
-    diff = abs(float(a) - float(b))
-    norm = min(abs(float(a)) + abs(float(b)), np.finfo(np.float32).max)
-    return diff < max(abs_tol, rel_tol * norm)
-
-
 def _to_f64(x) -> np.ndarray:
     if isinstance(x, torch.Tensor):
         return x.detach().to("cpu").to(torch.float64).contiguous().numpy().reshape(-1)

@@ -187,7 +187,8 @@ __global__ __launch_bounds__(256) void next_token_kernel(unsigned long long* key
                                                          const uint16_t* __restrict__ emb,
                                                          uint16_t* __restrict__ x,
                                                          int32_t* token_log, int log_stride,
-                                                         int32_t* step, int B, int D, int vocab) {
+                                                         int log_len, int32_t* step, int B, int D,
+                                                         int vocab) {
   __shared__ int32_t s_tok[64];
   __shared__ int32_t s_step;
   if (threadIdx.x < B) {
@@ -201,7 +202,9 @@ __global__ __launch_bounds__(256) void next_token_kernel(unsigned long long* key
   __syncthreads();
   if (threadIdx.x < B) {
     keys[threadIdx.x] = 0ull;
-    if (token_log) token_log[(size_t)threadIdx.x * log_stride + s_step] = s_tok[threadIdx.x];
+    // the log holds log_len entries per row; steps past it are counted but not logged
+    if (token_log && s_step >= 0 && s_step < log_len)
+      token_log[(size_t)threadIdx.x * log_stride + s_step] = s_tok[threadIdx.x];
   }
   if (threadIdx.x == 0 && step) *step = s_step + 1;
   if (emb) {
@@ -375,8 +378,8 @@ int iron_embed(const int32_t* tokens, const uint16_t* emb, uint16_t* x, int B, i
 }
 
 int iron_next_token(unsigned long long* keys, int32_t* tokens, const uint16_t* emb, uint16_t* x,
-                    int32_t* token_log, int log_stride, int32_t* step, int B, int D, int vocab,
-                    void* stream) {
+                    int32_t* token_log, int log_stride, int log_len, int32_t* step, int B, int D,
+                    int vocab, void* stream) {
   iron::clear_error();
   if (!keys || !tokens) return iron::fail(IRON_ERR_NULL, "iron_next_token: null keys/tokens");
   if (B <= 0 || B > 64 || vocab <= 0)
@@ -385,8 +388,11 @@ int iron_next_token(unsigned long long* keys, int32_t* tokens, const uint16_t* e
     return iron::fail(IRON_ERR_NULL, "iron_next_token: embedding gather needs x and D > 0");
   if (token_log && !step)
     return iron::fail(IRON_ERR_NULL, "iron_next_token: token_log needs a step counter");
+  if (token_log && (log_len <= 0 || (B > 1 && log_stride < log_len)))
+    return iron::fail(IRON_ERR_SHAPE, "iron_next_token: log_len=%d (row stride %d)", log_len,
+                      log_stride);
   hipLaunchKernelGGL(next_token_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, keys, tokens,
-                     emb, x, token_log, log_stride, step, B, D, vocab);
+                     emb, x, token_log, log_stride, log_len, step, B, D, vocab);
   return iron::check_launch("iron_next_token");
 }
 

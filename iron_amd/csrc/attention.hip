@@ -624,6 +624,232 @@ int launch_attention(AttnParams p, bool fused, int acc, int B, void* part_ws, si
   return iron::check_launch(fn);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Batch / verify mode (speculative-decode verify): n new tokens at positions base..base+n-1 each
+// query one shared KV cache; token t attends keys [0, min(base + t + 1, S)) when causal, all S
+// keys otherwise (iron/operators/decode_attn/op.py:40-48, design.py:243-276). The reference
+// streams the cache once per group of M queries; here a workgroup stages each 64-key K/V block in
+// LDS once and applies it to up to 64 query rows (4 wavefronts x 16 rows, row = t * HG + g for
+// query head kv * HG + g), so the cache is read once per 64 / HG tokens.
+//
+// Arithmetic: the reference kernel's (decode_attn.cc:117-311): bf16 operands, fp32 scores
+// (v_mfma_f32_16x16x32_bf16), exp2-domain online softmax in fp32, probabilities rounded to bf16
+// for the P.V product, fp32 accumulation, one division and bf16 rounding of the output. Splits
+// of the key range merge in the fp32 merge kernel above (maxima in the exp2 domain).
+//
+// MFMA layouts (checked on the device for the prefill kernel, prefill.hip): S^T = K Q^T per 16-key
+// tile leaves lane l with query l % 16 and keys 4 (l / 16) + i; a 32-key P.V step takes tiles 2s
+// and 2s + 1 in that order, which is the B-operand layout of P^T for O^T = V^T P^T when V^T reads
+// the same key permutation.
+// ---------------------------------------------------------------------------------------------
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 vbf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float vf32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float vf32x2;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 vbf16x2;
+
+constexpr int kVB = 64;  // keys per staged block
+
+struct VerifyParams {
+  const uint16_t* q;         // [n][H][D] token-major
+  const uint16_t* k;
+  const uint16_t* v;
+  long long sh, st;          // head and token strides of the caches (elements)
+  const int32_t* base_ptr;   // device S_kv_base, or null (base_const)
+  int base_const;
+  int causal, n, H, KV, HG, S, rows;  // rows = n * HG query rows per KV head
+  int chunk, nsplit, qgroups;
+  float c;                   // scale * log2(e)
+  float* part;               // [n][H][nsplit][D + 2]: o (unnormalised), m (exp2 domain), l
+  uint16_t* out;             // [n][H][D]
+};
+
+IRON_DEV vbf16x8 as_vbf16x8(const uint4 u) { return __builtin_bit_cast(vbf16x8, u); }
+
+IRON_DEV uint32_t pack2_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((vf32x2{lo, hi}), vbf16x2));
+}
+
+__global__ __launch_bounds__(256) void verify_attn_kernel(VerifyParams p) {
+  __shared__ __align__(16) uint16_t s_k[kVB][kD + 8];
+  __shared__ __align__(16) uint16_t s_vt[kD][kVB + 8];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int quarter = lane >> 4, col = lane & 15;
+  const int split = blockIdx.x;
+  const int kv = blockIdx.y / p.qgroups, qg = blockIdx.y % p.qgroups;
+  const int tile = qg * 4 + wave;              // this wavefront's 16 query rows
+  const bool live = tile * 16 < p.rows;         // wavefront-uniform
+  const int r = tile * 16 + col;               // this lane's query row
+  const bool rv = r < p.rows;
+  const int rc = rv ? r : 0;                   // rows past the end read row 0, never stored
+  const int t = rc / p.HG, h = kv * p.HG + rc % p.HG;
+  int base = p.base_ptr ? *p.base_ptr : p.base_const;
+  base = base < 0 ? 0 : base;
+  const int s_eff = p.causal ? min(base + p.n, p.S) : p.S;  // keys some query attends
+  const int bound = p.causal ? min(base + t + 1, p.S) : p.S;
+  const int k0 = split * p.chunk, k1 = min(k0 + p.chunk, s_eff);
+  const int lim = min(bound, k1);              // this lane's valid keys in the split: [k0, lim)
+
+  uint4 qf[kD / 32];                           // Q^T operand: dims 32 j + 8 quarter .. +8
+  const uint16_t* qrow = p.q + ((size_t)t * p.H + h) * kD;
+#pragma unroll
+  for (int j = 0; j < kD / 32; ++j) qf[j] = *(const uint4*)(qrow + 32 * j + quarter * 8);
+
+  const uint16_t* kb = p.k + (size_t)kv * p.sh;
+  const uint16_t* vb = p.v + (size_t)kv * p.sh;
+  // staging: K keys 4 (tid / 16) + i, dims 8 (tid % 16); V keys 4 (tid % 16) + i, dims
+  // 8 (tid / 16) (key groups fastest across lanes: the transposed writes spread over banks)
+  const int kg = tid >> 4, kd = (tid & 15) * 8, vg = tid & 15, vd = (tid >> 4) * 8;
+  uint4 kreg[4], vreg[4];
+  auto gload = [&](int kb0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int jk = min(kb0 + 4 * kg + i, k1 - 1), jv = min(kb0 + 4 * vg + i, k1 - 1);
+      kreg[i] = *(const uint4*)(kb + (size_t)jk * p.st + kd);
+      vreg[i] = *(const uint4*)(vb + (size_t)jv * p.st + vd);
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(uint4*)&s_k[4 * kg + i][kd] = kreg[i];
+    const uint32_t a[4][4] = {{vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w},
+                              {vreg[1].x, vreg[1].y, vreg[1].z, vreg[1].w},
+                              {vreg[2].x, vreg[2].y, vreg[2].z, vreg[2].w},
+                              {vreg[3].x, vreg[3].y, vreg[3].z, vreg[3].w}};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {  // dims vd + 2w (low halves) and vd + 2w + 1 (high halves)
+      *(uint2*)&s_vt[vd + 2 * w][4 * vg] =
+          make_uint2((a[0][w] & 0xffffu) | (a[1][w] << 16), (a[2][w] & 0xffffu) | (a[3][w] << 16));
+      *(uint2*)&s_vt[vd + 2 * w + 1][4 * vg] =
+          make_uint2((a[0][w] >> 16) | (a[1][w] & 0xffff0000u),
+                     (a[2][w] >> 16) | (a[3][w] & 0xffff0000u));
+    }
+  };
+
+  vf32x4 o[kD / 16];
+#pragma unroll
+  for (int dt = 0; dt < kD / 16; ++dt) o[dt] = vf32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;                // this lane's share of its query's statistics
+
+  if (k0 < k1) gload(k0);
+  for (int kb0 = k0; kb0 < k1; kb0 += kVB) {
+    __syncthreads();                           // the previous block's LDS reads are done
+    lstore();
+    __syncthreads();
+    if (kb0 + kVB < k1) gload(kb0 + kVB);      // in flight during this block's products
+    if (!live) continue;
+    vf32x4 sc[kVB / 16];
+#pragma unroll
+    for (int kt = 0; kt < kVB / 16; ++kt) {
+      sc[kt] = vf32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < kD / 32; ++j) {
+        const uint4 a = *(const uint4*)&s_k[16 * kt + col][32 * j + quarter * 8];
+        sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_vbf16x8(a), as_vbf16x8(qf[j]),
+                                                         sc[kt], 0, 0, 0);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < kVB / 16; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int jk = kb0 + 16 * kt + quarter * 4 + i;
+        if (jk >= lim) sc[kt][i] = -INFINITY;
+        mx = fmaxf(mx, sc[kt][i]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx * p.c);       // the scale is positive: max maps to max
+    const bool none = mn == -INFINITY;         // no valid key of this query yet
+    const float corr = none ? 1.f : exp2_f(m - mn);
+    m = mn;
+    float ps = 0.f;
+    vbf16x8 pb[kVB / 32];
+#pragma unroll
+    for (int ks = 0; ks < kVB / 32; ++ks) {
+      uint32_t w[4];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        float e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          e[i] = none ? 0.f : exp2_f(fmaf(sc[2 * ks + hh][i], p.c, -mn));
+          ps += e[i];
+        }
+        w[2 * hh] = pack2_bf16(e[0], e[1]);
+        w[2 * hh + 1] = pack2_bf16(e[2], e[3]);
+      }
+      pb[ks] = as_vbf16x8(make_uint4(w[0], w[1], w[2], w[3]));
+    }
+    l = l * corr + ps;
+#pragma unroll
+    for (int dt = 0; dt < kD / 16; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[dt][i] *= corr;
+#pragma unroll
+    for (int ks = 0; ks < kVB / 32; ++ks)
+#pragma unroll
+      for (int dt = 0; dt < kD / 16; ++dt) {
+        const uint16_t* vr = &s_vt[16 * dt + col][32 * ks + quarter * 4];
+        const uint2 v0 = *(const uint2*)vr;
+        const uint2 v1 = *(const uint2*)(vr + 16);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_vbf16x8(make_uint4(v0.x, v0.y, v1.x, v1.y)), pb[ks], o[dt], 0, 0, 0);
+      }
+  }
+  // the four lane quarters of a query hold disjoint keys under the same maximum
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (!rv) return;
+  const size_t row = (size_t)t * p.H + h;
+  if (p.nsplit == 1) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* orow = p.out + row * kD;
+#pragma unroll
+    for (int dt = 0; dt < kD / 16; ++dt)
+      *(uint2*)(orow + 16 * dt + quarter * 4) =
+          make_uint2(pack2_bf16(o[dt][0] * inv, o[dt][1] * inv),
+                     pack2_bf16(o[dt][2] * inv, o[dt][3] * inv));
+    return;
+  }
+  float* part = p.part + (row * p.nsplit + split) * (kD + 2);
+#pragma unroll
+  for (int dt = 0; dt < kD / 16; ++dt)
+    *(float4*)(part + 16 * dt + quarter * 4) = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+  if (quarter == 0) {
+    part[kD] = m;
+    part[kD + 1] = l;
+  }
+}
+
+struct VerifyPlan {
+  int nsplit, chunk, qgroups;
+};
+
+VerifyPlan plan_verify(int n, int H, int KV, int max_ctx) {
+  VerifyPlan vp;
+  const int rows = n * (H / KV);
+  vp.qgroups = (rows + 63) / 64;
+  const int per_split = KV * vp.qgroups;
+  const int max_ns = (max_ctx + kVB - 1) / kVB;
+  int ns = (512 + per_split - 1) / per_split;
+  ns = ns > max_ns ? max_ns : ns;
+  ns = ns > kMaxSplit ? kMaxSplit : (ns < 1 ? 1 : ns);
+  int chunk = (max_ctx + ns - 1) / ns;
+  chunk = (chunk + kVB - 1) / kVB * kVB;
+  vp.chunk = chunk;
+  vp.nsplit = (max_ctx + chunk - 1) / chunk;
+  return vp;
+}
+
+size_t verify_ws_bytes(int n, int H, int KV, int max_ctx) {
+  const VerifyPlan vp = plan_verify(n, H, KV, max_ctx);
+  if (vp.nsplit == 1) return 0;
+  return (((size_t)n * H * vp.nsplit * (kD + 2) * sizeof(float)) + 255) & ~(size_t)255;
+}
+
+constexpr int kVerifyMaxTokens = 4096;
+
 }  // namespace
 
 extern "C" {
@@ -725,6 +951,78 @@ int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
   p.scale = (double)scale;
   return launch_attention(p, true, acc, B, (char*)workspace + raw_bytes,
                           workspace_bytes - raw_bytes, s, fn);
+}
+
+
+size_t iron_decode_attn_verify_workspace(int n_new, int H, int KV, int D, int max_ctx) {
+  if (n_new <= 0 || n_new > kVerifyMaxTokens || H <= 0 || KV <= 0 || D != kD || H % KV ||
+      max_ctx <= 0)
+    return 0;
+  const size_t n = verify_ws_bytes(n_new, H, KV, max_ctx);
+  return n ? n : 256;
+}
+
+int iron_decode_attn_verify(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                            long long kv_sh, long long kv_st, const int32_t* base,
+                            int base_const, int causal, uint16_t* out, int n_new, int H, int KV,
+                            int D, int max_ctx, float scale, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  iron::clear_error();
+  const char* fn = "iron_decode_attn_verify";
+  if (!q || !k_cache || !v_cache || !out) return iron::fail(IRON_ERR_NULL, "%s: null tensor", fn);
+  int st = check_attn_shape(fn, 1, H, KV, D, max_ctx);
+  if (st) return st;
+  if (n_new <= 0 || n_new > kVerifyMaxTokens)
+    return iron::fail(IRON_ERR_SHAPE, "%s: n_new=%d outside [1, %d]", fn, n_new,
+                      kVerifyMaxTokens);
+  if (kv_st % 8 || kv_sh % 8 || kv_st < kD || !iron::aligned(k_cache, 16) ||
+      !iron::aligned(v_cache, 16) || !iron::aligned(q, 16) || !iron::aligned(out, 16))
+    return iron::fail(IRON_ERR_ALIGN, "%s: Q/O/K/V rows must be 16-byte aligned", fn);
+  if (!base && (base_const < 0 || base_const > max_ctx))
+    return iron::fail(IRON_ERR_SHAPE, "%s: base_const=%d outside [0, %d]", fn, base_const,
+                      max_ctx);
+  if (!(scale > 0.f)) return iron::fail(IRON_ERR_SHAPE, "%s: scale must be positive", fn);
+  const VerifyPlan vp = plan_verify(n_new, H, KV, max_ctx);
+  VerifyParams p = {};
+  p.q = q;
+  p.k = k_cache;
+  p.v = v_cache;
+  p.sh = kv_sh;
+  p.st = kv_st;
+  p.base_ptr = base;
+  p.base_const = base_const;
+  p.causal = causal ? 1 : 0;
+  p.n = n_new;
+  p.H = H;
+  p.KV = KV;
+  p.HG = H / KV;
+  p.S = max_ctx;
+  p.rows = n_new * p.HG;
+  p.chunk = vp.chunk;
+  p.nsplit = vp.nsplit;
+  p.qgroups = vp.qgroups;
+  p.c = scale * 1.4426950408889634f;
+  p.out = out;
+  if (vp.nsplit > 1) {
+    const size_t need = verify_ws_bytes(n_new, H, KV, max_ctx);
+    if (!workspace || workspace_bytes < need)
+      return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes,
+                        need);
+    if (!iron::aligned(workspace, 256))
+      return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
+    p.part = (float*)workspace;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(verify_attn_kernel, dim3(vp.nsplit, KV * vp.qgroups), dim3(256), 0, s, p);
+  st = iron::check_launch(fn);
+  if (st || vp.nsplit == 1) return st;
+  AttnParams mp = {};
+  mp.part = p.part;
+  mp.nsplit = vp.nsplit;
+  mp.H = H;
+  mp.out = out;
+  hipLaunchKernelGGL(attn_merge_kernel<true>, dim3(H, n_new), dim3(256), 0, s, mp);
+  return iron::check_launch(fn);
 }
 
 }  // extern "C"

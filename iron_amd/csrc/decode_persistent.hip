@@ -31,9 +31,12 @@
 // and the workgroup stops; waiting workgroups also stop once they see that word set, so the grid
 // drains within about one spin limit (the caller then reports the error).
 //
-// Buffer reuse is safe because each phase consumes ALL of an earlier phase's words (the RMSNorm
-// of x, the Wo / down inputs, the split merge), so a word is only rewritten after every reader of
-// its previous value has finished.
+// Buffer reuse: a hand-off buffer is rewritten by the same phase of the next layer (gh: four
+// layers later). Its producers reach that phase only after they have consumed a later phase's
+// words, which every workgroup produces only after it has read this buffer -- provided every
+// workgroup that reads the buffer also produces in a phase that the producers wait on. For the
+// Qwen3-0.6B shape every workgroup produces in every phase; in smaller shapes workgroups that own
+// no rows of the Wo, gate/up or down phase read nothing in that phase (skip_gather).
 #include "attn_core.h"
 #include "common.h"
 #include "gemv_core.h"
@@ -45,6 +48,7 @@ using namespace iron::dev;
 
 constexpr int kNT = 256;                     // workgroups (one per CU of an MI355X)
 constexpr int kPhases = 7;                   // tag slots per layer: six phases + the input row
+constexpr int kMaxLayers = 128;              // tag slots per launch: kPhases * kMaxLayers
 constexpr long long kSpinLimit = 1ll << 18;  // polls of one word before a wait fails (~0.3 s)
 // s_waitcnt immediate: vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding)
 constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);
@@ -169,8 +173,13 @@ IRON_DEV GemvParams gemv_of(const WireGeom& g, const void* w, int M, int K) {
 // ---------------------------------------------------------------------------------------------
 // Tagged words
 // ---------------------------------------------------------------------------------------------
+// A launch's tags take the fixed range [epoch * kPhases * kMaxLayers, +kPhases * kMaxLayers), so
+// launches with different layer counts on one workspace never expect a tag an earlier launch left
+// in a word (a stride of kPhases * n_layers would let epoch e with n layers overlap epoch e - 1
+// with more layers).
 IRON_DEV uint32_t phase_tag(uint32_t epoch, int n_layers, int layer, int phase) {
-  const unsigned long long v = (unsigned long long)epoch * (unsigned long long)(kPhases * n_layers) +
+  (void)n_layers;
+  const unsigned long long v = (unsigned long long)epoch * (unsigned long long)(kPhases * kMaxLayers) +
                                (unsigned long long)(kPhases * layer + phase);
   return (uint32_t)(v % 0xffffffffull) + 1u;  // never 0, the value of a cleared word
 }
@@ -262,6 +271,18 @@ IRON_DEV void issue_fenced(Issue issue) {
   __builtin_amdgcn_sched_barrier(0);
   issue();
   __builtin_amdgcn_sched_barrier(0);
+}
+
+// A workgroup that owns no rows of a phase reads none of its input: it only keeps the phase
+// structure (the opening barrier and the retired loads of gather_words) and issues the later
+// phase's loads. Not reading words it does not need also keeps it from waiting on a word whose
+// buffer a faster workgroup may already have rewritten for the next layer.
+template <class Issue>
+IRON_DEV bool skip_gather(Issue issue) {
+  __syncthreads();
+  retire_loads();
+  issue_fenced(issue);
+  return true;
 }
 
 template <int NPT, int DELAY = kFirstPollDelay, class Src, class Issue>
@@ -1005,6 +1026,7 @@ IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s
   const int row0 = row0_of<S>(wg, R);
   GemvParams g = gemv_of(p.g_o, nullptr, S::D, S::QD);
   g.pro = PRO_BF16;
+  if (wg * 4 * R >= S::D) return skip_gather(issue);  // no Wo rows here (small shapes)
   {
     const uint32_t ta = phase_tag(ep, p.n_layers, l, 2);
     unsigned long long* const att = copy_for(p.ATT, kCopyWords, wg);
@@ -1043,6 +1065,7 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
   g.pro = PRO_RES_RMS_F32;
   g.eps = p.eps;
   g.x2 = (const uint16_t*)p.AO;  // marks the residual term (read from LDS here)
+  if (wg * 4 * R >= S::FF) return skip_gather(issue);  // no gate/up rows here (small shapes)
   {
     // a only: the layer input x is still in s_x from this workgroup's QKV phase
     const uint32_t ta = phase_tag(ep, p.n_layers, l, 3);
@@ -1105,6 +1128,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   // LDS words [0, FF): gh; the residual (a and x of this workgroup's 4R rows) is in s_own
   unsigned long long* const gh =
       copy_for(p.GH, S::GH_COPY, wg) + (l % kGhBuffers) * S::GH_WORDS;
+  if (wg * 4 * R >= S::D) return skip_gather(issue);  // no down rows here (small shapes)
   {
     const uint32_t tg = phase_tag(ep, p.n_layers, l, 4);
     // gate/up workgroup q writes rows [GH_ROWS q, GH_ROWS (q + 1)) into block q, the last one
@@ -1381,8 +1405,9 @@ static int decode_persistent(const char* fn, const iron_decode_gen* gen,
   if (id == SHAPE_NONE)
     return iron::fail(IRON_ERR_UNSUPPORTED, "%s: no persistent kernel for D=%d FF=%d Hq=%d Hkv=%d "
                       "HD=%d", fn, D, FF, Hq, Hkv, HD);
-  if (n_layers <= 0 || max_seq <= 0)
-    return iron::fail(IRON_ERR_SHAPE, "%s: n_layers=%d max_seq=%d", fn, n_layers, max_seq);
+  if (n_layers <= 0 || n_layers > kMaxLayers || max_seq <= 0)
+    return iron::fail(IRON_ERR_SHAPE, "%s: n_layers=%d (at most %d) max_seq=%d", fn, n_layers,
+                      kMaxLayers, max_seq);
   if (kv_st % 8 || kv_sh % 8 || kv_st < HD || kv_sh < (long long)max_seq * kv_st / 2)
     return iron::fail(IRON_ERR_SHAPE, "%s: KV strides sh=%lld st=%lld", fn, kv_sh, kv_st);
   const int QD = Hq * HD, MQKV = QD + 2 * Hkv * HD;

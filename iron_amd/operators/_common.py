@@ -63,6 +63,10 @@ class RuntimeParams:
     def read(self, name: str) -> np.ndarray:
         return self._tensors[name].cpu().numpy()
 
+    def snapshot(self) -> dict:
+        """Current values of every parameter (host copies), for the CPU goldens."""
+        return {n: t.cpu().numpy() for n, t in self._tensors.items()}
+
     def sync(self) -> None:
         pass
 

@@ -7,7 +7,8 @@ Drop-in for iron/operators/swiglu_mlp_dp/op_ours.py:46-582. Spec order as in the
 
 Wires are the row-block int8 wire (iron_amd/operators/wire.py); Wg/Wu use ``tile_rows_gu`` rows
 per block and Wd ``tile_rows_gu // (FF // D)`` (the reference's shared-tile identity,
-qwen3_npu_int8.py:525-530). Wo uses a plain ``tile_rows_o``-row wire instead of the reference's
+qwen3_npu_int8.py:525-530), or 4-row blocks for both when FF is not a multiple of D (the
+reference's Qwen3-4B chunked-down arm, op_ours.py:91-117, without its zero padding of FF). Wo uses a plain ``tile_rows_o``-row wire instead of the reference's
 NPU per-core overlap windows (op_ours.py:357-369) -- those duplicated pad rows only exist to
 feed eight AIE columns. ``gh_scratch`` is the operator's device workspace (fp32 gh, which the
 golden keeps unrounded) sized by ``iron_swiglu_mlp_workspace``; ``a_scratch`` receives
@@ -53,10 +54,19 @@ class SwiGLUMLPDataParallelOurs(SwiGLUMLPDataParallel):
             self.group_size = 128
         super().__post_init__()
         if self.FF % self.D:
-            raise NotImplementedError("the chunked-down arm (FF % D != 0) is not implemented")
-        R = self.FF // self.D
-        if self.tile_rows_gu % R:
-            raise ValueError(f"tile_rows_gu={self.tile_rows_gu} must be a multiple of FF/D={R}")
+            # The reference's chunked-down arm (Qwen3-4B: D=2560, FF=9728; op_ours.py:91-117)
+            # pads FF with zero rows to a multiple of D only to give its eight AIE columns equal
+            # work, and uses 4-row tiles for gate/up and down alike. The GEMV and MFMA kernels
+            # here take any FF (a multiple of the group), so the wires keep FF rows: the same
+            # products without the 5% of zero padding.
+            self.tile_rows_gu = 4
+            if self.FF % self.tile_rows_gu or self.D % self.tile_rows_gu:
+                raise ValueError(f"FF={self.FF} and D={self.D} must be multiples of 4")
+        else:
+            R = self.FF // self.D
+            if self.tile_rows_gu % R:
+                raise ValueError(f"tile_rows_gu={self.tile_rows_gu} must be a multiple of "
+                                 f"FF/D={R}")
         for what, K in (("D", self.D), ("FF", self.FF)) + ((("QD", self.QD),) if self.fuse_o else ()):
             if K % self.group_size:
                 raise ValueError(f"{what}={K} not a multiple of group_size={self.group_size}")
@@ -70,6 +80,11 @@ class SwiGLUMLPDataParallelOurs(SwiGLUMLPDataParallel):
 
     @property
     def tile_rows_d(self) -> int:
+        """Row-block height of the Wd wire: tile_rows_gu / (FF/D) (the reference's shared-tile
+        identity, qwen3_npu_int8.py:525-530), or tile_rows_gu itself when FF % D != 0 (its
+        chunked-down arm sets TSI_D == TSI_GU, op_ours.py:110-117)."""
+        if self.FF % self.D:
+            return self.tile_rows_gu
         return self.tile_rows_gu // (self.FF // self.D)
 
     def wire_bytes(self, which: str) -> int:

@@ -9,7 +9,11 @@ Follows:
   * the torch.softmax form of the decode-attention scripts (decode_attn/test_seqpos_runtime.py:
     26-34) -- identical in exact arithmetic, used as an independent check;
   * causal prefill MHA -- iron/operators/mha/reference.py:73-81 (SDPA, is_causal, GQA by
-    repeat_interleave of K/V heads).
+    repeat_interleave of K/V heads);
+  * batch / verify decode attention -- the DecodeAttention batch mode
+    (iron/operators/decode_attn/op.py:40-48, design.py:243-276; the CPU reference of its test,
+    decode_attn/test_batch.py:31-45): n new tokens at positions base..base+n-1, token t attends
+    keys [0, base + t] when causal and the whole cache [0, S) otherwise.
 """
 
 import math
@@ -94,3 +98,24 @@ def causal_prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     mask = torch.ones(S, S, dtype=torch.bool).tril()
     s = s.masked_fill(~mask, float("-inf"))
     return torch.softmax(s, dim=-1) @ vv
+
+
+def verify_bounds(n_new: int, base: int, S: int, causal: bool) -> list[int]:
+    """Keys each new token attends (decode_attn/design.py:255-262): base + t + 1 when causal
+    (the per-query boundary S_kv_base + g*M + m + 1 with t = g*M + m), S otherwise; at most S."""
+    return [min(base + t + 1, S) if causal else S for t in range(n_new)]
+
+
+def decode_attention_verify(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, base: int,
+                            causal: bool = True, scale: float | None = None,
+                            dt=EXACT) -> torch.Tensor:
+    """q (n, H, D) token-major; k, v (KV, S, D) one cache -> (n, H, D) bf16.
+
+    Token t is a decode query over its own bound (``verify_bounds``); the grouping of queries
+    (batch_queries) only changes how the cache is streamed, not the result."""
+    n, H, D = q.shape
+    KV, S = k.shape[0], k.shape[1]
+    bounds = verify_bounds(n, base, S, causal)
+    kk = k.unsqueeze(0).expand(n, KV, S, D)
+    vv = v.unsqueeze(0).expand(n, KV, S, D)
+    return decode_attention(q, kk, vv, bounds, scale, dt)

@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iron_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.iron_abi_version() == _lib.ABI_VERSION == 6
 
 
 def test_wire_bytes(lib):
@@ -187,3 +187,17 @@ def test_persistent_layer_check(lib):
     d.n_kn = None
     assert lib.iron_decode_persistent_check_layer(ctypes.byref(d), *args) == _lib.IRON_ERR_NULL
     assert lib.iron_decode_persistent_check_layer(None, *args) == _lib.IRON_ERR_NULL
+
+
+def test_next_token_validation(lib):
+    """The token log is bounded: a log needs a positive length (and a row stride that holds it
+    when B > 1); these checks fail before anything is launched."""
+    f = lib.iron_next_token
+    fake = 1 << 20
+    # keys, tokens, emb, x, token_log, log_stride, log_len, step, B, D, vocab, stream
+    assert f(None, fake, None, None, None, 0, 0, None, 1, 1024, 100, None) == _lib.IRON_ERR_NULL
+    assert f(fake, fake, None, None, fake, 0, 8, None, 1, 1024, 100, None) == _lib.IRON_ERR_NULL
+    assert f(fake, fake, None, None, fake, 0, 0, fake, 1, 1024, 100, None) == _lib.IRON_ERR_SHAPE
+    assert b"log_len" in lib.iron_last_error()
+    assert f(fake, fake, None, None, fake, 4, 8, fake, 2, 1024, 100, None) == _lib.IRON_ERR_SHAPE
+    assert f(fake, fake, None, None, None, 0, 0, None, 65, 1024, 100, None) == _lib.IRON_ERR_SHAPE

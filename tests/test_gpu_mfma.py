@@ -83,6 +83,8 @@ def test_gemm_mfma(M, K, G, tile_m, B, domain):
 @pytest.mark.parametrize("D,FF,QD,fuse_o,G,B", [
     (2048, 6144, 0, False, 32, 8),      # BASELINE config 2, batch 8 (Qwen3-1.7B MLP)
     (1024, 3072, 2048, True, 32, 16),   # Qwen3-0.6B chain arm at batch 16
+    (4096, 12288, 4096, True, 32, 16),  # Qwen3-8B layer MLP at BASELINE config 5 (B=16)
+    (2560, 9728, 4096, True, 32, 8),    # Qwen3-4B: FF % D != 0 (the chunked-down arm)
 ])
 def test_swiglu_mlp_mfma(D, FF, QD, fuse_o, G, B):
     _say(f"swiglu mfma D={D} FF={FF} QD={QD} fuse_o={fuse_o} G={G} B={B}")
@@ -117,11 +119,18 @@ def test_swiglu_mlp_mfma(D, FF, QD, fuse_o, G, B):
     torch.cuda.synchronize()
     want, want_a = oblk.swiglu_mlp(cur, cx, n_pf, wg, wu, wd, 1e-6, wo=wo)
     assert not verify_buffer(nxt.cpu(), "nxt", want, RTOL, ATOL)
-    lit, _ = oblk.swiglu_mlp(cur, cx, n_pf, wg, wu, wd, 1e-6, wo=wo, dt=LITERAL)
+    if fuse_o:
+        # a = bf16(Wo . cx) is within one ulp of exact; a one-ulp step of a moves nxt by the same
+        # amount through the residual x1 = cur + a, which is many ulps of a small (cancelled) nxt,
+        # so the rest of the block is checked from the device's own a, stage by stage
+        assert_within_one_ulp(a_s, want_a, "mlp a")
+        a_dev = a_s.cpu().reshape(B, D)
+        want, _ = oblk.swiglu_mlp(cur, a_dev, n_pf, wg, wu, wd, 1e-6)
+        lit, _ = oblk.swiglu_mlp(cur, a_dev, n_pf, wg, wu, wd, 1e-6, dt=LITERAL)
+    else:
+        lit, _ = oblk.swiglu_mlp(cur, cx, n_pf, wg, wu, wd, 1e-6, wo=wo, dt=LITERAL)
     assert not verify_buffer(nxt.cpu(), "nxt", lit, RTOL, ATOL)
     assert_within_one_ulp(nxt, want, "mlp nxt")
-    if fuse_o:
-        assert_within_one_ulp(a_s, want_a, "mlp a")
 
 
 def test_qkv_attention_mfma_batch16():
@@ -163,6 +172,65 @@ def test_qkv_attention_mfma_batch16():
     for b in range(B):
         p = int(pos[b])
         assert_within_one_ulp(kc[b, :, p].cpu(), wk[b].reshape(Hkv, HD), f"k@{b}")
+
+
+def test_qwen3_8b_layer_b16_context_8192():
+    """One Qwen3-8B layer exactly as BASELINE config 5's decode step runs it (the bench's
+    c5_decode_b16): B = 16 rows at positions near 8192, the fused QKV head + attention with the
+    exact fp64 core (a split plan of several splits, each several tiles), then the MLP with the
+    output projection folded in (Wo 4096 x 4096, gate/up 12288 x 4096 with the SwiGLU-planes
+    epilogue, down 4096 x 12288) on MFMA. Attention within rel/abs 1e-2 of the oracle (its raw
+    QKV comes from MFMA sums, one ulp from exact); the MLP, fed the device's attention output,
+    within one bf16 ulp of the exact oracle."""
+    D, Hq, Hkv, HD, S, G, FF, B = 4096, 32, 8, 128, 8192, 32, 12288, 16
+    QD, M = Hq * HD, (Hq + 2 * Hkv) * HD
+    _say(f"qwen3-8b layer B={B} context ~{S}")
+    gen = torch.Generator().manual_seed(88)
+
+    def lin(Mr, K, std=0.02):
+        return ogemv.rtn_quantize(torch.randn(Mr, K, generator=gen) * std, G)
+
+    wqkv, wo, wg, wu, wd = lin(M, D), lin(D, QD), lin(FF, D), lin(FF, D), lin(D, FF)
+    cur = torch.randn(B, D, generator=gen).to(torch.bfloat16)
+    n_in, n_pf = [(torch.rand(D, generator=gen) + 0.5).to(torch.bfloat16) for _ in range(2)]
+    n_qn, n_kn = [(torch.rand(HD, generator=gen) + 0.5).to(torch.bfloat16) for _ in range(2)]
+    pos = torch.randint(S - 200, S, (B,), generator=gen)
+    table = onorm.rope_angle_table(S, HD, 1e6)
+    k0 = torch.randn(B, Hkv, S, HD, generator=gen).to(torch.bfloat16)
+    v0 = torch.randn(B, Hkv, S, HD, generator=gen).to(torch.bfloat16)
+    qa = QKVHeadAttention(D=D, HD=HD, Hq=Hq, Hkv=Hkv, max_seq=S, group_size=G, tile_size_input=16,
+                          kv_layout="separate", batch=B, num_aie_columns=1, accumulate="f64",
+                          kernel_source="mv_int8_signed.cc")
+    fa = qa.get_callable()
+    fa.params.write(qa.kv_offset_parameter, (pos * HD).numpy())
+    kc, vc = k0.to(DEV), v0.to(DEV)
+    attn = torch.zeros(B * QD, dtype=torch.bfloat16, device=DEV)
+    fa(cur.reshape(-1).to(DEV), n_in.to(DEV),
+       pack_wire(*wqkv, 16, "signed").view(torch.bfloat16).to(DEV), n_qn.to(DEV), n_kn.to(DEV),
+       table[pos].reshape(-1).to(DEV), kc.reshape(-1), vc.reshape(-1), attn)
+    mlp = SwiGLUMLPDataParallelOurs(D=D, FF=FF, QD=QD, fuse_o=True, group_size=G, epsilon=1e-6,
+                                    batch=B, kernel_source="mv_int8_signed.cc")
+    ws = torch.zeros(mlp.workspace_bytes(), dtype=torch.uint8, device=DEV)
+    a_s = torch.zeros(B * D, dtype=torch.bfloat16, device=DEV)
+    nxt = torch.zeros(B * D, dtype=torch.bfloat16, device=DEV)
+    wires = [pack_wire(*wo, mlp.tile_rows_o, "signed"), pack_wire(*wg, mlp.tile_rows_gu, "signed"),
+             pack_wire(*wu, mlp.tile_rows_gu, "signed"), pack_wire(*wd, mlp.tile_rows_d, "signed")]
+    mlp.get_callable()(cur.reshape(-1).to(DEV), attn, n_pf.to(DEV),
+                       *[w.view(torch.bfloat16).to(DEV) for w in wires], ws, a_s, nxt)
+    torch.cuda.synchronize()
+    wq, wk, wv = oblk.qkv_head(cur, n_in, *wqkv, n_qn, n_kn, table[pos], Hq, Hkv, HD, 1e-6)
+    kk, vv = k0.clone(), v0.clone()
+    for b in range(B):
+        kk[b, :, int(pos[b])] = wk[b].reshape(Hkv, HD)
+        vv[b, :, int(pos[b])] = wv[b].reshape(Hkv, HD)
+    want_att = oatt.decode_attention(wq.reshape(B, Hq, HD), kk, vv, (pos + 1).tolist())
+    assert not verify_buffer(attn.cpu(), "attn", want_att.reshape(-1), RTOL, ATOL)
+    got_att = attn.cpu().reshape(B, QD)
+    want, want_a = oblk.swiglu_mlp(cur, got_att, n_pf, wg, wu, wd, 1e-6, wo=wo)
+    assert_within_one_ulp(a_s, want_a, "8b layer a")
+    assert_within_one_ulp(nxt, want, "8b layer nxt")
+    lit, _ = oblk.swiglu_mlp(cur, got_att, n_pf, wg, wu, wd, 1e-6, wo=wo, dt=LITERAL)
+    assert not verify_buffer(nxt.cpu(), "nxt", lit, RTOL, ATOL)
 
 
 @pytest.mark.parametrize("H,KV,S,D,dist", [

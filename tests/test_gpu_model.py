@@ -120,8 +120,8 @@ def test_compare_mode_raises_on_wrong_reference(tiny, oracle_provider):
     fc()  # correct reference: passes
     assert not any(s["mismatch"] for s in fc.last_step_stats)
 
-    def wrong(op_, *inputs):
-        return oracle_provider(op_, *inputs) * 1.5
+    def wrong(op_, *inputs, **kw):
+        return oracle_provider(op_, *inputs, **kw) * 1.5
 
     register_reference_provider(wrong)
     try:
@@ -153,6 +153,77 @@ def test_reference_dispatch_matches_hip(tiny, oracle_provider):
         fc()
         ys.append(fc.get_buffer("y").torch_view()[:M].cpu())
     assert not verify_buffer(ys[0], "y", ys[1], rel_tol=1e-2, abs_tol=1e-2)
+
+
+@pytest.mark.parametrize("fuse_attention,kv_layout", [(True, "separate"), (False, "separate"),
+                                                       (True, "interleaved")])
+def test_compare_dispatch_runs_the_default_runlist(tiny, oracle_provider, fuse_attention,
+                                                   kv_layout):
+    """Qwen3NPU(dispatch=compare): every runlist entry of a decode step (QKV head + attention,
+    or the fused QKVHeadAttention; the MLP; the final norm; the LM head's argmax) is checked
+    against its CPU golden on the same inputs, with zero tolerance (exact arithmetic on both
+    sides), over several positions (sequence.py:1002-1085 in the reference)."""
+    from iron_amd.common.sequence import CompareDispatch
+
+    _say(f"compare dispatch, fuse_attention={fuse_attention} kv_layout={kv_layout}")
+    cfg, w = tiny
+    m = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, kv_layout=kv_layout,
+                 fuse_attention=fuse_attention, dispatch=CompareDispatch(0.0, 0.0))
+    assert not m.persistent
+    ref = Qwen3CpuChain(cfg, w, 64)
+    tok = 13
+    for pos in range(4):
+        got = m.step_token(tok, pos)
+        stats = m.fc.last_step_stats
+        assert len(stats) == len(m.seq.runlist)
+        assert not any(st["mismatch"] for st in stats), stats
+        want = Qwen3CpuChain.argmax(ref.step(tok, pos))
+        assert got == want
+        tok = got
+
+
+def test_compare_dispatch_catches_a_planted_attention_error(tiny, oracle_provider):
+    """A mistake planted in the oracle's fused QKV-head + attention golden (CPU side) must make
+    compare dispatch raise at that entry."""
+    from iron_amd.common.base import register_reference_provider
+    from iron_amd.common.sequence import CompareDispatch
+
+    _say("compare dispatch, planted attention error")
+    cfg, w = tiny
+    m = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, dispatch=CompareDispatch(1e-2, 1e-2))
+
+    def planted(op_, *inputs, **kw):
+        out = oracle_provider(op_, *inputs, **kw)
+        if type(op_).__name__ == "QKVHeadAttention":
+            out = out.clone()
+            out[5] = out[5].float() + 1.0          # one output element off by 1.0
+        return out
+
+    register_reference_provider(planted)
+    try:
+        with pytest.raises(RuntimeError, match="QKVHeadAttention"):
+            m.step_token(3, 0)
+    finally:
+        register_reference_provider(oracle_provider)
+
+
+def test_reference_dispatch_model_matches_hip(tiny, oracle_provider):
+    """Qwen3NPU(dispatch=reference) runs the whole runlist through the CPU goldens (KV appends
+    included, positions from the runtime parameters); its tokens and logits equal the HIP
+    path's bit for bit."""
+    _say("reference dispatch, whole model")
+    cfg, w = tiny
+    hip = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, persistent=False)
+    cpu = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, dispatch="reference")
+    assert not cpu.persistent
+    a = b = 21
+    for pos in range(5):
+        a = hip.step_token(a, pos)
+        b = cpu.step_token(b, pos)
+        assert a == b, f"tokens differ at {pos}"
+        assert torch.equal(hip.logits().view(torch.int16), cpu.logits().view(torch.int16))
+    with pytest.raises(ValueError):
+        Qwen3NPU(config=cfg, weights=w, max_seq_len=64, dispatch="reference", persistent=True)
 
 
 @pytest.mark.slow

@@ -195,6 +195,60 @@ def test_decode_attention_combined_layouts(interleaved, oracle_provider):
     assert_bit_exact(o, op.reference(q, kv), "attention combined")
 
 
+@pytest.mark.parametrize("H,KV,S,n,M,base,layout", [
+    (16, 8, 256, 16, 8, 192, "interleaved"),   # the reference's batch test (test_batch.py)
+    (32, 8, 512, 16, 8, 480, "interleaved"),   # its Qwen3-4B heads case (test_batch_4b.py)
+    (16, 8, 4096, 16, 8, 4000, "separate"),    # long cache: several splits, then the merge
+    (16, 8, 256, 1, 1, 100, "separate"),       # M = 1: a plain decode step
+    (16, 2, 1024, 5, 5, 1019, "blocked"),      # GQA 8, odd n, bounds clamped at S
+])
+@pytest.mark.parametrize("causal", [True, False])
+def test_decode_attention_verify(H, KV, S, n, M, base, layout, causal, oracle_provider):
+    """Batch / verify mode (decode_attn/op.py:40-48, design.py:243-276): every new token's
+    output against the exact oracle and the torch.softmax form at rel/abs 1e-2 (the reference's
+    own batch tests use cosine > 0.99); pad rows of a taller O stay untouched."""
+    _say(f"decode_attn verify H={H} KV={KV} S={S} n={n} M={M} base={base} {layout} "
+         f"causal={causal}")
+    D = 128
+    gen = torch.Generator().manual_seed(S + n + base)
+    q = (torch.randn(n, H, D, generator=gen) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(KV, S, D, generator=gen) * 0.3).to(torch.bfloat16)
+    v = (torch.randn(KV, S, D, generator=gen) * 0.3).to(torch.bfloat16)
+    pad = 3
+    op = DecodeAttention(num_heads=H, num_kv_heads=KV, head_dim=D, seq_len_kv=S,
+                         use_runtime_seq_len=True, batch_queries=M, num_new_tokens=n,
+                         causal=causal, out_buffer_tokens=n + pad,
+                         kv_layout="separate" if layout == "separate" else "combined",
+                         kv_token_interleaved=layout == "interleaved")
+    fn = op.get_callable()
+    fn.params.write("S_kv_base", base)
+    o = torch.full(((n + pad) * H, D), 7.0, dtype=torch.bfloat16, device=DEV)
+    if layout == "separate":
+        args = [k.reshape(KV, S * D).to(DEV), v.reshape(KV, S * D).to(DEV)]
+    elif layout == "interleaved":
+        args = [torch.stack([k, v], dim=2).reshape(KV, 2 * S * D).to(DEV)]
+    else:
+        args = [torch.cat([k.reshape(KV, S * D), v.reshape(KV, S * D)], dim=1).to(DEV)]
+    fn(q.reshape(n * H, D).to(DEV), *args, o)
+    torch.cuda.synchronize()
+    got = o.cpu()[: n * H].reshape(n, H, D)
+    assert torch.all(o.cpu()[n * H:].float() == 7.0), "rows past the new tokens were written"
+    want = oatt.decode_attention_verify(q, k, v, base, causal)
+    assert not verify_buffer(got, "verify o", want, RTOL, ATOL)
+    bounds = oatt.verify_bounds(n, base, S, causal)
+    sm = torch.zeros(n, H, D)
+    for t in range(n):
+        sm[t] = oatt.decode_attention_softmax(q[t:t + 1], k[None], v[None], bounds[t])[0].float()
+    assert not verify_buffer(got, "verify o (softmax form)", sm, RTOL, ATOL)
+    cos = torch.nn.functional.cosine_similarity(got.float().reshape(-1), want.float().reshape(-1),
+                                                dim=0)
+    assert cos > 0.999
+    # the golden through the operator's reference() on the same inputs (S_kv_base from params)
+    ref = op.reference(q.reshape(n * H, D), *[a.cpu() for a in args],
+                       params=fn.params.snapshot())
+    assert torch.equal(bf16_bits(ref.reshape(-1)), bf16_bits(want.reshape(-1)))
+
+
 def _qkv_case(D, Hq, Hkv, S, G, B, seed):
     HD = 128
     gen = torch.Generator().manual_seed(seed)
@@ -332,6 +386,8 @@ def test_qkv_attention_fused(D, Hq, Hkv, S, G, tm, layout, pos):
     (2048, 6144, 0, False, 32, 1),      # BASELINE config 2, B=1
     (2048, 6144, 0, False, 32, 2),
     (1024, 3072, 2048, True, 128, 2),   # reference group size
+    (2560, 9728, 4096, True, 32, 1),    # Qwen3-4B: FF % D != 0 (the chunked-down arm)
+    (2560, 9728, 4096, True, 128, 1),
 ])
 def test_swiglu_mlp(D, FF, QD, fuse_o, G, B):
     _say(f"swiglu D={D} FF={FF} QD={QD} fuse_o={fuse_o} G={G} B={B}")
@@ -403,8 +459,8 @@ def test_lm_head_argmax(kind, lib):
               1e-6, logits.data_ptr(), keys.data_ptr(), 1, V, D, G, tm, 0,
               torch.cuda.current_stream().cuda_stream)
     tokens = torch.zeros(1, dtype=torch.int32, device=DEV)
-    _lib.call("iron_next_token", keys.data_ptr(), tokens.data_ptr(), None, None, None, 0, None, 1,
-              D, V, torch.cuda.current_stream().cuda_stream)
+    _lib.call("iron_next_token", keys.data_ptr(), tokens.data_ptr(), None, None, None, 0, 0,
+              None, 1, D, V, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     got = logits.cpu()
     assert_bit_exact(got, want, "logits")

@@ -7,9 +7,11 @@ The kernel runs every layer of a token with the arithmetic of the per-operator e
   for the separate and the reference's interleaved KV layouts, bf16 and int8 LM heads;
 * the same model through the runlist (one HIP graph of per-operator kernels) and through the
   persistent kernel: identical logits, tokens and KV-cache rows;
-* Qwen3-0.6B architecture (BASELINE config 4 shape) with the KV cache prefilled past 2048
-  positions, so every split of the attention phase walks more than one tile: the device greedy
-  loop (graph-captured persistent launches) gives the same tokens and caches as the runlist path;
+* contexts past one attention tile per split (a split covers ceil(ctx / NS) positions and a tile
+  80, so one tile holds up to 80 * NS: 10240 for the tiny shape, NS = 128, and 2560 for Qwen3-0.6B,
+  NS = 32): the tiny model at context ~11000 against the exact CPU chain and the runlist, and the
+  Qwen3-0.6B architecture with the KV cache prefilled to 2700 positions, whose device greedy loop
+  (graph-captured persistent launches) gives the same tokens and caches as the runlist path;
 * the generation entry point (iron_decode_persistent_gen) keeps its token log within its length
   while the step counter, position and context length advance every token.
 """
@@ -111,6 +113,44 @@ def test_persistent_matches_runlist_tiny_prefilled():
         assert torch.equal(_bits(ca[i][1]), _bits(cb[i][1])), f"V cache of layer {i} differs"
 
 
+def test_persistent_multi_tile_context_tiny():
+    """Context 11000 > 80 * NS = 10240: every split walks two tiles (the in-loop K/V loads and
+    the rescale of the running maximum, sum and output); logits equal the exact CPU chain and
+    the runlist path, and the appended K/V rows equal the runlist's."""
+    cfg = Qwen3Config.tiny()
+    P0, n = 11000, 3
+    S = 11072
+    _say(f"persistent multi-tile: tiny, KV prefilled to {P0}, {n} steps")
+    w = random_qwen3_weights(cfg, seed=23)
+    k0, v0 = synthetic_kv(cfg, P0, seed=9)
+    chain = Qwen3CpuChain(cfg, w, S, kv_init=(k0, v0))
+    runs = []
+    for persistent in (True, False):
+        m = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, persistent=persistent)
+        assert m.persistent == persistent
+        m.load_kv(k0, v0)
+        toks, logits = [], []
+        tok = 77
+        for pos in range(P0, P0 + n):
+            tok = m.step_token(tok, pos)
+            toks.append(tok)
+            logits.append(m.logits())
+        caches = [tuple(c[:, P0:P0 + n].cpu() for c in m.kv_caches(i)) for i in range(cfg.n_layers)]
+        runs.append((toks, logits, caches))
+        if persistent:
+            assert m.persistent_errors() == 0
+    (ta, la, ca), (tb, lb, cb) = runs
+    tok = 77
+    for i, pos in enumerate(range(P0, P0 + n)):
+        lc = chain.step(tok, pos)
+        assert torch.equal(_bits(la[i]), _bits(lc)), f"persistent logits differ from the oracle @{pos}"
+        tok = ta[i]
+    assert ta == tb
+    for i in range(cfg.n_layers):
+        assert torch.equal(_bits(ca[i][0]), _bits(cb[i][0])) and torch.equal(_bits(ca[i][1]),
+                                                                             _bits(cb[i][1]))
+
+
 def test_persistent_epoch_advances_per_token():
     _say("persistent epoch / error words")
     cfg = Qwen3Config.tiny()
@@ -128,7 +168,7 @@ def test_persistent_epoch_advances_per_token():
 @pytest.mark.slow
 def test_persistent_qwen3_0_6b_matches_runlist():
     cfg = Qwen3Config.qwen3_0_6b()
-    P0, n_prompt, n_new = 2100, 8, 24
+    P0, n_prompt, n_new = 2700, 8, 24   # past 80 * 32 = 2560: every split walks two tiles
     S = (P0 + n_prompt + n_new + 63) // 64 * 64
     _say(f"qwen3-0.6b persistent vs runlist: KV {P0}, prompt {n_prompt}, {n_new} tokens")
     w = random_qwen3_weights(cfg, seed=2024, device="cuda")

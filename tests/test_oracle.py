@@ -290,6 +290,41 @@ def test_attention_invariants():
                                                                v3[b_:b_ + 1], n))
 
 
+def test_verify_attention_pins():
+    """Batch/verify decode attention (decode_attn/design.py:243-276): token t of a causal block
+    is a single-query decode at context base + t + 1, the non-causal block attends the whole
+    cache, n = 1 reduces to the decode step, bounds clamp at the cache length, and the
+    torch.softmax form of the reference's own batch test (test_batch.py:31-45) agrees."""
+    g = torch.Generator().manual_seed(11)
+    H, KV, D, S, n, base = 4, 2, 128, 96, 6, 40
+    q = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+    k = (torch.randn(KV, S, D, generator=g) * 0.5).to(torch.bfloat16)
+    v = torch.randn(KV, S, D, generator=g).to(torch.bfloat16)
+    got = oatt.decode_attention_verify(q, k, v, base, causal=True)
+    for t in range(n):
+        one = oatt.decode_attention(q[t:t + 1], k[None], v[None], base + t + 1)
+        assert torch.equal(bf16_bits(got[t]), bf16_bits(one[0]))
+    full = oatt.decode_attention_verify(q, k, v, base, causal=False)
+    for t in range(n):
+        one = oatt.decode_attention(q[t:t + 1], k[None], v[None], S)
+        assert torch.equal(bf16_bits(full[t]), bf16_bits(one[0]))
+    assert not torch.equal(bf16_bits(got), bf16_bits(full))       # the mask matters
+    assert oatt.verify_bounds(4, 94, S, True) == [95, 96, 96, 96]   # clamped at S
+    assert oatt.verify_bounds(3, 5, S, False) == [S, S, S]
+    # the reference test's closed form, restated with torch.softmax in fp32
+    sm = torch.zeros(n, H, D)
+    for t in range(n):
+        nk = base + t + 1
+        for h in range(H):
+            kv = h // (H // KV)
+            sc = q[t, h].float() @ k[kv, :nk].float().t() / math.sqrt(D)
+            sm[t, h] = torch.softmax(sc, 0) @ v[kv, :nk].float()
+    assert torch.allclose(got.float(), sm, rtol=1e-2, atol=1e-2)
+    # a wrong GQA map (h // 2 -> h % 2) changes the result
+    bad = oatt.decode_attention(q[:1, [0, 2, 1, 3]], k[None], v[None], base + 1)
+    assert not torch.equal(bf16_bits(bad[0][[0, 2, 1, 3]]), bf16_bits(got[0]))
+
+
 def test_causal_prefill_first_row_and_bruteforce():
     g = torch.Generator().manual_seed(15)
     q = torch.randn(4, 9, 128, generator=g)
