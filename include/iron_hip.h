@@ -170,6 +170,22 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
                      float scale, int acc, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* Bytes of the library-owned scratch array that iron_decode_attn_noalloc uses on each GPU. */
+#define IRON_ATTN_NOALLOC_SCRATCH_BYTES (4u << 20)
+
+/* iron_decode_attn without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, allocator-free serving loops, harnesses that forbid hipMalloc).
+ * No reference counterpart. The split-K partials go to a file-scope device array of
+ * IRON_ATTN_NOALLOC_SCRATCH_BYTES held by each GPU until the process ends; the entry point calls
+ * no allocating routine, and returns IRON_ERR_WORKSPACE when the partials of (B, H, max_ctx) would
+ * not fit (iron_decode_attn_workspace() > the scratch). Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (different streams, or threads without ordering) race and
+ * must be serialised by the caller. Results equal iron_decode_attn's bit for bit. */
+int iron_decode_attn_noalloc(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                             long long kv_sb, long long kv_sh, long long kv_st,
+                             const int32_t* ctx_len, int ctx_const, uint16_t* out, int B, int H,
+                             int KV, int D, int max_ctx, float scale, int acc, void* stream);
+
 /* Workspace bytes for iron_decode_attn_verify (split-K partials, fp32; 256 when none are needed;
  * 0 for an invalid shape). */
 size_t iron_decode_attn_verify_workspace(int n_new, int H, int KV, int D, int max_ctx);

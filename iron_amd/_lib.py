@@ -90,6 +90,9 @@ SIGNATURES = {
     "iron_decode_attn": (_c_int, [_c_vp, _c_vp, _c_vp, _c_ll, _c_ll, _c_ll, _c_vp, _c_int,
                                   _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _c_int,
                                   _c_vp, _c_sz, _c_vp]),
+    "iron_decode_attn_noalloc": (_c_int, [_c_vp, _c_vp, _c_vp, _c_ll, _c_ll, _c_ll, _c_vp,
+                                          _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                          _c_f, _c_int, _c_vp]),
     "iron_decode_attn_verify_workspace": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "iron_decode_attn_verify": (_c_int, [_c_vp, _c_vp, _c_vp, _c_ll, _c_ll, _c_vp, _c_int,
                                          _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,

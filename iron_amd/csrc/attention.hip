@@ -26,6 +26,7 @@
 // known (bounded by max_ctx, masked afterwards), which takes the length's load off the critical
 // path; with several sequences the length is read first so that short sequences read nothing
 // beyond their context.
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -850,23 +851,52 @@ size_t verify_ws_bytes(int n, int H, int KV, int max_ctx) {
 
 constexpr int kVerifyMaxTokens = 4096;
 
+// ---------------------------------------------------------------------------------------------
+// Library-owned scratch for iron_decode_attn_noalloc: the split-K partials of callers that cannot
+// allocate. Each GPU the library runs on holds its own copy of this array (at its own address)
+// until the process ends. Host code never passes the array's name to a kernel: in host code it is
+// a stand-in, not a device address. The device address comes from hipGetSymbolAddress, looked up
+// once per device with that device current, and is the only handle used afterwards.
+// ---------------------------------------------------------------------------------------------
+constexpr size_t kNoallocScratchBytes = IRON_ATTN_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+int scratch_of_current_device(void** out, const char* fn);
+
 }  // namespace
 
-extern "C" {
+static __device__ __align__(256) unsigned char scratch[IRON_ATTN_NOALLOC_SCRATCH_BYTES];
 
-size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx) {
-  if (B <= 0 || H <= 0 || KV <= 0 || D != kD || H % KV || max_ctx <= 0) return 0;
-  const size_t n = attn_ws_bytes(B, H, KV, max_ctx);
-  return n ? n : 256;
+namespace {
+
+int scratch_of_current_device(void** out, const char* fn) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return iron::fail(IRON_ERR_HIP, "%s: no current HIP device", fn);
+  if (dev < 0 || dev >= kMaxDevices)
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: device %d (at most %d devices)", fn, dev,
+                      kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return iron::fail(IRON_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn,
+                        dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return IRON_OK;
 }
 
-int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                     long long kv_sb, long long kv_sh, long long kv_st, const int32_t* ctx_len,
-                     int ctx_const, uint16_t* out, int B, int H, int KV, int D, int max_ctx,
-                     float scale, int acc, void* workspace, size_t workspace_bytes,
-                     void* stream) {
-  iron::clear_error();
-  const char* fn = "iron_decode_attn";
+// Validation and launch shared by iron_decode_attn and iron_decode_attn_noalloc.
+int decode_attn_entry(const char* fn, const uint16_t* q, const uint16_t* k_cache,
+                      const uint16_t* v_cache, long long kv_sb, long long kv_sh, long long kv_st,
+                      const int32_t* ctx_len, int ctx_const, uint16_t* out, int B, int H, int KV,
+                      int D, int max_ctx, float scale, int acc, void* workspace,
+                      size_t workspace_bytes, bool noalloc, void* stream) {
   if (!q || !k_cache || !v_cache || !out) return iron::fail(IRON_ERR_NULL, "%s: null tensor", fn);
   int st = check_attn_shape(fn, B, H, KV, D, max_ctx);
   if (st) return st;
@@ -875,6 +905,17 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
     return iron::fail(IRON_ERR_ALIGN, "%s: K/V/Q rows must be 16-byte aligned", fn);
   if (!ctx_len && (ctx_const < 0 || ctx_const > max_ctx))
     return iron::fail(IRON_ERR_SHAPE, "%s: ctx_const=%d outside [0, %d]", fn, ctx_const, max_ctx);
+  if (acc != IRON_ACCUM_F64 && acc != IRON_ACCUM_F32)
+    return iron::fail(IRON_ERR_SHAPE, "%s: unknown accumulation mode %d", fn, acc);
+  if (noalloc) {
+    const size_t need = attn_ws_bytes(B, H, KV, max_ctx);
+    if (need > kNoallocScratchBytes)
+      return iron::fail(IRON_ERR_WORKSPACE, "%s: the split partials of B=%d H=%d max_ctx=%d need "
+                        "%zu bytes, more than the %zu-byte scratch (use iron_decode_attn with a "
+                        "workspace)", fn, B, H, max_ctx, need, kNoallocScratchBytes);
+    workspace_bytes = kNoallocScratchBytes;
+    if ((st = scratch_of_current_device(&workspace, fn))) return st;
+  }
   AttnParams p = {};
   p.q = q;
   p.k = const_cast<uint16_t*>(k_cache);
@@ -891,6 +932,37 @@ int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
   p.scale = (double)scale;
   return launch_attention(p, false, acc, B, workspace, workspace_bytes, (hipStream_t)stream,
                           fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx) {
+  if (B <= 0 || H <= 0 || KV <= 0 || D != kD || H % KV || max_ctx <= 0) return 0;
+  const size_t n = attn_ws_bytes(B, H, KV, max_ctx);
+  return n ? n : 256;
+}
+
+int iron_decode_attn(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                     long long kv_sb, long long kv_sh, long long kv_st, const int32_t* ctx_len,
+                     int ctx_const, uint16_t* out, int B, int H, int KV, int D, int max_ctx,
+                     float scale, int acc, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  iron::clear_error();
+  return decode_attn_entry("iron_decode_attn", q, k_cache, v_cache, kv_sb, kv_sh, kv_st, ctx_len,
+                           ctx_const, out, B, H, KV, D, max_ctx, scale, acc, workspace,
+                           workspace_bytes, false, stream);
+}
+
+int iron_decode_attn_noalloc(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                             long long kv_sb, long long kv_sh, long long kv_st,
+                             const int32_t* ctx_len, int ctx_const, uint16_t* out, int B, int H,
+                             int KV, int D, int max_ctx, float scale, int acc, void* stream) {
+  iron::clear_error();
+  return decode_attn_entry("iron_decode_attn_noalloc", q, k_cache, v_cache, kv_sb, kv_sh, kv_st,
+                           ctx_len, ctx_const, out, B, H, KV, D, max_ctx, scale, acc, nullptr, 0,
+                           true, stream);
 }
 
 size_t iron_qkv_attn_workspace(int B, int D, int Hq, int Hkv, int HD, int max_seq) {
