@@ -42,6 +42,9 @@ LM_HEAD_BF16_TRAFFIC = 311_802_528
 # HBM bytes per launch of the persistent layers kernel (all 28 layers), same method:
 # FETCH_SIZE 382599.72 KiB x 2.0 + WRITE_SIZE 73624.03 KiB x 1.0 at context 2048..2057.
 PERSISTENT_TRAFFIC = 858_955_232
+# HBM bytes per launch of the one-launch token (layers + folded LM head), same method; None until
+# measured for the current kernel.
+PERSISTENT_TOKEN_TRAFFIC = None
 
 
 def parse():
@@ -125,20 +128,43 @@ def main():
         kv_per_pos + cfg.vocab_size * 2
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    if model.persistent:
-        layers_us, lm_us = time_persistent(model)
-    else:
-        layers_us, lm_us = None, time_runlist_lm_head(model)
     lm_bytes = wb["lm_head"] + cfg.emb_dim * 2 + cfg.vocab_size * 2
-    lm_gbs = lm_bytes / (lm_us * 1e-6) / 1e9
-    lm_roofline = {"bound": "hbm", "kernel": "lm_head GEMV (bf16 [151936x1024], RMSNorm prologue, "
-                                             "argmax epilogue)" if args.lm_head == "bf16" else
-                   "lm_head GEMV (int8 G=32, argmax epilogue)",
-                   "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                   "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
-                   "traffic": LM_HEAD_BF16_TRAFFIC if args.lm_head == "bf16" else None,
-                   "bytes_per_launch": lm_bytes, "avg_launch_us": round(lm_us, 2)}
-    if model.persistent:
+    lm_roofline = None
+    if model.persistent and model.fold_lm_head:
+        token_us = time_folded_token(model)
+        layers_us = lm_us = None
+    else:
+        token_us = None
+        if model.persistent:
+            layers_us, lm_us = time_persistent(model)
+        else:
+            layers_us, lm_us = None, time_runlist_lm_head(model)
+        lm_gbs = lm_bytes / (lm_us * 1e-6) / 1e9
+        lm_roofline = {
+            "bound": "hbm",
+            "kernel": "lm_head GEMV (bf16 [151936x1024], RMSNorm prologue, argmax epilogue)"
+            if args.lm_head == "bf16" else "lm_head GEMV (int8 G=32, argmax epilogue)",
+            "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
+            "traffic": LM_HEAD_BF16_TRAFFIC if args.lm_head == "bf16" else None,
+            "bytes_per_launch": lm_bytes, "avg_launch_us": round(lm_us, 2)}
+    if token_us is not None:
+        # one launch per token: the 28 layers, the final norm, the bf16 LM head and its argmax;
+        # algorithmic bytes: every layer's weights once, the KV read at the timed context and the
+        # rows appended, the embedding row in, the LM head and final norm, the logits out
+        ctx = start + args.steps + 1
+        tok_bytes = (wb["layers"] + kv_per_pos * ctx + kv_per_pos + cfg.emb_dim * 2 +
+                     lm_bytes + wb["final_norm"])
+        tok_gbs = tok_bytes / (token_us * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "kernel": "decode_persistent_kernel (28 layers: QKV, "
+                                              "attention, merge, Wo, gate/up, down; final "
+                                              "RMSNorm, bf16 LM head, argmax)",
+                    "achieved": round(tok_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(tok_gbs / HBM_PEAK_GBS, 4),
+                    "traffic": PERSISTENT_TOKEN_TRAFFIC,
+                    "bytes_per_launch": int(tok_bytes), "avg_launch_us": round(token_us, 2),
+                    "context": ctx}
+    elif model.persistent:
         # the persistent kernel is the step's dominant launch (all 28 layers); its algorithmic
         # bytes: every layer's weights once, the KV cache read at the timed context, the K/V
         # rows appended, the embedding row in and the hidden state out
@@ -175,7 +201,7 @@ def main():
                    "layers": cfg.n_layers, "group_size": cfg.group_size},
         "decode_path": "persistent" if model.persistent else "runlist",
         "roofline": roofline,
-        "lm_head": lm_roofline,
+        "lm_head": lm_roofline if lm_roofline is not None else "folded into the token launch",
         "step_roofline": {"bytes_per_step": int(step_bytes), "achieved": round(step_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
@@ -187,8 +213,9 @@ def main():
         from iron_amd import benchmarks
         rc = benchmarks.read_probe()
         for r in (result["roofline"], result["lm_head"]):
-            r["achievable_read_GB_s"] = rc["GB_s"]
-            r["frac_of_achievable"] = round(r["achieved"] / rc["GB_s"], 4)
+            if isinstance(r, dict):
+                r["achievable_read_GB_s"] = rc["GB_s"]
+                r["frac_of_achievable"] = round(r["achieved"] / rc["GB_s"], 4)
         # the other BASELINE configurations, each timed standalone over >= 512 MiB of rotating
         # operands (iron_amd/benchmarks.py); config 5 includes the 36-layer Qwen3-8B B=16 stack
         del model, w
@@ -225,6 +252,26 @@ def time_persistent(model, n_rep: int = 24):
     layers_us = sum(e0.elapsed_time(e1) for e0, e1, _ in ev) * 1e3 / n_rep
     lm_us = sum(e1.elapsed_time(e2) for _, e1, e2 in ev) * 1e3 / n_rep
     return layers_us, lm_us
+
+
+def time_folded_token(model, n_rep: int = 24):
+    """Average duration of the one-launch greedy step (layers + final norm + LM head + argmax),
+    from HIP events on the stream it runs on; each launch decodes the next position."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    gs = model._gen_state()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n_rep)]
+    model.persistent_gen_launch(model._p_keys, gs)
+    for e0, e1 in ev:
+        e0.record(stream)
+        model.persistent_gen_launch(model._p_keys, gs)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    if model.persistent_errors():
+        raise RuntimeError("persistent kernel reported a hand-off timeout while timing")
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) * 1e3 / n_rep
 
 
 def time_runlist_lm_head(model, n_rep: int = 32):

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 6
+#define IRON_ABI_VERSION 7
 
 enum iron_status {
   IRON_OK = 0,
@@ -318,7 +318,8 @@ int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, i
 
 /* Device state of a greedy decode loop run by iron_decode_persistent_gen. */
 typedef struct iron_decode_gen {
-  unsigned long long* keys;   /* [1] the previous iron_lm_head's argmax key; reset to 0 */
+  unsigned long long* keys;   /* argmax keys: [1] the previous iron_lm_head's, reset to 0; or,
+                                 with lm_head, [2] slots the launches alternate between */
   const uint16_t* emb;        /* bf16 [vocab][D] embedding table (16-byte aligned) */
   int32_t* tokens;            /* [1] receives the decoded token */
   int32_t* token_log;         /* [log_len] token by step, or NULL */
@@ -326,6 +327,10 @@ typedef struct iron_decode_gen {
   int32_t* ctx;               /* [1] receives the new position + 1, or NULL */
   const uint16_t* rope_table; /* bf16 [max_seq][HD] RoPE rows, or NULL */
   int vocab, log_len;
+  const uint16_t* lm_head;    /* bf16 [vocab][D]: fold the final RMSNorm, LM head and argmax into
+                                 the launch (NULL: the layers only) */
+  const uint16_t* lm_norm;    /* bf16 [D] final RMSNorm weight (with lm_head) */
+  uint16_t* logits;           /* bf16 [vocab] logits out (with lm_head), or NULL */
 } iron_decode_gen;
 
 /* iron_decode_persistent with the greedy loop's per-token work folded in:
@@ -335,7 +340,12 @@ typedef struct iron_decode_gen {
  *   ang = rope_table[*pos] (when *pos < max_seq).
  * The results equal iron_next_token (emb, log) + iron_decode_persistent + iron_advance_positions
  * (delta 1), the per-token loop of the reference decode (qwen3_npu_int8.py:594-621) in one
- * launch. */
+ * launch. With gen->lm_head the launch also runs the final RMSNorm (lm_norm), the bf16 LM head
+ * (logits) and its argmax, i.e. iron_lm_head as well: a whole greedy step in ONE launch, the
+ * reference's single dispatch per token with its host argmax (qwen3_npu_int8.py:249-281,
+ * 612-621). The keys then alternate by epoch e (workspace control word 0 at launch): the launch
+ * reads the previous token from keys[e & 1], clears keys[(e + 1) & 1] and leaves its argmax there
+ * (so after a launch the latest key is keys[epoch & 1] with the advanced epoch). */
 int iron_decode_persistent_gen(const iron_layer_desc* layers, int n_layers, int D, int FF,
                                int Hq, int Hkv, int HD, int max_seq, long long kv_sh,
                                long long kv_st, int G, int tile_qkv, int tile_o, int tile_gu,

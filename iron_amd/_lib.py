@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
-ABI_VERSION = 6          # IRON_ABI_VERSION of include/iron_hip.h
+ABI_VERSION = 7          # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2
@@ -58,7 +58,8 @@ class DecodeGen(ctypes.Structure):
 
     _fields_ = [(name, _c_vp) for name in ("keys", "emb", "tokens", "token_log", "step", "ctx",
                                            "rope_table")] + [("vocab", _c_int),
-                                                             ("log_len", _c_int)]
+                                                             ("log_len", _c_int)] + \
+        [(name, _c_vp) for name in ("lm_head", "lm_norm", "logits")]
 
 
 # name -> (restype, argtypes). Kept in the order of include/iron_hip.h.

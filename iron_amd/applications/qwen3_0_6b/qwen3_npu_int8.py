@@ -76,7 +76,7 @@ class Qwen3NPU:
                  kv_layout: str = "separate", lm_head: str | None = None,
                  dispatch: str = "auto", context: AIEContext | None = None,
                  fuse_attention: bool = True, attn_accumulate: str = "f64",
-                 persistent: bool | None = None):
+                 persistent: bool | None = None, fold_lm_head: bool = True):
         self.cfg = cfg = config or Qwen3Config.qwen3_0_6b()
         self.max_seq_len = max_seq_len
         self.kv_layout = kv_layout
@@ -103,6 +103,9 @@ class Qwen3NPU:
                                  f"{self._dispatch_name(dispatch)!r})")
             persistent = False
         self.persistent = self._setup_persistent(persistent)
+        # the device greedy loop folds the final norm, bf16 LM head and argmax into the
+        # persistent launch (one launch per token); an int8 head keeps its own launch
+        self.fold_lm_head = bool(fold_lm_head and self.persistent and self.lm_head_kind == "bf16")
 
     @staticmethod
     def _dispatch_name(dispatch) -> str:
@@ -263,6 +266,8 @@ class Qwen3NPU:
                                                       cfg.n_kv_heads, cfg.head_dim)
         self._p_ws = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         self._p_xout = torch.zeros(cfg.emb_dim, dtype=torch.bfloat16, device=self.device)
+        # the folded head's two argmax slots (launches alternate between them by epoch)
+        self._p_keys = torch.zeros(2, dtype=torch.int64, device=self.device)
         torch.cuda.synchronize(self.device)
         return True
 
@@ -289,7 +294,8 @@ class Qwen3NPU:
 
     def persistent_gen_launch(self, keys, gs):
         """Launch iron_decode_persistent_gen: one greedy step's layers plus its token decode,
-        embedding gather, token log and position advance."""
+        embedding gather, token log and position advance; with ``keys`` the model's two folded
+        argmax slots (``self._p_keys``), also the final norm, the LM head and its argmax."""
         cfg, lib, mlp = self.cfg, _lib.load(), self.mlp_xdna
         stream = torch.cuda.current_stream(self.device).cuda_stream
         view = lambda name, dt: self.fc.get_buffer(name).torch_view(dt)  # noqa: E731
@@ -300,6 +306,10 @@ class Qwen3NPU:
                              ctx=self.fc.params.tensor("S_kv_eff").data_ptr(),
                              rope_table=self.rope_table.data_ptr(), vocab=cfg.vocab_size,
                              log_len=gs["log"].numel())
+        if self.fold_lm_head and keys is self._p_keys:
+            gen.lm_head = view("W_out_head", torch.uint8).data_ptr()
+            gen.lm_norm = view("W_final_norm", torch.bfloat16).data_ptr()
+            gen.logits = view("logits", torch.bfloat16).data_ptr()
         _lib.check(lib.iron_decode_persistent_gen(
             self._p_layers.data_ptr(), cfg.n_layers, cfg.emb_dim, cfg.hidden_dim, cfg.n_heads,
             cfg.n_kv_heads, cfg.head_dim, self.max_seq_len, sh, st, cfg.group_size, QKV_TSI,
@@ -413,7 +423,11 @@ class Qwen3NPU:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         keys = self.fc.get_buffer("argmax_key").torch_view(torch.int64)
         if self.persistent:
-            # token decode, embedding, log and position advance inside the layers' kernel
+            # token decode, embedding, log and position advance inside the layers' kernel, and
+            # with the folded head the LM head as well: one launch per token
+            if self.fold_lm_head:
+                self.persistent_gen_launch(self._p_keys, gs)
+                return
             self.persistent_gen_launch(keys, gs)
             self.lm_head_launch()
             return
@@ -451,9 +465,19 @@ class Qwen3NPU:
         gs["step"].zero_()
         self._gen_pos = start_pos
         self._set_position(start_pos)
-        self.fc.get_buffer("argmax_key").torch_view(torch.int64)[:1].fill_(
-            _encode_token(first_token))
+        if self.fold_lm_head:
+            # the next launch (epoch e) reads keys[e & 1] and clears keys[(e + 1) & 1]
+            e = self._epoch()
+            self._p_keys[e & 1].fill_(_encode_token(first_token))
+            self._p_keys[(e + 1) & 1].zero_()
+        else:
+            self.fc.get_buffer("argmax_key").torch_view(torch.int64)[:1].fill_(
+                _encode_token(first_token))
         torch.cuda.synchronize(self.device)
+
+    def _epoch(self) -> int:
+        """The persistent workspace's epoch (control word 0): the next launch's."""
+        return int(self._p_ws[:4].view(torch.int32).item()) & 0xFFFFFFFF
 
     def decode_steps(self, n: int):
         """Replay the per-token graph n times (no host synchronisation).
@@ -474,6 +498,9 @@ class Qwen3NPU:
         cfg, gs = self.cfg, self._gen_state()
         stream = torch.cuda.current_stream(self.device).cuda_stream
         keys = self.fc.get_buffer("argmax_key").torch_view(torch.int64)
+        if self.fold_lm_head:
+            torch.cuda.synchronize(self.device)
+            keys = self._p_keys[self._epoch() & 1:]   # the last launch's argmax slot
         _lib.call("iron_next_token", keys.data_ptr(), gs["tokens"].data_ptr(), None, None,
                   gs["log"].data_ptr(), 0, gs["log"].numel(), gs["step"].data_ptr(), 1,
                   cfg.emb_dim, cfg.vocab_size, stream)

@@ -37,6 +37,8 @@
 // workgroup that reads the buffer also produces in a phase that the producers wait on. For the
 // Qwen3-0.6B shape every workgroup produces in every phase; in smaller shapes workgroups that own
 // no rows of the Wo, gate/up or down phase read nothing in that phase (skip_gather).
+#include <type_traits>
+
 #include "attn_core.h"
 #include "common.h"
 #include "gemv_core.h"
@@ -155,6 +157,13 @@ struct PParams {
   int32_t *token, *token_log, *step, *pos_next, *ctx;
   const uint16_t* rope_table;  // bf16 [max_seq][HD] RoPE rows
   uint16_t* ang_next;          // the buffer `ang` points to, given the next position's row
+  // the final RMSNorm + bf16 LM head + argmax folded into the launch (lm_w null: not folded).
+  // The argmax keys then alternate between two slots by epoch: launch e reads the previous
+  // token from key[e & 1] and accumulates its own argmax into key[(e + 1) & 1], which workgroup 0
+  // clears at the start of the launch.
+  const uint16_t* lm_w;        // bf16 [vocab][D]
+  const uint16_t* lm_norm;     // bf16 [D]
+  uint16_t* logits;            // bf16 [vocab], or null
 };
 
 IRON_DEV GemvParams gemv_of(const WireGeom& g, const void* w, int M, int K) {
@@ -1164,6 +1173,168 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   return true;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Phase H (folded LM head): logits = bf16(W_head . bf16(RMSNorm(x) * n_final)), argmax key.
+// Workgroup wg owns a contiguous range of 16-row blocks; in each block wavefront w takes rows
+// 4w..4w+3 (lane l: elements c*512 + 8l .. +8 of each 512-wide chunk, one 16-byte load per row
+// and chunk). Blocks stream through a ring of kLmStages register stages, so kLmStages - 1 blocks
+// of loads are in flight while one is multiplied; the first two stages are issued as soon as the
+// last layer's output has arrived, so they stream while the final RMSNorm is computed.
+// Arithmetic of iron_lm_head's bf16 path: exact bf16 products summed in fp64, one bf16 rounding.
+// ---------------------------------------------------------------------------------------------
+constexpr int kLmRows = 4;     // rows per wavefront per block
+constexpr int kLmStages = 3;   // register stages of the block ring (3 or 4; 3 measured faster)
+
+template <class S>
+struct LmRing {
+  static constexpr int NC = cdiv(S::D, 512);  // 512-wide chunks of a row
+  uint4 w[kLmStages][kLmRows][NC];
+};
+
+template <class S>
+IRON_DEV int lm_blocks(int vocab) { return (vocab + 4 * kLmRows - 1) / (4 * kLmRows); }
+
+template <class S>
+IRON_DEV void lm_range(int vocab, int wg, int& b0, int& b1) {
+  const int nb = lm_blocks<S>(vocab);
+  b0 = (int)(((long long)nb * wg) / kNT);
+  b1 = (int)(((long long)nb * (wg + 1)) / kNT);
+}
+
+// Loads block b (rows 16b + 4 wave + r; rows past the head clamp to row 0 and are never stored)
+// into ring stage st.
+template <class S>
+IRON_DEV void lm_fetch(const PParams& p, int b, int st, LmRing<S>& ring) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < kLmRows; ++r) {
+    const int row = b * 4 * kLmRows + wave * kLmRows + r;
+    const size_t at = (size_t)(row < p.vocab ? row : 0) * S::D;
+#pragma unroll
+    for (int c = 0; c < LmRing<S>::NC; ++c) {
+      const int e = c * 512 + lane * 8;  // elements past D: a clamped load, multiplied by x = 0
+      ring.w[st][r][c] = ld_global((const uint4*)(p.lm_w + at + (e < S::D ? e : 0)));
+    }
+  }
+}
+
+// The first two blocks of this workgroup's range (issued during the last layer).
+template <class S>
+IRON_DEV void lm_prefetch(const PParams& p, int wg, LmRing<S>& ring) {
+  int b0, b1;
+  lm_range<S>(p.vocab, wg, b0, b1);
+#pragma unroll
+  for (int st = 0; st < kLmStages - 1; ++st)
+    if (b0 + st < b1) lm_fetch<S>(p, b0 + st, st, ring);
+}
+
+template <class S>
+IRON_DEV bool phase_lm_head(const PParams& p, int wg, uint32_t ep, uint32_t* s_in,
+                            unsigned long long* key_out, LmRing<S>& ring) {
+  constexpr int NC = LmRing<S>::NC;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  {
+    const uint32_t tx = x_tag(ep, p.n_layers, p.n_layers);
+    unsigned long long* const xs = copy_for(p.X, kCopyWords, wg);
+    auto src = [&](int j, uint32_t& t) { t = tx; return xs + spread_word(j); };
+    if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src,
+                                           [&]() { lm_prefetch<S>(p, wg, ring); }, s_in,
+                                           p.ctrl + 1))
+      return false;
+  }
+  // xn = bf16(RMSNorm(x) * n_final) for this lane's elements c*512 + 8 lane .. +8
+  GemvParams g = {};
+  g.pro = PRO_RMS_BF16;
+  g.K = S::D;
+  g.eps = p.eps;
+  uint4 xl[NC][2], x2l[NC][1] = {}, nwl[NC][1];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int e = c * 512 + lane * 8;
+    const bool in = e < S::D;  // elements past D are zero (they add nothing to the statistic)
+    xl[c][0] = in ? ((const uint4*)s_in)[e / 8] : make_uint4(0u, 0u, 0u, 0u);
+    xl[c][1] = make_uint4(0u, 0u, 0u, 0u);
+    nwl[c][0] = ld_global((const uint4*)(p.lm_norm + (in ? e : 0)));
+  }
+  float xf[NC][8];
+  prologue_lane<NC, 8>(g, lane, xl, x2l, nwl, xf);
+  double xv[NC][8];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[c][j] = xf[c][j];
+
+  __shared__ double s_lrows[4][kLmRows][64];
+  __shared__ unsigned long long s_kbest[4];
+  int b0, b1;
+  lm_range<S>(p.vocab, wg, b0, b1);
+  unsigned long long best = 0ull;
+  // block b's products from ring stage ST (a compile-time index, so the ring stays in registers
+  // and the compiler waits only for that stage's loads, not for the younger ones in flight)
+  auto block = [&](auto st_c, int b) {
+    constexpr int ST = decltype(st_c)::value;
+    double v[kLmRows];
+#pragma unroll
+    for (int r = 0; r < kLmRows; ++r) {
+      double pa = 0.0, pb = 0.0;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 w4 = ring.w[ST][r][c];
+        const uint32_t dd[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          pa = fma((double)bf16lo_to_f32(dd[j]), xv[c][2 * j], pa);
+          pb = fma((double)bf16hi_to_f32(dd[j]), xv[c][2 * j + 1], pb);
+        }
+      }
+      v[r] = pa + pb;
+    }
+    const double tot = rows_sum_d<kLmRows>(v, s_lrows[wave]);  // row lane/8 in lanes 8r..8r+7
+    const int r = lane >> 3, row = b * 4 * kLmRows + wave * kLmRows + r;
+    if ((lane & 7) == 0 && r < kLmRows && row < p.vocab) {
+      const uint16_t h = f64_to_bf16(tot);
+      if (p.logits) p.logits[row] = h;
+      const unsigned long long key = ((unsigned long long)bf16_order_key(h) << 32) |
+                                     (unsigned long long)(~(uint32_t)row);
+      best = key > best ? key : best;
+    }
+  };
+  // stages 0 .. kLmStages - 2 hold blocks b0 .. (lm_prefetch); block b0 + k sits in stage
+  // k % kLmStages: before block b + k is multiplied, block b + k + kLmStages - 1 is issued into the
+  // stage that block b + k - 1 has just left
+  auto step = [&](auto k_c, int b) {
+    constexpr int K = decltype(k_c)::value;
+    if (b + K + kLmStages - 1 < b1)
+      lm_fetch<S>(p, b + K + kLmStages - 1, (K + kLmStages - 1) % kLmStages, ring);
+    block(std::integral_constant<int, K>(), b + K);
+  };
+  for (int b = b0; b < b1; b += kLmStages) {
+    step(std::integral_constant<int, 0>(), b);
+    if (b + 1 >= b1) break;
+    step(std::integral_constant<int, 1>(), b);
+    if (b + 2 >= b1) break;
+    step(std::integral_constant<int, 2>(), b);
+    if constexpr (kLmStages == 4) {
+      if (b + 3 >= b1) break;
+      step(std::integral_constant<int, 3>(), b);
+    }
+  }
+  // the workgroup's best key, then one atomic
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) {
+    const unsigned long long o = __shfl_xor(best, k);
+    best = o > best ? o : best;
+  }
+  if (lane == 0) s_kbest[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = s_kbest[0];
+    for (int i = 1; i < 4; ++i) k = s_kbest[i] > k ? s_kbest[i] : k;
+    if (k) atomicMax(key_out, k);
+  }
+  return true;
+}
+
 // Each phase's weights are issued from an earlier phase's wait (gather_words' `issue` hook):
 //   A waits -> B's first K/V tile;  B waits -> D's Wo;  C waits -> E's Wg/Wu;
 //   D waits -> F's Wd;  E waits -> the next layer's Wqkv.
@@ -1184,12 +1355,27 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
   W8<S::RA, S::CA> wqkv;
   uint4 n_in[S::CA][2];
   prefetch_qkv<S>(p, p.layers[0], wg, wqkv, n_in);
+  // the previous token's argmax key, and (folded head) the slot this launch's argmax goes to
+  unsigned long long* const key_in = p.lm_w ? p.key + (ep & 1u) : p.key;
+  unsigned long long* const key_out = p.lm_w ? p.key + ((ep + 1u) & 1u) : nullptr;
+  if (p.lm_w && wg == 0) {
+    // Clear this launch's argmax slot before workgroup 0 publishes anything: every workgroup's
+    // atomicMax into it follows (through the hand-offs) this workgroup's later stores, and the
+    // returned value makes the exchange complete before them. The slot was last read at the start
+    // of the previous launch.
+    __shared__ uint32_t s_cleared;
+    if (threadIdx.x == 0)
+      s_cleared = (uint32_t)__hip_atomic_exchange(key_out, 0ull, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    (void)s_cleared;
+  }
   // the greedy loop's input: the embedding row of the token the previous LM head chose (key =
   // (order(max) << 32) | ~index; a zero key is token 0)
   const uint16_t* x_in = p.x_in;
   int32_t tok = 0;
   if (p.key) {
-    const unsigned long long k = *p.key;
+    const unsigned long long k = *key_in;
     tok = k ? (int32_t)(~(uint32_t)(k & 0xffffffffull)) : 0;
     tok = tok < 0 ? 0 : (tok >= p.vocab ? p.vocab - 1 : tok);
     x_in = p.emb + (size_t)tok * S::D;
@@ -1203,6 +1389,8 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
     const int word = wg * S::XW + threadIdx.x;
     s_own[S::XW + threadIdx.x] = word < S::D / 2 ? ((const uint32_t*)x_in)[word] : 0u;
   }
+  LmRing<S> lm;
+  bool ok = true;
   for (int l = 0; l < p.n_layers; ++l) {
     const iron_layer_desc L = p.layers[l];
     KVPrefetch kv;
@@ -1210,7 +1398,7 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
     W8<S::RE, S::CE> wgate, wup;
     uint4 n_post[S::CE][2];
     W8<S::RF, S::CF> wdown;
-    const bool ok =
+    ok =
         phase_qkv<S>(p, l, wg, ep, s_x, s_out, wqkv, n_in,
                      [&]() { prefetch_attn<S>(p, L, wg, pos, kv); }) &&
         phase_attn<S>(p, L, l, wg, ep, pos, s_in, kv, [&]() { prefetch_wo<S>(p, L, wg, wo); }) &&
@@ -1224,6 +1412,7 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
         phase_down<S>(p, l, wg, ep, s_in, s_out, s_own, wdown, []() {});
     if (!ok) break;
   }
+  if (ok && p.lm_w) phase_lm_head<S>(p, wg, ep, s_in, key_out, lm);
   // Advance the epoch for the next launch. Workgroup 0 finishes only after every workgroup has
   // contributed to the last layer, so every workgroup has read `ep`, the key, the position and
   // (in its attention phase) the RoPE row by now: the greedy loop's state advances here too.
@@ -1231,7 +1420,7 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
   if (p.key) {
     const int next = pos + 1;
     if (threadIdx.x == 0) {
-      *p.key = 0ull;
+      if (!p.lm_w) *p.key = 0ull;  // folded: the slot is cleared when it next receives a key
       *p.token = tok;
       if (p.token_log) {
         const int32_t s = *p.step;
@@ -1400,6 +1589,14 @@ static int decode_persistent(const char* fn, const iron_decode_gen* gen,
       return iron::fail(IRON_ERR_NULL, "%s: token_log needs a step counter and a length", fn);
     if (!iron::aligned(gen->emb, 16) || (gen->rope_table && !iron::aligned(gen->rope_table, 16)))
       return iron::fail(IRON_ERR_ALIGN, "%s: emb and rope_table must be 16-byte aligned", fn);
+    if (gen->lm_head) {
+      if (!gen->lm_norm)
+        return iron::fail(IRON_ERR_NULL, "%s: the folded LM head needs its norm weight", fn);
+      if (!iron::aligned(gen->lm_head, 16) || !iron::aligned(gen->lm_norm, 16) ||
+          !iron::aligned(gen->keys, 16))
+        return iron::fail(IRON_ERR_ALIGN, "%s: lm_head, lm_norm and keys must be 16-byte "
+                          "aligned", fn);
+    }
   }
   const ShapeId id = shape_id(D, FF, Hq, Hkv, HD);
   if (id == SHAPE_NONE)
@@ -1464,6 +1661,9 @@ static int decode_persistent(const char* fn, const iron_decode_gen* gen,
     p.ctx = gen->ctx;
     p.rope_table = gen->rope_table;
     p.ang_next = ang;
+    p.lm_w = gen->lm_head;
+    p.lm_norm = gen->lm_norm;
+    p.logits = gen->logits;
   }
   hipStream_t s = (hipStream_t)stream;
   if (id == SHAPE_0_6B)

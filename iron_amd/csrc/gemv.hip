@@ -351,10 +351,6 @@ IRON_DEV void dot_w16_lane(const uint4 (&w)[R][NCH], const float (&xf)[NCH][8],
   for (int r = 0; r < R; ++r) acc[r][0] = wave_sum_d(acc[r][0]);
 }
 
-IRON_DEV uint32_t bf16_order_key(uint16_t h) {
-  return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);
-}
-
 template <int B, int R>
 IRON_DEV void store_rows(const GemvParams& p, int row0, int lane, const double (&acc)[R][B],
                          const double (&acc2)[R][B], unsigned long long (&best)[B]) {

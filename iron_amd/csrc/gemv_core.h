@@ -239,6 +239,11 @@ IRON_DEV void dot_w8_lane(const GemvParams& p, const uint4 (&w)[R][NCH],
   }
 }
 
+// Order-preserving key of a bf16 value (the argmax epilogues pack it above ~row).
+IRON_DEV uint32_t bf16_order_key(uint16_t h) {
+  return (h & 0x8000u) ? (uint32_t)(~h & 0xffffu) : (uint32_t)(h | 0x8000u);
+}
+
 // SiLU(g) * u in fp64 with the golden's numerically stable sigmoid
 // (iron/operators/swiglu_mlp_dp/reference.py:28-33).
 IRON_DEV double silu_mul(double g, double u) {

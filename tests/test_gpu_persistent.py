@@ -66,7 +66,8 @@ def test_persistent_gen_short_log():
     w = random_qwen3_weights(cfg, seed=5)
     S, n = 64, 6
     want = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, persistent=True).generate([3], n)
-    m = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, persistent=True)
+    # the two-launch form (layers kernel, then iron_lm_head), driven by hand
+    m = Qwen3NPU(config=cfg, weights=w, max_seq_len=S, persistent=True, fold_lm_head=False)
     m.start_generation(3, 0)
     gs = m._gen_state()
     log = torch.full((8,), -7, dtype=torch.int32, device="cuda")
@@ -149,6 +150,43 @@ def test_persistent_multi_tile_context_tiny():
     for i in range(cfg.n_layers):
         assert torch.equal(_bits(ca[i][0]), _bits(cb[i][0])) and torch.equal(_bits(ca[i][1]),
                                                                              _bits(cb[i][1]))
+
+
+@pytest.mark.parametrize("kv_layout", ["separate", "interleaved"])
+def test_folded_lm_head_generation(kv_layout):
+    """The whole greedy step in one launch (layers + final norm + bf16 LM head + argmax,
+    iron_decode_persistent_gen with lm_head): the same tokens and bit-identical final logits as
+    the two-launch loop (layers, then iron_lm_head) and as the exact CPU chain fed those tokens;
+    the key slots alternate by epoch across re-armed runs."""
+    _say(f"folded LM head, tiny, {kv_layout}")
+    cfg = Qwen3Config.tiny()
+    w = random_qwen3_weights(cfg, seed=31)
+    prompt, n_new = [9, 4, 33], 12
+    runs = []
+    for fold in (True, False):
+        m = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, kv_layout=kv_layout,
+                     persistent=True, fold_lm_head=fold)
+        assert m.fold_lm_head == fold
+        toks = m.generate(prompt, n_new)
+        runs.append((toks, m.logits()))
+        again = m.generate(prompt, n_new)          # re-armed at a later epoch: same tokens
+        assert again == toks
+        assert m.persistent_errors() == 0
+    (ta, la), (tb, lb) = runs
+    assert ta == tb
+    assert torch.equal(_bits(la), _bits(lb))
+    chain = Qwen3CpuChain(cfg, w, 64)
+    pos = 0
+    for t in prompt[:-1]:
+        chain.step(t, pos)
+        pos += 1
+    tok = prompt[-1]
+    for i in range(n_new):
+        lc = chain.step(tok, pos)
+        assert Qwen3CpuChain.argmax(lc) == ta[i], f"step {i}"
+        tok, pos = ta[i], pos + 1
+    # the last launch consumed ta[-2]; its logits are the chain's at that step
+    assert torch.equal(_bits(la), _bits(lc))
 
 
 def test_persistent_epoch_advances_per_token():
