@@ -63,14 +63,16 @@ constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 constexpr int kRows = 5;
 constexpr int kTileTokens = 16 * kRows;
 
-// gh, the widest hand-off, is read with cached loads (see gather_blocks); layers rotate over
-// kGhBuffers copies, so a line an XCD's L2 kept from the previous layer is never the one read (a
-// stale copy would carry an old tag and be re-read coherently). One copy per layer measured no
-// better than four.
-// Each gate/up workgroup's words lie in one 128-byte cache line at the start of its block of
-// kGhBlock words (written with one store instruction), so seeing its last word means the whole
-// line has been written. Blocks 256 bytes apart spread the 256 polled lines over more memory
-// channels than 128 bytes apart (-2.7 us per token; 512 bytes measured the same as 256).
+// gh, the widest hand-off (every workgroup reads all FF fp32 values), travels in packed words: a
+// 16-bit tag over a 48-bit payload, so one gate/up workgroup's 12 values fill 8 words, one
+// 64-byte sector at the start of its block of kGhBlock words, and a consumer polls every word of
+// the block in one round trip. (With a 32-bit tag per 32-bit value, a consumer polled one
+// sentinel word and then read the block: two round trips, 4.7 us against 3.0 us in isolation.)
+// Blocks 256 bytes apart spread the 256 polled sectors over more memory channels than 128 bytes
+// apart (-2.7 us per token; 512 bytes measured the same as 256). Layers rotate over kGhBuffers
+// buffers: one buffer for every layer measured 43 us per token slower than four (the polled
+// sectors are then the ones the previous layer's producers wrote). A launch with fewer layers than
+// buffers clears the blocks of the buffers it leaves unused, which the short tags rely on.
 constexpr int kGhBuffers = 4;
 // Every hand-off buffer that many workgroups poll (x, raw qkv, the attention output, a, gh) is
 // written in kCopies copies kCopyWords words (32 KiB) apart, and the workgroups of XCD c (wg % 8)
@@ -108,6 +110,7 @@ struct Shape {
   static constexpr int GH_ROWS = 4 * RE;               // gh rows one workgroup produces
   static constexpr int GH_PROD = cdiv(FF, GH_ROWS);    // gate/up workgroups with rows
   static constexpr int GH_WORDS = GH_PROD * kGhBlock;  // one gh buffer, blocked per producer
+  static constexpr int GH_PACKED = cdiv(2 * GH_ROWS, 3);  // 48-bit words of one producer's block
   static constexpr int XW = 2 * RF;  // words of x (and of a) one down (Wo) workgroup writes
   // Whether every workgroup owns rows of the Wo / down phases (RD == RF) and of gate/up. Where
   // they do, the skip branch is compiled out: its second call site of the phase's `issue` hook
@@ -125,7 +128,7 @@ struct Shape {
   static_assert(NS * MERGE_PER == 256 && (NS == 32 || NS == 64 || NS == 128),
                 "one merge thread per (split, dim)");
   static_assert(D % 16 == 0 && FF % 16 == 0 && MQKV % 2 == 0, "GEMV widths");
-  static_assert(GH_ROWS <= kGhBlock && GH_PROD <= kNT, "gh blocks");
+  static_assert(GH_PACKED <= kGhBlock && GH_PROD <= kNT, "gh blocks");
   static_assert(RD == RF, "the Wo and down phases own the same rows");
   static_assert(spread_word(D / 2 - 1) < kCopyWords && spread_word(QD / 2 - 1) < kCopyWords,
                 "spread x, a and attention-output words in one copy");
@@ -228,6 +231,27 @@ IRON_DEV void put_double(unsigned long long* dst, double v, uint32_t tag) {
 
 IRON_DEV double word_double(uint32_t lo, uint32_t hi) {
   return __hiloint2double((int)hi, (int)lo);
+}
+
+// Packed words (gh): tag in bits 48..63, payload in bits 0..47. The 16-bit tag is the full tag
+// reduced to 1..65535 (never 0, the value of a cleared word). Every launch rewrites or clears every
+// gh block, so a stale word is at most one completed launch old (plus launches that failed before
+// their layer), i.e. a few multiples of kPhases * kMaxLayers full tags behind, never 65535.
+IRON_DEV uint32_t short_tag(uint32_t tag) { return tag % 0xffffu + 1u; }
+
+IRON_DEV void put_packed_copies(unsigned long long* dst, size_t stride, unsigned long long payload,
+                                uint32_t stag) {
+  const unsigned long long w = ((unsigned long long)stag << 48) | (payload & 0xffffffffffffull);
+#pragma unroll
+  for (int c = 0; c < kCopies; ++c)
+    __hip_atomic_store(dst + c * stride, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Word i (bits [48 i, 48 i + 48)) of the little-endian concatenation of n 32-bit values.
+IRON_DEV unsigned long long pack48(const uint32_t* v, int n, int i) {
+  const int v0 = (3 * i) >> 1;
+  const unsigned long long a = v0 < n ? v[v0] : 0u, b = v0 + 1 < n ? v[v0 + 1] : 0u;
+  return (i & 1) ? ((a >> 16) | (b << 16)) : (a | ((b & 0xffffull) << 32));
 }
 
 // Waits for n tagged words and puts their payloads in LDS. Thread t owns slots j = t + 256 k < n;
@@ -338,65 +362,52 @@ IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t*
   return ok;
 }
 
-// Waits for a wide input published in per-producer blocks, plus n_ext single words, and puts the
-// payloads in LDS. Block q (q < n_blk) is `rows` <= ROWS words at blk(q, rows); its producer writes
-// them with one store instruction, the last word (the sentinel) included, and they go to
-// dst[ROWS q + r]. Thread q polls only block q's sentinel, which keeps the polling traffic at one
-// word per producer; once the sentinel is in, the same thread reads the block's other words (they
-// are normally in by then; any whose tag is still old is read again next round). So a block from
-// an early producer is read while slower producers are still computing, and only the last
-// block's read follows the last sentinel. Extra word i < n_ext (ext(i, tag)) goes to
-// dst[ROWS n_blk + i] and is polled by thread i. Same contract as gather_words otherwise, with
-// one tag for the blocks.
-template <int ROWS, int DELAY = kFirstPollDelay, class Blk, class Ext, class Issue>
-IRON_DEV bool gather_blocks(int n_blk, Blk blk, uint32_t tag, int n_ext, Ext ext, Issue issue,
-                            uint32_t* dst, uint32_t* err) {
-  static_assert(ROWS >= 1 && ROWS <= 32, "block words");
+// Waits for the gh blocks of n_blk producers and puts their values in LDS. Producer q's ROWS
+// 32-bit values travel as the first W = ceil(2 ROWS / 3) packed words (put_packed_copies) of the
+// block at blk + q kGhBlock, word i holding bits [48 i, 48 i + 48) of their little-endian
+// concatenation; they land as dst32[ROWS q + r]. Every pending word is polled each round (8 per
+// thread for the Qwen3-0.6B shape: 2048 words, 64 contiguous bytes per producer). Same contract
+// as gather_words otherwise, with one short tag for all words.
+template <int ROWS, int NPT, int DELAY = kFirstPollDelay, class Issue>
+IRON_DEV bool gather_gh(int n_blk, unsigned long long* blk, uint32_t stag, Issue issue,
+                        uint32_t* dst32, uint32_t* err) {
+  constexpr int W = cdiv(2 * ROWS, 3);
   __syncthreads();
   retire_loads();
   first_poll_delay<DELAY>();
-  const int t = threadIdx.x;
-  int rows = 0;
-  unsigned long long* bp = t < n_blk ? blk(t, rows) : nullptr;
-  bool sent_in = t >= n_blk;
-  uint32_t body = t < n_blk ? (1u << (rows - 1)) - 1u : 0u;  // block words still to read
-  uint32_t ewant = 0;
-  bool ext_pending = t < n_ext;
-  unsigned long long* ep = ext_pending ? ext(t, ewant) : nullptr;
-  uint32_t* bdst = dst + ROWS * t;
-  bool missing = false, first = true;
+  uint16_t* const dst = (uint16_t*)dst32;
+  const int n = n_blk * W;
+  bool pending[NPT];
+  unsigned long long* ptr[NPT];
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    const int j = threadIdx.x + 256 * k;
+    pending[k] = j < n;
+    ptr[k] = pending[k] ? blk + (j / W) * kGhBlock + j % W : nullptr;
+  }
+  bool missing = false;
   for (long long spins = 0;; ++spins) {
-    unsigned long long ws = 0, we = 0;
-    if (!sent_in) ws = poll_word(bp + rows - 1);
-    if (ext_pending) we = poll_word(ep);
-    if (!sent_in && (uint32_t)(ws >> 32) == tag) {
-      sent_in = true;
-      bdst[rows - 1] = (uint32_t)ws;
-    }
-    if (ext_pending && (uint32_t)(we >> 32) == ewant) {
-      ext_pending = false;
-      dst[ROWS * n_blk + t] = (uint32_t)we;
-    }
-    if (sent_in && body != 0u) {
-      // the first read of a block goes through the L2, so the workgroups of an XCD share one
-      // fetch of its line; a copy that is stale there (an old tag) is read again coherently
-      unsigned long long wb[ROWS - 1 > 0 ? ROWS - 1 : 1];
+    unsigned long long w[NPT];
 #pragma unroll
-      for (int r = 0; r < ROWS - 1; ++r) {
-        if (!((body >> r) & 1u)) continue;
-        wb[r] = first ? __hip_atomic_load(bp + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT)
-                      : poll_word(bp + r);
-      }
-      first = false;
+    for (int k = 0; k < NPT; ++k)
+      if (pending[k]) w[k] = poll_word(ptr[k]);
+    missing = false;
 #pragma unroll
-      for (int r = 0; r < ROWS - 1; ++r) {
-        if (((body >> r) & 1u) && (uint32_t)(wb[r] >> 32) == tag) {
-          bdst[r] = (uint32_t)wb[r];
-          body &= ~(1u << r);
-        }
+    for (int k = 0; k < NPT; ++k) {
+      if (!pending[k]) continue;
+      if ((uint32_t)(w[k] >> 48) == stag) {
+        // 16-bit half c of word i is half 3 i + c of the block (2 ROWS halves; the last word of a
+        // block may carry fewer than three)
+        const int j = threadIdx.x + 256 * k, q = j / W, i = j % W;
+        uint16_t* d = dst + q * 2 * ROWS + 3 * i;
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+          if (3 * W == 2 * ROWS || 3 * i + c < 2 * ROWS) d[c] = (uint16_t)(w[k] >> (16 * c));
+        pending[k] = false;
+      } else {
+        missing = true;
       }
     }
-    missing = !sent_in || body != 0u || ext_pending;
     if (!missing || gave_up(spins, err)) break;
   }
   if (missing) atomicOr(err, 1u);
@@ -404,11 +415,6 @@ IRON_DEV bool gather_blocks(int n_blk, Blk blk, uint32_t tag, int n_ext, Ext ext
   issue_fenced(issue);
   return ok;
 }
-
-// No extra words for gather_blocks.
-struct NoExt {
-  IRON_DEV unsigned long long* operator()(int, uint32_t&) const { return nullptr; }
-};
 
 // This lane's activation slices from LDS, in the layout load_x_lane produces from global memory:
 // bf16 elements [c*1024 + 16 lane, +16) as two uint4, or fp32 ones as four.
@@ -1122,10 +1128,12 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
   const float gh = (float)silu_mul(tot, u_r);  // lane 16r: SiLU(gate r) * up r
   if ((lane & 15) == 0 && (lane >> 4) < R) s_gh[wave * R + (lane >> 4)] = gh;
   __syncthreads();
-  const int t = threadIdx.x, row = wg * S::GH_ROWS + t;
-  if (t < S::GH_ROWS && row < S::FF)
-    put_word_copies(p.GH + (l % kGhBuffers) * S::GH_WORDS + wg * kGhBlock + t, S::GH_COPY,
-                    __float_as_uint(s_gh[t]), phase_tag(ep, p.n_layers, l, 4));
+  // the block's GH_PACKED words: 16-bit halves 3 t .. 3 t + 2 of the GH_ROWS values
+  const int t = threadIdx.x;
+  if (t < S::GH_PACKED)
+    put_packed_copies(p.GH + (l % kGhBuffers) * S::GH_WORDS + wg * kGhBlock + t, S::GH_COPY,
+                      pack48((const uint32_t*)s_gh, S::GH_ROWS, t),
+                      short_tag(phase_tag(ep, p.n_layers, l, 4)));
   return true;
 }
 
@@ -1147,18 +1155,12 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   if constexpr (!S::WO_ALL)
     if (wg * 4 * R >= S::D) return skip_gather(issue);  // no down rows here (small shapes)
   {
-    const uint32_t tg = phase_tag(ep, p.n_layers, l, 4);
-    // gate/up workgroup q writes rows [GH_ROWS q, GH_ROWS (q + 1)) into block q, the last one
-    // (the sentinel) included, with one store instruction
+    // gate/up workgroup q publishes rows [GH_ROWS q, GH_ROWS (q + 1)) in block q
     static_assert(S::GH_ROWS * S::GH_PROD == S::FF, "whole gh blocks");
-    auto blk = [&](int q, int& rows) {
-      rows = S::FF - q * S::GH_ROWS < S::GH_ROWS ? S::FF - q * S::GH_ROWS : S::GH_ROWS;
-      return gh + q * kGhBlock;
-    };
-    // gh's producers finish last in the layer and its hand-off is the longest: a later first
-    // poll measured best here (24 units: -7 to -17 us per step against 10; 32 and 40 worse)
-    if (!gather_blocks<S::GH_ROWS, 24>(S::GH_PROD, blk, tg, 0, NoExt(), issue, s_in,
-                                       p.ctrl + 1))
+    // gh's producers finish last in the layer: a later first poll measured best here (18
+    // units: -4 us per step against 24 and -2 against 12)
+    if (!gather_gh<S::GH_ROWS, cdiv(S::GH_PROD * S::GH_PACKED, 256), 18>(
+            S::GH_PROD, gh, short_tag(phase_tag(ep, p.n_layers, l, 4)), issue, s_in, p.ctrl + 1))
       return false;
   }
   uint4 xl[NCH][4], x2l[NCH][2] = {}, nwl[NCH][2] = {};
@@ -1397,6 +1399,11 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
     const int word = wg * S::XW + threadIdx.x;
     s_own[S::XW + threadIdx.x] = word < S::D / 2 ? ((const uint32_t*)x_in)[word] : 0u;
   }
+  // gh buffers no layer of this launch uses: clear this workgroup's block (nothing reads them in
+  // this launch; a later launch with more layers then finds zeros there, never an old short tag)
+  if (p.n_layers < kGhBuffers && wg < S::GH_PROD && threadIdx.x < S::GH_PACKED)
+    for (int b = p.n_layers; b < kGhBuffers; ++b)
+      put_packed_copies(p.GH + b * S::GH_WORDS + wg * kGhBlock + threadIdx.x, S::GH_COPY, 0ull, 0u);
   LmRing<S> lm;
   bool ok = true;
   for (int l = 0; l < p.n_layers; ++l) {
