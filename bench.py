@@ -36,15 +36,16 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the bf16 LM-head GEMV from two rocprofv3 --pmc passes over this bench:
-# FETCH_SIZE 152066.19 KiB x 2.0 + WRITE_SIZE 362.28 KiB x 1.0, the factors being what the same
-# counters read for a plain 256 MiB device copy (profiles/decode_qwen3_0_6b_hbm_traffic.md).
-LM_HEAD_BF16_TRAFFIC = 311_802_528
-# HBM bytes per launch of the persistent layers kernel (all 28 layers), same method:
-# FETCH_SIZE 382599.72 KiB x 2.0 + WRITE_SIZE 73624.03 KiB x 1.0 at context 2048..2057.
-PERSISTENT_TRAFFIC = 858_955_232
-# HBM bytes per launch of the one-launch token (layers + folded LM head), same method; None until
-# measured for the current kernel.
-PERSISTENT_TOKEN_TRAFFIC = None
+# FETCH_SIZE 152067.06 KiB x 2.0 + WRITE_SIZE 361.44 KiB x 1.0, the factors being what the same
+# counters read for a plain 256 MiB device copy (131083.5 KiB fetched, 262144 KiB written).
+LM_HEAD_BF16_TRAFFIC = 311_776_133
+# HBM bytes per launch of the persistent layers kernel (all 28 layers, LM head separate), same
+# method: FETCH_SIZE 382703.56 KiB x 2.0 + WRITE_SIZE 71832.03 KiB x 1.0 at context 1985..2047.
+PERSISTENT_TRAFFIC = 855_093_317
+# HBM bytes per launch of the one-launch token (layers + final norm + LM head + argmax), same
+# method, as a least-squares line in the context over 25 launches at contexts 2057..2081
+# (FETCH_SIZE 536762.06 KiB, WRITE_SIZE 72140.22 KiB at the median): bytes = A + B x context.
+PERSISTENT_TOKEN_TRAFFIC = (964_977_681, 100_530.5)
 
 
 def parse():
@@ -161,7 +162,9 @@ def main():
                                               "RMSNorm, bf16 LM head, argmax)",
                     "achieved": round(tok_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(tok_gbs / HBM_PEAK_GBS, 4),
-                    "traffic": PERSISTENT_TOKEN_TRAFFIC,
+                    "traffic": int(PERSISTENT_TOKEN_TRAFFIC[0] + PERSISTENT_TOKEN_TRAFFIC[1] * ctx),
+                    "traffic_ratio": round((PERSISTENT_TOKEN_TRAFFIC[0] +
+                                            PERSISTENT_TOKEN_TRAFFIC[1] * ctx) / tok_bytes, 3),
                     "bytes_per_launch": int(tok_bytes), "avg_launch_us": round(token_us, 2),
                     "context": ctx}
     elif model.persistent:
@@ -320,13 +323,16 @@ def cpu_baseline(cfg, w, kv0, prompt, gpu_tokens, start, S, n_sample):
     for t in prompt[:-1]:
         chain.step(t, pos)
         pos += 1
-    chain.step(prompt[-1], pos)                           # the armed token at start-1
+    lg = chain.step(prompt[-1], pos)                      # the armed token at start-1
     pos += 1
+    # greedy agreement: the chain's argmax at each step against the token the GPU chose there
+    agree = int(Qwen3CpuChain.argmax(lg) == gpu_tokens[0])
     tok = gpu_tokens[0]
     t0 = time.perf_counter()
     for i in range(n_sample):
-        chain.step(tok, pos)
+        lg = chain.step(tok, pos)
         tok = gpu_tokens[i + 1]
+        agree += int(Qwen3CpuChain.argmax(lg) == tok)
         pos += 1
     dt = time.perf_counter() - t0
     cpu_model = "unknown"
@@ -338,7 +344,7 @@ def cpu_baseline(cfg, w, kv0, prompt, gpu_tokens, start, S, n_sample):
     except OSError:
         pass
     return {"value": round(n_sample / dt, 3), "unit": "tokens/s", "cores": cores,
-            "kind": "port",
+            "kind": "port", "greedy_agreement": f"{agree}/{n_sample + 1}",
             "sample": f"{n_sample} decode steps at context {start + 2}..{start + 1 + n_sample} "
                       "fed the GPU's tokens (after the same 1984-position KV prefill and 64-token "
                       f"prompt); the reference goldens composed in torch fp32 on {cpu_model}"}

@@ -23,6 +23,13 @@ from . import _lib
 
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
+# MFMA busy fraction per kernel (SQ_VALU_MFMA_BUSY_CYCLES over the 1024 SIMDs / (GRBM_GUI_ACTIVE / 8
+# XCDs x 1024)), measured with rocprofv3 --pmc over `--only c5_prefill` and `--only c5_decode`;
+# a counter run, so quoted here rather than measured in the timed run.
+MFMA_BUSY = {"prefill_attn_kernel": 0.152,
+             "gemm_w8_mfma_kernel (gate/up, SwiGLU, 3 activation planes)": 0.078,
+             "gemm_w8_mfma_kernel (down, 3 activation planes)": 0.054,
+             "gemm_w8_mfma_kernel (QKV)": 0.013, "gemm_w8_mfma_kernel (Wo)": 0.012}
 ROTATE_BYTES = 512 << 20
 DEV = "cuda"
 
@@ -211,7 +218,8 @@ def config5_decode(lib, steps: int = 3, acc: str = "f64"):
     return {"ms_per_step": round(med / 1e3, 3), "tokens_per_s": round(B / (med * 1e-6), 1),
             "bytes_per_step": int(nbytes), "GB_s": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "shape": "Qwen3-8B int8 G=32, 36 layers, B=16, context 8192", "accumulate": acc}
+            "shape": "Qwen3-8B int8 G=32, 36 layers, B=16, context 8192", "accumulate": acc,
+            "gemm_mfma_busy": {k: v for k, v in MFMA_BUSY.items() if k.startswith("gemm")}}
 
 
 def config5_prefill(lib):
@@ -234,7 +242,8 @@ def config5_prefill(lib):
     tf = flops / (med * 1e-6) / 1e12
     return {"us_median": round(med, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
             "flops": flops, "TFLOP_s": round(tf, 1), "frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
-            "shape": "H=32 KV=8 S=2048 D=128 causal"}
+            "shape": "H=32 KV=8 S=2048 D=128 causal",
+            "mfma_busy": MFMA_BUSY["prefill_attn_kernel"]}
 
 
 def run_all(include_c5: bool = True) -> dict:
@@ -302,6 +311,8 @@ if __name__ == "__main__":
                     help="run one configuration (for profiling)")
     ap.add_argument("--acc", choices=["f64", "f32"], default="f64",
                     help="attention accumulation for --only c3 / c5_decode")
+    ap.add_argument("--batch", type=int, default=None,
+                    help="batch for --only c2 (default 1) / c3 (default 8, ragged when > 1)")
     a = ap.parse_args()
     if a.copy_probe:
         print(json.dumps(copy_probe()), flush=True)
@@ -309,8 +320,9 @@ if __name__ == "__main__":
         print(json.dumps(read_probe()), flush=True)
     elif a.only:
         lib = _lib.load()
-        one = {"c1": lambda: config1(lib), "c2": lambda: config2(lib, 1),
-               "c3": lambda: config3(lib, 8, True, a.acc),
+        b2, b3 = a.batch or 1, a.batch or 8
+        one = {"c1": lambda: config1(lib), "c2": lambda: config2(lib, b2),
+               "c3": lambda: config3(lib, b3, b3 > 1, a.acc),
                "c5_prefill": lambda: config5_prefill(lib),
                "c5_decode": lambda: config5_decode(lib, acc=a.acc)}[a.only]
         print(json.dumps(one()), flush=True)
