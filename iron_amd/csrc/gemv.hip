@@ -22,7 +22,8 @@
 // wavefront load instruction reads 1 KiB of one row. A workgroup owns one group of 4*R rows: it
 // first issues every weight/scale load of the group (R*NCH 128-bit loads per lane, all in
 // flight) behind the activation loads, then stages x into LDS (the prologue, overlapping the
-// weight latency), then reduces.
+// weight latency), then reduces. A batch whose rows do not all fit in LDS at once (long rows)
+// runs as batch groups, one workgroup per row group and batch group (gemv_kernel, MULTI).
 #include "common.h"
 #include "gemv_core.h"
 #include "internal.h"
@@ -32,19 +33,22 @@ namespace {
 using namespace iron::dev;
 
 // ------------------------------------------------------------------------------------------
-// Prologue: stage B vectors of length K into LDS as fp64 (K % 8 == 0, 16-byte aligned rows).
+// Prologue: stage B vectors of length K into LDS as fp32 (K % 8 == 0, 16-byte aligned rows).
+// Every staged value is an exact fp32: a bf16 activation, an fp32 one, or the fp32 (or bf16)
+// rounding of the RMSNorm output, so the dot products see the same numbers as from fp64 staging
+// in half the LDS (a 4 x 6144 batch fits).
 //
-// LDS layout: lane-contiguous pairs. A lane of the dot product consumes J consecutive pairs
-// (x[2P], x[2P+1]) per chunk (J = 8 for int8 chunks of 1024, 4 for bf16 chunks of 512); pair P
-// lives at slot (c*J + j)*64 + lane with c = P / (64*J), lane = (P % (64*J)) / J, j = P % J, so
+// LDS layout: lane-contiguous quads. A lane of the dot product consumes J consecutive quads
+// x[4Q .. 4Q+3] per chunk (J = 4 for int8 chunks of 1024, 2 for bf16 chunks of 512); quad Q
+// lives at slot (c*J + j)*64 + lane with c = Q / (64*J), lane = (Q % (64*J)) / J, j = Q % J, so
 // one ds_read_b128 of a wavefront reads 64 consecutive 16-byte slots (no bank conflicts). A
-// vector occupies ceil(K / chunk) * chunk doubles.
+// vector occupies ceil(K / chunk) * chunk floats.
 // ------------------------------------------------------------------------------------------
 template <bool INT8>
-IRON_DEV int pair_slot(int P) {
-  constexpr int J = INT8 ? 8 : 4;
-  constexpr int PC = 64 * J;  // pairs per chunk
-  const int c = P / PC, rem = P % PC;
+IRON_DEV int quad_slot(int Q) {
+  constexpr int J = INT8 ? 4 : 2;
+  constexpr int QC = 64 * J;  // quads per chunk
+  const int c = Q / QC, rem = Q % QC;
   return (c * J + (rem % J)) * 64 + rem / J;
 }
 
@@ -54,11 +58,11 @@ IRON_DEV int padded_k(int K) {
   return (K + chunk - 1) / chunk * chunk;
 }
 
-// thread t's 8 elements x[8t..8t+7] are pairs 4t..4t+3
+// thread t's 8 elements x[8t..8t+7] are quads 2t, 2t+1
 template <bool INT8>
-IRON_DEV void put8(double2* dst, int i, const double (&v)[8]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) dst[pair_slot<INT8>(4 * i + j)] = make_double2(v[2 * j], v[2 * j + 1]);
+IRON_DEV void put8(float4* dst, int i, const float (&v)[8]) {
+  dst[quad_slot<INT8>(2 * i)] = make_float4(v[0], v[1], v[2], v[3]);
+  dst[quad_slot<INT8>(2 * i + 1)] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
 // The activation side is loaded into registers before the weight loads are issued: loads
@@ -81,7 +85,7 @@ IRON_DEV void load_x(const GemvParams& p, uint4 (&xa)[B][S], uint4 (&xb)[B][S], 
       const int i = threadIdx.x + 256 * r;
       xa[b][r] = make_uint4(0u, 0u, 0u, 0u);
       xb[b][r] = make_uint4(0u, 0u, 0u, 0u);
-      if (i < n8) {
+      if (i < n8 && b < p.nb) {
         if (p.pro == PRO_F32) {
           const uint4* src = (const uint4*)((const float*)p.x + (size_t)b * p.x_stride);
           xa[b][r] = src[2 * i];
@@ -101,16 +105,18 @@ IRON_DEV void load_x(const GemvParams& p, uint4 (&xa)[B][S], uint4 (&xb)[B][S], 
   }
 }
 
+// Rows b >= p.nb are not staged (their LDS rows keep older values; their results are not stored).
 template <int B, int S, bool INT8>
 IRON_DEV void stage_x(const GemvParams& p, const uint4 (&xa)[B][S], const uint4 (&xb)[B][S],
-                      const uint4 (&xn)[S], double* __restrict__ xs, double* red) {
+                      const uint4 (&xn)[S], float* __restrict__ xs, double* red) {
   const int K = p.K;
   const int n8 = K >> 3;
   const int KP = padded_k<INT8>(K);
   const int tid = threadIdx.x;
 #pragma unroll
   for (int b = 0; b < B; ++b) {
-    double2* dst = (double2*)(xs + (size_t)b * KP);
+    if (b >= p.nb) break;  // workgroup-uniform
+    float4* dst = (float4*)(xs + (size_t)b * KP);
     if (p.pro == PRO_F32) {
       const uint4* src = (const uint4*)((const float*)p.x + (size_t)b * p.x_stride);
 #pragma unroll
@@ -118,17 +124,17 @@ IRON_DEV void stage_x(const GemvParams& p, const uint4 (&xa)[B][S], const uint4 
         const int i = tid + 256 * r;
         if (i < n8) {
           const uint4 lo = xa[b][r], hi = xb[b][r];
-          const double v[8] = {__uint_as_float(lo.x), __uint_as_float(lo.y), __uint_as_float(lo.z),
-                               __uint_as_float(lo.w), __uint_as_float(hi.x), __uint_as_float(hi.y),
-                               __uint_as_float(hi.z), __uint_as_float(hi.w)};
+          const float v[8] = {__uint_as_float(lo.x), __uint_as_float(lo.y), __uint_as_float(lo.z),
+                              __uint_as_float(lo.w), __uint_as_float(hi.x), __uint_as_float(hi.y),
+                              __uint_as_float(hi.z), __uint_as_float(hi.w)};
           put8<INT8>(dst, i, v);
         }
       }
       for (int i = tid + 256 * S; i < n8; i += 256) {
         const uint4 lo = src[2 * i], hi = src[2 * i + 1];
-        const double v[8] = {__uint_as_float(lo.x), __uint_as_float(lo.y), __uint_as_float(lo.z),
-                             __uint_as_float(lo.w), __uint_as_float(hi.x), __uint_as_float(hi.y),
-                             __uint_as_float(hi.z), __uint_as_float(hi.w)};
+        const float v[8] = {__uint_as_float(lo.x), __uint_as_float(lo.y), __uint_as_float(lo.z),
+                            __uint_as_float(lo.w), __uint_as_float(hi.x), __uint_as_float(hi.y),
+                            __uint_as_float(hi.z), __uint_as_float(hi.w)};
         put8<INT8>(dst, i, v);
       }
       continue;
@@ -141,19 +147,13 @@ IRON_DEV void stage_x(const GemvParams& p, const uint4 (&xa)[B][S], const uint4 
         if (i < n8) {
           float f[8];
           unpack8(xa[b][r], f);
-          double v[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = f[j];
-          put8<INT8>(dst, i, v);
+          put8<INT8>(dst, i, f);
         }
       }
       for (int i = tid + 256 * S; i < n8; i += 256) {
         float f[8];
         unpack8(src[i], f);
-        double v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = f[j];
-        put8<INT8>(dst, i, v);
+        put8<INT8>(dst, i, f);
       }
       continue;
     }
@@ -192,11 +192,11 @@ IRON_DEV void stage_x(const GemvParams& p, const uint4 (&xa)[B][S], const uint4 
           slot_values(src[i], has_x2 ? src2[i] : make_uint4(0u, 0u, 0u, 0u), has_x2, f);
           unpack8(wsrc[i], wf);
         }
-        double v[8];
+        float v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const double y = ((double)f[j] * inv) * (double)wf[j];
-          v[j] = to_bf16 ? (double)round_bf16((float)y) : (double)(float)y;
+          v[j] = to_bf16 ? round_bf16((float)y) : (float)y;
         }
         put8<INT8>(dst, i, v);
       }
@@ -207,7 +207,7 @@ IRON_DEV void stage_x(const GemvParams& p, const uint4 (&xa)[B][S], const uint4 
 
 template <int B, int R, int NCH>
 IRON_DEV void dot_w8(const GemvParams& p, const uint4 (&w)[R][NCH], const uint32_t (&sc)[R][NCH],
-                     const double* __restrict__ xs, int row0, int lane, double (&acc)[R][B]) {
+                     const float* __restrict__ xs, int row0, int lane, double (&acc)[R][B]) {
   const int K = p.K;
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -221,13 +221,15 @@ IRON_DEV void dot_w8(const GemvParams& p, const uint4 (&w)[R][NCH], const uint32
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       if (e < K) {
-        // pairs (c*8 + j)*64 + lane, j = 0..7 (the lane-contiguous staging layout)
-        const double2* src = (const double2*)(xs + (size_t)b * padded_k<true>(K)) + c * 512 + lane;
+        // quads (c*4 + j)*64 + lane, j = 0..3 (the lane-contiguous staging layout)
+        const float4* src = (const float4*)(xs + (size_t)b * padded_k<true>(K)) + c * 256 + lane;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const double2 t = src[j * 64];
-          xv[b][2 * j] = t.x;
-          xv[b][2 * j + 1] = t.y;
+        for (int j = 0; j < 4; ++j) {
+          const float4 t = src[j * 64];
+          xv[b][4 * j] = t.x;
+          xv[b][4 * j + 1] = t.y;
+          xv[b][4 * j + 2] = t.z;
+          xv[b][4 * j + 3] = t.w;
         }
       } else {
 #pragma unroll
@@ -277,7 +279,7 @@ IRON_DEV void fetch_w16(const GemvParams& p, int row0, int lane, uint4 (&w)[R][N
 
 template <int B, int R, int NCH>
 IRON_DEV void dot_w16(const GemvParams& p, const uint4 (&w)[R][NCH],
-                      const double* __restrict__ xs, int lane, double (&acc)[R][B]) {
+                      const float* __restrict__ xs, int lane, double (&acc)[R][B]) {
   const int K = p.K;
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -291,13 +293,15 @@ IRON_DEV void dot_w16(const GemvParams& p, const uint4 (&w)[R][NCH],
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       if (e < K) {
-        // pairs (c*4 + j)*64 + lane, j = 0..3
-        const double2* src = (const double2*)(xs + (size_t)b * padded_k<false>(K)) + c * 256 + lane;
+        // quads (c*2 + j)*64 + lane, j = 0..1
+        const float4* src = (const float4*)(xs + (size_t)b * padded_k<false>(K)) + c * 128 + lane;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const double2 t = src[j * 64];
-          xv[b][2 * j] = t.x;
-          xv[b][2 * j + 1] = t.y;
+        for (int j = 0; j < 2; ++j) {
+          const float4 t = src[j * 64];
+          xv[b][4 * j] = t.x;
+          xv[b][4 * j + 1] = t.y;
+          xv[b][4 * j + 2] = t.z;
+          xv[b][4 * j + 3] = t.w;
         }
       } else {
 #pragma unroll
@@ -360,6 +364,7 @@ IRON_DEV void store_rows(const GemvParams& p, int row0, int lane, const double (
     if (row >= p.M) continue;
 #pragma unroll
     for (int b = 0; b < B; ++b) {
+      if (b >= p.nb) break;  // rows past the batch (a partial group)
       const double v = acc[r][b];
       const size_t o = (size_t)b * p.y_stride + row;
       if (p.epi == EPI_BF16_ARGMAX) {
@@ -390,18 +395,76 @@ IRON_DEV void store_rows(const GemvParams& p, int row0, int lane, const double (
 // stage it once per workgroup in LDS: every wavefront loading the whole vector costs more).
 constexpr bool xreg_path(int B, int NCH) { return B == 1 && NCH <= 2; }
 
+// The parameters of batch rows [b0, b0 + B) of a launch over p.nb rows: operands advanced by b0
+// rows, nb the rows of the group that exist.
+template <int B>
+IRON_DEV GemvParams batch_group(const GemvParams& p, int b0) {
+  GemvParams q = p;
+  if (b0 == 0) {
+    q.nb = p.nb < B ? p.nb : B;
+    return q;
+  }
+  q.nb = p.nb - b0 < B ? p.nb - b0 : B;
+  if (p.pro == PRO_F32) q.x = (const float*)p.x + (size_t)b0 * p.x_stride;
+  else q.x = (const uint16_t*)p.x + (size_t)b0 * p.x_stride;
+  if (p.x2) q.x2 = p.x2 + (size_t)b0 * p.x2_stride;
+  if (p.epi == EPI_F32 || p.epi == EPI_SWIGLU_F32) q.y = (float*)p.y + (size_t)b0 * p.y_stride;
+  else q.y = (uint16_t*)p.y + (size_t)b0 * p.y_stride;
+  if (p.r1) q.r1 = p.r1 + (size_t)b0 * p.r_stride;
+  if (p.r2) q.r2 = p.r2 + (size_t)b0 * p.r_stride;
+  if (p.argmax) q.argmax = p.argmax + b0;
+  return q;
+}
+
+// One candidate per workgroup and batch row; an atomic only when it beats the value already
+// published (a stale read costs at most a redundant atomicMax, never a wrong result). Resets best.
+template <int B>
+IRON_DEV void publish_argmax(const GemvParams& p, int wave, int lane,
+                             unsigned long long (&best)[B], unsigned long long (*s_best)[4]) {
+  if (lane == 0) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) s_best[wave][b] = best[b];
+  }
+  __syncthreads();
+  if (threadIdx.x < B && (int)threadIdx.x < p.nb) {
+    const int b = threadIdx.x;
+    unsigned long long k = s_best[0][b];
+    for (int i = 1; i < 4; ++i) k = s_best[i][b] > k ? s_best[i][b] : k;
+    const unsigned long long cur =
+        __hip_atomic_load(p.argmax + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (k > cur) atomicMax(p.argmax + b, k);
+  }
+  __syncthreads();  // s_best is read before a later group rewrites it
+#pragma unroll
+  for (int b = 0; b < B; ++b) best[b] = 0ull;
+}
+
 // IT: row blocks per workgroup (register-activation path only). A workgroup then streams IT
 // consecutive blocks of 4R rows: fewer, longer workgroups read HBM faster (a 311 MB bf16 LM head:
 // 5.7 TB/s with one block, 6.3 TB/s with four, measured with the same access pattern).
-template <int B, int R, int NCH, bool INT8, bool DUAL, int IT = 1>
+// p.nb batch rows: at most B, or with MULTI p.n_bgroups groups of B rows, one workgroup per
+// (row group, batch group). The workgroups of one octet of row groups and one batch group are 8
+// consecutive workgroups, the octet's batch groups follow each other: a workgroup w sits on XCD
+// w % 8 (the dispatcher's round robin), so the batch groups of a row group run on one XCD at the
+// same time and their reads of its weights meet in that XCD's L2 (HBM streams each weight once).
+template <int B, int R, int NCH, bool INT8, bool DUAL, int IT = 1, bool MULTI = false>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
-  extern __shared__ double xs[];
+  extern __shared__ float xs[];
   __shared__ double red[4];
   __shared__ unsigned long long s_best[4][4];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   static_assert(IT == 1 || xreg_path(B, NCH), "row-block loop on the register path only");
-  int row0 = (blockIdx.x * IT * 4 + wave) * R;
+  static_assert(!MULTI || !xreg_path(B, NCH), "batch groups on the LDS path only");
+  int blk = blockIdx.x;
+  if constexpr (MULTI) {
+    const int ng = p.n_bgroups;
+    const int bg = (blk / 8) % ng;
+    blk = (blk / (8 * ng)) * 8 + blk % 8;
+    if (blk * 4 * R >= p.M) return;  // the last octet's padding (workgroup-uniform)
+    p = batch_group<B>(p, bg * B);
+  }
+  int row0 = (blk * IT * 4 + wave) * R;
 
   uint4 w[R][NCH];
   uint32_t sc[R][NCH];
@@ -446,42 +509,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
         fetch_weights();
       }
     }
+    if (p.epi == EPI_BF16_ARGMAX) publish_argmax<B>(p, wave, lane, best, s_best);
   } else {
-  // 1. the activation side first, then every weight load of this wavefront's rows
-  constexpr int S = x_slots<B>();
-  uint4 xa[B][S], xb[B][S], xn[S];
-  load_x<B, S>(p, xa, xb, xn);
-  fetch_weights();
-
-  // 2. the prologue runs while the weights are in flight
-  stage_x<B, S, INT8>(p, xa, xb, xn, xs, red);
-
-  // 3. reduce
-  if constexpr (INT8) {
-    dot_w8<B, R, NCH>(p, w, sc, xs, row0, lane, acc);
-    if constexpr (DUAL) dot_w8<B, R, NCH>(p, w2, sc2, xs, row0, lane, acc2);
-  } else {
-    dot_w16<B, R, NCH>(p, w, xs, lane, acc);
-  }
-  if (row0 < p.M) store_rows<B, R>(p, row0, lane, acc, acc2, best);
-  }
-
-  if (p.epi == EPI_BF16_ARGMAX) {
-    // One candidate per workgroup; an atomic only when it beats the value already published
-    // (a stale read costs at most a redundant atomicMax, never a wrong result).
-    if (lane == 0) {
-#pragma unroll
-      for (int b = 0; b < B; ++b) s_best[wave][b] = best[b];
+    // 1. the activation side first, then every weight load of this wavefront's rows
+    constexpr int S = x_slots<B>();
+    uint4 xa[B][S], xb[B][S], xn[S];
+    load_x<B, S>(p, xa, xb, xn);
+    fetch_weights();
+    // 2. the prologue runs while the weights are in flight
+    stage_x<B, S, INT8>(p, xa, xb, xn, xs, red);
+    // 3. reduce
+    if constexpr (INT8) {
+      dot_w8<B, R, NCH>(p, w, sc, xs, row0, lane, acc);
+      if constexpr (DUAL) dot_w8<B, R, NCH>(p, w2, sc2, xs, row0, lane, acc2);
+    } else {
+      dot_w16<B, R, NCH>(p, w, xs, lane, acc);
     }
-    __syncthreads();
-    if (threadIdx.x < B) {
-      const int b = threadIdx.x;
-      unsigned long long k = s_best[0][b];
-      for (int i = 1; i < 4; ++i) k = s_best[i][b] > k ? s_best[i][b] : k;
-      const unsigned long long cur =
-          __hip_atomic_load(p.argmax + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (k > cur) atomicMax(p.argmax + b, k);
-    }
+    if (row0 < p.M) store_rows<B, R>(p, row0, lane, acc, acc2, best);
+    if (p.epi == EPI_BF16_ARGMAX) publish_argmax<B>(p, wave, lane, best, s_best);
   }
 }
 
@@ -543,6 +588,14 @@ constexpr long long kLongGroups = 4096;
 
 template <bool INT8, bool DUAL, int B, int R, int NCH>
 void launch_one(const GemvParams& p, int grid, size_t lds, hipStream_t s) {
+  if constexpr (!xreg_path(B, NCH) && (B == 4 || B == 3 || B == 2)) {
+    if (p.nb > B) {  // batches above the staged rows: a workgroup per row group and batch group
+      const long long octets = (grid + 7) / 8;
+      hipLaunchKernelGGL((gemv_kernel<B, R, NCH, INT8, DUAL, 1, true>),
+                         dim3((unsigned)(octets * 8 * p.n_bgroups)), dim3(256), lds, s, p);
+      return;
+    }
+  }
   if constexpr (B == 1 && !DUAL && R == 8 && xreg_path(B, NCH)) {
     if (grid >= kLongGroups) {
       hipLaunchKernelGGL((gemv_kernel<B, R, NCH, INT8, DUAL, 4>), dim3((grid + 3) / 4),
@@ -578,14 +631,28 @@ bool launch_nch(const GemvParams& p, int NCH, int R, int grid, size_t lds, hipSt
 }
 
 template <bool INT8, bool DUAL>
-int launch_gemv(const GemvParams& p, int B, hipStream_t stream, const char* fn) {
+int launch_gemv(GemvParams p, int B, hipStream_t stream, const char* fn) {
+  if (B < 1 || B > iron::kGemvMaxBatch)
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: batch %d outside the GEMV path's 1..%d", fn, B,
+                      iron::kGemvMaxBatch);
+  p.nb = B;
   const int chunk = INT8 ? 1024 : 512;
-  size_t lds = (size_t)B * ((p.K + chunk - 1) / chunk * chunk) * sizeof(double);
+  const size_t row_bytes = (size_t)((p.K + chunk - 1) / chunk * chunk) * sizeof(float);
+  // kernel batch: the rows staged in LDS at once (at most 4, fewer for long rows); larger
+  // batches run in groups of BK rows over the same weight registers
+  int BK = B < 4 ? B : 4;
+  while (BK > 1 && (size_t)BK * row_bytes > (size_t)kMaxLdsBytes) --BK;
+  p.n_bgroups = (B + BK - 1) / BK;
+  size_t lds = (size_t)BK * row_bytes;
   if (lds > (size_t)kMaxLdsBytes)
-    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: B*K = %d*%d exceeds the LDS-staged GEMV limit",
-                      fn, B, p.K);
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: K=%d exceeds the LDS-staged GEMV limit", fn,
+                      p.K);
   const int NCH = round_pow2((p.K + chunk - 1) / chunk);
-  if (xreg_path(B, NCH)) lds = 0;  // the activation stays in registers
+  if (xreg_path(BK, NCH)) {
+    if (B > 1)  // the register path holds one row (only short rows take it, and they fit 4)
+      return iron::fail(IRON_ERR_UNSUPPORTED, "%s: batch %d with K=%d", fn, B, p.K);
+    lds = 0;  // the activation stays in registers
+  }
   const int slices = (DUAL ? 2 : 1) * NCH;
   if (slices > kMaxSlices)
     return iron::fail(IRON_ERR_UNSUPPORTED, "%s: K=%d too long for the resident-slice GEMV", fn,
@@ -600,13 +667,15 @@ int launch_gemv(const GemvParams& p, int B, hipStream_t stream, const char* fn) 
   if (groups > (1ll << 30)) return iron::fail(IRON_ERR_SHAPE, "%s: M too large", fn);
   const int grid = (int)groups;
   bool ok = false;
-  switch (B) {
+  if (p.n_bgroups > 1 && BK == 1)
+    return iron::fail(IRON_ERR_UNSUPPORTED, "%s: batch %d with K=%d", fn, B, p.K);
+  if ((long long)grid * p.n_bgroups + 8ll * p.n_bgroups > (1ll << 30))
+    return iron::fail(IRON_ERR_SHAPE, "%s: M too large", fn);
+  switch (BK) {
     case 1: ok = launch_nch<INT8, DUAL, 1>(p, NCH, R, grid, lds, stream); break;
     case 2: ok = launch_nch<INT8, DUAL, 2>(p, NCH, R, grid, lds, stream); break;
     case 3: ok = launch_nch<INT8, DUAL, 3>(p, NCH, R, grid, lds, stream); break;
-    case 4: ok = launch_nch<INT8, DUAL, 4>(p, NCH, R, grid, lds, stream); break;
-    default:
-      return iron::fail(IRON_ERR_UNSUPPORTED, "%s: batch %d > 4 needs the MFMA path", fn, B);
+    default: ok = launch_nch<INT8, DUAL, 4>(p, NCH, R, grid, lds, stream); break;
   }
   if (!ok) return iron::fail(IRON_ERR_UNSUPPORTED, "%s: no kernel for K=%d R=%d", fn, p.K, R);
   return iron::check_launch(fn);

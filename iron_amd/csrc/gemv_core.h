@@ -48,6 +48,8 @@ struct GemvParams {
   const uint16_t* r2;
   int r_stride;
   unsigned long long* argmax;  // [B] packed (ordered bf16 << 32 | ~row)
+  int nb;               // batch rows of the launch (gemv.hip; rows past it are not read or written)
+  int n_bgroups;        // batch groups of a multi-group launch (gemv.hip)
 };
 
 IRON_DEV void unpack8(const uint4 v, float (&f)[8]) {

@@ -59,7 +59,7 @@ def test_gemv_rejects_bad_arguments(lib):
     # misaligned wire
     assert f(fake + 2, fake, fake, 1, 64, 128, 32, 4, 0, None) == _lib.IRON_ERR_ALIGN
     # batch > 4 -> unsupported (MFMA path)
-    assert f(fake, fake, fake, 8, 64, 128, 32, 4, 0, None) == _lib.IRON_ERR_UNSUPPORTED
+    assert f(fake, fake, fake, 5, 64, 128, 32, 4, 0, None) == _lib.IRON_ERR_UNSUPPORTED
     # unknown domain
     assert f(fake, fake, fake, 1, 64, 128, 32, 4, 7, None) == _lib.IRON_ERR_SHAPE
 

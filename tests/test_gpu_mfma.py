@@ -53,7 +53,7 @@ def _weights(M, K, G, gen):
     (6144, 4096, 32, 4, 16, "signed"),    # Qwen3-8B fused QKV, BASELINE config 5 batch
     (4096, 12288, 32, 4, 16, "signed"),   # Qwen3-8B down projection
     (6144, 2048, 32, 12, 8, "signed"),    # Qwen3-1.7B gate/up at BASELINE config 2 batch 8
-    (256, 512, 64, 16, 5, "biased"),
+    (256, 512, 64, 16, 5, "biased"),      # the smallest batch on MFMA
     (64, 128, 128, 8, 11, "signed"),
 ])
 def test_gemm_mfma(M, K, G, tile_m, B, domain):
