@@ -208,11 +208,20 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   }
 
   __shared__ double s_mx[2][4][HB];
+  // Tiles alternate between two register sets, the next tile's rows in flight while one is
+  // processed (separate named sets: a copy between them would wait for the loads). Every load is
+  // issued, rows clamped below t_lim (rows at or past t_end are masked where they are used).
+  uint4 kr2[4], vr2[4];
+  if (!p.spec && t_begin < t_end) load_kv_tile(p, c, t_begin, t_lim, kr, vr);
   int it = 0;
-  for (int t0 = t_begin; t0 < t_end; t0 += kTile, ++it) {
-    if (!(p.spec && t0 == t_begin)) load_kv_tile(p, c, t0, t_end, kr, vr);
+  for (int t0 = t_begin; t0 < t_end; t0 += 2 * kTile, it += 2) {
+    load_kv_tile(p, c, t0 + kTile, t_lim, kr2, vr2);
     attn_tile_f64<HB, FUSED>(kr, vr, t0, t_end, has_new, pos, s_new, qf, p.scale, it, m, l, o,
                              s_mx, wave, lane, row, dl);
+    if (t0 + kTile >= t_end) break;
+    load_kv_tile(p, c, t0 + 2 * kTile, t_lim, kr, vr);
+    attn_tile_f64<HB, FUSED>(kr2, vr2, t0 + kTile, t_end, has_new, pos, s_new, qf, p.scale,
+                             it + 1, m, l, o, s_mx, wave, lane, row, dl);
   }
 
   attn_finish_f64<HB>(m, l, o, wave, row, dl, [&](int oh, int od, double O, double L, double M) {

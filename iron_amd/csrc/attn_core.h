@@ -94,34 +94,85 @@ IRON_DEV void norm_rope8(const uint4 xr, const uint4 wr, const uint4 a0, const u
   }
 }
 
+// Row transpose-sum: v[0..N) in every lane of a 16-lane row (N = 4, 8 or 16); afterwards lane dl
+// holds the sum over the row's 16 lanes of v[dl % N]. log2(N) exchange steps each halve the values
+// a lane keeps (it keeps one half of its current set, sends the other to its partner and adds
+// what the partner sends: partners differ in bit 3 (row_ror:8), bit 2 (row_half_mirror, lane
+// 7 - l within each half), bit 1 (quad_perm [2,3,0,1]) and bit 0 (quad_perm [1,0,3,2]), taken
+// from bit log2(N) - 1 down), then plain sums over the remaining high bits (rotations by 4 and 8,
+// which pair lanes with the same low bits). 15 exchanged values
+// for N = 16, against 16 four-step row sums. The order of the additions differs from a row sum
+// per value; the q.k sums it serves are exact in fp64 (bf16 products), so the totals do not.
+template <int STEP_CTRL, int N>
+IRON_DEV void tsum_step(const double (&in)[N], double (&out)[N / 2], bool upper) {
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const double keep = upper ? in[N / 2 + i] : in[i];
+    const double send = upper ? in[i] : in[N / 2 + i];
+    out[i] = keep + dpp_d<STEP_CTRL>(send);
+  }
+}
+
+template <int N>
+IRON_DEV double row16_transpose_sum(const double (&v)[N], int dl) {
+  static_assert(N == 4 || N == 8 || N == 16, "4, 8 or 16 values");
+  double r;
+  if constexpr (N == 16) {
+    double a[8], b[4], c[2];
+    tsum_step<0x128, 16>(v, a, (dl & 8) != 0);
+    tsum_step<0x141, 8>(a, b, (dl & 4) != 0);
+    tsum_step<0x4e, 4>(b, c, (dl & 2) != 0);
+    double d[1];
+    tsum_step<0xb1, 2>(c, d, (dl & 1) != 0);
+    r = d[0];
+  } else if constexpr (N == 8) {
+    double b[4], c[2], d[1];
+    tsum_step<0x141, 8>(v, b, (dl & 4) != 0);
+    tsum_step<0x4e, 4>(b, c, (dl & 2) != 0);
+    tsum_step<0xb1, 2>(c, d, (dl & 1) != 0);
+    r = d[0];
+    r += dpp_d<0x128>(r);
+  } else {
+    double c[2], d[1];
+    tsum_step<0x4e, 4>(v, c, (dl & 2) != 0);
+    tsum_step<0xb1, 2>(c, d, (dl & 1) != 0);
+    r = d[0];
+    r += dpp_d<0x124>(r);  // row_ror:4, then row_ror:8: the four lanes with this dl % 4
+    r += dpp_d<0x128>(r);
+  }
+  return r;
+}
+
 // One 64-token tile of the exact (fp64) core. Lane (wave, row, dl) holds the K/V rows
 // t0 + 16u + 4 wave + row (u = 0..3), head dims 8 dl..+8; rows at or past t_end are masked and,
 // with FUSED and has_new, the row at `pos` is replaced by the current token's rows (s_new).
 // Updates the running maximum m, sum l and unnormalised output o of the HB heads; `it` is the
 // tile's index within this workgroup's sequence (0 = the first tile, which starts from zero).
 // s_mx is the workgroup's tile-maximum exchange; the function ends past its one barrier.
+// Score (u, h) of a row is reduced into lane dl = u HB + h (row16_transpose_sum), which also
+// evaluates its exponential; lane h evaluates head h's rescale factor; both are broadcast over
+// the row (row_newbcast).
 template <int HB, bool FUSED, int U = 4>
 IRON_DEV void attn_tile_f64(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, bool has_new,
                             int pos, const uint4 (&s_new)[2][16], const double (&qf)[HB][8],
                             double scale, int it, double (&m)[HB], double (&l)[HB],
                             double (&o)[HB][8], double (&s_mx)[2][4][HB], int wave, int lane,
                             int row, int dl) {
-  static_assert(U * HB <= 16, "one exponential per lane of a 16-lane row");
-  bool tv[U];
+  constexpr int N = U * HB;
+  static_assert(N == 4 || N == 8 || N == 16, "one score per lane of a 16-lane row");
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int t = t0 + u * 16 + wave * 4 + row;
-    tv[u] = t < t_end;
     if constexpr (FUSED) {
       if (has_new && t == pos) {
         kr[u] = s_new[0][dl];
         vr[u] = s_new[1][dl];
       }
     }
-    if (!tv[u]) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // rows past the context may hold NaNs
+    if (t >= t_end) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // rows past the context may hold NaNs
   }
-  // scores s[u][h], identical in every lane of the row
-  double s[U][HB];
+  // this lane's 8-dim partials of every (u, h), then the row sums, score (u, h) in lane u HB + h
+  double part[N];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     double kf[8];
@@ -131,25 +182,32 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, b
       double a = 0.0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) a = fma(qf[h][j], kf[j], a);
-      a = row16_sum_d(a) * scale;
-      s[u][h] = tv[u] ? a : -INFINITY;
+      part[u * HB + h] = a;
     }
   }
-  // workgroup-wide tile maximum per head
-  double mx[HB];
+  const int si = dl % N, sh = si % HB;
+  const bool sv = t0 + (si / HB) * 16 + wave * 4 + row < t_end;
+  double tot = row16_transpose_sum<N>(part, dl);
+  // The exchange must run with every lane of the row active: its DPP moves read partner lanes,
+  // and the compiler would otherwise sink it into the branch on sv below (sv differs between the
+  // lanes of a row), where the masked lanes' values would be read stale.
+  __asm__ volatile("" : "+v"(tot));
+  const double sc = sv ? tot * scale : -INFINITY;
+  // workgroup-wide tile maximum per head: over the U lanes of head sh in the row (lanes sh + k HB,
+  // k < U: rotations by HB, 2 HB, ... within the 16-lane row), the wavefront's rows, the waves
+  double v = sc;
+  if constexpr (HB * U >= 2 && HB < 16) {
 #pragma unroll
-  for (int h = 0; h < HB; ++h) {
-    double v = s[0][h];
-#pragma unroll
-    for (int u = 1; u < U; ++u) v = fmax(v, s[u][h]);
-    v = fmax(v, __shfl_xor(v, 16));
-    v = fmax(v, __shfl_xor(v, 32));
-    mx[h] = v;
+    for (int k = HB; k < 16; k *= 2) {
+      if (k == 1) v = fmax(v, dpp_d<0x121>(v));
+      else if (k == 2) v = fmax(v, dpp_d<0x122>(v));
+      else if (k == 4) v = fmax(v, dpp_d<0x124>(v));
+      else v = fmax(v, dpp_d<0x128>(v));
+    }
   }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < HB; ++h) s_mx[it & 1][wave][h] = mx[h];
-  }
+  v = fmax(v, __shfl_xor(v, 16));
+  v = fmax(v, __shfl_xor(v, 32));
+  if (lane < HB) s_mx[it & 1][wave][lane] = v;  // lane h < HB holds head h's maximum
   __syncthreads();
   double mn[HB];
 #pragma unroll
@@ -159,23 +217,35 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, b
     mn[h] = fmax(m[h], t);
   }
   // every tile of the loop holds at least one valid token, so mn is finite here
-  // lane dl < U*HB evaluates exponential (u, h) = (dl / HB, dl % HB)
-  double arg = -INFINITY;
+  double mn_s = mn[0], m_s = m[0];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-#pragma unroll
-    for (int h = 0; h < HB; ++h)
-      if (dl == u * HB + h) arg = s[u][h] - mn[h];
-  const double ev = arg == -INFINITY ? 0.0 : exp(arg);
+  for (int h = 1; h < HB; ++h)
+    if (sh == h) {
+      mn_s = mn[h];
+      m_s = m[h];
+    }
+  const double ev = sc == -INFINITY ? 0.0 : exp(sc - mn_s);
   double pe[U][HB];
   share_all<HB, U>(ev, pe, std::make_integer_sequence<int, 16>{});
-  if (it > 0) {  // rescale the running sums (the first tile starts from zero)
+  // rescale the running sums (the first tile starts from zero): lane h has head h's factor.
+  // Skipped when no maximum moved (every factor would be e^0 = 1 exactly); workgroup-uniform.
+  bool moved = false;
+#pragma unroll
+  for (int h = 0; h < HB; ++h) moved = moved || mn[h] != m[h];
+  if (it > 0 && moved) {
+    const double cf = m_s == -INFINITY ? 0.0 : exp(m_s - mn_s);
+    double c[HB];
+    if constexpr (HB == 1) c[0] = row_share_d<0>(cf);
+    else if constexpr (HB == 2) { c[0] = row_share_d<0>(cf); c[1] = row_share_d<1>(cf); }
+    else {
+      c[0] = row_share_d<0>(cf); c[1] = row_share_d<1>(cf);
+      c[2] = row_share_d<2>(cf); c[3] = row_share_d<3>(cf);
+    }
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
-      const double c = m[h] == -INFINITY ? 0.0 : exp(m[h] - mn[h]);
-      l[h] *= c;
+      l[h] *= c[h];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[h][j] *= c;
+      for (int j = 0; j < 8; ++j) o[h][j] *= c[h];
     }
   }
 #pragma unroll
