@@ -13,13 +13,16 @@
 // their producers), three MFMAs per step. The result is within the fp32 rounding of the per-group sums of the exact value (the
 // parity bar is the north star's rel/abs 1e-2; measured errors are a few fp32 ulps).
 //
-// Mapping: a workgroup (4 wavefronts) owns 64 rows x 16 batch columns over a K range (split-K
-// when the row tiles alone do not cover the chip). Per 128-wide K step the workgroup stages the
-// weight tile (64 rows x 128 int8 per matrix), its group scales and x (16 x 128, bf16 planes) in LDS
-// (double buffered: the next step's global loads are in flight while this one computes).
-// Wavefront w multiplies rows 16w..16w+15: lane l reads A = 8 int8 of row l%16 at k = (l/16)*8
-// and B = 8 bf16 of batch column l%16 at the same k; its 4 accumulators are rows (l/16)*4 + i,
-// column l%16 (the gfx950 16x16x32 operand layout, checked on the device).
+// Mapping: a workgroup (8 wavefronts, two per SIMD) owns 64 rows x 16 batch columns over a K range
+// (split-K when the row tiles alone do not cover the chip). Per 128-wide K step the workgroup
+// stages the weight tile (64 rows x 128 int8 per matrix), its group scales and x (16 x 128, bf16
+// planes) in LDS (double buffered: the next step's global loads are in flight while this one
+// computes). Wavefront w multiplies rows 16 (w % 4) .. +15 over the step's 64-wide half w / 4:
+// lane l reads A = 8 int8 of row l%16 at k = (l/16)*8 and B = 8 bf16 of batch column l%16 at the
+// same k; its 4 accumulators are rows (l/16)*4 + i, column l%16 (the gfx950 16x16x32 operand
+// layout, checked on the device). The two halves' fp64 sums add through LDS at the end. With one
+// wavefront per SIMD every step waited out its own LDS -> convert -> MFMA -> scale chain (about
+// 1.6 us a step); the second wavefront per SIMD overlaps them.
 #include "common.h"
 #include "internal.h"
 
@@ -102,14 +105,16 @@ IRON_DEV bf16x8 q8_to_bf16(uint32_t lo, uint32_t hi, uint32_t xm) {
 }
 
 template <bool DUAL, bool XPL>
-__global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
+__global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
   constexpr int NM = DUAL ? 2 : 1;
   constexpr int NX = XPL ? 3 : 1;    // bf16 planes of x (fp32 x: hi, mid, lo)
   __shared__ __align__(16) uint8_t s_w[2][NM][kTM][kWRow];
   __shared__ __align__(16) uint16_t s_s[2][NM][kTM][kKS / 32];
   __shared__ __align__(16) uint16_t s_x[2][NX][kBN][kXRow];
+  __shared__ __align__(16) double s_acc[4][NM][4][64];  // the upper half's sums (end)
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int half = wave >> 2;  // the 64-wide half of every step this wavefront multiplies
   const int row0 = blockIdx.x * kTM;
   const int split = blockIdx.y;
   const int step0 = split * p.ksteps;
@@ -118,7 +123,7 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
   const int G = 1 << p.gshift;
 
   // ---- global -> register staging of one pipeline step
-  const int lrow = tid >> 2, lpart = tid & 3;  // weight tile: row, 32-byte quarter
+  const int lrow = tid >> 3, lpart = tid & 7;  // weight tile: row, 16-byte eighth
   const uint8_t* wbase[NM];
   const uint16_t* sbase[NM];
   {
@@ -132,10 +137,11 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
       sbase[mi] = (const uint16_t*)(base + (size_t)p.tile_m * p.K) + (size_t)in * ng;
     }
   }
-  const int xb = tid >> 4, xk = (tid & 15) * 8;  // x tile: batch row, 8-element chunk
-  // registers of one pipeline step: the weight quarter-rows of matrix 0 (and 1), their
+  // x tile: batch row, 8-element chunk (wavefronts 4..7 load the same x as 0..3 and store none)
+  const int xb = (tid >> 4) & 15, xk = (tid & 15) * 8;
+  // registers of one pipeline step: the weight eighth-rows of matrix 0 (and 1), their
   // scales, and 8 x values of each plane
-  uint4 wa0, wa1, wb0, wb1, rx0, rx1, rx2;
+  uint4 wa0, wb0, rx0, rx1, rx2;
   uint32_t sa, sb;
   const int gpr = kKS / G;  // groups per step (G <= kKS)
   const uint8_t* wsrc0 = wbase[0];
@@ -147,14 +153,10 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
   do {                                                                                         \
     const int k0_ = (step_) * kKS;                                                             \
     const int gi_ = (k0_ >> p.gshift) + (lpart < gpr ? lpart : 0);                             \
-    const uint4* s0_ = (const uint4*)(wsrc0 + k0_ + lpart * 32);                               \
-    wa0 = s0_[0];                                                                              \
-    wa1 = s0_[1];                                                                              \
+    wa0 = *(const uint4*)(wsrc0 + k0_ + lpart * 16);                                           \
     sa = ssrc0[gi_];                                                                           \
     if (DUAL) {                                                                                \
-      const uint4* s1_ = (const uint4*)(wsrc1 + k0_ + lpart * 32);                             \
-      wb0 = s1_[0];                                                                            \
-      wb1 = s1_[1];                                                                            \
+      wb0 = *(const uint4*)(wsrc1 + k0_ + lpart * 16);                                         \
       sb = ssrc1[gi_];                                                                         \
     }                                                                                          \
     rx0 = *(const uint4*)(p.x + xrow + k0_ + xk);                                              \
@@ -165,20 +167,18 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
   } while (0)
 #define GEMM_LSTORE(buf_)                                                                      \
   do {                                                                                         \
-    uint4* d0_ = (uint4*)&s_w[(buf_)][0][lrow][lpart * 32];                                    \
-    d0_[0] = wa0;                                                                              \
-    d0_[1] = wa1;                                                                              \
+    *(uint4*)&s_w[(buf_)][0][lrow][lpart * 16] = wa0;                                          \
     if (lpart < kKS / 32) s_s[(buf_)][0][lrow][lpart] = (uint16_t)sa;                          \
     if (DUAL) {                                                                                \
-      uint4* d1_ = (uint4*)&s_w[(buf_)][NM - 1][lrow][lpart * 32];                             \
-      d1_[0] = wb0;                                                                            \
-      d1_[1] = wb1;                                                                            \
+      *(uint4*)&s_w[(buf_)][NM - 1][lrow][lpart * 16] = wb0;                                   \
       if (lpart < kKS / 32) s_s[(buf_)][NM - 1][lrow][lpart] = (uint16_t)sb;                   \
     }                                                                                          \
-    *(uint4*)&s_x[(buf_)][0][xb][xk] = xb < p.B ? rx0 : make_uint4(0u, 0u, 0u, 0u);            \
-    if (XPL) {                                                                                 \
-      *(uint4*)&s_x[(buf_)][NX - 2][xb][xk] = xb < p.B ? rx1 : make_uint4(0u, 0u, 0u, 0u);     \
-      *(uint4*)&s_x[(buf_)][NX - 1][xb][xk] = xb < p.B ? rx2 : make_uint4(0u, 0u, 0u, 0u);     \
+    if (tid < 256) {                                                                           \
+      *(uint4*)&s_x[(buf_)][0][xb][xk] = xb < p.B ? rx0 : make_uint4(0u, 0u, 0u, 0u);          \
+      if (XPL) {                                                                               \
+        *(uint4*)&s_x[(buf_)][NX - 2][xb][xk] = xb < p.B ? rx1 : make_uint4(0u, 0u, 0u, 0u);   \
+        *(uint4*)&s_x[(buf_)][NX - 1][xb][xk] = xb < p.B ? rx2 : make_uint4(0u, 0u, 0u, 0u);   \
+      }                                                                                        \
     }                                                                                          \
   } while (0)
 
@@ -191,10 +191,11 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
   f32x4 c[NM];
 #pragma unroll
   for (int mi = 0; mi < NM; ++mi) c[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int arow = wave * 16 + (lane & 15);      // A operand row (tile-relative)
+  const int wrow = (wave & 3) * 16;              // this wavefront's 16 rows (tile-relative)
+  const int arow = wrow + (lane & 15);           // A operand row
   const int kq = (lane >> 4) * 8;                // k offset of this lane in a 32-step
   const int bcol = lane & 15;                    // B operand / C column (batch)
-  const int crow = wave * 16 + (lane >> 4) * 4;  // first C row (tile-relative)
+  const int crow = wrow + (lane >> 4) * 4;       // first C row
 
   GEMM_GLOAD(step0);
   GEMM_LSTORE(0);
@@ -203,8 +204,11 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
     const int buf = it & 1;
     if (it + 1 < nsteps) GEMM_GLOAD(step0 + it + 1);
     const int k0 = (step0 + it) * kKS;
+    // this wavefront's two 32-wide steps: the group sums are flushed at every group end and at the
+    // end of the half (a group longer than 64 continues in the other half's wavefront)
 #pragma unroll
-    for (int j = 0; j < kKS / 32; ++j) {
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * half + jj;
       bf16x8 bx[NX];
 #pragma unroll
       for (int xi = 0; xi < NX; ++xi)
@@ -217,7 +221,7 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
         for (int xi = 0; xi < NX; ++xi)
           c[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bx[xi], c[mi], 0, 0, 0);
       }
-      if (((k0 + 32 * (j + 1)) & (G - 1)) == 0) {  // end of a quantization group
+      if (jj == 1 || ((k0 + 32 * (j + 1)) & (G - 1)) == 0) {  // end of a group or of the half
         const int gl = (32 * j) >> p.gshift;        // group index within this step
 #pragma unroll
         for (int mi = 0; mi < NM; ++mi) {
@@ -236,7 +240,19 @@ __global__ __launch_bounds__(256) void gemm_w8_mfma_kernel(GemmParams p) {
 
 #undef GEMM_GLOAD
 #undef GEMM_LSTORE
-  // ---- write
+  // ---- the upper half's sums join the lower half's (in that order), then the write
+  if (half) {
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_acc[wave & 3][mi][i][lane] = acc[mi][i];
+  }
+  __syncthreads();
+  if (half) return;
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[mi][i] += s_acc[wave][mi][i][lane];
   if (bcol >= p.B) return;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -345,11 +361,11 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
   }
   dim3 grid(M / kTM, pl.splits);
   if (dual) {
-    if (x_f32) hipLaunchKernelGGL((gemm_w8_mfma_kernel<true, true>), grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((gemm_w8_mfma_kernel<true, false>), grid, dim3(256), 0, stream, p);
+    if (x_f32) hipLaunchKernelGGL((gemm_w8_mfma_kernel<true, true>), grid, dim3(512), 0, stream, p);
+    else hipLaunchKernelGGL((gemm_w8_mfma_kernel<true, false>), grid, dim3(512), 0, stream, p);
   } else {
-    if (x_f32) hipLaunchKernelGGL((gemm_w8_mfma_kernel<false, true>), grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((gemm_w8_mfma_kernel<false, false>), grid, dim3(256), 0, stream, p);
+    if (x_f32) hipLaunchKernelGGL((gemm_w8_mfma_kernel<false, true>), grid, dim3(512), 0, stream, p);
+    else hipLaunchKernelGGL((gemm_w8_mfma_kernel<false, false>), grid, dim3(512), 0, stream, p);
   }
   st = check_launch(fn);
   if (st || pl.splits == 1) return st;
