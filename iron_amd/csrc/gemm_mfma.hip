@@ -8,10 +8,10 @@
 //
 // Arithmetic: q is exact in bf16 (|q| <= 127), so one v_mfma_f32_16x16x32_bf16 per 32-wide k
 // step multiplies q by x exactly and sums 32 products in fp32; at the end of each quantization
-// group the fp32 partial is scaled by s (in fp64) and added to an fp64 accumulator. fp32 inputs
-// (the MLP's hf and gh) arrive as their three exact bf16 planes (hi + mid + lo, written so by
-// their producers), three MFMAs per step. The result is within the fp32 rounding of the per-group sums of the exact value (the
-// parity bar is the north star's rel/abs 1e-2; measured errors are a few fp32 ulps).
+// group the fp32 partial is scaled by s (in fp64) and added to an fp64 accumulator. fp32 inputs (the MLP's hf and gh) arrive as their three exact bf16 planes (hi +
+// mid + lo, written so by their producers), three MFMAs per step. The result is within the fp32
+// rounding of the per-group sums of the exact value (the parity bar is the north star's rel/abs
+// 1e-2, and every output within one bf16 ulp of exact).
 //
 // Mapping: a workgroup (8 wavefronts, two per SIMD) owns 64 rows x 16 batch columns over a K range
 // (split-K when the row tiles alone do not cover the chip). Per 128-wide K step the workgroup
@@ -89,19 +89,19 @@ IRON_DEV void store_out(const GemmParams& p, int b, int m, double a0, double a1)
   }
 }
 
-// 8 int8 (two dwords, signed after the domain xor) -> 8 bf16 (exact)
-IRON_DEV bf16x8 q8_to_bf16(uint32_t lo, uint32_t hi, uint32_t xm) {
-  lo ^= xm;
-  hi ^= xm;
-  bf16x8 r;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float f0 = (float)(int)(((int32_t)(lo << (24 - 8 * j))) >> 24);
-    const float f1 = (float)(int)(((int32_t)(hi << (24 - 8 * j))) >> 24);
-    r[j] = __builtin_bit_cast(__bf16, (uint16_t)(__float_as_uint(f0) >> 16));
-    r[4 + j] = __builtin_bit_cast(__bf16, (uint16_t)(__float_as_uint(f1) >> 16));
-  }
-  return r;
+// 8 int8 weights as biased bytes u = q + 128 (two dwords) -> 8 bf16 of q (exact: |q| <= 128 has
+// at most 8 significant bits, so the high half of f32(q) is its bf16). f32(u) is one
+// v_cvt_f32_ubyte per byte, f32(u) - 128 = f32(q) exactly, and one v_perm_b32 packs two high
+// halves: 20 VALU instructions for 8 weights where a sign extension, convert and shift per byte
+// took 28.
+IRON_DEV bf16x8 u8_to_bf16q(uint32_t lo, uint32_t hi) {
+  auto two = [](uint32_t d, int sh) {
+    const float f0 = (float)((d >> sh) & 0xffu) - 128.f;
+    const float f1 = (float)((d >> (sh + 8)) & 0xffu) - 128.f;
+    return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+  };
+  const uint4 r = make_uint4(two(lo, 0), two(lo, 16), two(hi, 0), two(hi, 16));
+  return __builtin_bit_cast(bf16x8, r);
 }
 
 template <bool DUAL, bool XPL>
@@ -191,6 +191,7 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
   f32x4 c[NM];
 #pragma unroll
   for (int mi = 0; mi < NM; ++mi) c[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t to_u = p.xor_mask ^ 0x80808080u;  // stored bytes -> q + 128
   const int wrow = (wave & 3) * 16;              // this wavefront's 16 rows (tile-relative)
   const int arow = wrow + (lane & 15);           // A operand row
   const int kq = (lane >> 4) * 8;                // k offset of this lane in a 32-step
@@ -216,11 +217,12 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) {
         const uint2 qa = *(const uint2*)&s_w[buf][mi][arow][32 * j + kq];
-        const bf16x8 a = q8_to_bf16(qa.x, qa.y, p.xor_mask);
+        const bf16x8 a = u8_to_bf16q(qa.x ^ to_u, qa.y ^ to_u);
 #pragma unroll
         for (int xi = 0; xi < NX; ++xi)
           c[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bx[xi], c[mi], 0, 0, 0);
       }
+
       if (jj == 1 || ((k0 + 32 * (j + 1)) & (G - 1)) == 0) {  // end of a group or of the half
         const int gl = (32 * j) >> p.gshift;        // group index within this step
 #pragma unroll
@@ -282,10 +284,21 @@ struct GemmPlan {
   int splits, ksteps;
 };
 
+// Split K until about 512 workgroups cover the chip (two per CU), keeping at least kMinSteps
+// pipeline steps per split: measured per shape at B=16, 6144x4096 20.3 -> 17.0 us and 4096x12288
+// 28.8 -> 24.4 us against one workgroup per CU, while 2048x6144 (48 steps) was best at 8 splits
+// of 6 steps (16 splits of 3: 14.9 against 13.1 us).
+constexpr int kSplitTarget = 512;
+constexpr int kMinSteps = 6;
 GemmPlan plan_gemm(int M, int K) {
   const int tiles = M / kTM;
   const int steps = K / kKS;
-  int splits = (256 + tiles - 1) / tiles;  // about one workgroup per CU
+  int splits = (kSplitTarget + tiles - 1) / tiles;
+  const int by_steps = steps / kMinSteps > 1 ? steps / kMinSteps : 1;
+  if (splits > by_steps) splits = by_steps;
+  // never fewer workgroups than one per CU would give (short K: 4096x1024 keeps 4 splits)
+  const int per_cu = (256 + tiles - 1) / tiles;
+  if (splits < per_cu) splits = per_cu;
   if (splits > steps) splits = steps;
   while (splits > 1 && steps % splits) --splits;
   return {splits, steps / splits};
@@ -301,10 +314,10 @@ size_t gemm_workspace_bytes(int M, int K, bool dual) {
   return (size_t)(dual ? 2 : 1) * pl.splits * kBN * M * sizeof(double);
 }
 
-// An upper bound over every K (the split count never exceeds ceil(256 / (M / 64))).
+// An upper bound over every K (the split count never exceeds ceil(kSplitTarget / (M / 64))).
 size_t gemm_workspace_bound(int M, bool dual) {
   if (M <= 0 || M % kTM) return 0;
-  const size_t splits = (256 + M / kTM - 1) / (M / kTM);
+  const size_t splits = (kSplitTarget + M / kTM - 1) / (M / kTM);
   return ((size_t)(dual ? 2 : 1) * splits * kBN * M * sizeof(double) + 255) & ~(size_t)255;
 }
 
