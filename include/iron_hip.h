@@ -4,6 +4,11 @@
  * launches HIP kernels on `stream` (a hipStream_t passed as void*, NULL = the null stream) and
  * returns. Device memory is always owned by the caller; the library never allocates. Entry points
  * that need scratch memory take a caller-provided workspace and export a size query.
+ * Workspaces are zero-filled once before their first use. The entry points that can run the
+ * batched MFMA GEMM (iron_gemm_w8a16, iron_qkv_head, iron_qkv_attn, iron_swiglu_mlp) keep its
+ * split-K arrival counters in the first 16 KiB of their workspace, for every batch size, and
+ * leave them zero after each call; a workspace serves one of these entry points (any B), and
+ * calls on one workspace are stream-ordered.
  *
  * Return value: IRON_OK (0) or a negative iron_status; iron_last_error() then returns a
  * thread-local message. Validation errors (IRON_ERR_NULL/SHAPE/ALIGN/WORKSPACE/UNSUPPORTED) are
@@ -25,7 +30,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 7
+#define IRON_ABI_VERSION 8
 
 enum iron_status {
   IRON_OK = 0,

@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
-ABI_VERSION = 7          # IRON_ABI_VERSION of include/iron_hip.h
+ABI_VERSION = 8          # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2

@@ -1008,7 +1008,7 @@ int iron_qkv_attn(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
   if (!iron::aligned(workspace, 256))
     return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
   hipStream_t s = (hipStream_t)stream;
-  uint16_t* raw = (uint16_t*)workspace;
+  uint16_t* raw = iron::qkv_raw_of(workspace);
   const size_t raw_bytes = iron::qkv_raw_bytes(B, D, M);
   st = iron::qkv_raw_internal(wqkv, cur, n_in, workspace, raw_bytes, B, M, D, G, tile_m, domain,
                               eps, s, fn);

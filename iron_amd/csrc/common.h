@@ -16,6 +16,13 @@
 
 #define IRON_DEV __device__ __forceinline__
 
+// s_waitcnt immediate: vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding)
+constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);
+// Buffer resource word 3 for raw (stride 0) buffers on CDNA: 32-bit data format, no swizzle.
+constexpr int kBufferDword3 = 0x00020000;
+// Cache-policy operand of the buffer builtins: sc1 (device scope: the load misses this XCD's L2).
+constexpr int kCpolSc1 = 16;
+
 // ---------------------------------------------------------------------------------------------
 // bf16 <-> fp32
 // ---------------------------------------------------------------------------------------------

@@ -52,8 +52,6 @@ constexpr int kNT = 256;                     // workgroups (one per CU of an MI3
 constexpr int kPhases = 7;                   // tag slots per layer: six phases + the input row
 constexpr int kMaxLayers = 128;              // tag slots per launch: kPhases * kMaxLayers
 constexpr long long kSpinLimit = 1ll << 18;  // polls of one word before a wait fails (~0.3 s)
-// s_waitcnt immediate: vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding)
-constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);
 
 constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 

@@ -51,6 +51,7 @@ struct GemmParams {
   int B, x_stride;
   int splits, ksteps;     // split s covers pipeline steps [s*ksteps, (s+1)*ksteps)
   double* part;           // [2][splits][kBN][M] fp64 partials (splits > 1)
+  unsigned int* ctr;      // [M / kTM] arrival counts of the splits (splits > 1; zero between calls)
   int epi;
   void* y;
   int y_stride;
@@ -250,34 +251,66 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
       for (int i = 0; i < 4; ++i) s_acc[wave & 3][mi][i][lane] = acc[mi][i];
   }
   __syncthreads();
-  if (half) return;
+  if (!half) {
 #pragma unroll
-  for (int mi = 0; mi < NM; ++mi)
+    for (int mi = 0; mi < NM; ++mi)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[mi][i] += s_acc[wave][mi][i][lane];
-  if (bcol >= p.B) return;
+      for (int i = 0; i < 4; ++i) acc[mi][i] += s_acc[wave][mi][i][lane];
+  }
+  if (p.splits == 1) {
+    if (!half && bcol < p.B) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = row0 + crow + i;
-    if (p.splits == 1) {
-      store_out(p, bcol, m, acc[0][i], NM > 1 ? acc[NM - 1][i] : 0.0);
-    } else {
+      for (int i = 0; i < 4; ++i)
+        store_out(p, bcol, row0 + crow + i, acc[0][i], NM > 1 ? acc[NM - 1][i] : 0.0);
+    }
+    return;
+  }
+  // Split K: this split's fp64 partials go to memory (agent-scope stores write through the L2),
+  // and the last split of the row tile to arrive (one atomic count per tile) sums them in split
+  // order -- the order a separate reduce kernel used -- and applies the epilogue, then clears
+  // the count for the next call. Every thread's stores are complete before the count.
+  if (!half && bcol < p.B) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = row0 + crow + i;
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi)
-        p.part[(((size_t)mi * p.splits + split) * kBN + bcol) * p.M + m] = acc[mi][i];
+        __hip_atomic_store(p.part + (((size_t)mi * p.splits + split) * kBN + bcol) * p.M + m,
+                           acc[mi][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-}
-
-// Split-K reduction in split order, then the epilogue. grid (M / 256, B), 256 threads.
-__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmParams p, int dual) {
-  const int m = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
-  if (m >= p.M) return;
-  double a[2] = {0.0, 0.0};
-  for (int mi = 0; mi <= dual; ++mi)
-    for (int s = 0; s < p.splits; ++s)
-      a[mi] += p.part[(((size_t)mi * p.splits + s) * kBN + b) * p.M + m];
-  store_out(p, b, m, a[0], a[1]);
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  __shared__ unsigned int s_last;
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(p.ctr + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == (unsigned int)(p.splits - 1);
+  __syncthreads();
+  if (!s_last) return;
+  // The partials are read past this XCD's L2 (which may hold lines of an earlier call) with
+  // device-scope (sc1) buffer loads, eight in flight per thread; the sum runs in split order.
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      p.part, 0, NM * p.splits * kBN * p.M * (int)sizeof(double), kBufferDword3);
+  for (int t = tid; t < kTM * p.B; t += 512) {
+    const int b = t / kTM, m = row0 + t % kTM;
+    double a[2] = {0.0, 0.0};
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+      for (int s0 = 0; s0 < p.splits; s0 += 8) {
+        double v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int sp = s0 + j < p.splits ? s0 + j : p.splits - 1;
+          v[j] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(
+              rs, (((mi * p.splits + sp) * kBN + b) * p.M + m) * (int)sizeof(double), 0, kCpolSc1));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (s0 + j < p.splits) a[mi] += v[j];
+      }
+    store_out(p, b, m, a[0], a[1]);
+  }
+  if (tid == 0) __hip_atomic_store(p.ctr + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct GemmPlan {
@@ -308,6 +341,9 @@ GemmPlan plan_gemm(int M, int K) {
 
 namespace iron {
 
+constexpr int kMaxTiles = (int)(kGemmCtrBytes / sizeof(unsigned int));  // M <= 262144
+
+// Bytes of fp64 split-K partials (none without a split).
 size_t gemm_workspace_bytes(int M, int K, bool dual) {
   const GemmPlan pl = plan_gemm(M, K);
   if (pl.splits == 1) return 0;
@@ -326,6 +362,8 @@ int gemm_check(const char* fn, int B, int M, int K, int G) {
   if (B < 1 || B > kBN)
     return fail(IRON_ERR_UNSUPPORTED, "%s: MFMA batch %d outside [1, %d]", fn, B, kBN);
   if (M % kTM) return fail(IRON_ERR_UNSUPPORTED, "%s: M=%d not a multiple of %d", fn, M, kTM);
+  if (M / kTM > kMaxTiles)
+    return fail(IRON_ERR_UNSUPPORTED, "%s: M=%d above %d on the MFMA path", fn, M, kMaxTiles * kTM);
   if (K % kKS) return fail(IRON_ERR_UNSUPPORTED, "%s: K=%d not a multiple of %d", fn, K, kKS);
   if (G < 32 || G > kKS)
     return fail(IRON_ERR_UNSUPPORTED, "%s: group size %d outside [32, %d] on the MFMA path", fn,
@@ -336,7 +374,8 @@ int gemm_check(const char* fn, int B, int M, int K, int G) {
 int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile_m, int domain,
                    const uint16_t* x, size_t x_plane, int B, int x_stride, int epi, void* y,
                    int y_stride, size_t y_plane, const uint16_t* r1, const uint16_t* r2,
-                   int r_stride, void* ws, size_t ws_bytes, hipStream_t stream, const char* fn) {
+                   int r_stride, unsigned int* ctr, void* part, size_t part_bytes,
+                   hipStream_t stream, const char* fn) {
   int st = gemm_check(fn, B, M, K, G);
   if (st) return st;
   const bool dual = w1 != nullptr;
@@ -367,10 +406,12 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
   p.r_stride = r_stride;
   if (pl.splits > 1) {
     const size_t need = gemm_workspace_bytes(M, K, dual);
-    if (!ws || ws_bytes < need)
-      return fail(IRON_ERR_WORKSPACE, "%s: MFMA workspace %zu < %zu bytes", fn, ws_bytes, need);
-    if (!aligned(ws, 256)) return fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
-    p.part = (double*)ws;
+    if (!part || !ctr || part_bytes < need)
+      return fail(IRON_ERR_WORKSPACE, "%s: MFMA partials %zu < %zu bytes", fn, part_bytes, need);
+    if (!aligned(part, 256) || !aligned(ctr, 256))
+      return fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
+    p.part = (double*)part;
+    p.ctr = ctr;
   }
   dim3 grid(M / kTM, pl.splits);
   if (dual) {
@@ -380,10 +421,6 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
     if (x_f32) hipLaunchKernelGGL((gemm_w8_mfma_kernel<false, true>), grid, dim3(512), 0, stream, p);
     else hipLaunchKernelGGL((gemm_w8_mfma_kernel<false, false>), grid, dim3(512), 0, stream, p);
   }
-  st = check_launch(fn);
-  if (st || pl.splits == 1) return st;
-  hipLaunchKernelGGL(gemm_reduce_kernel, dim3((M + 255) / 256, B), dim3(256), 0, stream, p,
-                     dual ? 1 : 0);
   return check_launch(fn);
 }
 
@@ -396,7 +433,7 @@ size_t iron_gemm_w8a16_workspace(int B, int M, int K, int G) {
   (void)G;
   if (M <= 0 || K <= 0 || M % kTM || K % kKS) return 0;
   const size_t n = iron::gemm_workspace_bytes(M, K, false);
-  return n ? n : 256;
+  return n ? iron::kGemmCtrBytes + n : 256;
 }
 
 int iron_gemm_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int M, int K, int G,
@@ -408,9 +445,11 @@ int iron_gemm_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int
   int st = iron::check_wire(fn, wire, M, K, G, tile_m, domain);
   if (st) return st;
   if (!iron::aligned(x, 16)) return iron::fail(IRON_ERR_ALIGN, "%s: x not 16-byte aligned", fn);
+  const size_t ctr = workspace_bytes >= iron::kGemmCtrBytes ? iron::kGemmCtrBytes : 0;
   return iron::gemm_w8_launch(wire, nullptr, M, K, G, tile_m, domain, x, 0, B, K,
-                              iron::GEMM_EPI_BF16, y, M, 0, nullptr, nullptr, 0, workspace,
-                              workspace_bytes, (hipStream_t)stream, fn);
+                              iron::GEMM_EPI_BF16, y, M, 0, nullptr, nullptr, 0,
+                              (unsigned int*)workspace, workspace ? (char*)workspace + ctr : nullptr,
+                              workspace_bytes - ctr, (hipStream_t)stream, fn);
 }
 
 }  // extern "C"

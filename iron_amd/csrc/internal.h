@@ -58,6 +58,11 @@ constexpr int kGemmMaxBatch = 16;
 // bf16(f32(r1 + r2) + acc).
 enum : int { GEMM_EPI_BF16 = 0, GEMM_EPI_SWIGLU_PLANES = 1, GEMM_EPI_RES_BF16 = 2 };
 int gemm_check(const char* fn, int B, int M, int K, int G);
+// The split-K arrival counters of the MFMA GEMM: a block at offset 0 of the workspace of every
+// entry point that can run that GEMM (whatever B, so one workspace serves every batch size).
+// The block is zero before the first call, and every call leaves it zero.
+constexpr size_t kGemmCtrBytes = 16384;
+// Bytes of fp64 split-K partials a GEMM of M rows needs, over every K.
 size_t gemm_workspace_bound(int M, bool dual);
 // x: bf16 [B][x_stride], or (x_plane > 0) an fp32 activation as three exact bf16 planes
 // [3][B][x_stride] with plane stride x_plane elements. y_plane: the plane stride of the planes
@@ -65,11 +70,14 @@ size_t gemm_workspace_bound(int M, bool dual);
 int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile_m, int domain,
                    const uint16_t* x, size_t x_plane, int B, int x_stride, int epi, void* y,
                    int y_stride, size_t y_plane, const uint16_t* r1, const uint16_t* r2,
-                   int r_stride, void* ws, size_t ws_bytes, hipStream_t stream, const char* fn);
+                   int r_stride, unsigned int* ctr, void* part, size_t part_bytes,
+                   hipStream_t stream, const char* fn);
 
 
 // The raw-QKV stage shared by the QKV head and the fused QKV head + attention (qkv.hip).
 size_t qkv_raw_bytes(int B, int D, int M);
+// raw (bf16 [B][M]) sits after the GEMM counters at the front of the stage's workspace.
+inline uint16_t* qkv_raw_of(void* ws) { return (uint16_t*)((char*)ws + kGemmCtrBytes); }
 int qkv_raw_internal(const void* wqkv, const uint16_t* cur, const uint16_t* n_in, void* ws,
                      size_t ws_bytes, int B, int M, int D, int G, int tile_m, int domain,
                      float eps, hipStream_t s, const char* fn);

@@ -27,17 +27,19 @@ extern "C" {
 
 static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Layout, B <= 4: gh (fp32 [B][FF]) | a (bf16 [B][D]).
-// B > 4 (MFMA): gh (three bf16 planes [3][B][FF] of the fp32 values) | a (bf16 [B][D]) |
-// hf (planes [3][B][D]) | the split-K partials (shared by the GEMMs, which run in sequence).
+// Layout: the GEMM's split-K counters (kGemmCtrBytes, for every B), then for B <= 4:
+// gh (fp32 [B][FF]) | a (bf16 [B][D]); for B > 4 (MFMA): gh (three bf16 planes [3][B][FF] of
+// the fp32 values) | a (bf16 [B][D]) | hf (planes [3][B][D]) | the split-K partials (shared by
+// the GEMMs, which run in sequence).
 size_t iron_swiglu_mlp_workspace(int B, int D, int FF) {
   if (B <= 0 || D <= 0 || FF <= 0) return 0;
   if (B <= iron::kGemvMaxBatch)
-    return round256((size_t)B * FF * sizeof(float)) + round256((size_t)B * D * 2);
+    return iron::kGemmCtrBytes + round256((size_t)B * FF * sizeof(float)) +
+           round256((size_t)B * D * 2);
   size_t part = iron::gemm_workspace_bound(FF, true);
   const size_t pd = iron::gemm_workspace_bound(D, false);
   part = part > pd ? part : pd;
-  return round256((size_t)3 * B * FF * 2) + round256((size_t)B * D * 2) +
+  return iron::kGemmCtrBytes + round256((size_t)3 * B * FF * 2) + round256((size_t)B * D * 2) +
          round256((size_t)3 * B * D * 2) + part;
 }
 
@@ -73,13 +75,15 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
   if (!iron::aligned(workspace, 256))
     return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
   hipStream_t s = (hipStream_t)stream;
+  unsigned int* ctr = (unsigned int*)workspace;
+  char* const base = (char*)workspace + iron::kGemmCtrBytes;
+  workspace_bytes -= iron::kGemmCtrBytes;
   if (B > iron::kGemvMaxBatch) {
     // MFMA path: the prologue (x1 = cur + a, hf = RMSNorm(x1) * n_pf in fp32) runs once per
     // row in its own kernel, then three GEMMs with the SwiGLU / residual epilogues
     if ((st = iron::gemm_check(fn, B, FF, D, G)) || (st = iron::gemm_check(fn, B, D, FF, G)))
       return st;
     if (wo && (st = iron::gemm_check(fn, B, D, QD, G))) return st;
-    char* base = (char*)workspace;
     uint16_t* gh = (uint16_t*)base;
     uint16_t* a_buf = (uint16_t*)(base + round256((size_t)3 * B * FF * 2));
     uint16_t* hf = (uint16_t*)((char*)a_buf + round256((size_t)B * D * 2));
@@ -89,7 +93,7 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
     if (wo) {
       uint16_t* dst = a_out ? a_out : a_buf;
       st = iron::gemm_w8_launch(wo, nullptr, D, QD, G, tile_m_o, domain, cx_or_a, 0, B, QD,
-                                iron::GEMM_EPI_BF16, dst, D, 0, nullptr, nullptr, 0, part,
+                                iron::GEMM_EPI_BF16, dst, D, 0, nullptr, nullptr, 0, ctr, part,
                                 part_bytes, s, fn);
       if (st) return st;
       a = dst;
@@ -98,17 +102,17 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
     if (st) return st;
     st = iron::gemm_w8_launch(wg, wu, FF, D, G, tile_m_gu, domain, hf, (size_t)B * D, B, D,
                               iron::GEMM_EPI_SWIGLU_PLANES, gh, FF, (size_t)B * FF, nullptr,
-                              nullptr, 0, part, part_bytes, s, fn);
+                              nullptr, 0, ctr, part, part_bytes, s, fn);
     if (st) return st;
     return iron::gemm_w8_launch(wd, nullptr, D, FF, G, tile_m_d, domain, gh, (size_t)B * FF, B,
-                                FF, iron::GEMM_EPI_RES_BF16, nxt, D, 0, cur, a, D, part,
+                                FF, iron::GEMM_EPI_RES_BF16, nxt, D, 0, cur, a, D, ctr, part,
                                 part_bytes, s, fn);
   }
-  float* gh = (float*)workspace;
+  float* gh = (float*)base;
   const size_t gh_bytes = round256((size_t)B * FF * sizeof(float));
   const uint16_t* a = cx_or_a;
   if (wo) {
-    uint16_t* a_buf = a_out ? a_out : (uint16_t*)((char*)workspace + gh_bytes);
+    uint16_t* a_buf = a_out ? a_out : (uint16_t*)(base + gh_bytes);
     st = iron_gemv_w8a16(wo, cx_or_a, a_buf, B, D, QD, G, tile_m_o, domain, stream);
     if (st) return st;
     a = a_buf;

@@ -83,10 +83,10 @@ namespace iron {
 
 static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Bytes of the raw-QKV stage: raw (bf16 [B][M]), and for B > 4 the normalised input (bf16
-// [B][D]) and the MFMA split-K partials.
+// Bytes of the raw-QKV stage: the GEMM's split-K counters (kGemmCtrBytes, for every B), raw
+// (bf16 [B][M]), and for B > 4 the normalised input (bf16 [B][D]) and the split-K partials.
 size_t qkv_raw_bytes(int B, int D, int M) {
-  size_t n = round256((size_t)B * M * 2);
+  size_t n = kGemmCtrBytes + round256((size_t)B * M * 2);
   if (B > kGemvMaxBatch) n += round256((size_t)B * D * 2) + gemm_workspace_bound(M, false);
   return n;
 }
@@ -96,17 +96,17 @@ size_t qkv_raw_bytes(int B, int D, int M) {
 int qkv_raw_internal(const void* wqkv, const uint16_t* cur, const uint16_t* n_in, void* ws,
                      size_t ws_bytes, int B, int M, int D, int G, int tile_m, int domain,
                      float eps, hipStream_t s, const char* fn) {
-  uint16_t* raw = (uint16_t*)ws;
+  uint16_t* raw = qkv_raw_of(ws);
   if (B <= kGemvMaxBatch)
     return gemv_rms_internal(wqkv, cur, n_in, raw, B, M, D, G, tile_m, domain, eps, s, fn);
   int st = gemm_check(fn, B, M, D, G);
   if (st) return st;
-  uint16_t* hn = (uint16_t*)((char*)ws + round256((size_t)B * M * 2));
+  uint16_t* hn = (uint16_t*)((char*)raw + round256((size_t)B * M * 2));
   char* part = (char*)hn + round256((size_t)B * D * 2);
   st = rmsnorm_launch(cur, n_in, hn, B, D, eps, s);
   if (st) return st;
   return gemm_w8_launch(wqkv, nullptr, M, D, G, tile_m, domain, hn, 0, B, D, GEMM_EPI_BF16,
-                        raw, M, 0, nullptr, nullptr, 0, part,
+                        raw, M, 0, nullptr, nullptr, 0, (unsigned int*)ws, part,
                         ws_bytes - (size_t)(part - (char*)ws), s, fn);
 }
 
@@ -143,7 +143,7 @@ int iron_qkv_head(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
   if (!iron::aligned(workspace, 256))
     return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
   hipStream_t s = (hipStream_t)stream;
-  uint16_t* raw = (uint16_t*)workspace;
+  uint16_t* raw = iron::qkv_raw_of(workspace);
   st = iron::qkv_raw_internal(wqkv, cur, n_in, workspace, workspace_bytes, B, M, D, G, tile_m,
                               domain, eps, s, fn);
   if (st) return st;

@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iron_abi_version() == _lib.ABI_VERSION == 7
+    assert lib.iron_abi_version() == _lib.ABI_VERSION == 8
 
 
 def test_wire_bytes(lib):

@@ -133,6 +133,48 @@ def test_swiglu_mlp_mfma(D, FF, QD, fuse_o, G, B):
     assert_within_one_ulp(nxt, want, "mlp nxt")
 
 
+def test_mlp_workspace_reused_across_batches(lib):
+    """One workspace serves the MLP entry at every batch size: an MFMA call (B=8, split-K with
+    in-kernel reduction), a GEMV call (B=3) on the same memory, then the MFMA call again. The
+    split-K arrival counters sit in the first 16 KiB for every B, so the repeat gives the first
+    call's bits, the GEMV call gives a fresh workspace's bits, and the counters end at zero."""
+    import ctypes
+    from iron_amd import _lib
+
+    D, FF, G = 2048, 6144, 32
+    _say(f"mlp workspace reuse D={D} FF={FF} B=8,3,8")
+    gen = torch.Generator().manual_seed(77)
+
+    qs = [ogemv.rtn_quantize(torch.randn(M, K, generator=gen) * 0.05, G)
+          for M, K in ((FF, D), (FF, D), (D, FF))]
+    wg, wu, wd = [pack_wire(*w, tm, "signed").to(DEV) for w, tm in zip(qs, (12, 12, 4))]
+    nw = (torch.rand(D, generator=gen) + 0.5).to(torch.bfloat16).to(DEV)
+    cur = torch.randn(8, D, generator=gen).to(torch.bfloat16).to(DEV)
+    a = torch.randn(8, D, generator=gen).to(torch.bfloat16).to(DEV)
+    size = max(lib.iron_swiglu_mlp_workspace(8, D, FF), lib.iron_swiglu_mlp_workspace(3, D, FF))
+    ws = torch.zeros(size, dtype=torch.uint8, device=DEV)
+
+    def run(B, work):
+        out = torch.zeros(B, D, dtype=torch.bfloat16, device=DEV)
+        _lib.check(lib.iron_swiglu_mlp(cur.data_ptr(), a.data_ptr(), nw.data_ptr(), None,
+                                       wg.data_ptr(), wu.data_ptr(), wd.data_ptr(),
+                                       out.data_ptr(), None, B, D, FF, 0, G, 4, 12, 4, 0,
+                                       ctypes.c_float(1e-6), work.data_ptr(), work.numel(),
+                                       _lib.stream_handle()))
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    first = run(8, ws)
+    small = run(3, ws)
+    again = run(8, ws)
+    assert torch.equal(first.view(torch.int16), again.view(torch.int16))
+    fresh = run(3, torch.zeros(size, dtype=torch.uint8, device=DEV))
+    assert torch.equal(small.view(torch.int16), fresh.view(torch.int16))
+    assert int(ws[:16384].count_nonzero()) == 0, "split-K counters not left at zero"
+    want, _ = oblk.swiglu_mlp(cur.cpu(), a.cpu(), nw.cpu(), *qs, 1e-6)
+    assert_within_one_ulp(first, want, "mlp B=8")
+
+
 def test_qkv_attention_mfma_batch16():
     """Qwen3-8B heads (32 Q / 8 KV x 128, D = 4096) at batch 16: the raw QKV on MFMA, then the
     fused epilogue + attention; ragged positions."""
