@@ -14,6 +14,9 @@ REPO = Path(__file__).resolve().parent.parent
 if str(REPO) not in sys.path:
     sys.path.insert(0, str(REPO))
 
+# @pytest.mark.metrics, --csv-output and --iterations (the reference harness's metrics CSV)
+pytest_plugins = ["iron_amd.common.test_metrics"]
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X GPU and the built HIP library")
