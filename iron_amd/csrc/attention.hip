@@ -168,7 +168,7 @@ IRON_DEV bool rotate_query_side(const AttnParams& p, const AttnCoords& c, const 
 }
 
 template <int HB, bool FUSED>
-__global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnParams p) {
   const AttnCoords c = attn_coords<HB>(p);
   const int split = blockIdx.x, b = c.b, h0 = c.h0;
   const int wave = c.wave, lane = threadIdx.x & 63, row = c.row, dl = c.dl;
@@ -208,20 +208,33 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(AttnParams p) {
   }
 
   __shared__ double s_mx[2][4][HB];
-  // Tiles alternate between two register sets, the next tile's rows in flight while one is
-  // processed (separate named sets: a copy between them would wait for the loads). Every load is
-  // issued, rows clamped below t_lim (rows at or past t_end are masked where they are used).
-  uint4 kr2[4], vr2[4];
-  if (!p.spec && t_begin < t_end) load_kv_tile(p, c, t_begin, t_lim, kr, vr);
-  int it = 0;
-  for (int t0 = t_begin; t0 < t_end; t0 += 2 * kTile, it += 2) {
-    load_kv_tile(p, c, t0 + kTile, t_lim, kr2, vr2);
-    attn_tile_f64<HB, FUSED>(kr, vr, t0, t_end, has_new, pos, s_new, qf, p.scale, it, m, l, o,
-                             s_mx, wave, lane, row, dl);
-    if (t0 + kTile >= t_end) break;
-    load_kv_tile(p, c, t0 + 2 * kTile, t_lim, kr, vr);
-    attn_tile_f64<HB, FUSED>(kr2, vr2, t0 + kTile, t_end, has_new, pos, s_new, qf, p.scale,
-                             it + 1, m, l, o, s_mx, wave, lane, row, dl);
+  if constexpr (HB >= 4) {
+    // Four query heads hold 128 fp64 values per lane (q and the outputs): one register set of
+    // K/V rows keeps the kernel within half the register file, so two workgroups share each CU
+    // and one's tile loads overlap the other's arithmetic.
+    if (!p.spec && t_begin < t_end) load_kv_tile(p, c, t_begin, t_lim, kr, vr);
+    int it = 0;
+    for (int t0 = t_begin; t0 < t_end; t0 += kTile, ++it) {
+      if (t0 > t_begin) load_kv_tile(p, c, t0, t_lim, kr, vr);
+      attn_tile_f64<HB, FUSED>(kr, vr, t0, t_end, has_new, pos, s_new, qf, p.scale, it, m, l, o,
+                               s_mx, wave, lane, row, dl);
+    }
+  } else {
+    // Tiles alternate between two register sets, the next tile's rows in flight while one is
+    // processed (separate named sets: a copy between them would wait for the loads). Every load
+    // is issued, rows clamped below t_lim (rows at or past t_end are masked where they are used).
+    uint4 kr2[4], vr2[4];
+    if (!p.spec && t_begin < t_end) load_kv_tile(p, c, t_begin, t_lim, kr, vr);
+    int it = 0;
+    for (int t0 = t_begin; t0 < t_end; t0 += 2 * kTile, it += 2) {
+      load_kv_tile(p, c, t0 + kTile, t_lim, kr2, vr2);
+      attn_tile_f64<HB, FUSED>(kr, vr, t0, t_end, has_new, pos, s_new, qf, p.scale, it, m, l, o,
+                               s_mx, wave, lane, row, dl);
+      if (t0 + kTile >= t_end) break;
+      load_kv_tile(p, c, t0 + 2 * kTile, t_lim, kr, vr);
+      attn_tile_f64<HB, FUSED>(kr2, vr2, t0 + kTile, t_end, has_new, pos, s_new, qf, p.scale,
+                               it + 1, m, l, o, s_mx, wave, lane, row, dl);
+    }
   }
 
   attn_finish_f64<HB>(m, l, o, wave, row, dl, [&](int oh, int od, double O, double L, double M) {
