@@ -268,16 +268,25 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
   // Split K: this split's fp64 partials go to memory (agent-scope stores write through the L2),
   // and the last split of the row tile to arrive (one atomic count per tile) sums them in split
   // order -- the order a separate reduce kernel used -- and applies the epilogue, then clears
-  // the count for the next call. Every thread's stores are complete before the count.
-  if (!half && bcol < p.B) {
+  // the count for the next call. Every thread's stores are complete before the count. The
+  // partials pass through LDS (the weight tiles' space) so that consecutive threads store
+  // consecutive rows: write-through stores are not merged in the L2, so scattered 8-byte stores
+  // would each cost a whole memory sector.
+  // (rows padded to kTM + 1 doubles: the 16 batch columns a wavefront writes fall in distinct banks)
+  double (*const s_part)[kBN][kTM + 1] =
+      reinterpret_cast<double (*)[kBN][kTM + 1]>(&s_w[0][0][0][0]);
+  static_assert(sizeof(double) * NM * kBN * (kTM + 1) <= sizeof(s_w), "s_part fits in s_w");
+  if (!half) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = row0 + crow + i;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int mi = 0; mi < NM; ++mi)
-        __hip_atomic_store(p.part + (((size_t)mi * p.splits + split) * kBN + bcol) * p.M + m,
-                           acc[mi][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+      for (int mi = 0; mi < NM; ++mi) s_part[mi][bcol][crow + i] = acc[mi][i];
+  }
+  __syncthreads();
+  for (int t = tid; t < NM * p.B * kTM; t += 512) {
+    const int mi = t / (p.B * kTM), b = (t / kTM) % p.B, r = t % kTM;
+    __hip_atomic_store(p.part + (((size_t)mi * p.splits + split) * kBN + b) * p.M + row0 + r,
+                       s_part[mi][b][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
