@@ -222,11 +222,6 @@ IRON_DEV unsigned long long* copy_for(unsigned long long* base, size_t stride, i
   return base + (size_t)(wg % kCopies) * stride;
 }
 
-IRON_DEV void put_double(unsigned long long* dst, double v, uint32_t tag) {
-  put_word(dst, (uint32_t)__double2loint(v), tag);
-  put_word(dst + 1, (uint32_t)__double2hiint(v), tag);
-}
-
 IRON_DEV double word_double(uint32_t lo, uint32_t hi) {
   return __hiloint2double((int)hi, (int)lo);
 }
@@ -972,14 +967,24 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
                            lsum, o, wave, lane, row, dl);
   }
   const uint32_t tp = phase_tag(ep, p.n_layers, l, 1);
+  // Word 2 d + k of a partial holds half k of dim d. Each store instruction writes 64 consecutive
+  // words (the wavefront's 64 dims, exchanged so lane j holds word j): the hand-off stores write
+  // through the L2, which merges nothing, so a store per half would write every sector twice.
   attn_finish_pairs(m, lsum, o, wave, row, dl,
                     [&](int oh, int od, double O, double Ls, double M) {
     unsigned long long* part =
         p.PART + ((size_t)(head * HB + oh) * NS + split) * (2 * (kAttnD + 2));
-    put_double(part + 2 * od, O, tp);
-    if (od == 0) {
-      put_double(part + 2 * kAttnD, M, tp);
-      put_double(part + 2 * (kAttnD + 1), Ls, tp);
+    const int j = od & 63;
+    const int lo = __double2loint(O), hi = __double2hiint(O);
+    const int lo1 = __shfl(lo, j >> 1), hi1 = __shfl(hi, j >> 1);
+    const int lo2 = __shfl(lo, 32 + (j >> 1)), hi2 = __shfl(hi, 32 + (j >> 1));
+    unsigned long long* w = part + 2 * (od & 64);  // this wavefront's 128 words
+    put_word(w + j, (uint32_t)(j & 1 ? hi1 : lo1), tp);
+    put_word(w + 64 + j, (uint32_t)(j & 1 ? hi2 : lo2), tp);
+    if (od < 4) {  // m and l (the same in every thread of the head): words 2 kAttnD .. + 3
+      const double v = od < 2 ? M : Ls;
+      put_word(part + 2 * kAttnD + od,
+               (uint32_t)(od & 1 ? __double2hiint(v) : __double2loint(v)), tp);
     }
   });
   return true;
