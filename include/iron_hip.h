@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 8
+#define IRON_ABI_VERSION 9
 
 enum iron_status {
   IRON_OK = 0,
@@ -376,6 +376,24 @@ int iron_test_bf16_round(uint32_t* out, void* stream);
  * 1/blocks of the buffer, and writes one xor word per thread to out[blocks * 256]. Its time is
  * the achievable HBM read rate that the roofline figures are read against. */
 int iron_stream_read(const void* p, size_t bytes, uint32_t* out, int blocks, void* stream);
+
+/* Measurement hook (no reference counterpart): the grid-wide hand-off a persistent kernel needs
+ * between phases, timed alone. 256 workgroups of 256 threads (one per CU; the device needs 256
+ * CUs) run n_phases phases; in each, every workgroup publishes its n_words / 256 words of an
+ * n_words vector (a multiple of 256, at most 2048) and waits until it has every workgroup's:
+ *   IRON_HANDOFF_TAGGED  -- the persistent decode kernel's own hand-off code: 64-bit
+ *                           {tag, payload} words stored in 8 copies, polled from one copy;
+ *   IRON_HANDOFF_COUNTER -- one atomic arrival counter polled to the grid size (no vector);
+ *   IRON_HANDOFF_FLAGS   -- plain stores, device-scope fences and one flag per workgroup.
+ * Phase p of a launch uses tag base + p + 1: successive launches on one workspace pass distinct
+ * bases. The workspace (iron_handoff_probe_workspace bytes) is zero-filled before the first
+ * launch, and again before each IRON_HANDOFF_COUNTER launch (its counter starts at zero). Every
+ * wait is bounded: after the stream synchronises, a nonzero uint32 at byte
+ * iron_handoff_probe_workspace(n_words) - 4096 + 256 of the workspace means a wait gave up. */
+enum iron_handoff_mode { IRON_HANDOFF_TAGGED = 0, IRON_HANDOFF_COUNTER = 1, IRON_HANDOFF_FLAGS = 2 };
+size_t iron_handoff_probe_workspace(int n_words);
+int iron_handoff_probe(int mode, int n_words, int n_phases, unsigned int base, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

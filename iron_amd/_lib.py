@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
-ABI_VERSION = 8          # IRON_ABI_VERSION of include/iron_hip.h
+ABI_VERSION = 9          # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2
@@ -32,6 +32,9 @@ IRON_WEIGHT_BF16 = 1
 IRON_ACCUM_F64 = 0
 IRON_ACCUM_F32 = 1
 ACCUM = {"f64": IRON_ACCUM_F64, "f32": IRON_ACCUM_F32}
+IRON_HANDOFF_TAGGED = 0
+IRON_HANDOFF_COUNTER = 1
+IRON_HANDOFF_FLAGS = 2
 
 
 def accum_mode(name: str) -> int:
@@ -126,6 +129,8 @@ SIGNATURES = {
     "iron_test_fastdiv": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32]),
     "iron_test_bf16_round": (_c_int, [_c_vp, _c_vp]),
     "iron_stream_read": (_c_int, [_c_vp, _c_sz, _c_vp, _c_int, _c_vp]),
+    "iron_handoff_probe_workspace": (_c_sz, [_c_int]),
+    "iron_handoff_probe": (_c_int, [_c_int, _c_int, _c_int, ctypes.c_uint, _c_vp, _c_sz, _c_vp]),
 }
 
 _lock = threading.Lock()

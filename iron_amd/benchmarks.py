@@ -288,6 +288,41 @@ def read_probe(gib: int = 1, reps: int = 5) -> dict:
             "bytes": nbytes, "kernel": "iron_stream_read (16-byte loads, a contiguous chunk per workgroup)"}
 
 
+HANDOFF_MODES = {"tagged": _lib.IRON_HANDOFF_TAGGED, "counter": _lib.IRON_HANDOFF_COUNTER,
+                 "flags": _lib.IRON_HANDOFF_FLAGS}
+
+
+def handoff_probe(phases: int = 2000, reps: int = 3) -> dict:
+    """Microseconds per grid-wide hand-off phase (iron_handoff_probe: 256 workgroups, one per CU):
+    the tagged-word exchange at several vector sizes (words every workgroup polls), an atomic
+    counter barrier, and flags with device-scope fences. Best of `reps` launches of `phases`."""
+    lib = _lib.load()
+    cases = [("tagged", n) for n in (256, 512, 1024, 2048)] + [("counter", 256),
+                                                                ("flags", 1024)]
+    out, base = {}, 0
+    for name, n in cases:
+        nbytes = lib.iron_handoff_probe_workspace(n)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+        best = None
+        for _ in range(reps):
+            ws.zero_()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            _lib.check(lib.iron_handoff_probe(HANDOFF_MODES[name], n, phases, base, ws.data_ptr(),
+                                              nbytes, _st()))
+            e1.record()
+            e1.synchronize()
+            base += phases + 1
+            err = int(ws[nbytes - 4096 + 256: nbytes - 4096 + 260].view(torch.int32).item())
+            if err:
+                raise RuntimeError(f"iron_handoff_probe {name} n={n}: a wait gave up")
+            us = e0.elapsed_time(e1) * 1e3 / phases
+            best = us if best is None else min(best, us)
+        out[f"{name}_{n}"] = round(best, 3)
+    return {"us_per_phase": out, "phases": phases,
+            "kernel": "iron_handoff_probe (256 workgroups x 256 threads, one per CU)"}
+
+
 def copy_probe(mib: int = 256, reps: int = 4) -> dict:
     """A plain device copy of a known size: the calibration run for the HBM byte counters
     (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE read this kernel as mib MiB fetched / written)."""
@@ -307,6 +342,8 @@ if __name__ == "__main__":
                     help="run only the byte-counter calibration copy")
     ap.add_argument("--read-probe", action="store_true",
                     help="run only the achievable-read-bandwidth probe")
+    ap.add_argument("--handoff-probe", action="store_true",
+                    help="run only the grid-wide hand-off probe (us per phase per mechanism)")
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c5_prefill", "c5_decode"],
                     help="run one configuration (for profiling)")
     ap.add_argument("--acc", choices=["f64", "f32"], default="f64",
@@ -318,6 +355,8 @@ if __name__ == "__main__":
         print(json.dumps(copy_probe()), flush=True)
     elif a.read_probe:
         print(json.dumps(read_probe()), flush=True)
+    elif a.handoff_probe:
+        print(json.dumps(handoff_probe()), flush=True)
     elif a.only:
         lib = _lib.load()
         b2, b3 = a.batch or 1, a.batch or 8

@@ -1540,7 +1540,50 @@ WireGeom geom(int K, int G, int tile_m, int domain) {
   return g;
 }
 
+// The tagged-word hand-off of this kernel, alone (iron_handoff_probe, IRON_HANDOFF_TAGGED):
+// kNT workgroups, n_phases phases; in each, workgroup w publishes words [w per, (w + 1) per) of
+// an n-word vector with put_word_copies (the kCopies copies at the spread_word layout of the x, a
+// and attention-output buffers) and waits in gather_words for all n words from its XCD's copy.
+// Two buffers alternate by phase, as a buffer here is rewritten by the next layer's phase.
+__global__ __launch_bounds__(256, 1) void handoff_probe_tagged_kernel(unsigned long long* vec,
+                                                                      uint32_t* err, int n,
+                                                                      int n_phases,
+                                                                      uint32_t base) {
+  constexpr int NPT = iron::kHandoffMaxWords / kNT;
+  __shared__ uint32_t s_in[NPT * 256];
+  const int wg = blockIdx.x, per = n / kNT;
+  for (int ph = 0; ph < n_phases; ++ph) {
+    const uint32_t tag = base + (uint32_t)ph + 1u;
+    unsigned long long* buf = vec + (size_t)(ph & 1) * kCopies * kCopyWords;
+    if ((int)threadIdx.x < per)
+      put_word_copies(buf + spread_word(wg * per + threadIdx.x), kCopyWords,
+                      (uint32_t)(ph + wg), tag);
+    unsigned long long* const mine = copy_for(buf, kCopyWords, wg);
+    auto src = [&](int j, uint32_t& t) {
+      t = tag;
+      return mine + spread_word(j);
+    };
+    if (!gather_words<NPT>(n, src, [] {}, s_in, err)) return;  // workgroup-uniform
+  }
+}
+
+static_assert(spread_word(iron::kHandoffMaxWords - 1) < kCopyWords, "probe vector fits a copy");
+
 }  // namespace
+
+namespace iron {
+
+size_t handoff_tagged_bytes() { return (size_t)2 * kCopies * kCopyWords * 8; }
+
+// vec: handoff_tagged_bytes() of zero-filled (or earlier-tagged) words; err: one uint32.
+int handoff_tagged_launch(void* vec, uint32_t* err, int n, int n_phases, uint32_t base,
+                          hipStream_t s) {
+  hipLaunchKernelGGL(handoff_probe_tagged_kernel, dim3(kNT), dim3(256), 0, s,
+                     (unsigned long long*)vec, err, n, n_phases, base);
+  return check_launch("iron_handoff_probe");
+}
+
+}  // namespace iron
 
 extern "C" {
 

@@ -74,6 +74,13 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
                    hipStream_t stream, const char* fn);
 
 
+// The persistent kernel's tagged-word hand-off alone (decode_persistent.hip), for the hand-off
+// probe: n words (a multiple of 256, at most kHandoffMaxWords) over n_phases phases.
+constexpr int kHandoffMaxWords = 2048;
+size_t handoff_tagged_bytes();
+int handoff_tagged_launch(void* vec, uint32_t* err, int n, int n_phases, uint32_t base,
+                          hipStream_t s);
+
 // The raw-QKV stage shared by the QKV head and the fused QKV head + attention (qkv.hip).
 size_t qkv_raw_bytes(int B, int D, int M);
 // raw (bf16 [B][M]) sits after the GEMM counters at the front of the stage's workspace.

@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iron_abi_version() == _lib.ABI_VERSION == 8
+    assert lib.iron_abi_version() == _lib.ABI_VERSION == 9
 
 
 def test_wire_bytes(lib):
@@ -201,3 +201,20 @@ def test_next_token_validation(lib):
     assert b"log_len" in lib.iron_last_error()
     assert f(fake, fake, None, None, fake, 4, 8, fake, 2, 1024, 100, None) == _lib.IRON_ERR_SHAPE
     assert f(fake, fake, None, None, None, 0, 0, None, 65, 1024, 100, None) == _lib.IRON_ERR_SHAPE
+
+
+def test_handoff_probe_validation(lib):
+    """The hand-off probe's arguments are checked before the device is queried or anything is
+    launched."""
+    q = lib.iron_handoff_probe_workspace
+    assert q(1024) == q(256) == 2 * 8 * 4096 * 8 + 4096  # the tagged mode's 8 copies, twice
+    assert q(0) == 0 and q(1000) == 0 and q(2048 + 256) == 0
+    f = lib.iron_handoff_probe
+    ws, fake = q(1024), 1 << 20
+    assert f(3, 1024, 10, 0, fake, ws, None) == _lib.IRON_ERR_SHAPE
+    assert b"unknown mode" in lib.iron_last_error()
+    assert f(_lib.IRON_HANDOFF_TAGGED, 1000, 10, 0, fake, ws, None) == _lib.IRON_ERR_SHAPE
+    assert f(_lib.IRON_HANDOFF_TAGGED, 1024, 0, 0, fake, ws, None) == _lib.IRON_ERR_SHAPE
+    assert f(_lib.IRON_HANDOFF_FLAGS, 1024, 10, 0, None, ws, None) == _lib.IRON_ERR_WORKSPACE
+    assert f(_lib.IRON_HANDOFF_FLAGS, 1024, 10, 0, fake, ws - 8, None) == _lib.IRON_ERR_WORKSPACE
+    assert f(_lib.IRON_HANDOFF_COUNTER, 1024, 10, 0, fake + 8, ws, None) == _lib.IRON_ERR_ALIGN
