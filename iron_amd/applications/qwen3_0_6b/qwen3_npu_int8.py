@@ -335,7 +335,9 @@ class Qwen3NPU:
             _lib.IRON_DOMAIN_SIGNED, stream), "iron_lm_head")
 
     def persistent_errors(self, clear: bool = True) -> int:
-        """The persistent kernel's error word (nonzero: a hand-off wait timed out)."""
+        """The persistent kernel's error word: bit 0, a hand-off wait timed out; bit 1, the
+        workgroups with equal index mod 8 did not share an XCD, which the XCD-local hand-offs
+        of the Qwen3-0.6B shape assume."""
         if not self.persistent:
             return 0
         word = self._p_ws[4:8].view(torch.int32)
@@ -347,8 +349,12 @@ class Qwen3NPU:
     def _persistent_check(self):
         err = self.persistent_errors()
         if err:
-            raise RuntimeError(f"iron_decode_persistent: a hand-off wait timed out (flags {err:#x});"
-                               " the token's outputs are invalid")
+            what = "a hand-off wait timed out" if err & 1 else ""
+            if err & 2:
+                what += ("; " if what else "") + "workgroups with equal index mod 8 ran on " \
+                        "different XCDs"
+            raise RuntimeError(f"iron_decode_persistent: {what} (flags {err:#x}); the token's "
+                               "outputs are invalid")
 
     # ---------------- state helpers ----------------
     def kv_caches(self, layer: int):

@@ -101,6 +101,7 @@ struct Shape {
   static constexpr int RE = cdiv(FF, WAVES), CE = cdiv(D, 1024);
   static constexpr int RF = cdiv(D, WAVES), CF = cdiv(FF, 1024);
   static constexpr int MERGE_WPS = 2 * MERGE_PER + 4;  // words per split: o[PER], m, l as fp64
+  static constexpr size_t PART_WORDS = (size_t)HQ * NS * (HD + 2) * 2;  // all split partials
   // LDS words of the widest phase input
   static constexpr int LDS_WORDS =
       cmax(cmax(D, QD / 2), cmax(FF, cmax(NS * MERGE_WPS, (HB + 2) * 64)));
@@ -118,6 +119,13 @@ struct Shape {
   // words between the replicated copies of the kGhBuffers gh buffers (a multiple of kCopyWords)
   static constexpr size_t GH_COPY =
       (((size_t)kGhBuffers * GH_WORDS + kCopyWords - 1) / kCopyWords) * kCopyWords;
+  // One KV head per XCD: the 32 workgroups of XCD x (wg % 8 == x) compute KV head x's QKV rows
+  // (its two query heads, its key and value: 512 rows, 16 per workgroup), run its 32 attention
+  // splits and merge its two query heads' outputs, so the raw q/k/v and the split partials
+  // travel through that XCD's L2 (xcd_local_*), never through the fabric.
+  static constexpr bool XCD_LOCAL = HKV == kCopies && NS * HKV == kNT &&
+                                    (HB + 2) * HD == 4 * RA * NS && RA == 4 &&
+                                    MERGE_PER * NS == HB * HD;
 
   static_assert(HQ % HKV == 0 && HB == 2, "the attention phase handles GQA pairs");
   static_assert(kNT % HKV == 0 && NS <= 256, "splits per KV head");
@@ -226,6 +234,31 @@ IRON_DEV double word_double(uint32_t lo, uint32_t hi) {
   return __hiloint2double((int)hi, (int)lo);
 }
 
+// XCD-local hand-off (the raw q/k/v rows and the attention split partials of shapes with
+// Shape::XCD_LOCAL): producer and consumers are workgroups of one XCD, which share its L2. The
+// producer's store carries sc0 (written through the CU's L1 into the L2); a consumer polls with nt
+// loads, whose L1 policy is hit-evict, so a line its L1 held from an earlier read is dropped after
+// one read and the next poll is served by the L2. A 64-bit word is written and read whole, as
+// with the device-scope words. Both need the workgroups of one hand-off on one XCD, which the
+// kernel's mapping gives when workgroups with equal wg % 8 share an XCD (checked every launch).
+// Measured alone (32 workgroups per XCD, 2000 phases): 0.70 against 0.80 us per phase for 256
+// words, 1.15 against 1.44 us for 640, with device-scope words; sc0 polls returned stale words.
+constexpr int kCpolSc0 = 1;
+
+IRON_DEV __amdgpu_buffer_rsrc_t xcd_local_rsrc(unsigned long long* base, size_t words) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)(words * 8), kBufferDword3);
+}
+
+IRON_DEV void put_word_local(__amdgpu_buffer_rsrc_t rs, size_t word, uint32_t payload,
+                             uint32_t tag) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = {payload, tag};  // the low dword is the payload, the high one the tag
+  __builtin_amdgcn_raw_buffer_store_b64(v, rs, (int)(word * 8), 0, kCpolSc0);
+}
+
+// The hardware XCC id of the executing workgroup (HW_REG_XCC_ID, bits 3:0).
+IRON_DEV uint32_t xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xfu; }
+
 // Packed words (gh): tag in bits 48..63, payload in bits 0..47. The 16-bit tag is the full tag
 // reduced to 1..65535 (never 0, the value of a cleared word). Every launch rewrites or clears every
 // gh block, so a stale word is at most one completed launch old (plus launches that failed before
@@ -316,8 +349,25 @@ IRON_DEV bool skip_gather(Issue issue) {
   return true;
 }
 
-template <int NPT, int DELAY = kFirstPollDelay, class Src, class Issue>
-IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t* err) {
+// Polls of device-scope words (every hand-off but the XCD-local ones).
+struct AgentPoll {
+  static constexpr bool kPlainLoad = false;
+  IRON_DEV unsigned long long operator()(unsigned long long* w) const { return poll_word(w); }
+};
+
+// Polls of XCD-local words (put_word_local): nt loads. They are plain loads to the compiler (a
+// volatile one would be issued past every cache), so gather_words puts a compiler memory barrier
+// before each round to keep them in the loop.
+struct LocalPoll {
+  static constexpr bool kPlainLoad = true;
+  IRON_DEV unsigned long long operator()(unsigned long long* w) const {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) unsigned long long*)w);
+  }
+};
+
+template <int NPT, int DELAY = kFirstPollDelay, class Src, class Issue, class Poll = AgentPoll>
+IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t* err,
+                           Poll poll = Poll()) {
   __syncthreads();  // the previous phase's LDS reads are done before dst is rewritten
   retire_loads();
   first_poll_delay<DELAY>();
@@ -333,9 +383,10 @@ IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t*
   bool missing = false;
   for (long long spins = 0;; ++spins) {
     unsigned long long w[NPT];
+    if constexpr (Poll::kPlainLoad) asm volatile("" ::: "memory");
 #pragma unroll
     for (int k = 0; k < NPT; ++k)
-      if (pending[k]) w[k] = poll_word(ptr[k]);
+      if (pending[k]) w[k] = poll(ptr[k]);
     missing = false;
 #pragma unroll
     for (int k = 0; k < NPT; ++k) {
@@ -569,11 +620,47 @@ IRON_DEV int row0_of(int wg, int R) {
   return (wg * 4 + (int)(threadIdx.x >> 6)) * R;
 }
 
+// The QKV phase's block of 4 RA consecutive rows that workgroup wg computes. With XCD_LOCAL,
+// XCD x = wg % 8 computes KV head x's rows: i = wg / 8 < 16 the rows of query heads 2x, 2x + 1,
+// then 8 blocks of key head x and 8 of value head x; otherwise block wg.
+template <class S>
+IRON_DEV int qkv_block(int wg) {
+  if constexpr (S::XCD_LOCAL) {
+    constexpr int BR = 4 * S::RA, QB = S::HB * S::HD / BR, KB = S::HD / BR;
+    const int x = wg % S::HKV, i = wg / S::HKV;
+    return i < QB ? x * QB + i
+                  : (i < QB + KB ? (S::QD + x * S::HD) / BR + (i - QB)
+                                 : (S::QD + S::KVD + x * S::HD) / BR + (i - QB - KB));
+  } else {
+    return wg;
+  }
+}
+
+// The attention phase's KV head and split of workgroup wg (XCD_LOCAL: head wg % 8, so a head's
+// splits share the XCD that computed its raw rows).
+template <class S>
+IRON_DEV int attn_head(int wg) {
+  return S::XCD_LOCAL ? wg % S::HKV : wg / S::NS;
+}
+template <class S>
+IRON_DEV int attn_split(int wg) {
+  return S::XCD_LOCAL ? wg / S::HKV : wg % S::NS;
+}
+
+// The first of the MERGE_PER attention outputs (query head h, dim d at h * HD + d) that
+// workgroup wg merges (XCD_LOCAL: outputs of KV head wg % 8's query heads, on that XCD).
+template <class S>
+IRON_DEV int merge_o0(int wg) {
+  return S::XCD_LOCAL ? (wg % S::HKV) * S::HB * S::HD + (wg / S::HKV) * S::MERGE_PER
+                      : wg * S::MERGE_PER;
+}
+
 template <class S>
 IRON_DEV void prefetch_qkv(const PParams& p, const iron_layer_desc& L, int wg,
                            W8<S::RA, S::CA>& W, uint4 (&nw)[S::CA][2]) {
   const GemvParams g = gemv_of(p.g_qkv, L.wqkv, S::MQKV, S::D);
-  fetch_w8<S::RA, S::CA>(g, g.w, row0_of<S>(wg, S::RA), threadIdx.x & 63, W.w, W.sc);
+  fetch_w8<S::RA, S::CA>(g, g.w, row0_of<S>(qkv_block<S>(wg), S::RA), threadIdx.x & 63, W.w,
+                         W.sc);
   lane_weight<S::CA>(L.n_in, S::D, threadIdx.x & 63, nw);
 }
 
@@ -622,7 +709,7 @@ IRON_DEV SplitRange split_range(int ctx, int split) {
 template <class S>
 IRON_DEV void prefetch_attn(const PParams& p, const iron_layer_desc& L, int wg, int pos,
                             KVPrefetch& kv) {
-  const int head = wg / S::NS, split = wg % S::NS, lane = threadIdx.x & 63;
+  const int head = attn_head<S>(wg), split = attn_split<S>(wg), lane = threadIdx.x & 63;
   const SplitRange r = split_range<S>(context_of(p, pos), split);
   load_kv_rows(p, L, head, r.begin, r.end, kv.kr, kv.vr);
   kv.nq = (uint32_t)ld_global(L.n_qn + lane) | ((uint32_t)ld_global(L.n_qn + lane + 64) << 16);
@@ -688,7 +775,8 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
                         const uint4 (&nwl)[S::CA][2], Issue issue) {
   constexpr int R = S::RA, NCH = S::CA;
   const int lane = threadIdx.x & 63;
-  const int row0 = row0_of<S>(wg, R);
+  const int blk = qkv_block<S>(wg);
+  const int row0 = row0_of<S>(blk, R);
   GemvParams g = gemv_of(p.g_qkv, nullptr, S::MQKV, S::D);
   g.pro = PRO_RMS_BF16;
   g.eps = p.eps;
@@ -721,15 +809,20 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
     __shared__ uint32_t s_pairs[4 * R / 2];
     if ((lane & 15) == 0 && k < R / 2) s_pairs[wave * (R / 2) + k] = (hb & 0xffffu) | (hi << 16);
     __syncthreads();
-    const int t = threadIdx.x, row = wg * 4 * R + 2 * t;
-    if (t < 2 * R && row < S::MQKV)
-      put_word_copies(p.RAW + row / 2, kCopyWords, s_pairs[t], tag);
+    const int t = threadIdx.x, row = blk * 4 * R + 2 * t;
+    if (t < 2 * R && row < S::MQKV) {
+      if constexpr (S::XCD_LOCAL)  // read only by this XCD's attention workgroups: one copy
+        put_word_local(xcd_local_rsrc(p.RAW, S::MQKV / 2), row / 2, s_pairs[t], tag);
+      else
+        put_word_copies(p.RAW + row / 2, kCopyWords, s_pairs[t], tag);
+    }
   } else {
     dot_w8_lane<R, NCH>(g, W.w, W.sc, xf, row0, lane, acc);
     uint16_t h[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) h[r] = f64_to_bf16(acc[r][0]);
-    store_bf16_pairs<R>(h, wg, S::MQKV, p.RAW, tag, s_out, nullptr);
+    static_assert(!S::XCD_LOCAL, "the XCD-local raw rows leave from the even-R branch");
+    store_bf16_pairs<R>(h, blk, S::MQKV, p.RAW, tag, s_out, nullptr);
   }
   return true;
 }
@@ -907,7 +1000,7 @@ template <class S, class Issue>
 IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int wg, uint32_t ep,
                          int pos, uint32_t* s_in, KVPrefetch& kv, Issue issue) {
   constexpr int HB = S::HB, NS = S::NS;
-  const int head = wg / NS, split = wg % NS;
+  const int head = attn_head<S>(wg), split = attn_split<S>(wg);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, row = lane >> 4, dl = lane & 15;
   const bool pos_ok = pos >= 0 && pos < p.max_seq;
   const SplitRange range = split_range<S>(context_of(p, pos), split);
@@ -916,7 +1009,7 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
   {
     constexpr int n = (HB + 2) * 64;
     const uint32_t tr = phase_tag(ep, p.n_layers, l, 0);
-    unsigned long long* const raw = copy_for(p.RAW, kCopyWords, wg);
+    unsigned long long* const raw = S::XCD_LOCAL ? p.RAW : copy_for(p.RAW, kCopyWords, wg);
     auto src = [&](int j, uint32_t& t) {
       t = tr;
       const int seg = j >> 6, off = j & 63;
@@ -925,8 +1018,13 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
                                              : (S::QD + S::KVD + head * S::HD) / 2);
       return raw + base + off;
     };
-    if (!gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1))
-      return false;
+    bool ok;
+    if constexpr (S::XCD_LOCAL)
+      ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1,
+                                      LocalPoll{});
+    else
+      ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1);
+    if (!ok) return false;
   }
   const uint16_t* s_raw = (const uint16_t*)s_in;  // segment seg: 128 bf16
 
@@ -972,19 +1070,23 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
   // through the L2, which merges nothing, so a store per half would write every sector twice.
   attn_finish_pairs(m, lsum, o, wave, row, dl,
                     [&](int oh, int od, double O, double Ls, double M) {
-    unsigned long long* part =
-        p.PART + ((size_t)(head * HB + oh) * NS + split) * (2 * (kAttnD + 2));
+    const size_t part = ((size_t)(head * HB + oh) * NS + split) * (2 * (kAttnD + 2));
     const int j = od & 63;
     const int lo = __double2loint(O), hi = __double2hiint(O);
     const int lo1 = __shfl(lo, j >> 1), hi1 = __shfl(hi, j >> 1);
     const int lo2 = __shfl(lo, 32 + (j >> 1)), hi2 = __shfl(hi, 32 + (j >> 1));
-    unsigned long long* w = part + 2 * (od & 64);  // this wavefront's 128 words
-    put_word(w + j, (uint32_t)(j & 1 ? hi1 : lo1), tp);
-    put_word(w + 64 + j, (uint32_t)(j & 1 ? hi2 : lo2), tp);
-    if (od < 4) {  // m and l (the same in every thread of the head): words 2 kAttnD .. + 3
-      const double v = od < 2 ? M : Ls;
-      put_word(part + 2 * kAttnD + od,
-               (uint32_t)(od & 1 ? __double2hiint(v) : __double2loint(v)), tp);
+    const size_t w = part + 2 * (od & 64);  // this wavefront's 128 words
+    const double v = od < 2 ? M : Ls;       // m and l (the same in every thread of the head)
+    const uint32_t v32 = (uint32_t)(od & 1 ? __double2hiint(v) : __double2loint(v));
+    if constexpr (S::XCD_LOCAL) {  // read only by this XCD's merge workgroups
+      const __amdgpu_buffer_rsrc_t rs = xcd_local_rsrc(p.PART, S::PART_WORDS);
+      put_word_local(rs, w + j, (uint32_t)(j & 1 ? hi1 : lo1), tp);
+      put_word_local(rs, w + 64 + j, (uint32_t)(j & 1 ? hi2 : lo2), tp);
+      if (od < 4) put_word_local(rs, part + 2 * kAttnD + od, v32, tp);  // words 2 kAttnD .. + 3
+    } else {
+      put_word(p.PART + w + j, (uint32_t)(j & 1 ? hi1 : lo1), tp);
+      put_word(p.PART + w + 64 + j, (uint32_t)(j & 1 ? hi2 : lo2), tp);
+      if (od < 4) put_word(p.PART + part + 2 * kAttnD + od, v32, tp);
     }
   });
   return true;
@@ -998,7 +1100,7 @@ template <class S, class Issue>
 IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s_in,
                           Issue issue) {
   constexpr int PER = S::MERGE_PER, NS = S::NS, WPS = S::MERGE_WPS;
-  const int o0 = wg * PER, h = o0 / kAttnD, d0 = o0 % kAttnD;
+  const int o0 = merge_o0<S>(wg), h = o0 / kAttnD, d0 = o0 % kAttnD;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   {
     constexpr int n = NS * WPS;
@@ -1010,8 +1112,13 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
       unsigned long long* part = part_of(s);
       return k < 2 * PER ? part + 2 * d0 + k : part + 2 * kAttnD + (k - 2 * PER);
     };
-    if (!gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1))
-      return false;
+    bool ok;
+    if constexpr (S::XCD_LOCAL)
+      ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1,
+                                      LocalPoll{});
+    else
+      ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1);
+    if (!ok) return false;
   }
   // thread (split sp, dim d): sp = t % NS, d = t / NS holds o_sp[d0 + d], m_sp and l_sp; the
   // max and the two sums run over the NS threads of one d (a wavefront, or two for NS = 128)
@@ -1365,6 +1472,18 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
   const int wg = blockIdx.x;
   const uint32_t ep = p.ctrl[0];
   const int pos = *p.pos;
+  // The XCD-local hand-offs need the workgroups with equal wg % 8 on one XCD. The round-robin
+  // dispatch of a one-dimensional grid puts workgroup wg on XCD (wg + o) % 8, where the offset o
+  // depends on earlier dispatches (measured: not always 0). Each workgroup records its offset in
+  // control word 2 before its first hand-off store; workgroup 0 checks at the end of the launch
+  // that they agree (error flag 2 otherwise: a word the mapping strands in another XCD's L2 would
+  // make its wait time out, never deliver a stale value).
+  if constexpr (S::XCD_LOCAL)
+    if (threadIdx.x == 0) {
+      __hip_atomic_fetch_or(p.ctrl + 2, 1u << ((xcc_id() - (uint32_t)wg) & 7u), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    }
   W8<S::RA, S::CA> wqkv;
   uint4 n_in[S::CA][2];
   prefetch_qkv<S>(p, p.layers[0], wg, wqkv, n_in);
@@ -1435,6 +1554,12 @@ __global__ __launch_bounds__(256, 1) void decode_persistent_kernel(PParams p) {
   // contributed to the last layer, so every workgroup has read `ep`, the key, the position and
   // (in its attention phase) the RoPE row by now: the greedy loop's state advances here too.
   if (wg != 0) return;
+  if constexpr (S::XCD_LOCAL)
+    if (threadIdx.x == 0) {
+      const uint32_t offs = __hip_atomic_exchange(p.ctrl + 2, 0u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      if (__popc(offs) != 1) atomicOr(p.ctrl + 1, 2u);
+    }
   if (p.key) {
     const int next = pos + 1;
     if (threadIdx.x == 0) {
@@ -1476,7 +1601,7 @@ Layout layout_of() {
   lo.ctrl = take(32);
   lo.X = take(kCopies * kCopyWords);
   lo.RAW = take(kCopies * kCopyWords);
-  lo.PART = take((size_t)S::HQ * S::NS * (S::HD + 2) * 2);
+  lo.PART = take(S::PART_WORDS);
   lo.ATT = take(kCopies * kCopyWords);
   lo.AO = take(kCopies * kCopyWords);
   lo.GH = take((size_t)kCopies * S::GH_COPY);
