@@ -317,6 +317,9 @@ IRON_DEV bool workgroup_any(bool flag) {
 // trip. Measured per step: sleep 4 / 6 / 8 / 10 / 12 / 16 / 32 units -> -6 / -10 / -18 / -21 /
 // -18 / -5 / +47 us against no sleep.
 constexpr int kFirstPollDelay = 10;
+// The XCD-local waits (raw q/k/v, split partials) poll first after 4 units: their round trip is
+// shorter (measured per step against 10 units: 4 / 2: -5 / -4 us; 16: +5 us).
+constexpr int kLocalFirstPollDelay = 4;
 template <int UNITS>
 IRON_DEV void first_poll_delay() { __builtin_amdgcn_s_sleep(UNITS); }
 
@@ -1020,7 +1023,7 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
     };
     bool ok;
     if constexpr (S::XCD_LOCAL)
-      ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1,
+      ok = gather_words<cdiv(n, 256), kLocalFirstPollDelay>(n, src, issue, s_in, p.ctrl + 1,
                                       LocalPoll{});
     else
       ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1);
@@ -1114,7 +1117,7 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
     };
     bool ok;
     if constexpr (S::XCD_LOCAL)
-      ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1,
+      ok = gather_words<cdiv(n, 256), kLocalFirstPollDelay>(n, src, issue, s_in, p.ctrl + 1,
                                       LocalPoll{});
     else
       ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1);
