@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 9
+#define IRON_ABI_VERSION 10
 
 enum iron_status {
   IRON_OK = 0,
@@ -377,20 +377,43 @@ int iron_test_bf16_round(uint32_t* out, void* stream);
  * the achievable HBM read rate that the roofline figures are read against. */
 int iron_stream_read(const void* p, size_t bytes, uint32_t* out, int blocks, void* stream);
 
+/* Measurement hook (no reference counterpart): phase timestamps of the persistent decode kernel.
+ * While a buffer is set, iron_decode_persistent and iron_decode_persistent_gen launch a copy of
+ * the Qwen3-0.6B kernel (the other shape is rejected with IRON_ERR_UNSUPPORTED) that writes, per
+ * layer l and workgroup w, 16 readings of the 100 MHz constant clock to
+ * stamps[(l * 256 + w) * 16 + mark]: 0 QKV phase entry, 1 its input gathered, 2 its rows stored;
+ * 3 attention input gathered, 4 QK-norm/RoPE done, 15 attention tiles done, 5 partials stored;
+ * 6 merge input gathered, 7 outputs stored; 8 Wo input gathered, 9 rows stored; 10 gate/up input
+ * gathered, 11 its RMSNorm prologue done, 12 gh stored; 13 down input gathered, 14 rows stored.
+ * stamp_bytes must cover n_layers * 256 * 16 * 8 bytes (IRON_ERR_WORKSPACE otherwise). Results
+ * are those of the untraced kernel. NULL stops tracing. Process-wide, not thread-safe. */
+int iron_decode_persistent_set_trace(unsigned long long* stamps, size_t stamp_bytes);
+
 /* Measurement hook (no reference counterpart): the grid-wide hand-off a persistent kernel needs
  * between phases, timed alone. 256 workgroups of 256 threads (one per CU; the device needs 256
  * CUs) run n_phases phases; in each, every workgroup publishes its n_words / 256 words of an
- * n_words vector (a multiple of 256, at most 2048) and waits until it has every workgroup's:
+ * n_words vector (a multiple of 256, at most 2048; 32 for the XCD modes) and waits until it has
+ * every workgroup's:
  *   IRON_HANDOFF_TAGGED  -- the persistent decode kernel's own hand-off code: 64-bit
  *                           {tag, payload} words stored in 8 copies, polled from one copy;
  *   IRON_HANDOFF_COUNTER -- one atomic arrival counter polled to the grid size (no vector);
- *   IRON_HANDOFF_FLAGS   -- plain stores, device-scope fences and one flag per workgroup.
+ *   IRON_HANDOFF_FLAGS   -- plain stores, device-scope fences and one flag per workgroup;
+ *   IRON_HANDOFF_XCD_L2  -- the decode kernel's XCD-local hand-off: the 32 workgroups with equal
+ *                           index mod 8 (one XCD) exchange their own n_words vector through that
+ *                           XCD's L2 (sc0 stores, nt polls), 8 groups at once;
+ *   IRON_HANDOFF_XCD_AGENT -- the same groups with device-scope words.
  * Phase p of a launch uses tag base + p + 1: successive launches on one workspace pass distinct
  * bases. The workspace (iron_handoff_probe_workspace bytes) is zero-filled before the first
  * launch, and again before each IRON_HANDOFF_COUNTER launch (its counter starts at zero). Every
  * wait is bounded: after the stream synchronises, a nonzero uint32 at byte
  * iron_handoff_probe_workspace(n_words) - 4096 + 256 of the workspace means a wait gave up. */
-enum iron_handoff_mode { IRON_HANDOFF_TAGGED = 0, IRON_HANDOFF_COUNTER = 1, IRON_HANDOFF_FLAGS = 2 };
+enum iron_handoff_mode {
+  IRON_HANDOFF_TAGGED = 0,
+  IRON_HANDOFF_COUNTER = 1,
+  IRON_HANDOFF_FLAGS = 2,
+  IRON_HANDOFF_XCD_L2 = 3,
+  IRON_HANDOFF_XCD_AGENT = 4
+};
 size_t iron_handoff_probe_workspace(int n_words);
 int iron_handoff_probe(int mode, int n_words, int n_phases, unsigned int base, void* workspace,
                        size_t workspace_bytes, void* stream);

@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
-ABI_VERSION = 9          # IRON_ABI_VERSION of include/iron_hip.h
+ABI_VERSION = 10         # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2
@@ -35,6 +35,8 @@ ACCUM = {"f64": IRON_ACCUM_F64, "f32": IRON_ACCUM_F32}
 IRON_HANDOFF_TAGGED = 0
 IRON_HANDOFF_COUNTER = 1
 IRON_HANDOFF_FLAGS = 2
+IRON_HANDOFF_XCD_L2 = 3
+IRON_HANDOFF_XCD_AGENT = 4
 
 
 def accum_mode(name: str) -> int:
@@ -129,6 +131,7 @@ SIGNATURES = {
     "iron_test_fastdiv": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32]),
     "iron_test_bf16_round": (_c_int, [_c_vp, _c_vp]),
     "iron_stream_read": (_c_int, [_c_vp, _c_sz, _c_vp, _c_int, _c_vp]),
+    "iron_decode_persistent_set_trace": (_c_int, [_c_vp, _c_sz]),
     "iron_handoff_probe_workspace": (_c_sz, [_c_int]),
     "iron_handoff_probe": (_c_int, [_c_int, _c_int, _c_int, ctypes.c_uint, _c_vp, _c_sz, _c_vp]),
 }

@@ -289,16 +289,21 @@ def read_probe(gib: int = 1, reps: int = 5) -> dict:
 
 
 HANDOFF_MODES = {"tagged": _lib.IRON_HANDOFF_TAGGED, "counter": _lib.IRON_HANDOFF_COUNTER,
-                 "flags": _lib.IRON_HANDOFF_FLAGS}
+                 "flags": _lib.IRON_HANDOFF_FLAGS, "xcd_l2": _lib.IRON_HANDOFF_XCD_L2,
+                 "xcd_agent": _lib.IRON_HANDOFF_XCD_AGENT}
 
 
 def handoff_probe(phases: int = 2000, reps: int = 3) -> dict:
     """Microseconds per grid-wide hand-off phase (iron_handoff_probe: 256 workgroups, one per CU):
     the tagged-word exchange at several vector sizes (words every workgroup polls), an atomic
-    counter barrier, and flags with device-scope fences. Best of `reps` launches of `phases`."""
+    counter barrier, flags with device-scope fences, and the exchange inside each XCD's 32
+    workgroups through its L2 or with device-scope words. Best of `reps` launches of `phases`."""
     lib = _lib.load()
+    # xcd_*: 32-workgroup groups (one XCD each); 256 and 640 words are the decode kernel's raw
+    # q/k/v and split-partial gathers
     cases = [("tagged", n) for n in (256, 512, 1024, 2048)] + [("counter", 256),
-                                                                ("flags", 1024)]
+                                                                ("flags", 1024)] + \
+        [(m, n) for m in ("xcd_agent", "xcd_l2") for n in (256, 640)]
     out, base = {}, 0
     for name, n in cases:
         nbytes = lib.iron_handoff_probe_workspace(n)
@@ -323,6 +328,71 @@ def handoff_probe(phases: int = 2000, reps: int = 3) -> dict:
             "kernel": "iron_handoff_probe (256 workgroups x 256 threads, one per CU)"}
 
 
+STAMP_ORDER = (0, 1, 2, 3, 4, 15, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14)  # marks in program order
+
+
+def phase_trace(tokens: int = 6, ctx: int = 2048, first_layer: int = 4) -> dict:
+    """Per-phase timings of the persistent decode kernel (Qwen3-0.6B shape, B=1, random-init
+    weights, KV prefilled to `ctx`) from its phase stamps (iron_decode_persistent_set_trace), for
+    layers first_layer..27 of the last of `tokens` decode steps, medians over layers of:
+    compute -- the median workgroup's time from its input gathered to its output stored;
+    wait    -- the median workgroup's input-gathered time minus the last producer's store (the
+               attention and merge phases count only their own XCD's producers, the only ones
+               they poll);
+    spread  -- the last workgroup's store minus the median workgroup's;
+    and the layer period (QKV entry to QKV entry). Stamps read the 100 MHz constant clock."""
+    import numpy as np
+
+    from .applications.qwen3_0_6b.qwen3_npu_int8 import Qwen3NPU
+    from .applications.qwen3_0_6b.weights import Qwen3Config, random_qwen3_weights, synthetic_kv
+
+    lib = _lib.load()
+    cfg = Qwen3Config.qwen3_0_6b(group_size=32)
+    w = random_qwen3_weights(cfg, seed=2024, device=DEV)
+    k0, v0 = synthetic_kv(cfg, ctx, seed=7)
+    m = Qwen3NPU(config=cfg, weights=w, max_seq_len=(ctx + tokens + 63) // 64 * 64,
+                 persistent=True)
+    m.load_kv(k0, v0)
+    L, NT = cfg.n_layers, 256
+    st = torch.zeros(L * NT * 16, dtype=torch.int64, device=DEV)
+    _lib.check(lib.iron_decode_persistent_set_trace(st.data_ptr(), st.numel() * 8),
+               "iron_decode_persistent_set_trace")
+    try:
+        tok = 17
+        for i in range(tokens):
+            tok = m.step_token(tok, ctx + i)
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(lib.iron_decode_persistent_set_trace(None, 0), "iron_decode_persistent_set_trace")
+    t = st.view(L, NT, 16).cpu().numpy().astype(np.float64) * 0.01  # microseconds
+    grp = np.arange(NT) % 8
+    phases = {"A_qkv": (1, 2), "B_attention": (3, 5), "C_merge": (6, 7), "D_wo": (8, 9),
+              "E_gateup": (10, 12), "F_down": (13, 14)}
+    prev = {"A_qkv": (14, -1, False), "B_attention": (2, 0, True), "C_merge": (5, 0, True),
+            "D_wo": (7, 0, False), "E_gateup": (9, 0, False), "F_down": (12, 0, False)}
+    out = {}
+    for name, (got, end) in phases.items():
+        pm, dl, local = prev[name]
+        waits, comps, spreads = [], [], []
+        for l in range(first_layer, L):
+            pe = t[l + dl, :, pm]
+            last = np.array([pe[grp == g].max() for g in grp]) if local else pe.max()
+            waits.append(np.median(t[l, :, got] - last))
+            comps.append(np.median(t[l, :, end] - t[l, :, got]))
+            spreads.append(t[l, :, end].max() - np.median(t[l, :, end]))
+        out[name] = {"wait_us": round(float(np.median(waits)), 2),
+                     "compute_us": round(float(np.median(comps)), 2),
+                     "spread_us": round(float(np.median(spreads)), 2)}
+    per = [np.median(t[l + 1, :, 0] - t[l, :, 0]) for l in range(first_layer, L - 1)]
+    sub = lambda a, b: round(float(np.median([np.median(t[l, :, a] - t[l, :, b])
+                                              for l in range(first_layer, L)])), 2)
+    return {"phases": out, "layer_period_us": round(float(np.median(per)), 2),
+            "attention_norm_rope_us": sub(4, 3), "attention_tiles_us": sub(15, 4),
+            "attention_partials_us": sub(5, 15), "gateup_prologue_us": sub(11, 10),
+            "context": ctx, "layers": f"{first_layer}..{L - 1}",
+            "kernel": "decode_persistent_kernel<Traced<Shape<1024, 3072, 16, 8>>>"}
+
+
 def copy_probe(mib: int = 256, reps: int = 4) -> dict:
     """A plain device copy of a known size: the calibration run for the HBM byte counters
     (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE read this kernel as mib MiB fetched / written)."""
@@ -344,6 +414,8 @@ if __name__ == "__main__":
                     help="run only the achievable-read-bandwidth probe")
     ap.add_argument("--handoff-probe", action="store_true",
                     help="run only the grid-wide hand-off probe (us per phase per mechanism)")
+    ap.add_argument("--phase-trace", action="store_true",
+                    help="run only the persistent decode kernel's per-phase timing (stamps)")
     ap.add_argument("--only", choices=["c1", "c2", "c3", "c5_prefill", "c5_decode"],
                     help="run one configuration (for profiling)")
     ap.add_argument("--acc", choices=["f64", "f32"], default="f64",
@@ -357,6 +429,8 @@ if __name__ == "__main__":
         print(json.dumps(read_probe()), flush=True)
     elif a.handoff_probe:
         print(json.dumps(handoff_probe()), flush=True)
+    elif a.phase_trace:
+        print(json.dumps(phase_trace()), flush=True)
     elif a.only:
         lib = _lib.load()
         b2, b3 = a.batch or 1, a.batch or 8

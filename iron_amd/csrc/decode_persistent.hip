@@ -123,6 +123,7 @@ struct Shape {
   // (its two query heads, its key and value: 512 rows, 16 per workgroup), run its 32 attention
   // splits and merge its two query heads' outputs, so the raw q/k/v and the split partials
   // travel through that XCD's L2 (xcd_local_*), never through the fabric.
+  static constexpr bool TRACE = false;  // phase timestamps (Traced<>)
   static constexpr bool XCD_LOCAL = HKV == kCopies && NS * HKV == kNT &&
                                     (HB + 2) * HD == 4 * RA * NS && RA == 4 &&
                                     MERGE_PER * NS == HB * HD;
@@ -144,6 +145,12 @@ struct Shape {
 
 using ShapeQwen3_0_6B = Shape<1024, 3072, 16, 8>;
 using ShapeTiny = Shape<256, 768, 4, 2>;
+
+// A shape whose kernel also records phase timestamps (iron_decode_persistent_set_trace).
+template <class S>
+struct Traced : S {
+  static constexpr bool TRACE = true;
+};
 
 struct WireGeom {
   int gshift, tile_m;
@@ -178,7 +185,24 @@ struct PParams {
   const uint16_t* lm_w;        // bf16 [vocab][D]
   const uint16_t* lm_norm;     // bf16 [D]
   uint16_t* logits;            // bf16 [vocab], or null
+  // Traced<> kernels: kStampMarks realtime-clock stamps per (layer, workgroup)
+  unsigned long long* stamps;
 };
+
+// Phase stamps of a traced launch: stamps[(layer * kNT + wg) * kStampMarks + mark], the 100 MHz
+// constant clock (s_memrealtime) read by thread 0 of the workgroup at: 0 QKV phase entry, 1 its
+// input gathered, 2 its rows stored; 3 attention input gathered, 4 QK-norm/RoPE done, 15 tiles
+// done, 5 partials stored; 6 merge input gathered, 7 outputs stored; 8 Wo input gathered, 9 rows
+// stored; 10 gate/up input gathered, 11 prologue done, 12 gh stored; 13 down input gathered,
+// 14 rows stored.
+constexpr int kStampMarks = 16;
+
+template <class S>
+IRON_DEV void stamp(const PParams& p, int wg, int l, int mark) {
+  if constexpr (S::TRACE)
+    if (threadIdx.x == 0)
+      p.stamps[((size_t)l * kNT + wg) * kStampMarks + mark] = __builtin_amdgcn_s_memrealtime();
+}
 
 IRON_DEV GemvParams gemv_of(const WireGeom& g, const void* w, int M, int K) {
   GemvParams p = {};
@@ -778,6 +802,7 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
                         const uint4 (&nwl)[S::CA][2], Issue issue) {
   constexpr int R = S::RA, NCH = S::CA;
   const int lane = threadIdx.x & 63;
+  stamp<S>(p, wg, l, 0);
   const int blk = qkv_block<S>(wg);
   const int row0 = row0_of<S>(blk, R);
   GemvParams g = gemv_of(p.g_qkv, nullptr, S::MQKV, S::D);
@@ -791,6 +816,7 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
                                            p.ctrl + 1))
       return false;
   }
+  stamp<S>(p, wg, l, 1);
   uint4 xl[NCH][4], x2l[NCH][2] = {};
   lane_bf16<NCH>(s_in, S::D, lane, xl);
   float xf[NCH][16];
@@ -827,6 +853,7 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
     static_assert(!S::XCD_LOCAL, "the XCD-local raw rows leave from the even-R branch");
     store_bf16_pairs<R>(h, blk, S::MQKV, p.RAW, tag, s_out, nullptr);
   }
+  stamp<S>(p, wg, l, 2);
   return true;
 }
 
@@ -1029,6 +1056,7 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
       ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1);
     if (!ok) return false;
   }
+  stamp<S>(p, wg, l, 3);
   const uint16_t* s_raw = (const uint16_t*)s_in;  // segment seg: 128 bf16
 
   // QK RMSNorm + RoPE: wave h < HB rotates query head h; wave HB % 4 builds the current token's
@@ -1061,12 +1089,14 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[h][j] = 0.0;
   }
+  stamp<S>(p, wg, l, 4);
   int it = 0;
   for (int t0 = range.begin; t0 < range.end; t0 += kTileTokens, ++it) {
     if (it > 0) load_kv_rows(p, L, head, t0, range.end, kv.kr, kv.vr);
     attn_tile_pairs<kRows>(kv.kr, kv.vr, t0, range.end, has_new, pos, s_new, qf, p.scale, it, m,
                            lsum, o, wave, lane, row, dl);
   }
+  stamp<S>(p, wg, l, 15);
   const uint32_t tp = phase_tag(ep, p.n_layers, l, 1);
   // Word 2 d + k of a partial holds half k of dim d. Each store instruction writes 64 consecutive
   // words (the wavefront's 64 dims, exchanged so lane j holds word j): the hand-off stores write
@@ -1092,6 +1122,7 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
       if (od < 4) put_word(p.PART + part + 2 * kAttnD + od, v32, tp);
     }
   });
+  stamp<S>(p, wg, l, 5);
   return true;
 }
 
@@ -1123,6 +1154,7 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
       ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1);
     if (!ok) return false;
   }
+  stamp<S>(p, wg, l, 6);
   // thread (split sp, dim d): sp = t % NS, d = t / NS holds o_sp[d0 + d], m_sp and l_sp; the
   // max and the two sums run over the NS threads of one d (a wavefront, or two for NS = 128)
   const int t = threadIdx.x, sp = t % NS, d = t / NS;
@@ -1144,6 +1176,7 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
                     phase_tag(ep, p.n_layers, l, 2));
   (void)wave;
   (void)lane;
+  stamp<S>(p, wg, l, 7);
   return true;
 }
 
@@ -1169,6 +1202,7 @@ IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s
                                             p.ctrl + 1))
       return false;
   }
+  stamp<S>(p, wg, l, 8);
   uint4 xl[NCH][4], x2l[NCH][2] = {}, nwl[NCH][2] = {};
   lane_bf16<NCH>(s_in, S::QD, lane, xl);
   float xf[NCH][16];
@@ -1180,6 +1214,7 @@ IRON_DEV bool phase_wo(const PParams& p, int l, int wg, uint32_t ep, uint32_t* s
   for (int r = 0; r < R; ++r) h[r] = f64_to_bf16(acc[r][0]);
   store_bf16_pairs<R, true>(h, wg, S::D, p.AO, phase_tag(ep, p.n_layers, l, 3), s_out, nullptr);
   keep_own_words<R>(s_out, s_own);  // the down phase's residual a
+  stamp<S>(p, wg, l, 9);
   return true;
 }
 
@@ -1212,6 +1247,7 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
     if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src, issue, s_in, p.ctrl + 1))
       return false;
   }
+  stamp<S>(p, wg, l, 10);
   uint4 xl[NCH][4], al[NCH][4], x2l[NCH][2];
   lane_bf16<NCH>(s_x, S::D, lane, xl);
   lane_bf16<NCH>(s_in, S::D, lane, al);
@@ -1222,6 +1258,7 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
   }
   float xf[NCH][16];
   prologue_lane<NCH, 16>(g, lane, xl, x2l, nwl, xf);
+  stamp<S>(p, wg, l, 11);
   double acc[R][1], acc2[R][1];
   dot_w8_lane<R, NCH, false>(g, Wg.w, Wg.sc, xf, row0, lane, acc);
   dot_w8_lane<R, NCH, false>(g, Wu.w, Wu.sc, xf, row0, lane, acc2);
@@ -1247,6 +1284,7 @@ IRON_DEV bool phase_gateup(const PParams& p, int l, int wg, uint32_t ep, uint32_
     put_packed_copies(p.GH + (l % kGhBuffers) * S::GH_WORDS + wg * kGhBlock + t, S::GH_COPY,
                       pack48((const uint32_t*)s_gh, S::GH_ROWS, t),
                       short_tag(phase_tag(ep, p.n_layers, l, 4)));
+  stamp<S>(p, wg, l, 12);
   return true;
 }
 
@@ -1276,6 +1314,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
             S::GH_PROD, gh, short_tag(phase_tag(ep, p.n_layers, l, 4)), issue, s_in, p.ctrl + 1))
       return false;
   }
+  stamp<S>(p, wg, l, 13);
   uint4 xl[NCH][4], x2l[NCH][2] = {}, nwl[NCH][2] = {};
   lane_f32<NCH>(s_in, S::FF, lane, xl);
   float xf[NCH][16];
@@ -1293,6 +1332,7 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   store_bf16_pairs<R, true>(h, wg, S::D, p.X, phase_tag(ep, p.n_layers, l, 5), s_out,
                       l == p.n_layers - 1 ? p.x_out : nullptr);
   keep_own_words<R>(s_out, s_own + S::XW);  // the next layer's residual x (its reads are done)
+  stamp<S>(p, wg, l, 14);
   return true;
 }
 
@@ -1646,6 +1686,12 @@ int device_check(ShapeId id, const char* fn) {
               &nb, decode_persistent_kernel<ShapeQwen3_0_6B>, 256, 0)
         : hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_persistent_kernel<ShapeTiny>,
                                                        256, 0);
+    if (e == hipSuccess && id == SHAPE_0_6B) {
+      int nt = 0;
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &nt, decode_persistent_kernel<Traced<ShapeQwen3_0_6B>>, 256, 0);
+      nb = nt < nb ? nt : nb;
+    }
     if (e != hipSuccess) return iron::fail(IRON_ERR_HIP, "%s: occupancy query failed", fn);
     c = (ncu == kNT && nb >= 1) ? 1 : -1;
     if (c < 0)
@@ -1697,6 +1743,43 @@ __global__ __launch_bounds__(256, 1) void handoff_probe_tagged_kernel(unsigned l
 
 static_assert(spread_word(iron::kHandoffMaxWords - 1) < kCopyWords, "probe vector fits a copy");
 
+// The same exchange inside each XCD (iron_handoff_probe, IRON_HANDOFF_XCD_L2 / _XCD_AGENT): the
+// kCopies groups of workgroups with equal wg % kCopies (one XCD each, as the decode kernel maps
+// its KV heads) exchange n-word vectors in their own region; workgroup wg publishes words
+// [(wg / kCopies) per, +per) of its group's vector, per = n * kCopies / kNT, and waits for all n.
+// L2 = true: put_word_local stores and LocalPoll polls, the raw q/k/v and split-partial hand-off
+// of the kernel; false: device-scope words (one copy), for comparison.
+template <bool L2>
+__global__ __launch_bounds__(256, 1) void handoff_probe_xcd_kernel(unsigned long long* vec,
+                                                                   uint32_t* err, int n,
+                                                                   int n_phases, uint32_t base) {
+  constexpr int NPT = iron::kHandoffMaxWords / kNT;
+  __shared__ uint32_t s_in[NPT * 256];
+  const int wg = blockIdx.x, grp = wg % kCopies, per = n * kCopies / kNT;
+  for (int ph = 0; ph < n_phases; ++ph) {
+    const uint32_t tag = base + (uint32_t)ph + 1u;
+    unsigned long long* buf = vec + (size_t)(ph & 1) * kCopies * kCopyWords;
+    unsigned long long* mine = buf + (size_t)grp * kCopyWords;
+    if ((int)threadIdx.x < per) {
+      const int j = (wg / kCopies) * per + threadIdx.x;
+      if constexpr (L2)
+        put_word_local(xcd_local_rsrc(mine, (size_t)n), (size_t)j, (uint32_t)(ph + wg), tag);
+      else
+        put_word(mine + j, (uint32_t)(ph + wg), tag);
+    }
+    auto src = [&](int j, uint32_t& t) {
+      t = tag;
+      return mine + j;
+    };
+    bool ok;
+    if constexpr (L2)
+      ok = gather_words<NPT, kLocalFirstPollDelay>(n, src, [] {}, s_in, err, LocalPoll{});
+    else
+      ok = gather_words<NPT, kLocalFirstPollDelay>(n, src, [] {}, s_in, err);
+    if (!ok) return;  // workgroup-uniform
+  }
+}
+
 }  // namespace
 
 namespace iron {
@@ -1708,6 +1791,17 @@ int handoff_tagged_launch(void* vec, uint32_t* err, int n, int n_phases, uint32_
                           hipStream_t s) {
   hipLaunchKernelGGL(handoff_probe_tagged_kernel, dim3(kNT), dim3(256), 0, s,
                      (unsigned long long*)vec, err, n, n_phases, base);
+  return check_launch("iron_handoff_probe");
+}
+
+int handoff_xcd_launch(bool l2, void* vec, uint32_t* err, int n, int n_phases, uint32_t base,
+                       hipStream_t s) {
+  if (l2)
+    hipLaunchKernelGGL(handoff_probe_xcd_kernel<true>, dim3(kNT), dim3(256), 0, s,
+                       (unsigned long long*)vec, err, n, n_phases, base);
+  else
+    hipLaunchKernelGGL(handoff_probe_xcd_kernel<false>, dim3(kNT), dim3(256), 0, s,
+                       (unsigned long long*)vec, err, n, n_phases, base);
   return check_launch("iron_handoff_probe");
 }
 
@@ -1757,6 +1851,10 @@ int iron_decode_persistent_check_layer(const iron_layer_desc* layer, int D, int 
 }
 
 }  // extern "C"
+
+// The phase-stamp buffer of iron_decode_persistent_set_trace (null: launches are not traced).
+static unsigned long long* g_stamps = nullptr;
+static size_t g_stamp_bytes = 0;
 
 // Both entry points: `gen` null takes the input row from x_in; otherwise from the embedding row
 // of gen->keys[0]'s token, and the loop's state advances at the end (pos is then written).
@@ -1814,7 +1912,18 @@ static int decode_persistent(const char* fn, const iron_decode_gen* gen,
     return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
   int st = device_check(id, fn);
   if (st) return st;
+  const bool traced = g_stamps != nullptr;
+  if (traced) {
+    if (id != SHAPE_0_6B)
+      return iron::fail(IRON_ERR_UNSUPPORTED, "%s: phase stamps exist for the Qwen3-0.6B shape "
+                        "only", fn);
+    const size_t need = (size_t)n_layers * kNT * kStampMarks * sizeof(unsigned long long);
+    if (g_stamp_bytes < need)
+      return iron::fail(IRON_ERR_WORKSPACE, "%s: stamp buffer %zu < %zu bytes for %d layers", fn,
+                        g_stamp_bytes, need, n_layers);
+  }
   PParams p = {};
+  p.stamps = g_stamps;
   p.layers = layers;
   p.n_layers = n_layers;
   p.max_seq = max_seq;
@@ -1855,7 +1964,10 @@ static int decode_persistent(const char* fn, const iron_decode_gen* gen,
     p.logits = gen->logits;
   }
   hipStream_t s = (hipStream_t)stream;
-  if (id == SHAPE_0_6B)
+  if (traced)
+    hipLaunchKernelGGL(decode_persistent_kernel<Traced<ShapeQwen3_0_6B>>, dim3(kNT), dim3(256), 0,
+                       s, p);
+  else if (id == SHAPE_0_6B)
     hipLaunchKernelGGL(decode_persistent_kernel<ShapeQwen3_0_6B>, dim3(kNT), dim3(256), 0, s,
                        p);
   else
@@ -1877,6 +1989,16 @@ int iron_decode_persistent(const iron_layer_desc* layers, int n_layers, int D, i
                            domain, x_in, x_out, const_cast<int32_t*>(pos),
                            const_cast<uint16_t*>(ang), eps, scale, workspace, workspace_bytes,
                            stream);
+}
+
+int iron_decode_persistent_set_trace(unsigned long long* stamps, size_t stamp_bytes) {
+  iron::clear_error();
+  if (stamps && !iron::aligned(stamps, 8))
+    return iron::fail(IRON_ERR_ALIGN, "iron_decode_persistent_set_trace: stamps not 8-byte "
+                      "aligned");
+  g_stamps = stamps;
+  g_stamp_bytes = stamps ? stamp_bytes : 0;
+  return IRON_OK;
 }
 
 int iron_decode_persistent_gen(const iron_layer_desc* layers, int n_layers, int D, int FF,

@@ -10,7 +10,11 @@
 //                         arrived (a grid barrier; the vector is not exchanged);
 //   IRON_HANDOFF_FLAGS    the slice is written with plain stores, then one device-scope fence
 //                         (L2 write-back) and a per-workgroup flag; consumers poll all flags,
-//                         fence once (L2 invalidate) and read the vector with plain loads.
+//                         fence once (L2 invalidate) and read the vector with plain loads;
+//   IRON_HANDOFF_XCD_L2   the decode kernel's XCD-local hand-off (decode_persistent.hip): the
+//                         32 workgroups of each XCD exchange their own n-word vector through the
+//                         XCD's L2 (sc0 stores, nt polls);
+//   IRON_HANDOFF_XCD_AGENT the same groups with device-scope words, for comparison.
 //
 // Every wait is bounded; a workgroup whose wait fails raises the error word and stops, and the
 // others then fail their own waits, so the grid always drains.
@@ -102,8 +106,9 @@ extern "C" {
 // [2][n] vector), then 4 KiB: the counter at +0, the error word at +256, the flags at +1024.
 static size_t probe_vec_bytes() { return iron::handoff_tagged_bytes(); }
 
+// n_words: a multiple of 256 (a multiple of 32 is enough for the XCD modes), at most 2048.
 size_t iron_handoff_probe_workspace(int n_words) {
-  if (n_words <= 0 || n_words > kProbeMaxWords || n_words % kProbeWGs) return 0;
+  if (n_words <= 0 || n_words > kProbeMaxWords || n_words % (kProbeWGs / 8)) return 0;
   return probe_vec_bytes() + 4096;
 }
 
@@ -111,11 +116,14 @@ int iron_handoff_probe(int mode, int n_words, int n_phases, unsigned int base, v
                        size_t workspace_bytes, void* stream) {
   iron::clear_error();
   const char* fn = "iron_handoff_probe";
-  if (mode != IRON_HANDOFF_TAGGED && mode != IRON_HANDOFF_COUNTER && mode != IRON_HANDOFF_FLAGS)
+  if (mode != IRON_HANDOFF_TAGGED && mode != IRON_HANDOFF_COUNTER && mode != IRON_HANDOFF_FLAGS &&
+      mode != IRON_HANDOFF_XCD_L2 && mode != IRON_HANDOFF_XCD_AGENT)
     return iron::fail(IRON_ERR_SHAPE, "%s: unknown mode %d", fn, mode);
-  if (n_words <= 0 || n_words > kProbeMaxWords || n_words % kProbeWGs || n_phases <= 0)
+  const bool xcd = mode == IRON_HANDOFF_XCD_L2 || mode == IRON_HANDOFF_XCD_AGENT;
+  const int unit = xcd ? kProbeWGs / 8 : kProbeWGs;  // every workgroup publishes whole words
+  if (n_words <= 0 || n_words > kProbeMaxWords || n_words % unit || n_phases <= 0)
     return iron::fail(IRON_ERR_SHAPE, "%s: n_words %d (a multiple of %d up to %d), phases %d", fn,
-                      n_words, kProbeWGs, kProbeMaxWords, n_phases);
+                      n_words, unit, kProbeMaxWords, n_phases);
   const size_t need = iron_handoff_probe_workspace(n_words);
   if (!workspace || workspace_bytes < need)
     return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, workspace_bytes,
@@ -142,6 +150,9 @@ int iron_handoff_probe(int mode, int n_words, int n_phases, unsigned int base, v
   hipStream_t s = (hipStream_t)stream;
   if (mode == IRON_HANDOFF_TAGGED)
     return iron::handoff_tagged_launch(workspace, p.err, n_words, n_phases, base, s);
+  if (mode == IRON_HANDOFF_XCD_L2 || mode == IRON_HANDOFF_XCD_AGENT)
+    return iron::handoff_xcd_launch(mode == IRON_HANDOFF_XCD_L2, workspace, p.err, n_words,
+                                    n_phases, base, s);
   if (mode == IRON_HANDOFF_COUNTER)
     hipLaunchKernelGGL(handoff_probe_kernel<IRON_HANDOFF_COUNTER>, dim3(kProbeWGs), dim3(256), 0,
                        s, p);

@@ -80,6 +80,9 @@ constexpr int kHandoffMaxWords = 2048;
 size_t handoff_tagged_bytes();
 int handoff_tagged_launch(void* vec, uint32_t* err, int n, int n_phases, uint32_t base,
                           hipStream_t s);
+// The same words exchanged inside each XCD's group of 32 workgroups (l2: through its L2).
+int handoff_xcd_launch(bool l2, void* vec, uint32_t* err, int n, int n_phases, uint32_t base,
+                       hipStream_t s);
 
 // The raw-QKV stage shared by the QKV head and the fused QKV head + attention (qkv.hip).
 size_t qkv_raw_bytes(int B, int D, int M);

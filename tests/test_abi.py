@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iron_abi_version() == _lib.ABI_VERSION == 9
+    assert lib.iron_abi_version() == _lib.ABI_VERSION == 10
 
 
 def test_wire_bytes(lib):
@@ -209,12 +209,23 @@ def test_handoff_probe_validation(lib):
     q = lib.iron_handoff_probe_workspace
     assert q(1024) == q(256) == 2 * 8 * 4096 * 8 + 4096  # the tagged mode's 8 copies, twice
     assert q(0) == 0 and q(1000) == 0 and q(2048 + 256) == 0
+    assert q(640) == q(256)  # the XCD modes take multiples of 32
     f = lib.iron_handoff_probe
     ws, fake = q(1024), 1 << 20
-    assert f(3, 1024, 10, 0, fake, ws, None) == _lib.IRON_ERR_SHAPE
+    assert f(5, 1024, 10, 0, fake, ws, None) == _lib.IRON_ERR_SHAPE
     assert b"unknown mode" in lib.iron_last_error()
     assert f(_lib.IRON_HANDOFF_TAGGED, 1000, 10, 0, fake, ws, None) == _lib.IRON_ERR_SHAPE
+    assert f(_lib.IRON_HANDOFF_TAGGED, 640, 10, 0, fake, ws, None) == _lib.IRON_ERR_SHAPE
+    assert f(_lib.IRON_HANDOFF_XCD_L2, 650, 10, 0, fake, ws, None) == _lib.IRON_ERR_SHAPE
     assert f(_lib.IRON_HANDOFF_TAGGED, 1024, 0, 0, fake, ws, None) == _lib.IRON_ERR_SHAPE
     assert f(_lib.IRON_HANDOFF_FLAGS, 1024, 10, 0, None, ws, None) == _lib.IRON_ERR_WORKSPACE
     assert f(_lib.IRON_HANDOFF_FLAGS, 1024, 10, 0, fake, ws - 8, None) == _lib.IRON_ERR_WORKSPACE
     assert f(_lib.IRON_HANDOFF_COUNTER, 1024, 10, 0, fake + 8, ws, None) == _lib.IRON_ERR_ALIGN
+
+
+def test_persistent_trace_setter(lib):
+    """The phase-stamp setter checks alignment and is cleared with NULL (no device access)."""
+    f = lib.iron_decode_persistent_set_trace
+    assert f((1 << 20) + 4, 4096) == _lib.IRON_ERR_ALIGN
+    assert f(1 << 20, 4096) == _lib.IRON_OK
+    assert f(None, 0) == _lib.IRON_OK

@@ -13,7 +13,10 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("mode,n", [(_lib.IRON_HANDOFF_TAGGED, 256),
                                     (_lib.IRON_HANDOFF_TAGGED, 2048),
                                     (_lib.IRON_HANDOFF_COUNTER, 256),
-                                    (_lib.IRON_HANDOFF_FLAGS, 1024)])
+                                    (_lib.IRON_HANDOFF_FLAGS, 1024),
+                                    (_lib.IRON_HANDOFF_XCD_L2, 256),
+                                    (_lib.IRON_HANDOFF_XCD_L2, 640),
+                                    (_lib.IRON_HANDOFF_XCD_AGENT, 640)])
 def test_handoff_probe_completes(lib, mode, n):
     print(f"[case] handoff probe mode={mode} n={n}", flush=True)
     nbytes = lib.iron_handoff_probe_workspace(n)

@@ -230,3 +230,33 @@ def test_persistent_qwen3_0_6b_matches_runlist():
     assert torch.equal(_bits(la), _bits(lb))
     for a, b in zip(ca, cb):
         assert torch.equal(_bits(a[0]), _bits(b[0])) and torch.equal(_bits(a[1]), _bits(b[1]))
+
+
+def test_phase_trace_0_6b_keeps_results():
+    """The traced copy of the Qwen3-0.6B kernel (iron_decode_persistent_set_trace) gives the
+    untraced kernel's logits bit for bit, and every workgroup's 16 stamps of every layer are set
+    and in program order."""
+    from iron_amd import _lib
+    cfg = Qwen3Config.qwen3_0_6b()
+    P0 = 300
+    _say(f"phase trace: qwen3-0.6b, KV {P0}")
+    w = random_qwen3_weights(cfg, seed=11, device="cuda")
+    k0, v0 = synthetic_kv(cfg, P0, seed=5)
+    m = Qwen3NPU(config=cfg, weights=w, max_seq_len=384, persistent=True)
+    m.load_kv(k0, v0)
+    lib = _lib.load()
+    t0 = m.step_token(17, P0)
+    ref = m.logits().clone()
+    st = torch.zeros(cfg.n_layers * 256 * 16, dtype=torch.int64, device="cuda")
+    _lib.check(lib.iron_decode_persistent_set_trace(st.data_ptr(), st.numel() * 8))
+    try:
+        t1 = m.step_token(17, P0)  # the same position again: the same KV row is rewritten
+        torch.cuda.synchronize()
+    finally:
+        _lib.check(lib.iron_decode_persistent_set_trace(None, 0))
+    assert t1 == t0 and torch.equal(_bits(m.logits()), _bits(ref))
+    order = [0, 1, 2, 3, 4, 15, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14]
+    s_ = st.view(cfg.n_layers, 256, 16)[:, :, order].cpu()
+    assert bool((s_ > 0).all()), "a stamp was not written"
+    assert bool((s_[:, :, 1:] >= s_[:, :, :-1]).all()), "stamps out of program order"
+    assert bool((s_[1:, :, 0] >= s_[:-1, :, -1]).all()), "layers out of order"
