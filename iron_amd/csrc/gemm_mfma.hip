@@ -119,7 +119,7 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
   const int row0 = blockIdx.x * kTM;
   const int split = blockIdx.y;
   const int step0 = split * p.ksteps;
-  const int nsteps = p.ksteps;
+  const int nsteps = min(p.ksteps, p.K / kKS - step0);  // the last split may be shorter
   const int ng = p.K >> p.gshift;
   const int G = 1 << p.gshift;
 
@@ -327,23 +327,29 @@ struct GemmPlan {
 };
 
 // Split K until about 512 workgroups cover the chip (two per CU), keeping at least kMinSteps
-// pipeline steps per split: measured per shape at B=16, 6144x4096 20.3 -> 17.0 us and 4096x12288
-// 28.8 -> 24.4 us against one workgroup per CU, while 2048x6144 (48 steps) was best at 8 splits
-// of 6 steps (16 splits of 3: 14.9 against 13.1 us).
+// pipeline steps per split; the last split takes what is left (splits need not divide the steps).
+// Measured per shape at B=16: 6144x4096 20.3 -> 17.0 us and 4096x12288 28.8 -> 24.4 us against
+// one workgroup per CU; 2048x6144 (48 steps) best at 8 splits of 6 steps (16 splits of 3: 14.9
+// against 13.1 us). Config 2 at B=8 (16- and 48-step GEMMs): 33.6 -> 32.3 us with kMinSteps 4 and
+// uneven splits against 6 and even splits; config 5 unchanged (8.82 -> 8.84 ms). Issuing all the
+// loads of a split of at most 4 steps at its start measured slower (config 2 at B=8: 41.6 us; the
+// gate/up kernel then needs 131 VGPRs, one workgroup per CU; for the single-matrix GEMMs alone
+// 34.1 us).
 constexpr int kSplitTarget = 512;
-constexpr int kMinSteps = 6;
+constexpr int kMinSteps = 4;
 GemmPlan plan_gemm(int M, int K) {
   const int tiles = M / kTM;
   const int steps = K / kKS;
-  int splits = (kSplitTarget + tiles - 1) / tiles;
+  int splits = (kSplitTarget + tiles / 2) / tiles;  // nearest to the target
+  if (splits < 1) splits = 1;
   const int by_steps = steps / kMinSteps > 1 ? steps / kMinSteps : 1;
   if (splits > by_steps) splits = by_steps;
   // never fewer workgroups than one per CU would give (short K: 4096x1024 keeps 4 splits)
   const int per_cu = (256 + tiles - 1) / tiles;
   if (splits < per_cu) splits = per_cu;
   if (splits > steps) splits = steps;
-  while (splits > 1 && steps % splits) --splits;
-  return {splits, steps / splits};
+  const int ksteps = (steps + splits - 1) / splits;
+  return {(steps + ksteps - 1) / ksteps, ksteps};  // no empty split
 }
 
 }  // namespace
