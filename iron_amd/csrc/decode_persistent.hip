@@ -344,6 +344,10 @@ constexpr int kFirstPollDelay = 10;
 // The XCD-local waits (raw q/k/v, split partials) poll first after 4 units: their round trip is
 // shorter (measured per step against 10 units: 4 / 2: -5 / -4 us; 16: +5 us).
 constexpr int kLocalFirstPollDelay = 4;
+// The QKV phase's x wait and the down phase's gh wait, retuned after the XCD-local mapping (per
+// token against 10 and 18 units: 4 and 12 -5 us; 6 and 14 -4.5 us; 6 and 10 -1 us; QKV 14 +3 us,
+// down 22 +3 us; the Wo and gate/up waits at 6 or 14 units measured no better than 10).
+constexpr int kQkvFirstPollDelay = 4, kDownFirstPollDelay = 12;
 template <int UNITS>
 IRON_DEV void first_poll_delay() { __builtin_amdgcn_s_sleep(UNITS); }
 
@@ -812,7 +816,7 @@ IRON_DEV bool phase_qkv(const PParams& p, int l, int wg, uint32_t ep, uint32_t* 
     const uint32_t tx = x_tag(ep, p.n_layers, l);
     unsigned long long* const xs = copy_for(p.X, kCopyWords, wg);
     auto src = [&](int j, uint32_t& t) { t = tx; return xs + spread_word(j); };
-    if (!gather_words<cdiv(S::D / 2, 256)>(S::D / 2, src, issue, s_in,
+    if (!gather_words<cdiv(S::D / 2, 256), kQkvFirstPollDelay>(S::D / 2, src, issue, s_in,
                                            p.ctrl + 1))
       return false;
   }
@@ -1308,9 +1312,8 @@ IRON_DEV bool phase_down(const PParams& p, int l, int wg, uint32_t ep, uint32_t*
   {
     // gate/up workgroup q publishes rows [GH_ROWS q, GH_ROWS (q + 1)) in block q
     static_assert(S::GH_ROWS * S::GH_PROD == S::FF, "whole gh blocks");
-    // gh's producers finish last in the layer: a later first poll measured best here (18
-    // units: -4 us per step against 24 and -2 against 12)
-    if (!gather_gh<S::GH_ROWS, cdiv(S::GH_PROD * S::GH_PACKED, 256), 18>(
+    // first poll after kDownFirstPollDelay units (the gh producers finish last in the layer)
+    if (!gather_gh<S::GH_ROWS, cdiv(S::GH_PROD * S::GH_PACKED, 256), kDownFirstPollDelay>(
             S::GH_PROD, gh, short_tag(phase_tag(ep, p.n_layers, l, 4)), issue, s_in, p.ctrl + 1))
       return false;
   }
