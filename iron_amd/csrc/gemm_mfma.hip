@@ -326,12 +326,12 @@ struct GemmPlan {
   int splits, ksteps;
 };
 
-// Split K until about 512 workgroups cover the chip (two per CU), keeping at least kMinSteps
+// Split K until at most 512 workgroups cover the chip (two per CU), keeping at least kMinSteps
 // pipeline steps per split; the last split takes what is left (splits need not divide the steps).
 // Measured per shape at B=16: 6144x4096 20.3 -> 17.0 us and 4096x12288 28.8 -> 24.4 us against
 // one workgroup per CU; 2048x6144 (48 steps) best at 8 splits of 6 steps (16 splits of 3: 14.9
 // against 13.1 us). Config 2 at B=8 (16- and 48-step GEMMs): 33.6 -> 32.3 us with kMinSteps 4 and
-// uneven splits against 6 and even splits; config 5 unchanged (8.82 -> 8.84 ms). Issuing all the
+// uneven splits against 6 and even splits; config 5 8.82 -> 8.73 ms. Issuing all the
 // loads of a split of at most 4 steps at its start measured slower (config 2 at B=8: 41.6 us; the
 // gate/up kernel then needs 131 VGPRs, one workgroup per CU; for the single-matrix GEMMs alone
 // 34.1 us).
@@ -340,7 +340,9 @@ constexpr int kMinSteps = 4;
 GemmPlan plan_gemm(int M, int K) {
   const int tiles = M / kTM;
   const int steps = K / kKS;
-  int splits = (kSplitTarget + tiles / 2) / tiles;  // nearest to the target
+  // at most the target: the 192 row tiles of Qwen3-8B's gate/up took 49.9 us at 2 splits (384
+  // workgroups) against 51.4 us at 3 (576: more than two per CU)
+  int splits = kSplitTarget / tiles;
   if (splits < 1) splits = 1;
   const int by_steps = steps / kMinSteps > 1 ? steps / kMinSteps : 1;
   if (splits > by_steps) splits = by_steps;
