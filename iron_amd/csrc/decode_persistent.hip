@@ -261,8 +261,8 @@ IRON_DEV double word_double(uint32_t lo, uint32_t hi) {
 // XCD-local hand-off (the raw q/k/v rows and the attention split partials of shapes with
 // Shape::XCD_LOCAL): producer and consumers are workgroups of one XCD, which share its L2. The
 // producer's store carries sc0 (written through the CU's L1 into the L2); a consumer polls with nt
-// loads, whose L1 policy is hit-evict, so a line its L1 held from an earlier read is dropped after
-// one read and the next poll is served by the L2. A 64-bit word is written and read whole, as
+// loads (gather_pairs_local), whose L1 policy is hit-evict, so a line its L1 held from an earlier
+// read is dropped after one read and the next poll is served by the L2. A 64-bit word is written and read whole, as
 // with the device-scope words. Both need the workgroups of one hand-off on one XCD, which the
 // kernel's mapping gives when workgroups with equal wg % 8 share an XCD (checked every launch).
 // Measured alone (32 workgroups per XCD, 2000 phases): 0.70 against 0.80 us per phase for 256
@@ -380,25 +380,8 @@ IRON_DEV bool skip_gather(Issue issue) {
   return true;
 }
 
-// Polls of device-scope words (every hand-off but the XCD-local ones).
-struct AgentPoll {
-  static constexpr bool kPlainLoad = false;
-  IRON_DEV unsigned long long operator()(unsigned long long* w) const { return poll_word(w); }
-};
-
-// Polls of XCD-local words (put_word_local): nt loads. They are plain loads to the compiler (a
-// volatile one would be issued past every cache), so gather_words puts a compiler memory barrier
-// before each round to keep them in the loop.
-struct LocalPoll {
-  static constexpr bool kPlainLoad = true;
-  IRON_DEV unsigned long long operator()(unsigned long long* w) const {
-    return __builtin_nontemporal_load((const __attribute__((address_space(1))) unsigned long long*)w);
-  }
-};
-
-template <int NPT, int DELAY = kFirstPollDelay, class Src, class Issue, class Poll = AgentPoll>
-IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t* err,
-                           Poll poll = Poll()) {
+template <int NPT, int DELAY = kFirstPollDelay, class Src, class Issue>
+IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t* err) {
   __syncthreads();  // the previous phase's LDS reads are done before dst is rewritten
   retire_loads();
   first_poll_delay<DELAY>();
@@ -414,16 +397,64 @@ IRON_DEV bool gather_words(int n, Src src, Issue issue, uint32_t* dst, uint32_t*
   bool missing = false;
   for (long long spins = 0;; ++spins) {
     unsigned long long w[NPT];
-    if constexpr (Poll::kPlainLoad) asm volatile("" ::: "memory");
 #pragma unroll
     for (int k = 0; k < NPT; ++k)
-      if (pending[k]) w[k] = poll(ptr[k]);
+      if (pending[k]) w[k] = poll_word(ptr[k]);
     missing = false;
 #pragma unroll
     for (int k = 0; k < NPT; ++k) {
       if (!pending[k]) continue;
       if ((uint32_t)(w[k] >> 32) == want[k]) {
         dst[threadIdx.x + 256 * k] = (uint32_t)w[k];
+        pending[k] = false;
+      } else {
+        missing = true;
+      }
+    }
+    if (!missing || gave_up(spins, err)) break;
+  }
+  if (missing) atomicOr(err, 1u);
+  const bool ok = !workgroup_any(missing);
+  issue_fenced(issue);
+  return ok;
+}
+
+// gather_words for XCD-local words (put_word_local), taken two at a time: thread t polls the word
+// pairs (2p, 2p + 1), p = t + 256 k, with one 16-byte nt load (src(2p) is 16-byte aligned and
+// src(2p + 1) follows it), and checks each word of a pair against its own tag. nt loads are
+// plain loads to the compiler (a volatile one would be issued past every cache), so a compiler
+// memory barrier before each round keeps them in the loop. Polling pairs instead of single words
+// measured -2.5 us per token.
+template <int NPP, int DELAY, class Src, class Issue>
+IRON_DEV bool gather_pairs_local(int n, Src src, Issue issue, uint32_t* dst, uint32_t* err) {
+  __syncthreads();  // the previous phase's LDS reads are done before dst is rewritten
+  retire_loads();
+  first_poll_delay<DELAY>();
+  bool pending[NPP];
+  unsigned long long* ptr[NPP];
+  uint32_t want0[NPP], want1[NPP];
+#pragma unroll
+  for (int k = 0; k < NPP; ++k) {
+    const int j = 2 * ((int)threadIdx.x + 256 * k);
+    pending[k] = j < n;
+    ptr[k] = pending[k] ? src(j, want0[k]) : nullptr;
+    if (pending[k]) (void)src(j + 1, want1[k]);
+  }
+  bool missing = false;
+  for (long long spins = 0;; ++spins) {
+    iron_u32x4 w[NPP];
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < NPP; ++k)
+      if (pending[k])
+        w[k] = __builtin_nontemporal_load(
+            (const __attribute__((address_space(1))) iron_u32x4*)ptr[k]);
+    missing = false;
+#pragma unroll
+    for (int k = 0; k < NPP; ++k) {
+      if (!pending[k]) continue;
+      if (w[k].y == want0[k] && w[k].w == want1[k]) {  // {payload, tag} of words 2p and 2p + 1
+        *(uint2*)&dst[2 * ((int)threadIdx.x + 256 * k)] = make_uint2(w[k].x, w[k].z);
         pending[k] = false;
       } else {
         missing = true;
@@ -1054,8 +1085,8 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
     };
     bool ok;
     if constexpr (S::XCD_LOCAL)
-      ok = gather_words<cdiv(n, 256), kLocalFirstPollDelay>(n, src, issue, s_in, p.ctrl + 1,
-                                      LocalPoll{});
+      ok = gather_pairs_local<cdiv(n, 512), kLocalFirstPollDelay>(n, src, issue, s_in,
+                                                                  p.ctrl + 1);
     else
       ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1);
     if (!ok) return false;
@@ -1152,8 +1183,8 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
     };
     bool ok;
     if constexpr (S::XCD_LOCAL)
-      ok = gather_words<cdiv(n, 256), kLocalFirstPollDelay>(n, src, issue, s_in, p.ctrl + 1,
-                                      LocalPoll{});
+      ok = gather_pairs_local<cdiv(n, 512), kLocalFirstPollDelay>(n, src, issue, s_in,
+                                                                  p.ctrl + 1);
     else
       ok = gather_words<cdiv(n, 256)>(n, src, issue, s_in, p.ctrl + 1);
     if (!ok) return false;
@@ -1750,8 +1781,8 @@ static_assert(spread_word(iron::kHandoffMaxWords - 1) < kCopyWords, "probe vecto
 // kCopies groups of workgroups with equal wg % kCopies (one XCD each, as the decode kernel maps
 // its KV heads) exchange n-word vectors in their own region; workgroup wg publishes words
 // [(wg / kCopies) per, +per) of its group's vector, per = n * kCopies / kNT, and waits for all n.
-// L2 = true: put_word_local stores and LocalPoll polls, the raw q/k/v and split-partial hand-off
-// of the kernel; false: device-scope words (one copy), for comparison.
+// L2 = true: put_word_local stores and gather_pairs_local polls, the raw q/k/v and split-partial
+// hand-off of the kernel; false: device-scope words (one copy), for comparison.
 template <bool L2>
 __global__ __launch_bounds__(256, 1) void handoff_probe_xcd_kernel(unsigned long long* vec,
                                                                    uint32_t* err, int n,
@@ -1776,7 +1807,7 @@ __global__ __launch_bounds__(256, 1) void handoff_probe_xcd_kernel(unsigned long
     };
     bool ok;
     if constexpr (L2)
-      ok = gather_words<NPT, kLocalFirstPollDelay>(n, src, [] {}, s_in, err, LocalPoll{});
+      ok = gather_pairs_local<NPT / 2, kLocalFirstPollDelay>(n, src, [] {}, s_in, err);
     else
       ok = gather_words<NPT, kLocalFirstPollDelay>(n, src, [] {}, s_in, err);
     if (!ok) return;  // workgroup-uniform
