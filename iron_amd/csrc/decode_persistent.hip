@@ -672,23 +672,40 @@ IRON_DEV void keep_own_words(const uint16_t* s_out, uint32_t* own) {
 // over two wavefronts through LDS); every thread of the group receives the result. All 256 threads
 // call it together. Sums add in a fixed tree order.
 // Lane n's value, in every lane.
-IRON_DEV double readlane_d(double v, int n) {
-  return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), n),
-                          __builtin_amdgcn_readlane(__double2loint(v), n));
+// x and y exchange lanes: v_permlane32_swap (ROWS32) swaps x's lanes 32..63 with y's lanes 0..31,
+// v_permlane16_swap swaps x's 16-lane rows 1 and 3 with y's rows 0 and 2; each half of a double
+// moves with one instruction.
+template <bool ROWS32>
+IRON_DEV void swap_lanes_d(double& x, double& y) {
+  const uint32_t xl = (uint32_t)__double2loint(x), xh = (uint32_t)__double2hiint(x);
+  const uint32_t yl = (uint32_t)__double2loint(y), yh = (uint32_t)__double2hiint(y);
+  if constexpr (ROWS32) {
+    const auto lo = __builtin_amdgcn_permlane32_swap(xl, yl, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap(xh, yh, false, false);
+    x = __hiloint2double((int)hi[0], (int)lo[0]);
+    y = __hiloint2double((int)hi[1], (int)lo[1]);
+  } else {
+    const auto lo = __builtin_amdgcn_permlane16_swap(xl, yl, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap(xh, yh, false, false);
+    x = __hiloint2double((int)hi[0], (int)lo[0]);
+    y = __hiloint2double((int)hi[1], (int)lo[1]);
+  }
 }
 
+
 // Maximum / sum over groups of G consecutive lanes, in every lane of the group. G = 32: the four
-// 16-lane DPP steps, then the two rows of each half-wavefront through readlane -- the same
-// pairings as an xor butterfly (lane l with l ^ 1, 2, 4, 8, 16), so the same values, without
-// the LDS round trip of a cross-lane shuffle per step. Other G: xor shuffles, and for G > 64 the
-// wavefronts through LDS.
+// 16-lane DPP steps, then the two rows of each half-wavefront meet through v_permlane16_swap --
+// the same pairings as an xor butterfly (lane l with l ^ 1, 2, 4, 8, 16), so the same values,
+// without an LDS round trip (readlanes of rows 0, 16, 32 and 48 measured 1.4 us per token
+// slower, with the tile maximum's). Other G: xor shuffles, and for G > 64 the wavefronts through
+// LDS.
 template <int G>
 IRON_DEV double group_max(double v, double (&s_red)[4][2]) {
   if constexpr (G == 32) {
     v = row16_max_d(v);
-    const double a = fmax(readlane_d(v, 0), readlane_d(v, 16));
-    const double b = fmax(readlane_d(v, 32), readlane_d(v, 48));
-    return (threadIdx.x & 32) ? b : a;
+    double w = v;
+    swap_lanes_d<false>(v, w);  // rows 0 | 1 and 2 | 3 meet
+    return fmax(v, w);
   }
 #pragma unroll
   for (int k = 1; k < (G < 64 ? G : 64); k <<= 1) v = fmax(v, __shfl_xor(v, k));
@@ -706,9 +723,9 @@ template <int G>
 IRON_DEV double group_sum(double v, double (&s_red)[4][2]) {
   if constexpr (G == 32) {
     v = row16_sum_d(v);
-    const double a = readlane_d(v, 0) + readlane_d(v, 16);
-    const double b = readlane_d(v, 32) + readlane_d(v, 48);
-    return (threadIdx.x & 32) ? b : a;
+    double w = v;
+    swap_lanes_d<false>(v, w);
+    return v + w;
   }
 #pragma unroll
   for (int k = 1; k < (G < 64 ? G : 64); k <<= 1) v += __shfl_xor(v, k);
@@ -1027,11 +1044,11 @@ IRON_DEV void attn_tile_pairs(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end,
       for (int k = 0; k < w; ++k) v[k] += v[k + w];
     if (t0 + pt < t_end) s = v[0] * scale;
   }
-  // row maxima; rows r and r + 2 hold the same head (readlane: no LDS shuffle)
-  const double wm = row16_max_d(s);
-  const double m0 = fmax(readlane_d(wm, 0), readlane_d(wm, 32));
-  const double m1 = fmax(readlane_d(wm, 16), readlane_d(wm, 48));
-  if ((lane & 47) == 0) s_mx[wave][ph] = ph ? m1 : m0;  // lanes 0 and 16: heads 0 and 1
+  // row maxima; rows r and r + 2 hold the same head (a lane exchange: no LDS shuffle)
+  double wm = row16_max_d(s), wm2 = wm;
+  swap_lanes_d<true>(wm, wm2);  // rows r and r + 2 meet: row 0 holds head 0's maximum, row 1 head 1's
+  const double mh = fmax(wm, wm2);
+  if ((lane & 47) == 0) s_mx[wave][ph] = mh;  // lanes 0 and 16: heads 0 and 1
   __syncthreads();
   double mn[2];
 #pragma unroll
@@ -1071,26 +1088,6 @@ IRON_DEV void attn_tile_pairs(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end,
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[h][j] = fma(pe[u][h], vf[j], o[h][j]);
-  }
-}
-
-// x and y exchange lanes: v_permlane32_swap (ROWS32) swaps x's lanes 32..63 with y's lanes 0..31,
-// v_permlane16_swap swaps x's 16-lane rows 1 and 3 with y's rows 0 and 2; each half of a double
-// moves with one instruction.
-template <bool ROWS32>
-IRON_DEV void swap_lanes_d(double& x, double& y) {
-  const uint32_t xl = (uint32_t)__double2loint(x), xh = (uint32_t)__double2hiint(x);
-  const uint32_t yl = (uint32_t)__double2loint(y), yh = (uint32_t)__double2hiint(y);
-  if constexpr (ROWS32) {
-    const auto lo = __builtin_amdgcn_permlane32_swap(xl, yl, false, false);
-    const auto hi = __builtin_amdgcn_permlane32_swap(xh, yh, false, false);
-    x = __hiloint2double((int)hi[0], (int)lo[0]);
-    y = __hiloint2double((int)hi[1], (int)lo[1]);
-  } else {
-    const auto lo = __builtin_amdgcn_permlane16_swap(xl, yl, false, false);
-    const auto hi = __builtin_amdgcn_permlane16_swap(xh, yh, false, false);
-    x = __hiloint2double((int)hi[0], (int)lo[0]);
-    y = __hiloint2double((int)hi[1], (int)lo[1]);
   }
 }
 
