@@ -280,6 +280,14 @@ IRON_DEV void put_word_local(__amdgpu_buffer_rsrc_t rs, size_t word, uint32_t pa
   __builtin_amdgcn_raw_buffer_store_b64(v, rs, (int)(word * 8), 0, kCpolSc0);
 }
 
+// Words `word` and `word` + 1 (16-byte aligned) in one 16-byte store: {p0, tag, p1, tag}. Each
+// 64-bit word is written whole, as put_word_local writes it.
+IRON_DEV void put_pair_local(__amdgpu_buffer_rsrc_t rs, size_t word, uint32_t p0, uint32_t p1,
+                             uint32_t tag) {
+  const iron_u32x4 v = {p0, tag, p1, tag};
+  __builtin_amdgcn_raw_buffer_store_b128(v, rs, (int)(word * 8), 0, kCpolSc0);
+}
+
 // The hardware XCC id of the executing workgroup (HW_REG_XCC_ID, bits 3:0).
 IRON_DEV uint32_t xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xfu; }
 
@@ -1208,25 +1216,28 @@ IRON_DEV bool phase_attn(const PParams& p, const iron_layer_desc& L, int l, int 
   }
   stamp<S>(p, wg, l, 15);
   const uint32_t tp = phase_tag(ep, p.n_layers, l, 1);
-  // Word 2 d + k of a partial holds half k of dim d. Each store instruction writes 64 consecutive
-  // words (the wavefront's 64 dims, exchanged so lane j holds word j): the hand-off stores write
-  // through the L2, which merges nothing, so a store per half would write every sector twice.
+  // Word 2 d + k of a partial holds half k of dim d. XCD-local: thread (oh, od) writes dim od's
+  // two words with one 16-byte store (a wavefront's store covers 1 KB contiguously; against two
+  // lane-exchanged 8-byte stores, -4 us per token). Device-wide:
+  // each store instruction writes 64 consecutive words (the wavefront's 64 dims, exchanged so lane
+  // j holds word j): those stores write through the L2, which merges nothing, so a store per half
+  // would write every sector twice.
   attn_finish_pairs(m, lsum, o, wave, row, dl,
                     [&](int oh, int od, double O, double Ls, double M) {
     const size_t part = ((size_t)(head * HB + oh) * NS + split) * (2 * (kAttnD + 2));
-    const int j = od & 63;
-    const int lo = __double2loint(O), hi = __double2hiint(O);
-    const int lo1 = __shfl(lo, j >> 1), hi1 = __shfl(hi, j >> 1);
-    const int lo2 = __shfl(lo, 32 + (j >> 1)), hi2 = __shfl(hi, 32 + (j >> 1));
-    const size_t w = part + 2 * (od & 64);  // this wavefront's 128 words
     const double v = od < 2 ? M : Ls;       // m and l (the same in every thread of the head)
     const uint32_t v32 = (uint32_t)(od & 1 ? __double2hiint(v) : __double2loint(v));
     if constexpr (S::XCD_LOCAL) {  // read only by this XCD's merge workgroups
       const __amdgpu_buffer_rsrc_t rs = xcd_local_rsrc(p.PART, S::PART_WORDS);
-      put_word_local(rs, w + j, (uint32_t)(j & 1 ? hi1 : lo1), tp);
-      put_word_local(rs, w + 64 + j, (uint32_t)(j & 1 ? hi2 : lo2), tp);
+      put_pair_local(rs, part + 2 * od, (uint32_t)__double2loint(O), (uint32_t)__double2hiint(O),
+                     tp);
       if (od < 4) put_word_local(rs, part + 2 * kAttnD + od, v32, tp);  // words 2 kAttnD .. + 3
     } else {
+      const int j = od & 63;
+      const int lo = __double2loint(O), hi = __double2hiint(O);
+      const int lo1 = __shfl(lo, j >> 1), hi1 = __shfl(hi, j >> 1);
+      const int lo2 = __shfl(lo, 32 + (j >> 1)), hi2 = __shfl(hi, 32 + (j >> 1));
+      const size_t w = part + 2 * (od & 64);  // this wavefront's 128 words
       put_word(p.PART + w + j, (uint32_t)(j & 1 ? hi1 : lo1), tp);
       put_word(p.PART + w + 64 + j, (uint32_t)(j & 1 ? hi2 : lo2), tp);
       if (od < 4) put_word(p.PART + part + 2 * kAttnD + od, v32, tp);
