@@ -5,9 +5,11 @@ Workload: Qwen3-0.6B architecture (28 layers, D=1024, 16Q/8KV x 128, FF=3072, vo
 random-init weights, every linear layer int8 with per-group-32 bf16 scales, bf16 embedding /
 tied LM head / norms; the KV cache is prefilled to 2048 positions (1984 seeded synthetic
 positions + a 64-token seeded prompt run through the decode path), then greedy decoding at B=1.
-A step is one decode token: one HIP-graph replay that consumes the previous argmax on the device,
-runs the 28 layers (by default as one persistent kernel, ``--decode runlist`` for the
-per-operator graph), the final norm and the LM head (argmax fused). ``--warmup`` steps run first,
+A step is one decode token: one launch of the token kernel that consumes the previous argmax on
+the device, runs the 28 layers (by default as one persistent kernel, ``--decode runlist`` for the
+per-operator graph), the final norm and the LM head (argmax fused). The steps run as HIP-graph
+replays with no host synchronisation, 16 token launches per replay on the persistent path
+(Qwen3NPU.decode_steps) and one token per replay on the runlist path. ``--warmup`` steps run first,
 then the position is rewound and ``--steps`` steps are timed between two device
 synchronisations (positions 2048 .. 2048+steps-1).
 
