@@ -654,14 +654,16 @@ IRON_DEV void store_bf16_pairs(const uint16_t (&h)[R], int wg, int M, unsigned l
       if (lane == r) s_out[wave * R + r] = h[r];
   }
   __syncthreads();
-  const int t = threadIdx.x;
-  if (t < 2 * R) {
+  // thread c (2R) + t stores word t of copy c: one store instruction for all copies (-1 us per
+  // token against eight stores from each of 2R threads)
+  const int t = threadIdx.x % (2 * R), c = threadIdx.x / (2 * R);
+  if (c < kCopies) {
     const int row = wg * 4 * R + 2 * t;
     if (row < M) {
       const uint32_t pair = (uint32_t)s_out[2 * t] | ((uint32_t)s_out[2 * t + 1] << 16);
-      put_word_copies(dst + (SPREAD ? spread_word(row / 2) : (size_t)(row / 2)), kCopyWords,
-                      pair, tag);
-      if (plain) ((uint32_t*)plain)[row / 2] = pair;
+      put_word(dst + (size_t)c * kCopyWords +
+                   (SPREAD ? spread_word(row / 2) : (size_t)(row / 2)), pair, tag);
+      if (plain && c == 0) ((uint32_t*)plain)[row / 2] = pair;
     }
   }
 }
