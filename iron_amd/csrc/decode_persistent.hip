@@ -1293,10 +1293,13 @@ IRON_DEV bool phase_merge(const PParams& p, int l, int wg, uint32_t ep, uint32_t
   __shared__ uint16_t s_o16[PER];
   if (sp == 0) s_o16[d] = f64_to_bf16(Lt > 0.0 ? O / Lt : 0.0);
   __syncthreads();
-  if (t < PER / 2)
-    put_word_copies(p.ATT + spread_word((h * kAttnD + d0) / 2 + t), kCopyWords,
-                    (uint32_t)s_o16[2 * t] | ((uint32_t)s_o16[2 * t + 1] << 16),
-                    phase_tag(ep, p.n_layers, l, 2));
+  // thread c (PER / 2) + i stores word i of copy c: one store instruction for all copies (-0.7 us
+  // per token)
+  const int wi = t % (PER / 2), wc = t / (PER / 2);
+  if (wc < kCopies)
+    put_word(p.ATT + (size_t)wc * kCopyWords + spread_word((h * kAttnD + d0) / 2 + wi),
+             (uint32_t)s_o16[2 * wi] | ((uint32_t)s_o16[2 * wi + 1] << 16),
+             phase_tag(ep, p.n_layers, l, 2));
   (void)wave;
   (void)lane;
   stamp<S>(p, wg, l, 7);
