@@ -42,12 +42,12 @@ HBM_PEAK_GBS = 8000.0
 # counters read for a plain 256 MiB device copy (131083.5 KiB fetched, 262144 KiB written).
 LM_HEAD_BF16_TRAFFIC = 311_776_133
 # HBM bytes per launch of the persistent layers kernel (all 28 layers, LM head separate), same
-# method: FETCH_SIZE 350481.19 KiB x 2.0 + WRITE_SIZE 41165.31 KiB x 1.0 at context 1985..2047.
-PERSISTENT_TRAFFIC = 759_938_752
+# method: FETCH_SIZE 350383.56 KiB x 2.0 + WRITE_SIZE 41012.19 KiB x 1.0 at context 1985..2047.
+PERSISTENT_TRAFFIC = 759_582_016
 # HBM bytes per launch of the one-launch token (layers + final norm + LM head + argmax), same
 # method, as a least-squares line in the context over 25 launches at contexts 2057..2081
-# (FETCH_SIZE 505539.19 KiB, WRITE_SIZE 41566.16 KiB at the median): bytes = A + B x context.
-PERSISTENT_TOKEN_TRAFFIC = (829_111_468, 120_237.3)
+# (FETCH_SIZE 505495.62 KiB, WRITE_SIZE 41432.94 KiB at the median): bytes = A + B x context.
+PERSISTENT_TOKEN_TRAFFIC = (832_481_801, 118_479.0)
 
 
 def parse():
