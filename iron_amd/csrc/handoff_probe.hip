@@ -77,8 +77,11 @@ __global__ __launch_bounds__(256) void handoff_probe_kernel(ProbeParams p) {
         __hip_atomic_store(p.flags + wg, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       for (long long s = 0;; ++s) {  // thread t watches workgroup t's flag
-        if (__hip_atomic_load(p.flags + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag)
-          break;
+        // any tag at or past this phase's: a fast workgroup may already have raised its flag
+        // for the next phase before this watcher saw this phase's value
+        const unsigned int f =
+            __hip_atomic_load(p.flags + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((int)(f - tag) >= 0) break;
         if (s >= kProbeSpin ||
             __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
           failed = true;

@@ -7,7 +7,11 @@
 * the device-resident greedy loop reproduces the host-driven loop token for token;
 * compare mode raises on a planted wrong reference (sequence.py:284-324 in the reference tests);
 * Qwen3-0.6B architecture, int8 G=32, bf16 LM head, KV prefilled to 2048 positions, 128 greedy
-  steps: greedy-token agreement with the CPU chain >= 99% under teacher forcing.
+  steps: greedy-token agreement with the CPU chain >= 99% under teacher forcing, and at full size
+  the persistent kernel's last-step logits and the K/V rows it appended are bit-identical to the
+  exact (fp64) chain fed the same tokens; the same at a context past 2560 (every attention split
+  walks two tiles) and at the checkpoint's group size 128 (check_cosine_int8.py:61-70 is the
+  reference's own gate on the same chain).
 """
 
 import pytest
@@ -226,6 +230,41 @@ def test_reference_dispatch_model_matches_hip(tiny, oracle_provider):
         Qwen3NPU(config=cfg, weights=w, max_seq_len=64, dispatch="reference", persistent=True)
 
 
+def _bits(t):
+    return t.contiguous().view(torch.int16)
+
+
+def _teacher_forced_chain(cfg, w, S, kv_init, prompt, toks, start_pos):
+    """The exact CPU chain run over the prompt and then fed the GPU's tokens: returns the chain,
+    the number of steps whose argmax equals the GPU's token, the top1-top2 margins and the last
+    step's logits (the ones the GPU's last launch computed)."""
+    chain = Qwen3CpuChain(cfg, w, S, kv_init=kv_init)
+    pos = start_pos
+    for t in prompt[:-1]:
+        chain.step(t, pos)
+        pos += 1
+    agree, margins, lc = 0, [], None
+    tok = prompt[-1]
+    for i in range(len(toks)):
+        lc = chain.step(tok, pos)
+        top = torch.topk(lc.float(), 2).values
+        margins.append(float(top[0] - top[1]))
+        agree += int(Qwen3CpuChain.argmax(lc) == toks[i])
+        tok = toks[i]
+        pos += 1
+    return chain, agree, margins, lc
+
+
+def _assert_full_size_bits(model, chain, lc, start_pos, end, layers=(0, 13, 27)):
+    """The GPU's last logits and its appended K/V rows [start_pos, end) of a few layers equal the
+    exact chain's bit for bit."""
+    assert torch.equal(_bits(model.logits()), _bits(lc)), "last-step logits differ from the oracle"
+    for i in layers:
+        kg, vg = (c[:, start_pos:end].cpu() for c in model.kv_caches(i))
+        assert torch.equal(_bits(kg), _bits(chain.k_cache[i, :, start_pos:end])), f"K rows, layer {i}"
+        assert torch.equal(_bits(vg), _bits(chain.v_cache[i, :, start_pos:end])), f"V rows, layer {i}"
+
+
 @pytest.mark.slow
 def test_qwen3_0_6b_greedy_agreement():
     """BASELINE config 4 shape at full size; agreement measured under teacher forcing."""
@@ -241,22 +280,40 @@ def test_qwen3_0_6b_greedy_agreement():
     prompt = torch.randint(0, cfg.vocab_size, (n_prompt,), generator=gen).tolist()
     toks = model.generate(prompt, n_new, start_pos=P0)
     assert len(toks) == n_new
+    assert model.persistent and model.fold_lm_head, "config 4 runs the one-launch token"
     _say("qwen3-0.6b: exact CPU chain (teacher forced)")
-    chain = Qwen3CpuChain(cfg, w, S, kv_init=(k0, v0))
-    pos = P0
-    for t in prompt[:-1]:
-        chain.step(t, pos)
-        pos += 1
-    agree, margins = 0, []
-    tok = prompt[-1]
-    for i in range(n_new):
-        lc = chain.step(tok, pos).float()
-        top = torch.topk(lc, 2).values
-        margins.append(float(top[0] - top[1]))
-        agree += int(Qwen3CpuChain.argmax(lc) == toks[i])
-        tok = toks[i]
-        pos += 1
+    chain, agree, margins, lc = _teacher_forced_chain(cfg, w, S, (k0, v0), prompt, toks, P0)
     rate = agree / n_new
     print(f"greedy agreement {agree}/{n_new} = {rate:.4f}; top1-top2 margin min "
           f"{min(margins):.4g} median {sorted(margins)[len(margins) // 2]:.4g}", flush=True)
     assert rate >= 0.99
+    _assert_full_size_bits(model, chain, lc, P0, P0 + n_prompt + n_new - 1)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("group_size,P0,n_prompt,n_new", [
+    (32, 2700, 4, 20),    # past 80 * 32 = 2560 positions: every attention split walks two tiles
+    (128, 600, 4, 20),    # the checkpoint's group (qwen3_npu_int8.py:391)
+])
+def test_qwen3_0_6b_persistent_bit_exact(group_size, P0, n_prompt, n_new):
+    """Full Qwen3-0.6B shape through the one-launch token (persistent kernel with the folded
+    bf16 LM head; 20 steps = one 16-launch graph replay + four single replays): every greedy token
+    is the exact chain's argmax, and the last logits and the appended K/V rows are bit-identical."""
+    cfg = Qwen3Config.qwen3_0_6b(group_size=group_size)
+    S = (P0 + n_prompt + n_new + 63) // 64 * 64
+    _say(f"qwen3-0.6b persistent vs oracle: G={group_size}, KV {P0}, prompt {n_prompt}, "
+         f"{n_new} tokens")
+    w = random_qwen3_weights(cfg, seed=2024 + group_size, device="cuda")
+    k0, v0 = synthetic_kv(cfg, P0, seed=7)
+    model = Qwen3NPU(config=cfg, weights=w, max_seq_len=S)
+    assert model.persistent and model.fold_lm_head
+    model.load_kv(k0, v0)
+    prompt = torch.randint(0, cfg.vocab_size, (n_prompt,),
+                           generator=torch.Generator().manual_seed(65)).tolist()
+    toks = model.generate(prompt, n_new, start_pos=P0)
+    _say(f"qwen3-0.6b G={group_size}: exact CPU chain (teacher forced)")
+    chain, agree, margins, lc = _teacher_forced_chain(cfg, w, S, (k0, v0), prompt, toks, P0)
+    print(f"G={group_size}: argmax agreement {agree}/{n_new}; margin min {min(margins):.4g}",
+          flush=True)
+    assert agree == n_new
+    _assert_full_size_bits(model, chain, lc, P0, P0 + n_prompt + n_new - 1)

@@ -161,7 +161,8 @@ def test_folded_lm_head_generation(kv_layout):
     _say(f"folded LM head, tiny, {kv_layout}")
     cfg = Qwen3Config.tiny()
     w = random_qwen3_weights(cfg, seed=31)
-    prompt, n_new = [9, 4, 33], 12
+    # 20 steps: one replay of the 16-launch graph, then four single-launch replays
+    prompt, n_new = [9, 4, 33], 20
     runs = []
     for fold in (True, False):
         m = Qwen3NPU(config=cfg, weights=w, max_seq_len=64, kv_layout=kv_layout,

@@ -57,8 +57,15 @@ def test_noalloc_matches_workspace_entry_point(lib, acc):
 def test_noalloc_rejects_partials_beyond_the_scratch(lib):
     B, H, KV, L = 255, 8, 2, 128   # 510 workgroups per split: two splits of 4.24 MB
     assert lib.iron_decode_attn_workspace(B, H, KV, 128, L) > SCRATCH
-    fake = 1 << 20
-    rc = lib.iron_decode_attn_noalloc(fake, fake, fake, 0, L * 128, 128, None, L, fake, B, H, KV,
-                                      128, L, ctypes.c_float(0.088), 0, None)
+    print(f"[case] noalloc rejects B={B} H={H} KV={KV} L={L}", flush=True)
+    # real buffers of the declared shape (~17 MB), so that even a launch could not stray
+    q, k, v, _ = _case(B, H, KV, L, [L] * B, seed=3)
+    out = torch.zeros(B * H * 128, dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    rc = lib.iron_decode_attn_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), KV * L * 128,
+                                      L * 128, 128, None, L, out.data_ptr(), B, H, KV, 128, L,
+                                      ctypes.c_float(0.088), 0, s)
     assert rc == _lib.IRON_ERR_WORKSPACE
     assert b"scratch" in lib.iron_last_error()
+    torch.cuda.synchronize()
+    assert not bool(out.view(torch.int16).any()), "a rejected call wrote its output"
