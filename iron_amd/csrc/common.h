@@ -91,6 +91,14 @@ IRON_DEV uint4 ld_global<uint4>(const uint4* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+typedef unsigned int iron_u32x2 __attribute__((ext_vector_type(2)));
+
+template <>
+IRON_DEV uint2 ld_global<uint2>(const uint2* p) {
+  const iron_u32x2 v = *(const __attribute__((address_space(1))) iron_u32x2*)p;
+  return make_uint2(v.x, v.y);
+}
+
 template <>
 IRON_DEV void st_global<uint4>(uint4* p, const uint4& v) {
   const iron_u32x4 u = {v.x, v.y, v.z, v.w};

@@ -1,4 +1,5 @@
-// Batched int8-weight GEMM on MFMA for decode batches above the GEMV path (B = 5..16):
+// Batched int8-weight GEMM on MFMA for the fused blocks' decode batches above the GEMV path
+// (B = 5..16; the entry point iron_gemm_w8a16 takes any B = 1..16):
 //   Y[b][m] = EPI( sum_g s[m][g] * sum_{k in g} q[m][k] * x[b][k] )
 //
 // Reference: there is no int8 batched GEMM in the reference; its bf16 GEMM operator

@@ -1,4 +1,5 @@
-// Weight-streaming GEMV kernels for batch-1..4 decode on gfx950.
+// Weight-streaming GEMV kernels for batch-1..15 decode on gfx950 (the fused QKV head and MLP use
+// batches 1..4; 5..15 reach the batched kernel through iron_gemv_w8a16).
 //
 // Reference path: the int8 W8A16 matvec (aie_kernels/aie2p/mv_int8_signed.cc:60-113, biased
 // form mv_int8.cc:60-115) behind GEMVInt8 (iron/operators/gemv_int8/op.py:20-178), the fused
@@ -24,6 +25,8 @@
 // flight) behind the activation loads, then stages x into LDS (the prologue, overlapping the
 // weight latency), then reduces. A batch whose rows do not all fit in LDS at once (long rows)
 // runs as batch groups, one workgroup per row group and batch group (gemv_kernel, MULTI).
+#include <type_traits>
+
 #include "common.h"
 #include "gemv_core.h"
 #include "internal.h"
@@ -531,6 +534,307 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 }
 
 // ------------------------------------------------------------------------------------------
+// Batched GEMV (batches 5..15, int8 weights): the weights are streamed and converted once per
+// workgroup and multiplied with every batch row, where the batch-group form re-reads and
+// re-converts them per group of four rows.
+//
+// Mapping: wavefront w of workgroup blk owns rows (4 blk + w) R ..; K runs in chunks of kBKC = 512
+// elements, lane l taking elements [c + 8 l, +8) of every row (one 8-byte load per row and chunk,
+// eight weights inside one scale group since G >= 16). Every weight load of the wavefront's rows
+// is issued at the start (all chunks in flight at once: with one chunk ahead the kernel ran at a
+// tenth of the bandwidth). Per chunk the workgroup stages the nb activation rows of the chunk in
+// LDS as fp64 (exact: bf16 / fp32 values, or the fp32 / bf16 rounding of the RMSNorm prologue),
+// loaded one chunk ahead; each lane converts its weights once, q s (exact in fp64: an 8-bit by
+// 8-bit significand product), and runs nb fp64 FMA chains over them. The per-lane partial sums of
+// every (row, batch) output are added over the 64 lanes through LDS at the end.
+//
+// Arithmetic: sum_k (q_k s_g) x_k in fp64 -- every term exact, the accumulation within 2^-53 --
+// then the output rounding of the single-row kernels (the same correctly rounded values).
+// ------------------------------------------------------------------------------------------
+constexpr int kBKC = 512;   // K elements per chunk
+constexpr int kRedRow = 66;  // doubles between the LDS rows of the final lane reduction
+
+// Rows per wavefront for NB batch rows and NCK chunks held in registers: 2 or 1, whichever keeps
+// the weight registers (two per 8-byte slice, one per scale) within 96 and the fp64 accumulators
+// within 64 registers; 0 when neither does or the variant spilled to scratch when compiled (NB = 16
+// beyond 8 chunks): the batch-group kernel runs instead.
+template <int NB, bool DUAL, int NCK>
+constexpr int batch_rows() {
+  constexpr int m = DUAL ? 2 : 1;
+  if (NCK > (NB == 16 ? 8 : 16)) return 0;
+  return (NCK * 2 * m * 3 <= 96 && 2 * NB * m * 2 <= 64) ? 2
+         : (NCK * m * 3 <= 96 && NB * m * 2 <= 64)     ? 1
+                                                        : 0;
+}
+
+template <int NB, bool DUAL, int NCK>
+constexpr int batch_lds_doubles() {
+  constexpr int R = batch_rows<NB, DUAL, NCK>();
+  constexpr int xs = NB * kBKC, red = 4 * R * NB * kRedRow;
+  return xs > red ? xs : red;
+}
+
+// inv[b] = 1 / RMS of batch row b's prologue input (x, or f32(x + x2)), for the RMS prologues:
+// wavefront w reduces rows b = w, w + 4, ... over all of K.
+IRON_DEV void batch_inv_rms(const GemvParams& p, double* s_inv) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n8 = p.K >> 3;
+  for (int b = wave; b < p.nb; b += 4) {
+    const uint4* src = (const uint4*)((const uint16_t*)p.x + (size_t)b * p.x_stride);
+    const uint4* src2 = p.x2 ? (const uint4*)(p.x2 + (size_t)b * p.x2_stride) : nullptr;
+    double ss = 0.0;
+    for (int i = lane; i < n8; i += 64) {
+      float f[8];
+      slot_values(src[i], src2 ? src2[i] : make_uint4(0u, 0u, 0u, 0u), src2 != nullptr, f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
+    }
+    ss = wave_sum_d(ss);
+    if (lane == 0) s_inv[b] = inv_rms(ss, p.K, (double)p.eps);
+  }
+}
+
+// The activation slots of one chunk that thread t stages: slot t + 256 k (k < NB / 4) is row
+// b = slot / 64, elements [c0 + 8 (slot % 64), +8). Loaded a chunk ahead (batch_load), widened
+// and normalised into LDS when the chunk starts (batch_store)
+// (native vector types: a struct of HIP uint4 arrays is not split into registers, and lands in
+// scratch memory)
+template <int NB>
+struct XSlots {
+  iron_u32x4 a[NB / 4], b[NB / 4], n[NB / 4];  // x (bf16, or fp32 low half), x2 / fp32 high half, w
+};
+
+IRON_DEV iron_u32x4 ld16(const void* p) { return *(const iron_u32x4*)p; }
+IRON_DEV uint4 as_uint4(iron_u32x4 v) { return make_uint4(v.x, v.y, v.z, v.w); }
+
+template <int NB>
+IRON_DEV void batch_load(const GemvParams& p, int c0, XSlots<NB>& xr) {
+  constexpr int P8 = kBKC / 8;  // 8-element slots per row and chunk
+  const bool rms = p.pro == PRO_RMS_BF16 || p.pro == PRO_RES_RMS_F32;
+  const iron_u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int k = 0; k < NB / 4; ++k) {
+    const int t = threadIdx.x + 256 * k, b = t / P8, e = c0 + 8 * (t % P8);
+    iron_u32x4 va = zero, vb = zero, vn = zero;
+    if (b < p.nb && e < p.K) {
+      if (p.pro == PRO_F32) {
+        const float* src = (const float*)p.x + (size_t)b * p.x_stride + e;
+        va = ld16(src);
+        vb = ld16(src + 4);
+      } else {
+        va = ld16((const uint16_t*)p.x + (size_t)b * p.x_stride + e);
+        if (p.x2) vb = ld16(p.x2 + (size_t)b * p.x2_stride + e);
+        if (rms) vn = ld16(p.nw + e);
+      }
+    }
+    xr.a[k] = va;
+    xr.b[k] = vb;
+    xr.n[k] = vn;
+  }
+}
+
+// xs[b][e] (fp64) for the chunk's slots: the values stage_x puts in LDS, widened; zeros at or
+// past K. Rows past nb are not written (never read).
+template <int NB>
+IRON_DEV void batch_store(const GemvParams& p, const XSlots<NB>& xr, const double* s_inv,
+                          double* xs) {
+  constexpr int P8 = kBKC / 8;
+  const bool rms = p.pro == PRO_RMS_BF16 || p.pro == PRO_RES_RMS_F32;
+#pragma unroll
+  for (int k = 0; k < NB / 4; ++k) {
+    const int t = threadIdx.x + 256 * k, b = t / P8, i = t % P8;
+    if (b < p.nb) {
+      double v[8];
+      if (p.pro == PRO_F32) {
+        const uint32_t u[8] = {xr.a[k].x, xr.a[k].y, xr.a[k].z, xr.a[k].w,
+                               xr.b[k].x, xr.b[k].y, xr.b[k].z, xr.b[k].w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(u[j]);
+      } else {
+        float f[8];
+        slot_values(as_uint4(xr.a[k]), as_uint4(xr.b[k]), p.x2 != nullptr, f);
+        if (rms) {
+          float wf[8];
+          unpack8(as_uint4(xr.n[k]), wf);
+          const double inv = s_inv[b];
+          const bool to_bf16 = p.pro == PRO_RMS_BF16;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const double y = ((double)f[j] * inv) * (double)wf[j];
+            v[j] = to_bf16 ? round_bf16((float)y) : (float)y;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = f[j];
+        }
+      }
+      // piece j of slot i (elements 8 i + 2 j, +1) at double2 j * 64 + i: a wavefront's access
+      // to piece j covers 64 consecutive 16-byte slots (no bank conflicts; contiguous slots per
+      // lane measured 14.7 M conflict cycles per launch of the Qwen3-1.7B gate/up at batch 8)
+      double2* d = (double2*)(xs + (size_t)b * kBKC);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[j * 64 + i] = make_double2(v[2 * j], v[2 * j + 1]);
+    }
+  }
+}
+
+// Row r's 8-byte weight slice at element e of a chunk and its group scale (clamped addresses;
+// rows past M and elements past K are masked through a zero scale).
+template <int R>
+IRON_DEV void batch_fetch(const GemvParams& p, const uint8_t* __restrict__ wire, int row0, int e,
+                          uint2 (&w)[R], uint32_t (&sc)[R]) {
+  const int K = p.K, ng = K >> p.gshift;
+  const int ec = e < K ? e : 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = row0 + r;
+    const uint32_t rr = row < p.M ? (uint32_t)row : 0u;
+    const uint32_t blk = fastdiv(rr, p.tdiv);
+    const uint32_t in = rr - blk * (uint32_t)p.tile_m;
+    const uint8_t* base = wire + (size_t)blk * p.blk_bytes;
+    w[r] = ld_global((const uint2*)(base + (size_t)in * K + ec));
+    sc[r] = ld_global((const uint16_t*)(base + (size_t)p.tile_m * K) + (size_t)in * ng +
+                      (ec >> p.gshift));
+  }
+}
+
+// acc[r][b] += sum_j (q_j s) x[b][e + j] over this lane's 8 elements of the staged chunk, for the
+// M matrices of the call (two for gate/up, which then read each activation slice once).
+template <int NB, int R, int M>
+IRON_DEV void batch_fma(const GemvParams& p, const uint2 (&w)[M][R], const uint32_t (&sc)[M][R],
+                        int row0, int e, const double* xs, int lane, double (&acc)[M][R][NB]) {
+  double wf[M][R][8];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const double s = slice_scale(p, sc[m][r], row0 + r, e);
+    const uint32_t d[2] = {w[m][r].x ^ p.xor_mask, w[m][r].y ^ p.xor_mask};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wf[m][r][j] = sbyte(d[j >> 2], j & 3) * s;
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b < p.nb) {  // workgroup-uniform; a guarded body keeps acc[r][b] statically indexed
+      const double2* x2 = (const double2*)(xs + (size_t)b * kBKC);
+      double xv[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const double2 t = x2[j * 64 + lane];
+        xv[2 * j] = t.x;
+        xv[2 * j + 1] = t.y;
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[m][r][b] = fma(wf[m][r][j], xv[j], acc[m][r][b]);
+    }
+  }
+}
+
+// The 64-lane totals of this wavefront's R x NB partial sums: lanes 2o and 2o + 1 of output
+// o = r NB + b each add 32 of its 64 partials (through this wavefront's LDS rows), then the pair.
+// Returns output (lane / 2)'s total in lanes 2o, 2o + 1 (garbage in lanes past 2 R NB). Rows are
+// kRedRow doubles apart (16 bytes past a multiple of the 256-byte bank cycle, so the rows the
+// lanes read at one offset fall on different banks) and lane h of a pair reads the odd or even
+// 16-byte pieces of its row.
+
+template <int NB, int R>
+IRON_DEV double batch_reduce(const double (&acc)[R][NB], double* red) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) red[(r * NB + b) * kRedRow + lane] = acc[r][b];
+  // one wavefront's LDS accesses complete in order: its reads below see its writes
+  const int o = lane >> 1, h = lane & 1;
+  double t = 0.0;
+  if (o < R * NB) {
+    const double2* q = (const double2*)(red + o * kRedRow);
+    double v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const double2 d = q[2 * i + h];
+      v[i] = d.x + d.y;
+    }
+#pragma unroll
+    for (int wdt = 8; wdt >= 1; wdt >>= 1)
+#pragma unroll
+      for (int i = 0; i < wdt; ++i) v[i] += v[i + wdt];
+    t = v[0];
+  }
+  return t + dpp_d<0xb1>(t);  // quad_perm [1,0,3,2]: lanes 2o and 2o + 1
+}
+
+template <int NB, bool DUAL, int NCK>
+__global__ __launch_bounds__(256) void gemv_batch_kernel(GemvParams p) {
+  constexpr int R = batch_rows<NB, DUAL, NCK>();
+  static_assert(R > 0, "no register budget for this batch and K");
+  __shared__ __align__(16) double s_buf[batch_lds_doubles<NB, DUAL, NCK>()];
+  __shared__ double s_inv[NB];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + wave) * R;
+  const bool rms = p.pro == PRO_RMS_BF16 || p.pro == PRO_RES_RMS_F32;
+  constexpr int M = DUAL ? 2 : 1;  // matrices (gate, up)
+  uint2 w[NCK][M][R];
+  uint32_t sc[NCK][M][R];
+  XSlots<NB> xr;
+  const int nch = (p.K + kBKC - 1) / kBKC;  // <= NCK
+  // the first chunk's activations, then every weight load of this wavefront's rows, then the
+  // activation statistics while they are in flight
+  batch_load<NB>(p, 0, xr);
+#pragma unroll
+  for (int c = 0; c < NCK; ++c) {
+    if (c < nch) {
+      batch_fetch<R>(p, p.w, row0, c * kBKC + lane * 8, w[c][0], sc[c][0]);
+      if constexpr (DUAL) batch_fetch<R>(p, p.w2, row0, c * kBKC + lane * 8, w[c][M - 1],
+                                         sc[c][M - 1]);
+    }
+  }
+  if (rms) batch_inv_rms(p, s_inv);
+  double acc[M][R][NB];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[m][r][b] = 0.0;
+#pragma unroll
+  for (int c = 0; c < NCK; ++c) {
+    if (c < nch) {  // workgroup-uniform
+      const int e = c * kBKC + lane * 8;
+      __syncthreads();  // the previous chunk's LDS reads (and the statistics) are done
+      batch_store<NB>(p, xr, s_inv, s_buf);
+      if (c + 1 < nch) batch_load<NB>(p, (c + 1) * kBKC, xr);  // streams during this chunk
+      __syncthreads();
+      batch_fma<NB, R, M>(p, w[c], sc[c], row0, e, s_buf, lane, acc);
+    }
+  }
+  __syncthreads();  // the staged activations are no longer read: s_buf becomes the reduction
+  double* red = s_buf + (size_t)wave * R * NB * kRedRow;
+  const double v = batch_reduce<NB, R>(acc[0], red);
+  double v2 = 0.0;
+  if constexpr (DUAL) v2 = batch_reduce<NB, R>(acc[M - 1], red);
+  const int o = lane >> 1, r = o / NB, b = o % NB, row = row0 + r;
+  if ((lane & 1) || o >= R * NB || b >= p.nb || row >= p.M) return;
+  const size_t out = (size_t)b * p.y_stride + row;
+  if (p.epi == EPI_BF16) {
+    ((uint16_t*)p.y)[out] = f64_to_bf16(v);
+  } else if (p.epi == EPI_F32) {
+    ((float*)p.y)[out] = (float)v;
+  } else if (p.epi == EPI_RES_BF16) {
+    const size_t ro = (size_t)b * p.r_stride + row;
+    float x1 = bf16_to_f32(p.r1[ro]);
+    if (p.r2) x1 = x1 + bf16_to_f32(p.r2[ro]);
+    ((uint16_t*)p.y)[out] = f64_to_bf16((double)x1 + v);
+  } else if (p.epi == EPI_SWIGLU_F32) {
+    ((float*)p.y)[out] = (float)silu_mul(v, v2);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
 // Bit-exact dequant: w[m][k] = bf16(q[m][k] * s[m][k/G]). q*s is exact in fp32, so the single
 // RNE rounding is the only rounding (qwen3_npu_int8.py:350-379, op_ours.py:31-43,515-541).
 // ------------------------------------------------------------------------------------------
@@ -630,12 +934,46 @@ bool launch_nch(const GemvParams& p, int NCH, int R, int grid, size_t lds, hipSt
   return false;
 }
 
+// gemv_batch_kernel for batches 5..15 when its registers hold every chunk of K (false: use the
+// batch-group kernel).
+template <int NB, bool DUAL, int NCK>
+bool launch_batch_nck(const GemvParams& p, hipStream_t stream) {
+  constexpr int R = batch_rows<NB, DUAL, NCK>();
+  if constexpr (R == 0) {
+    return false;
+  } else {
+    const long long groups = ((long long)p.M + 4 * R - 1) / (4 * R);
+    if (groups > (1ll << 30)) return false;
+    hipLaunchKernelGGL((gemv_batch_kernel<NB, DUAL, NCK>), dim3((unsigned)groups), dim3(256), 0,
+                       stream, p);
+    return true;
+  }
+}
+
+template <int NB, bool DUAL>
+bool launch_batch_nb(const GemvParams& p, hipStream_t stream) {
+  const int nch = (p.K + kBKC - 1) / kBKC;
+  if (nch <= 4) return launch_batch_nck<NB, DUAL, 4>(p, stream);
+  if (nch <= 8) return launch_batch_nck<NB, DUAL, 8>(p, stream);
+  if (nch <= 16) return launch_batch_nck<NB, DUAL, 16>(p, stream);
+  return false;
+}
+
+template <bool DUAL>
+bool launch_batch(const GemvParams& p, int B, hipStream_t stream) {
+  return B <= 8 ? launch_batch_nb<8, DUAL>(p, stream) : launch_batch_nb<16, DUAL>(p, stream);
+}
+
 template <bool INT8, bool DUAL>
 int launch_gemv(GemvParams p, int B, hipStream_t stream, const char* fn) {
-  if (B < 1 || B > iron::kGemvMaxBatch)
+  if (B < 1 || B > iron::kGemvBatchedMax)
     return iron::fail(IRON_ERR_UNSUPPORTED, "%s: batch %d outside the GEMV path's 1..%d", fn, B,
-                      iron::kGemvMaxBatch);
+                      iron::kGemvBatchedMax);
   p.nb = B;
+  if constexpr (INT8) {
+    if (B > 4 && p.epi != EPI_BF16_ARGMAX && launch_batch<DUAL>(p, B, stream))
+      return iron::check_launch(fn);
+  }
   const int chunk = INT8 ? 1024 : 512;
   const size_t row_bytes = (size_t)((p.K + chunk - 1) / chunk * chunk) * sizeof(float);
   // kernel batch: the rows staged in LDS at once (at most 4, fewer for long rows); larger

@@ -52,7 +52,13 @@ int res_rmsnorm_planes_launch(const uint16_t* cur, const uint16_t* a, const uint
                               hipStream_t stream);
 
 // MFMA batched GEMM (gemm_mfma.hip) for decode batches above the GEMV limit.
+// The fused QKV head and MLP run batches up to kGemvMaxBatch on the GEMV kernels and larger ones
+// on the MFMA GEMM. The standalone GEMV entry point (iron_gemv_w8a16) also takes batches up to
+// kGemvBatchedMax on the exact batched kernel (gemv_batch_kernel); at batch 8 that kernel is bound
+// by its fp64 FMAs (one per weight and batch row) and measured 2x the MFMA GEMM's time on the
+// Qwen3-1.7B MLP, so the fused blocks keep the MFMA path from batch 5.
 constexpr int kGemvMaxBatch = 4;
+constexpr int kGemvBatchedMax = 15;
 constexpr int kGemmMaxBatch = 16;
 // Epilogues: bf16(acc) | silu(acc0) * acc1 in fp32 as three bf16 planes (dual) |
 // bf16(f32(r1 + r2) + acc).

@@ -27,7 +27,7 @@ extern "C" {
 
 static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Layout: the GEMM's split-K counters (kGemmCtrBytes, for every B), then for B <= 4:
+// Layout: the GEMM's split-K counters (kGemmCtrBytes, for every B), then for B <= 4 (GEMV):
 // gh (fp32 [B][FF]) | a (bf16 [B][D]); for B > 4 (MFMA): gh (three bf16 planes [3][B][FF] of
 // the fp32 values) | a (bf16 [B][D]) | hf (planes [3][B][D]) | the split-K partials (shared by
 // the GEMMs, which run in sequence).

@@ -84,7 +84,7 @@ namespace iron {
 static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Bytes of the raw-QKV stage: the GEMM's split-K counters (kGemmCtrBytes, for every B), raw
-// (bf16 [B][M]), and for B > 4 the normalised input (bf16 [B][D]) and the split-K partials.
+// (bf16 [B][M]), and for B > 4 (MFMA) the normalised input (bf16 [B][D]) and the split-K partials.
 size_t qkv_raw_bytes(int B, int D, int M) {
   size_t n = kGemmCtrBytes + round256((size_t)B * M * 2);
   if (B > kGemvMaxBatch) n += round256((size_t)B * D * 2) + gemm_workspace_bound(M, false);

@@ -58,8 +58,8 @@ def test_gemv_rejects_bad_arguments(lib):
     assert f(fake, fake, fake, 1, 64, 144, 48, 4, 0, None) == _lib.IRON_ERR_SHAPE
     # misaligned wire
     assert f(fake + 2, fake, fake, 1, 64, 128, 32, 4, 0, None) == _lib.IRON_ERR_ALIGN
-    # batch > 4 -> unsupported (MFMA path)
-    assert f(fake, fake, fake, 5, 64, 128, 32, 4, 0, None) == _lib.IRON_ERR_UNSUPPORTED
+    # batch 16 -> unsupported on the GEMV path (MFMA GEMM)
+    assert f(fake, fake, fake, 16, 64, 128, 32, 4, 0, None) == _lib.IRON_ERR_UNSUPPORTED
     # unknown domain
     assert f(fake, fake, fake, 1, 64, 128, 32, 4, 7, None) == _lib.IRON_ERR_SHAPE
 

@@ -84,6 +84,12 @@ def test_dequant_bit_exact(M, K, G, tile_m, domain):
     (2048, 6144, 32, 4, 4, "signed"),      # 1.7B down at batch 4 (4 x 6144 staged rows)
     (4096, 12288, 32, 4, 4, "biased"),     # Qwen3-8B down at batch 4: two workgroups of 3 + 1 rows
     (4096, 12288, 32, 4, 2, "signed"),
+    # batches 5..15 on the exact batched kernel (every weight converted once, all rows per pass)
+    (4096, 1024, 32, 4, 5, "signed"),      # Qwen3-0.6B fused QKV at batch 5
+    (6144, 2048, 32, 12, 8, "biased"),     # 1.7B gate/up shape at BASELINE config 2's batch 8
+    (2048, 6144, 32, 4, 8, "signed"),      # 1.7B down at batch 8
+    (1024, 3072, 128, 4, 15, "signed"),    # the largest GEMV batch, reference group size
+    (200, 1040, 16, 8, 13, "signed"),      # ragged K and rows, a partial last batch group
 ])
 def test_gemv_int8(M, K, G, tile_m, B, domain):
     _say(f"gemv M={M} K={K} G={G} tile_m={tile_m} B={B} {domain}")
