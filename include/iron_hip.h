@@ -157,8 +157,10 @@ int iron_qkv_head(const uint16_t* cur, const uint16_t* n_in, const void* wqkv,
                   int Hq, int Hkv, int max_seq, int G, int tile_m, int domain, float eps,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes for iron_decode_attn (split-K partials, sized for either accumulation mode;
- * contents need no initialisation). */
+/* Workspace bytes for iron_decode_attn (the in-kernel merge's arrival counters, then the split-K
+ * partials, sized for either accumulation mode). The first 16 KiB must be zero before the first
+ * call (a zero-filled workspace); every call leaves them zero, so one workspace serves every later
+ * call on the same stream. */
 size_t iron_decode_attn_workspace(int B, int H, int KV, int D, int max_ctx);
 
 /* GQA decode attention, one query token per sequence:
@@ -212,7 +214,8 @@ int iron_decode_attn_verify(const uint16_t* q, const uint16_t* k_cache, const ui
                             int D, int max_ctx, float scale, void* workspace,
                             size_t workspace_bytes, void* stream);
 
-/* Workspace bytes for iron_qkv_attn (raw QKV staging + split-K partials). */
+/* Workspace bytes for iron_qkv_attn (raw QKV staging + the attention's merge counters and split-K
+ * partials). Zero-filled before the first call; every call leaves the counters zero. */
 size_t iron_qkv_attn_workspace(int B, int D, int Hq, int Hkv, int HD, int max_seq);
 
 /* Fused QKV head + decode attention for one decode step, per batch row b (ctx = pos[b] + 1):

@@ -1,5 +1,6 @@
 // GQA decode attention (one query token per sequence) over a bf16 KV cache: split-K across
-// workgroups (flash-decoding), then a merge kernel. A fused variant also performs the QKV head's
+// workgroups (flash-decoding), the last split of each (sequence, head group) to finish merging
+// the group's partials in the same launch (arrival counters in the workspace). A fused variant also performs the QKV head's
 // per-head epilogue (QK RMSNorm, RoPE, KV-cache append) so that the QKV GEMV output feeds
 // attention directly.
 //
@@ -20,7 +21,7 @@
 // offset of a tile is the workgroup-wide maximum (one LDS exchange), so the token rows and the
 // wavefronts hold partial sums under the same offset and combine by plain addition. A row's lanes
 // split the tile's exponentials between them (one exp per (token, head)) and share them with DPP
-// row broadcasts. Splits merge in a second kernel.
+// row broadcasts. The last split to finish merges (merge_last).
 //
 // With one sequence (B == 1) the first tile's K/V loads are issued before the context length is
 // known (bounded by max_ctx, masked afterwards), which takes the length's load off the critical
@@ -41,6 +42,14 @@ using namespace iron::dev;
 constexpr int kD = 128;
 constexpr int kTile = 64;  // 4 waves x 4 rows x 4 unrolled groups
 constexpr int kMaxSplit = 256;  // the merge kernels hold one split weight per thread pair
+// Arrival counters of the in-kernel merge at the front of a split workspace: one per (sequence,
+// KV head, head group). Zero before the first call; the last split to arrive resets its counter,
+// so every call leaves the block zero.
+// Each counter has a 128-byte line of its own: the splits of different groups arrive at about the
+// same time, and device-scope atomics on one line serialise.
+constexpr size_t kAttnCtrBytes = 16384;
+constexpr int kAttnCtrStride = 32;  // words
+constexpr int kAttnCtrs = (int)(kAttnCtrBytes / sizeof(unsigned int)) / kAttnCtrStride;
 
 struct AttnParams {
   const uint16_t* q;       // [B][H][D] (plain mode)
@@ -63,7 +72,10 @@ struct AttnParams {
   int chunk, nsplit;
   double scale;
   float scale2;            // scale * log2(e) (fp32 kernels: scores in the exp2 domain)
-  void* part;              // [B][H][nsplit][D + 2] fp64 (or fp32): o (unnormalised), m, l
+  void* part;              // split partials, rows of D + 2 fp64 (or fp32): o (unnormalised), m, l
+  unsigned int* ctr;       // the in-kernel merge's arrival counters, or null (merge kernel)
+  int bal;                 // balanced split assignment (balanced_slot)
+  int nslot;               // nsplit * B: the workgroups of one head group
 };
 
 // Workgroup coordinates: grid (split, kv * head_groups, b), 256 threads.
@@ -85,6 +97,78 @@ IRON_DEV AttnCoords attn_coords(const AttnParams& p) {
   c.t_begin = blockIdx.x * p.chunk;
   c.t_lim = min(p.max_ctx, c.t_begin + p.chunk);
   return c;
+}
+
+IRON_DEV int wave_sum_int(int v) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+IRON_DEV int wave_scan_int(int v) {  // inclusive prefix sum over the lanes
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Balanced split assignment (B > 1 with per-sequence lengths and the in-kernel merge). The
+// nslot = nsplit * B workgroups of a head group are dealt to the sequences in proportion to their
+// 64-token tiles instead of nsplit each: with T tiles in all, sequence b gets
+//   n_b = min(1 + floor((nslot - B) tiles_b / T), tiles_b, kMaxSplit)
+// slots (one for an empty sequence), consecutive from slot0_b = sum of the earlier n_b', and its
+// tiles are cut into runs of ceil(tiles_b / n_b) tiles -- n_b' <= n_b runs, the last shorter. The
+// longest sequence of a ragged batch then spans about its share of the chip instead of nsplit
+// workgroups. Every wavefront computes the same assignment from the lengths (B <= 128: two per
+// lane); a slot past the last run returns false (no work, no arrival).
+static_assert(kAttnCtrs <= 128, "balanced_slot holds two sequences per lane");
+struct BalancedSlot {
+  int b, j, n, slot0, t_begin, t_lim;  // sequence, run, runs of the sequence, its first slot
+};
+
+template <bool FUSED>
+IRON_DEV bool balanced_slot(const AttnParams& p, int slot, BalancedSlot& a) {
+  const int B = gridDim.z, lane = threadIdx.x & 63;
+  int tl[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int b = lane + 64 * k;
+    int len = 0;
+    if (b < B) len = FUSED ? p.pos[b] + 1 : p.ctx_len[b];
+    len = len < 0 ? 0 : (len > p.max_ctx ? p.max_ctx : len);
+    tl[k] = (len + kTile - 1) / kTile;
+  }
+  const int T = wave_sum_int(tl[0] + tl[1]);
+  const int extra = p.nslot - B;
+  int start = 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int t = tl[k];
+    const bool valid = lane + 64 * k < B;
+    int n = 1 + (T > 0 ? (int)((long long)extra * t / T) : 0);
+    n = min(min(n, max(t, 1)), kMaxSplit);
+    const int ch = t > 0 ? (t + n - 1) / n : 0;  // tiles per run
+    const int nr = valid ? (t > 0 ? (t + ch - 1) / ch : 1) : 0;
+    const int incl = wave_scan_int(nr);
+    const int first = start + incl - nr;
+    const unsigned long long mine = __ballot(valid && slot >= first && slot < first + nr);
+    if (mine) {
+      const int L = __ffsll((long long)mine) - 1;
+      a.b = 64 * k + L;
+      a.slot0 = __builtin_amdgcn_readlane(first, L);
+      a.n = __builtin_amdgcn_readlane(nr, L);
+      a.j = slot - a.slot0;
+      const int chL = __builtin_amdgcn_readlane(ch, L);
+      a.t_begin = a.j * chL * kTile;
+      a.t_lim = min(p.max_ctx, a.t_begin + chL * kTile);
+      return true;
+    }
+    start += __builtin_amdgcn_readlane(incl, 63);
+  }
+  return false;
 }
 
 // One 64-token K/V tile: lane (wave, row, dl) loads rows t0 + 16u + 4 wave + row, dims 8 dl..+8.
@@ -167,10 +251,170 @@ IRON_DEV bool rotate_query_side(const AttnParams& p, const AttnCoords& c, const 
   return has_new;
 }
 
+IRON_DEV float exp2_f(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The split merge of one workgroup's HB query heads, run by the last split to finish (p.ctr): the
+// arithmetic of attn_merge_kernel --
+//   o = sum_s f_s O_s / sum_s f_s L_s,  f_s = e^(m_s - max m)  (exp2 in the fp32 mode)
+// -- with 4 / HB wavefronts per head: every wavefront computes its head's statistics over all
+// splits (lane l holds splits l, l + 64, ...) and sums the O partials of its share of the splits
+// for dims 2l, 2l + 1 (weights broadcast from LDS); the shares add in LDS in a fixed order. The
+// partials were stored write-through (st_agent) and are read with sc1 loads: the statistics, then
+// batches of kMergeW O rows per wavefront (16 at HB = 4, whose attention loop leaves fewer
+// registers), a batch's loads all in flight before the first wait. The code is branch-free and
+// short: only the last split of each group runs it, after every other workgroup has left, so each
+// instruction line it fetches is a cache miss on its critical path.
+// The group's ns split rows of query head h start at row r0 + h hs of p.part.
+template <bool F32, int HB>
+IRON_DEV void merge_last(const AttnParams& p, int b, int h0, int ns, size_t r0, size_t hs) {
+  constexpr int kMergeW = HB == 4 ? 16 : 32;
+  using T = typename std::conditional<F32, float, double>::type;
+  using T2 = typename std::conditional<F32, float2, double2>::type;
+  constexpr int WPH = 4 / HB;  // wavefronts per head
+  constexpr int kRow = (kD + 2) * (int)sizeof(T);  // bytes per split row
+  // wave-uniform in a scalar register, so the buffer descriptor below is scalar too
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
+  const int oh = wave / WPH, qi = wave % WPH, h = h0 + oh;
+  const int per = (ns + WPH - 1) / WPH;
+  const int s0 = qi * per, s1 = min(ns, s0 + per);
+  const T* base = (const T*)p.part + (r0 + (size_t)h * hs) * (kD + 2);
+  const __amdgpu_buffer_rsrc_t rs = agent_rsrc(base, (size_t)ns * kRow);
+  // this wavefront's share of the O rows; the buffer's range ends with it, so the loads of a batch
+  // past its end return zero (and add +0 below)
+  const __amdgpu_buffer_rsrc_t ro =
+      agent_rsrc(base + (size_t)s0 * (kD + 2), (size_t)max(s1 - s0, 0) * kRow);
+  auto ld_pair = [&](__amdgpu_buffer_rsrc_t r, int off) -> T2 {  // two T at byte offset off
+    if constexpr (F32) {
+      const iron_u32x2 v = ld_agent_b64(r, off);
+      return T2{__uint_as_float(v.x), __uint_as_float(v.y)};
+    } else {
+      const iron_u32x4 v = ld_agent_b128(r, off);
+      return T2{__hiloint2double((int)v.y, (int)v.x), __hiloint2double((int)v.w, (int)v.z)};
+    }
+  };
+  T ms[kMaxSplit / 64], ls[kMaxSplit / 64];
+#pragma unroll
+  for (int i = 0; i < kMaxSplit / 64; ++i) {
+    const int sp = l + 64 * i;
+    const T2 ml = ld_pair(rs, (sp < ns ? sp : 0) * kRow + kD * (int)sizeof(T));  // (m, l)
+    ms[i] = sp < ns ? ml.x : (T)-INFINITY;
+    ls[i] = sp < ns ? ml.y : (T)0;
+  }
+  auto issue = [&](int sb, T2 (&v)[kMergeW]) {
+#pragma unroll
+    for (int u = 0; u < kMergeW; ++u) v[u] = ld_pair(ro, (sb + u) * kRow + 2 * l * (int)sizeof(T));
+  };
+  T2 v[kMergeW];
+  issue(0, v);  // the first batch, in flight while the statistics are reduced
+  T mloc = ms[0];
+#pragma unroll
+  for (int i = 1; i < kMaxSplit / 64; ++i) mloc = F32 ? fmaxf(mloc, ms[i]) : fmax(mloc, ms[i]);
+  T M;
+  if constexpr (F32) {
+    M = row16_max(mloc);
+    M = fmaxf(M, __shfl_xor(M, 16));
+    M = fmaxf(M, __shfl_xor(M, 32));
+  } else {
+    M = row16_max_d(mloc);
+    M = fmax(M, __shfl_xor(M, 16));
+    M = fmax(M, __shfl_xor(M, 32));
+  }
+  // the split weights f_s (zero from split ns on), published in LDS for this wavefront's broadcast
+  // reads (a wavefront's LDS accesses complete in order, so its own writes need no barrier)
+  __shared__ T s_f[4][kMaxSplit + kMergeW];
+  T lloc = 0;
+#pragma unroll
+  for (int i = 0; i < kMaxSplit / 64; ++i) {
+    T f = 0;
+    if (64 * i < ns) {
+      if constexpr (F32) f = (M == -INFINITY || ms[i] == -INFINITY) ? 0.f : exp2_f(ms[i] - M);
+      else f = (M == -INFINITY || ms[i] == -INFINITY) ? 0.0 : exp(ms[i] - M);
+      lloc += f * ls[i];
+    }
+    s_f[wave][l + 64 * i] = f;
+  }
+  if (l < kMergeW) s_f[wave][kMaxSplit + l] = 0;
+  __builtin_amdgcn_wave_barrier();
+  const T L = F32 ? (T)wave_sum((float)lloc) : (T)wave_sum_d((double)lloc);
+  T a0[4] = {0, 0, 0, 0}, a1[4] = {0, 0, 0, 0};
+  auto accumulate = [&](int sb, const T2 (&v)[kMergeW]) {
+#pragma unroll
+    for (int u = 0; u < kMergeW; ++u) {
+      const T w = s_f[wave][s0 + sb + u];
+      a0[u & 3] = F32 ? fmaf(w, v[u].x, a0[u & 3]) : fma(w, v[u].x, a0[u & 3]);
+      a1[u & 3] = F32 ? fmaf(w, v[u].y, a1[u & 3]) : fma(w, v[u].y, a1[u & 3]);
+    }
+  };
+  accumulate(0, v);
+  for (int sb = kMergeW; sb < s1 - s0; sb += kMergeW) {  // shares longer than one batch
+    T2 vb[kMergeW];
+    issue(sb, vb);
+    accumulate(sb, vb);
+  }
+  __shared__ T2 s_m[4][64];
+  s_m[wave][l] = T2{(a0[0] + a0[2]) + (a0[1] + a0[3]), (a1[0] + a1[2]) + (a1[1] + a1[3])};
+  __syncthreads();
+  if (qi != 0) return;
+  T o0 = 0, o1 = 0;
+#pragma unroll
+  for (int q = 0; q < WPH; ++q) {
+    o0 += s_m[wave + q][l].x;
+    o1 += s_m[wave + q][l].y;
+  }
+  uint16_t e0, e1;
+  if constexpr (F32) {
+    e0 = f32_to_bf16(L > 0.f ? o0 / L : 0.f);
+    e1 = f32_to_bf16(L > 0.f ? o1 / L : 0.f);
+  } else {
+    e0 = f64_to_bf16(L > 0.0 ? o0 / L : 0.0);
+    e1 = f64_to_bf16(L > 0.0 ? o1 / L : 0.0);
+  }
+  *(uint32_t*)(p.out + ((size_t)b * p.H + h) * kD + 2 * l) = (uint32_t)e0 | ((uint32_t)e1 << 16);
+}
+
+// After this workgroup's partials are stored (write-through): count its arrival on its (sequence,
+// head group) counter; the last of the ns splits merges the group's heads (merge_last).
+template <bool F32, int HB>
+IRON_DEV void merge_if_last(const AttnParams& p, int b, int h0, int ns, size_t r0, size_t hs) {
+  if (!p.ctr) return;
+  const unsigned idx = (unsigned)(b * gridDim.y + blockIdx.y);
+  if (arrive_is_last_wt(p.ctr + idx * kAttnCtrStride, (unsigned)ns))
+    merge_last<F32, HB>(p, b, h0, ns, r0, hs);
+}
+
+// This workgroup's place in the split partials: its split, the splits of its sequence and the
+// rows (merge_last's r0, hs) -- [B][H][nsplit] rows, or in balanced mode [H][nslot] rows with a
+// sequence's runs in consecutive slots. Applies the balanced assignment to c; false: no work.
+struct SplitSlot {
+  int split, ns;
+  size_t r0, hs;
+};
+
+template <bool FUSED>
+IRON_DEV bool split_slot(const AttnParams& p, AttnCoords& c, SplitSlot& q) {
+  q.split = blockIdx.x;
+  q.ns = p.nsplit;
+  q.r0 = (size_t)c.b * p.H * p.nsplit;
+  q.hs = p.nsplit;
+  if (!p.bal) return true;
+  BalancedSlot a;
+  if (!balanced_slot<FUSED>(p, blockIdx.z * p.nsplit + blockIdx.x, a)) return false;
+  c.b = a.b;
+  c.t_begin = a.t_begin;
+  c.t_lim = a.t_lim;
+  q.split = a.j;
+  q.ns = a.n;
+  q.r0 = a.slot0;
+  q.hs = p.nslot;
+  return true;
+}
+
 template <int HB, bool FUSED>
 __global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnParams p) {
-  const AttnCoords c = attn_coords<HB>(p);
-  const int split = blockIdx.x, b = c.b, h0 = c.h0;
+  AttnCoords c = attn_coords<HB>(p);
+  SplitSlot q;
+  if (!split_slot<FUSED>(p, c, q)) return;
+  const int split = q.split, b = c.b, h0 = c.h0;
   const int wave = c.wave, lane = threadIdx.x & 63, row = c.row, dl = c.dl;
   const int t_begin = c.t_begin, t_lim = c.t_lim;
 
@@ -239,17 +483,18 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnParams p) {
 
   attn_finish_f64<HB>(m, l, o, wave, row, dl, [&](int oh, int od, double O, double L, double M) {
     const int hq = h0 + oh;
-    if (p.nsplit == 1) {
+    if (q.ns == 1) {
       p.out[((size_t)b * p.H + hq) * kD + od] = f64_to_bf16(L > 0.0 ? O / L : 0.0);
     } else {
-      double* part = (double*)p.part + (((size_t)b * p.H + hq) * p.nsplit + split) * (kD + 2);
-      part[od] = O;
+      double* part = (double*)p.part + (q.r0 + hq * q.hs + split) * (kD + 2);
+      st_agent(part + od, O);
       if (od == 0) {
-        part[kD] = M;
-        part[kD + 1] = L;
+        st_agent(part + kD, M);
+        st_agent(part + kD + 1, L);
       }
     }
   });
+  if (q.ns > 1) merge_if_last<false, HB>(p, b, h0, q.ns, q.r0, q.hs);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -287,12 +532,13 @@ IRON_DEV void share_all_f(float ev, float (&pe)[4][HB], std::integer_sequence<in
   (share_one_f<Ns, HB>(ev, pe), ...);
 }
 
-IRON_DEV float exp2_f(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int HB, bool FUSED>
 __global__ __launch_bounds__(256) void decode_attn_f32_kernel(AttnParams p) {
-  const AttnCoords c = attn_coords<HB>(p);
-  const int split = blockIdx.x, b = c.b;
+  AttnCoords c = attn_coords<HB>(p);
+  SplitSlot q;
+  if (!split_slot<FUSED>(p, c, q)) return;
+  const int split = q.split, b = c.b;
   const int wave = c.wave, lane = threadIdx.x & 63, row = c.row, dl = c.dl;
   const int t_begin = c.t_begin, t_lim = c.t_lim;
 
@@ -438,17 +684,18 @@ __global__ __launch_bounds__(256) void decode_attn_f32_kernel(AttnParams p) {
       L = fmaf(f[w], lw, L);
     }
     const int hq = c.h0 + oh;
-    if (p.nsplit == 1) {
+    if (q.ns == 1) {
       p.out[((size_t)b * p.H + hq) * kD + od] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
     } else {
-      float* part = (float*)p.part + (((size_t)b * p.H + hq) * p.nsplit + split) * (kD + 2);
-      part[od] = O;
+      float* part = (float*)p.part + (q.r0 + hq * q.hs + split) * (kD + 2);
+      st_agent(part + od, O);
       if (od == 0) {
-        part[kD] = M;
-        part[kD + 1] = L;
+        st_agent(part + kD, M);
+        st_agent(part + kD + 1, L);
       }
     }
   }
+  if (q.ns > 1) merge_if_last<true, HB>(p, b, c.h0, q.ns, q.r0, q.hs);
 }
 
 
@@ -579,10 +826,13 @@ SplitPlan plan_split(int B, int H, int KV, int max_ctx) {
   return sp;
 }
 
+// The split workspace: the merge's arrival counters (kAttnCtrBytes, zero before the first call
+// and after every call), then the partials.
 size_t attn_ws_bytes(int B, int H, int KV, int max_ctx) {
   const SplitPlan sp = plan_split(B, H, KV, max_ctx);
   if (sp.nsplit == 1) return 0;
-  return (((size_t)B * H * sp.nsplit * (kD + 2) * sizeof(double)) + 255) & ~(size_t)255;
+  return kAttnCtrBytes +
+         ((((size_t)B * H * sp.nsplit * (kD + 2) * sizeof(double)) + 255) & ~(size_t)255);
 }
 
 int check_attn_shape(const char* fn, int B, int H, int KV, int D, int max_ctx) {
@@ -609,6 +859,8 @@ int launch_attention(AttnParams p, bool fused, int acc, int B, void* part_ws, si
   const SplitPlan sp = plan_split(B, p.H, p.KV, p.max_ctx);
   p.HG = p.H / p.KV;
   p.HB = sp.hb;
+  p.ctr = nullptr;
+  p.bal = 0;
   p.chunk = sp.chunk;
   p.nsplit = sp.nsplit;
   p.spec = B == 1 ? 1 : 0;
@@ -618,8 +870,15 @@ int launch_attention(AttnParams p, bool fused, int acc, int B, void* part_ws, si
       return iron::fail(IRON_ERR_WORKSPACE, "%s: workspace %zu < %zu bytes", fn, part_bytes, need);
     if (!iron::aligned(part_ws, 256))
       return iron::fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
-    p.part = part_ws;
+    p.part = (char*)part_ws + kAttnCtrBytes;
+    // the last split of each (sequence, head group) merges in the kernel: one launch; with more
+    // groups than counters the merge kernel runs instead
+    const long long groups = (long long)B * p.KV * (p.HG / sp.hb);
+    p.ctr = groups <= kAttnCtrs ? (unsigned int*)part_ws : nullptr;
+    // per-sequence lengths at B > 1: deal the splits by length (B <= kAttnCtrs here)
+    p.bal = p.ctr && B > 1 && (fused || p.ctx_len) ? 1 : 0;
   }
+  p.nslot = sp.nsplit * B;
   dim3 grid(sp.nsplit, p.KV * (p.HG / sp.hb), B);
 #define IRON_ATTN_LAUNCH(HBV)                                                                  \
   do {                                                                                         \
@@ -639,7 +898,7 @@ int launch_attention(AttnParams p, bool fused, int acc, int B, void* part_ws, si
   }
 #undef IRON_ATTN_LAUNCH
   int st = iron::check_launch(fn);
-  if (st || sp.nsplit == 1) return st;
+  if (st || sp.nsplit == 1 || p.ctr) return st;
   if (f32)
     hipLaunchKernelGGL(attn_merge_kernel<true>, dim3(p.H, B), dim3(256), 0, s, p);
   else

@@ -273,6 +273,7 @@ IRON_DEV void attn_finish_f64(const double (&m)[HB], const double (&l)[HB],
                               const double (&o)[HB][8], int wave, int row, int dl, Emit emit) {
   __shared__ double s_o[16][HB][kAttnD];
   __shared__ double s_l[16][HB];
+  __shared__ double s_mm[HB];  // m is the workgroup's (s_mx): thread 0's copy, read by index
   const int rr = wave * 4 + row;
 #pragma unroll
   for (int h = 0; h < HB; ++h) {
@@ -280,6 +281,7 @@ IRON_DEV void attn_finish_f64(const double (&m)[HB], const double (&l)[HB],
     for (int j = 0; j < 8; j += 2)
       *(double2*)&s_o[rr][h][dl * 8 + j] = make_double2(o[h][j], o[h][j + 1]);
     if (dl == 0) s_l[rr][h] = l[h];
+    if (threadIdx.x == 0) s_mm[h] = m[h];
   }
   __syncthreads();
   for (int t = threadIdx.x; t < HB * kAttnD; t += 256) {
@@ -297,12 +299,7 @@ IRON_DEV void attn_finish_f64(const double (&m)[HB], const double (&l)[HB],
         so[r] += so[r + w];
         sl[r] += sl[r + w];
       }
-    const double O = so[0], L = sl[0];
-    double M = m[0];
-#pragma unroll
-    for (int h = 1; h < HB; ++h)
-      if (oh == h) M = m[h];
-    emit(oh, od, O, L, M);
+    emit(oh, od, so[0], sl[0], s_mm[oh]);
   }
 }
 

@@ -291,3 +291,44 @@ IRON_DEV bool arrive_is_last(unsigned int* counter, unsigned int expected) {
   __syncthreads();
   return s_last != 0u;
 }
+
+// The same hand-off without the agent-scope fences, for results the writers store write-through
+// (st_agent: agent-scope stores complete at the device's coherence point, past this XCD's L2) and
+// the merger reads with ld_agent_* (sc1 loads miss this XCD's L2, so no line it cached from an
+// earlier launch is seen). Each thread waits for its own stores (vmcnt 0) before the barrier, so
+// the count follows every store of the workgroup. An agent-scope release fence would instead
+// write back this XCD's whole L2 (buffer_wbl2) in every arriving workgroup, and the acquire would
+// invalidate it.
+IRON_DEV bool arrive_is_last_wt(unsigned int* counter, unsigned int expected) {
+  __shared__ unsigned int s_last_wt;
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned int prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+    s_last_wt = (prev == expected - 1u) ? 1u : 0u;
+    if (s_last_wt) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  return s_last_wt != 0u;
+}
+
+IRON_DEV void st_agent(double* p, double v) {
+  __hip_atomic_store((unsigned long long*)p, (unsigned long long)__double_as_longlong(v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+IRON_DEV void st_agent(float* p, float v) {
+  __hip_atomic_store((unsigned int*)p, __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// sc1 loads of 8 or 16 bytes at byte offset `off` of a raw buffer (up to 2 GiB).
+IRON_DEV __amdgpu_buffer_rsrc_t agent_rsrc(const void* base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufferDword3);
+}
+IRON_DEV iron_u32x2 ld_agent_b64(__amdgpu_buffer_rsrc_t rs, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kCpolSc1);
+}
+IRON_DEV iron_u32x4 ld_agent_b128(__amdgpu_buffer_rsrc_t rs, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kCpolSc1);
+}

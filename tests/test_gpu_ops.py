@@ -162,11 +162,17 @@ def _kv(B, KV, L, D, gen, scale=1.0):
     (3, 16, 2, 128, [0, 63, 64]),             # GQA 8, empty sequence
     (1, 16, 16, 8192, [8191]),                # long context, GQA 1
     (2, 32, 8, 8192, [8192, 5000]),           # Qwen3-8B attention shape, full context
+    (100, 4, 1, 512, "ragged0"),              # B > 64 (two sequences a lane in the split deal), empties
+    (70, 8, 2, 1024, "ragged0"),              # more (sequence, group) pairs than merge counters
 ])
 def test_decode_attention(B, H, KV, L, ctx):
     gen = torch.Generator().manual_seed(B * 100 + L)
     if ctx == "ragged":
         ctx = torch.randint(512, 4097, (B,), generator=gen).tolist()
+    elif ctx == "ragged0":                    # lengths 0..L, every seventh empty
+        ctx = torch.randint(0, L + 1, (B,), generator=gen)
+        ctx[::7] = 0
+        ctx = ctx.tolist()
     _say(f"decode_attn B={B} H={H} KV={KV} L={L} ctx={ctx}")
     D = 128
     q = torch.randn(B, H, D, generator=gen).to(torch.bfloat16)
