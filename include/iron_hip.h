@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define IRON_ABI_VERSION 10
+#define IRON_ABI_VERSION 11
 
 enum iron_status {
   IRON_OK = 0,
@@ -51,6 +51,8 @@ enum iron_weight_kind { IRON_WEIGHT_INT8 = 0, IRON_WEIGHT_BF16 = 1 };
  *                     exp2-form softmax and accumulation (within 1 bf16 ulp of the exact value on
  *                     the parity cases; the contract is rel/abs 1e-2). */
 enum iron_accum { IRON_ACCUM_F64 = 0, IRON_ACCUM_F32 = 1 };
+/* RoPE pairing (rope/op.py method_type): dims (i, i + cols/2), or (2i, 2i + 1). */
+enum iron_rope_method { IRON_ROPE_TWO_HALVES = 0, IRON_ROPE_INTERLEAVED = 1 };
 
 /* ABI version of the loaded library (IRON_ABI_VERSION). No reference counterpart. */
 int iron_abi_version(void);
@@ -97,6 +99,31 @@ int iron_gemm_w8a16(const void* wire, const uint16_t* x, uint16_t* y, int B, int
  * Replaces RMSNorm (iron/operators/rms_norm/op.py:21-130; kernel rms_norm.cc:83-147). */
 int iron_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols, float eps,
                  void* stream);
+
+/* RoPE of bf16 rows: y = bf16(x_a cos_i - x_b sin_i), bf16(x_b cos_i + x_a sin_i) for each pair
+ * (a, b) of `method` (IRON_ROPE_TWO_HALVES: (i, i + cols/2); IRON_ROPE_INTERLEAVED: (2i, 2i + 1)),
+ * i < cols/2, each output exact before its one rounding. angles: [angle_rows][cols] interleaved
+ * [cos_i, sin_i] rows; row r uses angle row r / (rows / angle_rows). cols even, angle_rows divides
+ * rows. Replaces RoPE (iron/operators/rope/op.py:19-96; kernel aie_kernels/generic/rope.cc,
+ * golden rope/reference.py:118-154). */
+int iron_rope(const uint16_t* x, const uint16_t* angles, uint16_t* y, int rows, int cols,
+              int angle_rows, int method, void* stream);
+
+/* Fused QK RMSNorm + RoPE + V copy of one decode QKV vector. qkv_in / qkv_out: bf16
+ * [Q (n_qk_heads - n_v_heads) | K (n_v_heads) | V (n_v_heads)] heads of head_dim; scratch: bf16
+ * [gamma (n_qk_heads x head_dim) | cos (head_dim) | sin (head_dim)]. Q and K head h:
+ * y = bf16(x / sqrt(mean(x^2) + eps) * gamma_h), then out_d = bf16(y_d cos_d - y_{d+m} sin_d)
+ * for d < m = head_dim/2 and bf16(y_d cos_d + y_{d-m} sin_d) above; V heads are copied. With
+ * kv_cache != NULL (the reference's kv_direct) the K heads' outputs and the V heads also go to
+ * the head-major cache [n_v_heads][max_seq][K_t | V_t] at the element offset *kv_offset (device
+ * int32, t * 2 * head_dim): head j's K at j * 2 * max_seq * head_dim + *kv_offset, its V
+ * head_dim later; an offset outside the cache writes nothing there. head_dim even and <= 1024.
+ * Replaces QKNormRoPE (iron/operators/qk_norm_rope/op.py:20-117; kernels
+ * aie_kernels/aie2p/qk_norm_rope.cc, qk_norm_rope_kv.cc; golden qk_norm_rope/reference.py:19-40,
+ * which rounds once at the end where the kernel rounds the normalised head first, as here). */
+int iron_qk_norm_rope(const uint16_t* qkv_in, const uint16_t* scratch, uint16_t* qkv_out,
+                      uint16_t* kv_cache, const int32_t* kv_offset, int head_dim, int n_qk_heads,
+                      int n_v_heads, int max_seq, float eps, void* stream);
 
 /* LM head: logits[b][v] = bf16(W[v] . xn[b]) with xn = bf16(RMSNorm(x[b]) * norm_w) when
  * norm_w != NULL (else xn = x), W int8 wire (w_kind IRON_WEIGHT_INT8) or bf16 [V][D]

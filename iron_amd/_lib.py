@@ -16,7 +16,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libiron_hip.so"
 
-ABI_VERSION = 10         # IRON_ABI_VERSION of include/iron_hip.h
+ABI_VERSION = 11         # IRON_ABI_VERSION of include/iron_hip.h
 IRON_OK = 0
 IRON_ERR_NULL = -1
 IRON_ERR_SHAPE = -2
@@ -32,6 +32,8 @@ IRON_WEIGHT_BF16 = 1
 IRON_ACCUM_F64 = 0
 IRON_ACCUM_F32 = 1
 ACCUM = {"f64": IRON_ACCUM_F64, "f32": IRON_ACCUM_F32}
+IRON_ROPE_TWO_HALVES = 0
+IRON_ROPE_INTERLEAVED = 1
 IRON_HANDOFF_TAGGED = 0
 IRON_HANDOFF_COUNTER = 1
 IRON_HANDOFF_FLAGS = 2
@@ -80,6 +82,9 @@ SIGNATURES = {
     "iron_gemm_w8a16": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                  _c_int, _c_vp, _c_sz, _c_vp]),
     "iron_rmsnorm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_f, _c_vp]),
+    "iron_rope": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp]),
+    "iron_qk_norm_rope": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int,
+                                   _c_int, _c_f, _c_vp]),
     "iron_lm_head": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_int, _c_int,
                               _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "iron_next_token": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp,

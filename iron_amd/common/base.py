@@ -54,7 +54,7 @@ class AIERuntimeArgSpec:
     def __post_init__(self) -> None:
         if self.direction not in {"in", "out", "inout"}:
             raise ValueError(
-                f"Invalid direction {self.direction!r}: must be one of 'in', 'out', 'inout'"
+                f"argument direction {self.direction!r} is not 'in', 'out' or 'inout'"
             )
 
     @property
@@ -137,7 +137,8 @@ class MLIROperator(AIEOperatorBase):
     def name(self) -> str:
         if not dataclasses.is_dataclass(self):
             raise NotImplementedError(
-                f"{type(self).__name__} must be a @dataclass or override the name property"
+                f"{type(self).__name__}: the operator name is built from dataclass fields; "
+                "declare the class with @dataclass or define its own name"
             )
         aliases = type(self)._name_aliases
         parts = (

@@ -10,10 +10,12 @@ _OPERATOR_MODULES = {
     "GEMV": "gemv",
     "GEMVInt8": "gemv_int8",
     "MHA": "mha",
+    "QKNormRoPE": "qk_norm_rope",
     "QKVHeadAttention": "qkv_attn",
     "QKVHeadDataParallel": "qkv_head_dp",
     "QKVHeadDataParallelOurs": "qkv_head_dp:op_ours",
     "RMSNorm": "rms_norm",
+    "RoPE": "rope",
     "SwiGLUMLPDataParallel": "swiglu_mlp_dp",
     "SwiGLUMLPDataParallelOurs": "swiglu_mlp_dp:op_ours",
 }

@@ -1,0 +1,1 @@
+"""Operator package (see op.py)."""

@@ -8,6 +8,12 @@ reference operator's own ``reference()`` method:
                                  packed argmax key is returned (the host argmax of
                                  qwen3_npu_int8.py:612-621)
   RMSNorm                     -- rms_norm/op.py:125-130
+  RoPE                        -- rope/op.py:84-96 (two halves; the interleaved method as
+                                 rope/reference.py:94-112)
+  QKNormRoPE                  -- qk_norm_rope/reference.py:19-40 with the kernel's bf16 normalised
+                                 head (qk_norm_rope.cc:42-108); with kv_direct (``params`` holding
+                                 the element offset) the K|V slice written into ``last``, the
+                                 cache returned after qkv_out is written into its argument
   DecodeAttention             -- decode_attn/reference.py:26-38; the runtime bound S_kv_eff when
                                  use_runtime_seq_len (else every key is valid); batch/verify mode
                                  (batch_queries > 0) with the per-query bound of
@@ -33,7 +39,7 @@ import torch
 from .attention import causal_prefill_attention, decode_attention, decode_attention_verify
 from .blocks import qkv_head, swiglu_mlp
 from .gemv import gemv_exact, unpack_wire
-from .norms import rms_norm
+from .norms import qk_norm_rope, rms_norm, rope, rope_interleaved
 
 
 def _domain(op) -> str:
@@ -111,6 +117,26 @@ def reference(op, *inputs, params=None, last=None):
         x = inputs[0]
         w = inputs[1] if op.weighted else None
         return rms_norm(x, w, op.epsilon)
+    if name == "RoPE":
+        x, ang = inputs[0].reshape(op.rows, op.cols), inputs[1].reshape(op.angle_rows, op.cols)
+        return (rope if op.method_type == 0 else rope_interleaved)(x, ang)
+    if name == "QKNormRoPE":
+        qkv, scratch = inputs[0].reshape(-1), inputs[2].reshape(-1)
+        out = qk_norm_rope(qkv, scratch, op.n_qk_heads, op.n_v_heads, op.head_dim, op.epsilon)
+        if not op.kv_direct:
+            return out
+        if last is None:
+            raise ValueError("the kv_direct golden needs the pre-step cache (last=)")
+        inputs[1].reshape(-1)[: out.numel()].copy_(out)
+        HD, S, nv, nq = op.head_dim, op.max_seq_len, op.n_v_heads, op.n_qk_heads - op.n_v_heads
+        off = _param(params, op.kv_offset_parameter, 1)[0]
+        cache = last.cpu().clone().reshape(-1)
+        if 0 <= off and off + 2 * HD <= 2 * S * HD:
+            for j in range(nv):
+                base = j * 2 * S * HD + off
+                cache[base: base + HD] = out[(nq + j) * HD: (nq + j + 1) * HD]
+                cache[base + HD: base + 2 * HD] = out[(nq + nv + j) * HD: (nq + nv + j + 1) * HD]
+        return cache
     if name == "DecodeAttention":
         H, KV, D, S, B = op.num_heads, op.num_kv_heads, op.head_dim, op.seq_len_kv, op.batch
         verify = op.batch_queries > 0

@@ -28,7 +28,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.iron_abi_version() == _lib.ABI_VERSION == 10
+    assert lib.iron_abi_version() == _lib.ABI_VERSION == 11
 
 
 def test_wire_bytes(lib):
@@ -87,6 +87,43 @@ def test_attention_rejects_bad_arguments(lib):
     assert call(L=4096, cc=4096) == _lib.IRON_ERR_WORKSPACE
     assert lib.iron_decode_attn_workspace(1, 16, 8, 128, 4096) > 0
     assert lib.iron_decode_attn_workspace(1, 16, 8, 64, 4096) == 0
+
+
+def test_rope_and_qk_norm_rope_reject_bad_arguments(lib):
+    fake = 1 << 20
+    r = lib.iron_rope
+    assert r(None, fake, fake, 4, 128, 4, 0, None) == _lib.IRON_ERR_NULL
+    assert r(fake, fake, fake, 4, 127, 4, 0, None) == _lib.IRON_ERR_SHAPE      # odd cols
+    assert r(fake, fake, fake, 6, 128, 4, 0, None) == _lib.IRON_ERR_SHAPE      # 4 does not divide 6
+    assert r(fake, fake, fake, 4, 128, 8, 0, None) == _lib.IRON_ERR_SHAPE      # more angle rows
+    assert r(fake, fake, fake, 4, 128, 0, 0, None) == _lib.IRON_ERR_SHAPE
+    assert r(fake, fake, fake, 4, 128, 4, 2, None) == _lib.IRON_ERR_UNSUPPORTED
+    assert b"method" in lib.iron_last_error()
+    q = lib.iron_qk_norm_rope
+    assert q(fake, None, fake, None, None, 128, 24, 8, 0, 1e-6, None) == _lib.IRON_ERR_NULL
+    assert q(fake, fake, fake, None, None, 127, 24, 8, 0, 1e-6, None) == _lib.IRON_ERR_SHAPE
+    assert q(fake, fake, fake, None, None, 2048, 24, 8, 0, 1e-6, None) == _lib.IRON_ERR_SHAPE
+    assert q(fake, fake, fake, None, None, 128, 8, 9, 0, 1e-6, None) == _lib.IRON_ERR_SHAPE
+    # the cache write needs the device offset and the cache length
+    assert q(fake, fake, fake, fake, None, 128, 24, 8, 512, 1e-6, None) == _lib.IRON_ERR_SHAPE
+    assert q(fake, fake, fake, fake, fake, 128, 24, 8, 0, 1e-6, None) == _lib.IRON_ERR_SHAPE
+
+
+def test_rope_operators_reject_invalid_shapes():
+    """The reference operators' constraints (rope/op.py:37-52) and the QKV layout."""
+    from iron_amd.operators import QKNormRoPE, RoPE
+    for kw in (dict(rows=32, cols=48), dict(rows=32, cols=64, angle_rows=12),
+               dict(rows=32, cols=64, angle_rows=64), dict(rows=32, cols=64, method_type=2),
+               dict(rows=6, cols=64, num_aie_columns=4)):
+        with pytest.raises(ValueError):
+            RoPE(**kw)
+    with pytest.raises(ValueError):
+        QKNormRoPE(qkv_dim=4000, head_dim=128, n_qk_heads=24, n_v_heads=8)
+    with pytest.raises(ValueError):
+        QKNormRoPE(qkv_dim=1280, head_dim=128, n_qk_heads=2, n_v_heads=8)
+    op = QKNormRoPE(qkv_dim=4096, head_dim=128, n_qk_heads=24, n_v_heads=8, kv_direct=True)
+    assert op.kv_cache_elems == 8 * 2 * 512 * 128
+    assert [s.shape for s in op.get_arg_spec()] == [(4096,), (4096,), (3328,), (1048576,)]
 
 
 def test_status_to_exception(lib):

@@ -226,6 +226,82 @@ def test_rope_angle_table_closed_form():
     assert abs(float(t[pos, 2 * i + 1]) - math.sin(ang)) <= 2 ** -8 * 2
 
 
+def test_rope_halves_pins():
+    """With duplicated halves it is ``rope`` (pinned above) bit for bit; closed forms at 0 and
+    90 degrees; with distinct halves the second half uses its own entries (a restatement that
+    reused cos[:m] / sin[:m] for both halves fails the last check)."""
+    HD, m = 128, 64
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(5, HD, generator=g).to(torch.bfloat16)
+    table = on.rope_angle_table(4096, HD, 1e6)
+    for pos in (0, 1, 777, 4095):
+        c, s = table[pos][0::2], table[pos][1::2]
+        got = on.rope_halves(x, torch.cat([c, c]), torch.cat([s, s]))
+        assert torch.equal(got, on.rope(x, table[pos]))
+    one, zero = torch.ones(HD, dtype=torch.bfloat16), torch.zeros(HD, dtype=torch.bfloat16)
+    assert torch.equal(on.rope_halves(x, one, zero), x)
+    assert torch.equal(on.rope_halves(x, zero, one), torch.cat([-x[:, m:], x[:, :m]], dim=-1))
+    cos = torch.cat([one[:m], zero[:m]])
+    sin = torch.cat([zero[:m], one[:m]])
+    want = torch.cat([x[:, :m], x[:, :m]], dim=-1)        # y1 = x1; y2 = x2*0 + x1*1
+    assert torch.equal(on.rope_halves(x, cos, sin), want)
+    reused = torch.cat([x[:, :m] * cos[:m] - x[:, m:] * sin[:m],
+                        x[:, m:] * cos[:m] + x[:, :m] * sin[:m]], dim=-1)
+    assert not torch.equal(reused, want)                   # the check tells the two apart
+
+
+def test_rope_interleaved_is_the_two_halves_form_on_permuted_dims():
+    """Gathering the even dims then the odd ones turns pairs (2i, 2i+1) into (i, i + m): the
+    interleaved method is ``rope`` (pinned above) conjugated by that permutation, also with
+    block-shared angle rows; plus the 90-degree closed form."""
+    HD, m = 128, 64
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(6, HD, generator=g).to(torch.bfloat16)
+    ang = on.rope_angle_table(512, HD, 1e4)[torch.tensor([5, 300, 511])]
+    perm = torch.cat([x[:, 0::2], x[:, 1::2]], dim=-1)
+    two = on.rope(perm, ang)
+    want = torch.empty_like(x)
+    want[:, 0::2], want[:, 1::2] = two[:, :m], two[:, m:]
+    assert torch.equal(on.rope_interleaved(x, ang), want)
+    quarter = torch.zeros(1, HD, dtype=torch.bfloat16)
+    quarter[0, 1::2] = 1.0                                    # cos 0, sin 1
+    y = on.rope_interleaved(x, quarter)
+    assert torch.equal(y[:, 0::2], -x[:, 1::2]) and torch.equal(y[:, 1::2], x[:, 0::2])
+
+
+def test_qk_norm_rope_pins():
+    """V is copied; at angle 0 each Q/K head is its RMSNorm with its own gamma row (pinned
+    above); a head's output depends on that head only (scaling one head's input by 4 leaves
+    every output but that head's unchanged, and that head's within one bf16 ulp); the golden's
+    single rounding stays within the reference test's tolerance of the kernel's two."""
+    n_q, n_v, HD = 4, 2, 128
+    n_qk = n_q + n_v
+    g = torch.Generator().manual_seed(12)
+    qkv = torch.randn((n_qk + n_v) * HD, generator=g).to(torch.bfloat16)
+    gamma = (torch.randn(n_qk * HD, generator=g) * 0.2 + 1.0).to(torch.bfloat16)
+    one, zero = torch.ones(HD, dtype=torch.bfloat16), torch.zeros(HD, dtype=torch.bfloat16)
+    out = on.qk_norm_rope(qkv, torch.cat([gamma, one, zero]), n_qk, n_v, HD, 1e-6)
+    assert torch.equal(out[n_qk * HD:], qkv[n_qk * HD:])
+    heads = qkv[: n_qk * HD].reshape(n_qk, HD)
+    want = on.rms_norm(heads, gamma.reshape(n_qk, HD), 1e-6)
+    assert torch.equal(out[: n_qk * HD].reshape(n_qk, HD), want)
+    table = on.rope_angle_table(1024, HD, 1e6)
+    c, s = table[321][0::2], table[321][1::2]
+    sc = torch.cat([gamma, c, c, s, s])
+    a = on.qk_norm_rope(qkv, sc, n_qk, n_v, HD, 1e-6)
+    scaled = qkv.clone()
+    scaled[2 * HD: 3 * HD] = (scaled[2 * HD: 3 * HD].float() * 4).to(torch.bfloat16)
+    b = on.qk_norm_rope(scaled, sc, n_qk, n_v, HD, 1e-6)
+    rest = torch.ones(a.numel(), dtype=torch.bool)
+    rest[2 * HD: 3 * HD] = False
+    assert torch.equal(a[rest], b[rest])
+    d = (a[2 * HD: 3 * HD].float() - b[2 * HD: 3 * HD].float()).abs()
+    assert (d <= a[2 * HD: 3 * HD].float().abs() * 2 ** -7 + 1e-30).all()
+    gold = on.qk_norm_rope(qkv, sc, n_qk, n_v, HD, 1e-6, round_norm=False)
+    err = (a.float() - gold.float()).abs()
+    assert (err <= 0.02 + 0.05 * gold.float().abs()).all()
+
+
 # ----------------------------------------------------------------------------------- attention
 
 
