@@ -44,10 +44,15 @@ LM_HEAD_BF16_TRAFFIC = 311_776_133
 # HBM bytes per launch of the persistent layers kernel (all 28 layers, LM head separate), same
 # method: FETCH_SIZE 350383.56 KiB x 2.0 + WRITE_SIZE 41012.19 KiB x 1.0 at context 1985..2047.
 PERSISTENT_TRAFFIC = 759_582_016
-# HBM bytes per launch of the one-launch token (layers + final norm + LM head + argmax), same
-# method, as a least-squares line in the context over 25 launches at contexts 2057..2081
-# (FETCH_SIZE 505495.62 KiB, WRITE_SIZE 41432.94 KiB at the median): bytes = A + B x context.
-PERSISTENT_TOKEN_TRAFFIC = (832_481_801, 118_479.0)
+# HBM bytes per launch of the one-launch token (layers + final norm + LM head + argmax): a profiled
+# constant, not measured in the run. Same method, over this bench's default run (128 steps): the
+# median of the 24 event-timed launches at context 2177, FETCH_SIZE 512911.72 KiB x 2.0 +
+# WRITE_SIZE 41840.75 KiB x 1.0. At another context the KV read term moves it by the cache bytes
+# per position.
+PERSISTENT_TOKEN_TRAFFIC = 1_093_288_128
+PERSISTENT_TOKEN_TRAFFIC_CTX = 2177
+TRAFFIC_SOURCE = ("profiled constant: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over this "
+                  "bench's default run (profiles/decode_qwen3_0_6b_hbm_traffic.md)")
 
 
 def parse():
@@ -159,14 +164,16 @@ def main():
         tok_bytes = (wb["layers"] + kv_per_pos * ctx + kv_per_pos + cfg.emb_dim * 2 +
                      lm_bytes + wb["final_norm"])
         tok_gbs = tok_bytes / (token_us * 1e-6) / 1e9
+        tok_traffic = int(PERSISTENT_TOKEN_TRAFFIC +
+                          kv_per_pos * (ctx - PERSISTENT_TOKEN_TRAFFIC_CTX))
         roofline = {"bound": "hbm", "kernel": "decode_persistent_kernel (28 layers: QKV, "
                                               "attention, merge, Wo, gate/up, down; final "
                                               "RMSNorm, bf16 LM head, argmax)",
                     "achieved": round(tok_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(tok_gbs / HBM_PEAK_GBS, 4),
-                    "traffic": int(PERSISTENT_TOKEN_TRAFFIC[0] + PERSISTENT_TOKEN_TRAFFIC[1] * ctx),
-                    "traffic_ratio": round((PERSISTENT_TOKEN_TRAFFIC[0] +
-                                            PERSISTENT_TOKEN_TRAFFIC[1] * ctx) / tok_bytes, 3),
+                    "traffic": tok_traffic,
+                    "traffic_ratio": round(tok_traffic / tok_bytes, 3),
+                    "traffic_source": TRAFFIC_SOURCE,
                     "bytes_per_launch": int(tok_bytes), "avg_launch_us": round(token_us, 2),
                     "context": ctx}
     elif model.persistent:
@@ -227,7 +234,7 @@ def main():
         torch.cuda.empty_cache()
         from iron_amd import benchmarks
         print("[bench] configs 1, 2, 3, 5", file=sys.stderr, flush=True)
-        result["configs"] = benchmarks.run_all()
+        result["configs"] = benchmarks.run_all(read_ceiling=rc)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, w_cpu, (k0, v0), prompt, tokens, start, S,
                                               args.cpu_sample_steps)

@@ -113,7 +113,13 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
   __shared__ __align__(16) uint8_t s_w[2][NM][kTM][kWRow];
   __shared__ __align__(16) uint16_t s_s[2][NM][kTM][kKS / 32];
   __shared__ __align__(16) uint16_t s_x[2][NX][kBN][kXRow];
-  __shared__ __align__(16) double s_acc[4][NM][4][64];  // the upper half's sums (end)
+  // the upper half's sums at the end, in the weight tiles' space past the split-K staging (s_part
+  // below): 16 KiB less LDS, so two dual workgroups fit on a CU (measured neutral: the kernel is
+  // bound by its issue, not its occupancy)
+  constexpr size_t kAccOff = (sizeof(double) * NM * kBN * (kTM + 1) + 255) & ~(size_t)255;
+  static_assert(kAccOff + sizeof(double) * 4 * NM * 4 * 64 <= sizeof(s_w), "s_acc fits in s_w");
+  double (*const s_acc)[NM][4][64] =
+      reinterpret_cast<double (*)[NM][4][64]>(&s_w[0][0][0][0] + kAccOff);
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int half = wave >> 2;  // the 64-wide half of every step this wavefront multiplies
