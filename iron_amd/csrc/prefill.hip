@@ -62,18 +62,27 @@ IRON_DEV StageIdx stage_idx(int tid) {
   return StageIdx{tid / TPG, (tid % TPG) * 8, tid % NG, (tid / NG) * 8};
 }
 
+// The K and V of one (sequence, KV head) as raw buffers of S rows: a block's loads take its byte
+// offset as the scalar operand and each thread's fixed offset (rows 4 g .. +3 of the block,
+// dims d .. +8; the row steps are immediates), so a block costs no address arithmetic. Keys past
+// S (the last block at D = 64 when S is not a multiple of 128) read as zero: they lie past every
+// query, so the causal mask drops their scores and their probabilities are zero.
+struct KVSrc {
+  __amdgpu_buffer_rsrc_t k, v;
+  int koff, voff;  // this thread's byte offsets within a block
+};
+
 template <int D, int KB>
-IRON_DEV void pf_gload(const uint16_t* kbase, const uint16_t* vbase, int kb, const StageIdx& x,
-                       int S, KVRegs& r) {
-  const int k0 = kb * KB + 4 * x.kg, v0 = kb * KB + 4 * x.vg;
-  r.k0 = *(const u32x4*)(kbase + (size_t)min(k0, S - 1) * D + x.kd);
-  r.k1 = *(const u32x4*)(kbase + (size_t)min(k0 + 1, S - 1) * D + x.kd);
-  r.k2 = *(const u32x4*)(kbase + (size_t)min(k0 + 2, S - 1) * D + x.kd);
-  r.k3 = *(const u32x4*)(kbase + (size_t)min(k0 + 3, S - 1) * D + x.kd);
-  r.v0 = *(const u32x4*)(vbase + (size_t)min(v0, S - 1) * D + x.vd);
-  r.v1 = *(const u32x4*)(vbase + (size_t)min(v0 + 1, S - 1) * D + x.vd);
-  r.v2 = *(const u32x4*)(vbase + (size_t)min(v0 + 2, S - 1) * D + x.vd);
-  r.v3 = *(const u32x4*)(vbase + (size_t)min(v0 + 3, S - 1) * D + x.vd);
+IRON_DEV void pf_gload(const KVSrc& src, int kb, KVRegs& r) {
+  const int sb = kb * KB * D * 2;
+  r.k0 = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.koff, sb, 0);
+  r.k1 = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.koff + D * 2, sb, 0);
+  r.k2 = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.koff + 2 * D * 2, sb, 0);
+  r.k3 = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.koff + 3 * D * 2, sb, 0);
+  r.v0 = __builtin_amdgcn_raw_buffer_load_b128(src.v, src.voff, sb, 0);
+  r.v1 = __builtin_amdgcn_raw_buffer_load_b128(src.v, src.voff + D * 2, sb, 0);
+  r.v2 = __builtin_amdgcn_raw_buffer_load_b128(src.v, src.voff + 2 * D * 2, sb, 0);
+  r.v3 = __builtin_amdgcn_raw_buffer_load_b128(src.v, src.voff + 3 * D * 2, sb, 0);
 }
 
 // dims dc + 2w (low halves) and dc + 2w + 1 (high halves) of the 4 keys, one 8-byte write each
@@ -84,7 +93,7 @@ IRON_DEV void pf_vt_pair(uint16_t* lo_row, uint16_t* hi_row, uint32_t a0, uint32
 }
 
 template <int D, int KB>
-IRON_DEV void pf_lstore(uint16_t (*s_k)[D + 8], uint16_t (*s_vt)[KB + 8], const StageIdx& x,
+IRON_DEV void pf_lstore(uint16_t (*s_k)[D + 8], uint16_t (*s_vt)[KB + 4], const StageIdx& x,
                         const KVRegs& r) {
   *(u32x4*)&s_k[4 * x.kg][x.kd] = r.k0;
   *(u32x4*)&s_k[4 * x.kg + 1][x.kd] = r.k1;
@@ -117,7 +126,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   constexpr int ND = D / 16;           // 16-wide head-dim tiles of O
   constexpr int PW = 4 / HW;           // tile pairs per workgroup
   __shared__ __align__(16) uint16_t s_k[2][KB][D + 8];
-  __shared__ __align__(16) uint16_t s_vt[2][D][KB + 8];
+  // V^T rows of KB + 4 elements (34 dwords at D = 128): the 8-byte reads of 16 consecutive rows
+  // hit distinct banks (at KB + 8 rows r and r + 8 shared them: 3x the bank-conflict cycles)
+  __shared__ __align__(16) uint16_t s_vt[2][D][KB + 4];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int quarter = lane >> 4, col = lane & 15;
@@ -143,8 +154,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   const int pmin = pblk * PW;
   const int nkb = (16 * (NT - 1 - pmin) + 15) / KB + 1;
 
-  const uint16_t* kbase = p.k + ((size_t)b * p.KV + kv) * S * D;
-  const uint16_t* vbase = p.v + ((size_t)b * p.KV + kv) * S * D;
+  const size_t kvo = ((size_t)b * p.KV + kv) * S * D;
 
   // Q^T operands: lane l holds query row r0[t] + l%16 (clamped), d = 32 j + (l/16)*8 .. +8
   uint4 qf[2][NJ];
@@ -157,6 +167,13 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   }
 
   const StageIdx sx = stage_idx<D, KB>(tid);
+  KVSrc src;
+  src.k = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.k + kvo), 0, S * D * 2,
+                                            kBufferDword3);
+  src.v = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.v + kvo), 0, S * D * 2,
+                                            kBufferDword3);
+  src.koff = (4 * sx.kg * D + sx.kd) * 2;
+  src.voff = (4 * sx.vg * D + sx.vd) * 2;
   KVRegs ra, rb;  // two register sets: block i + 2 is fetched while block i + 1 waits
 
   // O^T accumulators: tile (t, dt) is 16 dims x 16 queries; lane l holds query r0[t] + l%16,
@@ -169,8 +186,8 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};  // this lane's share of query stats
   const float c = p.scale_log2;
 
-  pf_gload<D, KB>(kbase, vbase, 0, sx, S, ra);
-  if (nkb > 1) pf_gload<D, KB>(kbase, vbase, 1, sx, S, rb);
+  pf_gload<D, KB>(src, 0, ra);
+  if (nkb > 1) pf_gload<D, KB>(src, 1, rb);
   pf_lstore<D, KB>(s_k[0], s_vt[0], sx, ra);
   __syncthreads();
   // iteration kbi: fetch block kbi + 2 into the set that held block kbi, compute block kbi, then
@@ -178,20 +195,22 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   auto iteration = [&](int kbi, KVRegs& fetch, KVRegs& stage) {
     const int buf = kbi & 1;
     const int kb0 = kbi * KB;
-    if (kbi + 2 < nkb) pf_gload<D, KB>(kbase, vbase, kbi + 2, sx, S, fetch);
+    if (kbi + 2 < nkb) pf_gload<D, KB>(src, kbi + 2, fetch);
     // tile t takes part while the block starts at or before its last row (wave-uniform)
     const bool act[2] = {live && !twin && kb0 <= r0[0] + 15, live && kb0 <= r0[1] + 15};
     f32x4 st[2][NKT];
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
-      st[0][kt] = st[1][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
         const bf16x8 a = as_bf16x8(*(const uint4*)&s_k[buf][16 * kt + col][32 * j + quarter * 8]);
         if (act[0])
-          st[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[0][j]), st[0][kt], 0, 0, 0);
+          st[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[0][j]),
+                                                              j ? st[0][kt] : zero, 0, 0, 0);
         if (act[1])
-          st[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[1][j]), st[1][kt], 0, 0, 0);
+          st[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[1][j]),
+                                                              j ? st[1][kt] : zero, 0, 0, 0);
       }
     }
     bf16x8 pb[2][NKS];
@@ -200,14 +219,18 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
       if (!act[t]) continue;
       const int qi = r0[t] + col;
       const bool diag = kb0 + KB - 1 > r0[t];  // some key may lie past some query: mask
+      if (diag) {  // wave-uniform: only the blocks that reach past a query need the mask
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kb0 + 16 * kt + quarter * 4 + i > qi) st[t][kt][i] = -INFINITY;
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (diag && kb0 + 16 * kt + quarter * 4 + i > qi) st[t][kt][i] = -INFINITY;
-          mx = fmaxf(mx, st[t][kt][i]);
-        }
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[t][kt][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       // running maximum in the exp2 domain (scale > 0, so the raw maximum maps to it)
@@ -232,10 +255,12 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
         pb[t][ks] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
       }
       lsum[t] = lsum[t] * corr + ps;
+      if (__ballot(corr != 1.f)) {  // no lane's maximum moved: every factor is exactly 1
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
+        for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[t][dt][i] *= corr;
+          for (int i = 0; i < 4; ++i) o[t][dt][i] *= corr;
+      }
     }
     // O^T += V^T P^T; each V^T operand serves both query tiles
 #pragma unroll
