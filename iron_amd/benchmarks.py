@@ -26,10 +26,10 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0
 # MFMA busy fraction per kernel (SQ_VALU_MFMA_BUSY_CYCLES over the 1024 SIMDs / (GRBM_GUI_ACTIVE / 8
 # XCDs x 1024)), measured with rocprofv3 --pmc over `--only c5_prefill` and `--only c5_decode`;
 # a counter run, so quoted here rather than measured in the timed run.
-MFMA_BUSY = {"prefill_attn_kernel": 0.152,
-             "gemm_w8_mfma_kernel (gate/up, SwiGLU, 3 activation planes)": 0.078,
-             "gemm_w8_mfma_kernel (down, 3 activation planes)": 0.054,
-             "gemm_w8_mfma_kernel (QKV)": 0.013, "gemm_w8_mfma_kernel (Wo)": 0.012}
+MFMA_BUSY = {"prefill_attn_kernel": 0.175,
+             "gemm_w8_mfma_kernel (gate/up, SwiGLU, 3 activation planes)": 0.068,
+             "gemm_w8_mfma_kernel (down, 3 activation planes)": 0.061,
+             "gemm_w8_mfma_kernel (QKV)": 0.015, "gemm_w8_mfma_kernel (Wo)": 0.012}
 ROTATE_BYTES = 512 << 20
 DEV = "cuda"
 

@@ -205,12 +205,13 @@ def test_qkv_attention_fused_f32(D, Hq, Hkv, S, G, tm, layout, pos):
 @pytest.mark.slow
 def test_qwen3_0_6b_greedy_agreement_f32():
     """BASELINE config 4 with the fp32 attention core, teacher forced against the exact CPU chain
-    over 128 steps. Random-init weights give near-uniform logits whose top two are often within
-    a bf16 ulp of each other (ulp 1/16 at |logit| ~ 10): fp32 rounding anywhere in 28 layers can
-    flip such a tie, so this path is held to agreement wherever the exact chain's top-1/top-2
-    margin exceeds MARGIN, and its overall agreement is printed. (The default exact path agrees
-    on every step, test_gpu_model.py.)"""
-    MARGIN = 0.25
+    over 128 steps. Random-init weights give near-uniform logits whose top two bf16 values are
+    sometimes equal: there the argmax is the first of the tied indices, and fp32 rounding anywhere
+    in 28 layers decides which one that is. So this path is held to agreement on every step whose
+    exact top-1/top-2 margin is nonzero (measured: 123 of 128 steps, every one agreeing; the 5
+    others exact ties), and to >= 95 % overall. (The default exact path agrees on every step,
+    test_gpu_model.py.)"""
+    MARGIN = 0.0
     cfg = Qwen3Config.qwen3_0_6b()
     P0, n_prompt, n_new = 1984, 64, 128
     S = P0 + n_prompt + n_new
@@ -249,3 +250,4 @@ def test_qwen3_0_6b_greedy_agreement_f32():
     print(f"greedy agreement (f32 attention) {agree}/{n_new}; {decided_agree}/{decided} where "
           f"the margin exceeds {MARGIN}", flush=True)
     assert decided_agree == decided
+    assert agree >= 0.95 * n_new
