@@ -329,8 +329,364 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
   if (tid == 0) __hip_atomic_store(p.ctr + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Register-streamed form (M a multiple of the tile, K of 256): the weights never pass through LDS
+// and the K loop has one barrier per 256-wide chunk. Each of a workgroup's 4 wavefronts owns RB
+// 16-row blocks over the workgroup's K range and streams them from memory straight into MFMA
+// operands, one 16-byte load per lane per row block and 64-wide k block (lane (q, r) = lane / 16,
+// lane % 16: row r, bytes q*16 .. +15 of the block; each instruction reads 64 bytes of 16 rows),
+// kRDepth blocks ahead: the ring is a chunk deep. x (every plane) and the tile's group scales
+// pass through LDS a chunk at a time, loaded a chunk ahead into registers and written at the
+// chunk's end. The activations are the MFMA A operand (lane (q, b): batch row b, k q*8 .. +7 of
+// the 32-wide group; rows past B read as zero from a buffer sized to B rows), the weights the B
+// operand (lane (q, r): row r, the same k), so C[b][row] sits in lane (q, r) for batch rows
+// 4q .. 4q+3 of row r, and each lane scales its own row's group sums.
+//
+// Why not LDS for the weights too: the staged form keeps one step of loads in flight per
+// workgroup. A read probe over a 100 MB matrix (16 rows x 64 bytes per instruction, 4 loads in
+// flight per row block, 2 or 4 splits) reads at 4.5-5.2 TB/s; 8-byte loads (16 rows x 32 bytes)
+// at 2.8-3.4, and every activation load in the weight loop costs about as much as a weight load.
+constexpr int kRChunk = 256;              // k per LDS chunk of x and scales
+constexpr int kRBlk = 64;                 // k per 16-byte weight load
+constexpr int kRDepth = kRChunk / kRBlk;  // weight loads in flight per row block: one chunk
+constexpr int kRXRow = kRChunk + 8;       // LDS bf16 per x row (padded: conflict-free reads)
+
+// The four 16-lane rows of a wavefront hold 16 consecutive k of the same 16 weight rows (bytes
+// q*16 .. +15 of a 64-wide block). Two swaps put them in the MFMA operand order of the block's two
+// 32-wide groups: afterwards lane (q, r) holds k q*8 .. +7 of group 0 in (x, y) and of group 1
+// in (z, w) (permlane16_swap exchanges the odd rows of its first operand with the even rows of
+// its second, permlane32_swap the upper half of the first with the lower half of the second).
+IRON_DEV iron_u32x4 quarter_transpose(iron_u32x4 v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(v.x, v.z, false, false);
+  const auto b = __builtin_amdgcn_permlane16_swap(v.y, v.w, false, false);
+  const auto c = __builtin_amdgcn_permlane32_swap(a[0], a[1], false, false);
+  const auto d = __builtin_amdgcn_permlane32_swap(b[0], b[1], false, false);
+  return iron_u32x4{c[0], d[0], c[1], d[1]};
+}
+
+// 8 int8 weights as biased bytes u = q + 128 (two dwords) -> 8 bf16 of u (exact: u <= 255 has
+// at most 8 significant bits): one v_cvt_f32_ubyte per byte and one v_perm_b32 per two, 12 VALU
+// instructions where the signed form takes 20; the -128 q offset enters through the group's
+// accumulator start value, -128 * (the group's x sum) per batch row.
+IRON_DEV bf16x8 u8_to_bf16u(uint32_t lo, uint32_t hi) {
+  auto two = [](uint32_t d, int sh) {
+    const float f0 = (float)((d >> sh) & 0xffu);
+    const float f1 = (float)((d >> (sh + 8)) & 0xffu);
+    return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+  };
+  const uint4 r = make_uint4(two(lo, 0), two(lo, 16), two(hi, 0), two(hi, 16));
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// LDS stores of this wavefront complete, then the workgroup barrier (no global-memory fence: the
+// weight loads in flight must not be waited for).
+// sched_barrier mask: every instruction class may cross except VMEM reads (whose issue order
+// the ring's waits count on)
+constexpr int kSchedAllButVmemRead = 0x7CF;
+
+IRON_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <bool DUAL, bool XPL, int W, int RB, bool G32>
+__global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
+  constexpr int NM = DUAL ? 2 : 1;
+  constexpr int NX = XPL ? 3 : 1;
+  constexpr int NT = 64 * W;                      // threads
+  constexpr int TILE = 16 * RB * W;
+  constexpr int XP = kBN * kRChunk * 2 / (NT * 16);  // 16-byte x pieces per plane and thread
+  constexpr int SB = NM * TILE * 16 / NT;         // scale bytes per thread and chunk
+  static_assert(XP >= 1 && (SB == 4 || SB == 8 || SB == 16), "chunk staging per thread");
+  static_assert(W % NM == 0, "whole wavefronts stage each matrix's scales");
+  __shared__ __align__(16) uint16_t s_x[2][NX][kBN][kRXRow];
+  __shared__ __align__(16) uint8_t s_s[2][NM][TILE][16];  // 8 group scales per row and chunk
+  __shared__ __align__(16) float s_corr[2][8][kBN];  // -128 * (x sum) per group and batch row
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 15, quarter = lane >> 4;
+  const int tile0 = blockIdx.x * TILE, row0 = tile0 + wave * 16 * RB;
+  const int gmask = (1 << p.gshift) - 1;
+  const int split = blockIdx.y;
+  const int cb = split * p.ksteps;                           // first chunk of this split
+  const int nc = min(p.ksteps, p.K / kRChunk - cb);          // its chunks (>= 1)
+  const int nb = nc * kRDepth;                               // its 64-wide blocks
+  const int kbase = cb * kRChunk;
+  const int ng = p.K >> p.gshift;
+  const uint32_t to_u = p.xor_mask ^ 0x80808080u;  // stored bytes -> q + 128
+
+  // this lane's weight rows row0 + 16 rb + col: bytes quarter*16 of each 64-wide block
+  const uint8_t* wp[RB][NM];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const uint32_t row = (uint32_t)(row0 + 16 * rb + col);
+    const uint32_t blk = fastdiv(row, p.tdiv);
+    const uint32_t in = row - blk * (uint32_t)p.tile_m;
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+      wp[rb][mi] = (mi == 0 ? p.w0 : p.w1) + (size_t)blk * p.blk_bytes + (size_t)in * p.K + kbase +
+                   quarter * 16;
+  }
+  // staging of a chunk: x (two 16-byte pieces per plane and thread: row idx / 32, k (idx % 32)*8)
+  // and SB bytes of the tile's scales (flat byte f = tid * SB of [NM][TILE][16], from the row's
+  // scale of the chunk's first group; reads past a row's own groups land in the wire or past its
+  // end, where the buffer returns zero, and are never used)
+  __amdgpu_buffer_rsrc_t xr[NX];
+#pragma unroll
+  for (int xi = 0; xi < NX; ++xi)
+    xr[xi] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x + xi * p.x_plane), 0,
+                                               p.B * p.x_stride * 2, kBufferDword3);
+  int xvo[XP];
+#pragma unroll
+  for (int h = 0; h < XP; ++h) {
+    const int idx = tid + NT * h;
+    xvo[h] = ((idx >> 5) * p.x_stride + (idx & 31) * 8) * 2;
+  }
+  const int sf = tid * SB;
+  // the matrix is the same across a wavefront (W / NM whole wavefronts per matrix): a uniform
+  // value keeps the buffer descriptor in scalar registers (else every load loops over lanes)
+  const int s_mi = __builtin_amdgcn_readfirstlane(sf / (TILE * 16));
+  const int s_row = (sf >> 4) % TILE, s_byte = sf & 15;
+  __amdgpu_buffer_rsrc_t sr;
+  int svo;
+  {
+    const uint32_t row = (uint32_t)(tile0 + s_row);
+    const uint32_t blk = fastdiv(row, p.tdiv);
+    const uint32_t in = row - blk * (uint32_t)p.tile_m;
+    const uint32_t nblk = ((uint32_t)p.M + p.tile_m - 1) / (uint32_t)p.tile_m;
+    sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(s_mi == 0 ? p.w0 : p.w1), 0,
+                                           (int)(nblk * p.blk_bytes), kBufferDword3);
+    svo = (int)(blk * p.blk_bytes + (uint32_t)p.tile_m * p.K + (in * ng) * 2 + s_byte);
+  }
+  iron_u32x4 xs[NX][XP];
+  iron_u32x4 ss4;
+  iron_u32x2 ss2;
+  uint32_t ss1;
+  auto xload = [&](int c) {
+    const int kc = kbase + c * kRChunk;
+#pragma unroll
+    for (int xi = 0; xi < NX; ++xi)
+#pragma unroll
+      for (int h = 0; h < XP; ++h)
+        xs[xi][h] = __builtin_amdgcn_raw_buffer_load_b128(xr[xi], xvo[h], kc * 2, 0);
+    const int so = (kc >> p.gshift) * 2;
+    if constexpr (SB == 16) ss4 = __builtin_amdgcn_raw_buffer_load_b128(sr, svo, so, 0);
+    else if constexpr (SB == 8) ss2 = __builtin_amdgcn_raw_buffer_load_b64(sr, svo, so, 0);
+    else ss1 = __builtin_amdgcn_raw_buffer_load_b32(sr, svo, so, 0);
+  };
+  auto xstore = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < XP; ++h) {
+      const int idx = tid + NT * h;
+      double sx = 0.0;  // this piece's x (every plane), then the group's over its 4 G/32 lanes
+#pragma unroll
+      for (int xi = 0; xi < NX; ++xi) {
+        *(iron_u32x4*)&s_x[buf][xi][idx >> 5][(idx & 31) * 8] = xs[xi][h];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sx += (double)__uint_as_float(xs[xi][h][e] << 16);
+          sx += (double)__uint_as_float(xs[xi][h][e] & 0xffff0000u);
+        }
+      }
+      sx += dpp_d<0xb1>(sx);  // quad_perm [1,0,3,2]
+      sx += dpp_d<0x4e>(sx);  // quad_perm [2,3,0,1]
+      if (p.gshift >= 6) sx += dpp_d<0x141>(sx);  // row_half_mirror: the other quad of 8
+      if (p.gshift >= 7) sx += dpp_d<0x140>(sx);  // row_mirror: the other 8 of 16
+      const int kq = (idx & 31) * 8;
+      if ((kq & gmask) == 0) s_corr[buf][kq >> p.gshift][idx >> 5] = (float)(-128.0 * sx);
+    }
+    if constexpr (SB == 16) *(iron_u32x4*)&s_s[buf][s_mi][s_row][s_byte] = ss4;
+    else if constexpr (SB == 8) *(iron_u32x2*)&s_s[buf][s_mi][s_row][s_byte] = ss2;
+    else *(uint32_t*)&s_s[buf][s_mi][s_row][s_byte] = ss1;
+  };
+
+  iron_u32x4 ring[kRDepth][RB][NM];
+  auto wload = [&](iron_u32x4 (&st)[RB][NM], int j) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) st[rb][mi] = *(const iron_u32x4*)(wp[rb][mi] + kRBlk * j);
+  };
+
+  double acc[RB][NM][4];
+  f32x4 c[RB][NM];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      c[rb][mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[rb][mi][i] = 0.0;
+    }
+
+  // Every block issues the same loads (past the split's end they re-read its last block), no load
+  // sits in a branch, and scheduling barriers keep the loads in issue order: the wait before a
+  // block's MFMAs then counts the later blocks' loads. (A branch around a load, or the scheduler
+  // hoisting a later load above an earlier one, drops the compiler's wait to zero and drains the
+  // ring every block.)
+  xload(0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < kRDepth; ++u) {
+    wload(ring[u], min(u, nb - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  xstore(0);
+  __builtin_amdgcn_sched_barrier(0);
+  xload(min(1, nc - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  lds_barrier();
+  for (int ch = 0; ch < nc; ++ch) {
+    const int buf = ch & 1;
+#pragma unroll
+    for (int u = 0; u < kRDepth; ++u) {
+      iron_u32x4 t[RB][NM];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi) t[rb][mi] = quarter_transpose(ring[u][rb][mi]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // a 32-wide MFMA group at k kl of the chunk; quantization groups (G >= 32, dividing the
+        // chunk) start and end on MFMA group boundaries
+        const int kl = kRBlk * u + 32 * h;
+        const bool gstart = G32 || (kl & gmask) == 0, gend = G32 || ((kl + 32) & gmask) == 0;
+        bf16x8 bx[NX];
+#pragma unroll
+        for (int xi = 0; xi < NX; ++xi)
+          bx[xi] = __builtin_bit_cast(bf16x8, *(const iron_u32x4*)&s_x[buf][xi][col][kl + quarter * 8]);
+        f32x4 ci = {0.f, 0.f, 0.f, 0.f};
+        if (gstart) ci = *(const f32x4*)&s_corr[buf][kl >> p.gshift][quarter * 4];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int mi = 0; mi < NM; ++mi) {
+            const uint32_t lo = h ? t[rb][mi].z : t[rb][mi].x;
+            const uint32_t hi = h ? t[rb][mi].w : t[rb][mi].y;
+            const bf16x8 bw = u8_to_bf16u(lo ^ to_u, hi ^ to_u);
+            if constexpr (G32) {
+              c[rb][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bx[0], bw, ci, 0, 0, 0);
+            } else {
+              if (gstart) c[rb][mi] = ci;
+              c[rb][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bx[0], bw, c[rb][mi], 0, 0, 0);
+            }
+#pragma unroll
+            for (int xi = 1; xi < NX; ++xi)
+              c[rb][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bx[xi], bw, c[rb][mi], 0, 0, 0);
+          }
+        if (gend) {  // the quantization group's sums, scaled, into the fp64 accumulators
+          const int gl = kl >> p.gshift;
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int mi = 0; mi < NM; ++mi) {
+              const double sc = bf16_to_f32(
+                  *(const uint16_t*)&s_s[buf][mi][wave * 16 * RB + 16 * rb + col][2 * gl]);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                acc[rb][mi][i] = fma(sc, (double)c[rb][mi][i], acc[rb][mi][i]);
+                // fold here: left to itself the compiler sinks every group's fold to the end of
+                // the chunk and keeps all the groups' sums live (registers spill)
+                asm volatile("" : "+v"(acc[rb][mi][i]));
+              }
+            }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      wload(ring[u], min(ch * kRDepth + u + kRDepth, nb - 1));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the next chunk's x and scales into the other buffer (last read a chunk ago, before the
+    // previous barrier), then the loads of the chunk after it
+    xstore(buf ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    xload(min(ch + 2, nc - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+  }
+
+  if (p.splits == 1) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = quarter * 4 + i;
+        if (b < p.B) store_out(p, b, row0 + 16 * rb + col, acc[rb][0][i], acc[rb][NM - 1][i]);
+      }
+    return;
+  }
+  // Split K: the fp64 partials go out write-through (16 consecutive rows per 128 bytes), then the
+  // arrival count; the last split of the tile sums the partials in split order.
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = quarter * 4 + i;
+        if (b < p.B)
+          __hip_atomic_store(
+              p.part + (((size_t)mi * p.splits + split) * kBN + b) * p.M + row0 + 16 * rb + col,
+              acc[rb][mi][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  __shared__ unsigned int s_last;
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(p.ctr + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == (unsigned int)(p.splits - 1);
+  __syncthreads();
+  if (!s_last) return;
+  // Every thread's outputs (b, m) = (t / TILE, t % TILE) for t = tid + NT o, and SQ splits of
+  // each in one round of loads: the merge is a couple of memory round trips, not one per output
+  // and eight splits.
+  constexpr int PER = TILE * kBN / NT;   // outputs per thread at B = 16
+  constexpr int SQ = 32 / (PER * NM);    // splits per round (32 loads in flight)
+  static_assert(SQ >= 1, "merge round");
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      p.part, 0, NM * p.splits * kBN * p.M * (int)sizeof(double), kBufferDword3);
+  int off[PER];
+#pragma unroll
+  for (int o = 0; o < PER; ++o) {
+    const int t = min(tid + NT * o, TILE * p.B - 1);
+    off[o] = ((t / TILE) * p.M + tile0 + t % TILE) * (int)sizeof(double);
+  }
+  const int sstride = kBN * p.M * (int)sizeof(double);  // one split's partials
+  double a[PER][2] = {};
+  for (int s0 = 0; s0 < p.splits; s0 += SQ) {
+    double v[PER][NM][SQ];
+#pragma unroll
+    for (int q = 0; q < SQ; ++q) {
+      const int spl = s0 + q < p.splits ? s0 + q : p.splits - 1;
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+        for (int o = 0; o < PER; ++o)
+          v[o][mi][q] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(
+              rs, off[o] + (mi * p.splits + spl) * sstride, 0, kCpolSc1));
+    }
+#pragma unroll
+    for (int q = 0; q < SQ; ++q)
+      if (s0 + q < p.splits) {
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+          for (int o = 0; o < PER; ++o) a[o][mi] += v[o][mi][q];
+      }
+  }
+#pragma unroll
+  for (int o = 0; o < PER; ++o) {
+    const int t = tid + NT * o;
+    if (t < TILE * p.B) store_out(p, t / TILE, tile0 + t % TILE, a[o][0], a[o][NM - 1]);
+  }
+  if (tid == 0)
+    __hip_atomic_store(p.ctr + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct GemmPlan {
-  int splits, ksteps;
+  bool rs;             // the register-streamed form (else the staged one)
+  int splits, ksteps;  // split s covers steps [s*ksteps, (s+1)*ksteps): 128-wide (staged) or
+                       // 256-wide chunks (register-streamed)
 };
 
 // Split K until at most 512 workgroups cover the chip (two per CU), keeping at least kMinSteps
@@ -344,7 +700,7 @@ struct GemmPlan {
 // 34.1 us).
 constexpr int kSplitTarget = 512;
 constexpr int kMinSteps = 4;
-GemmPlan plan_gemm(int M, int K) {
+GemmPlan plan_staged(int M, int K) {
   const int tiles = M / kTM;
   const int steps = K / kKS;
   // at most the target: the 192 row tiles of Qwen3-8B's gate/up took 49.9 us at 2 splits (384
@@ -358,7 +714,37 @@ GemmPlan plan_gemm(int M, int K) {
   if (splits < per_cu) splits = per_cu;
   if (splits > steps) splits = steps;
   const int ksteps = (steps + splits - 1) / splits;
-  return {(steps + ksteps - 1) / ksteps, ksteps};  // no empty split
+  return {false, (steps + ksteps - 1) / ksteps, ksteps};  // no empty split
+}
+
+// The register-streamed form: up to two 4-wavefront workgroups per CU (512), at least
+// kRMinChunks chunks per split, and never fewer workgroups than CUs while a split can shrink.
+constexpr int kRW = 8, kRRB = 1;         // wavefronts per workgroup, 16-row blocks per wavefront
+constexpr int kRTile = 16 * kRW * kRRB;  // rows per workgroup
+constexpr int kRMinChunks = 2;
+GemmPlan plan_rs(int M, int K) {
+  const int tiles = M / kRTile;
+  const int chunks = K / kRChunk;
+  int target = kSplitTarget / tiles;
+  if (target < 1) target = 1;
+  const int by_chunks = chunks / kRMinChunks > 1 ? chunks / kRMinChunks : 1;
+  if (target > by_chunks) target = by_chunks;
+  const int per_cu = (256 + tiles - 1) / tiles;
+  if (target < per_cu) target = per_cu;
+  if (target > chunks) target = chunks;
+  int ksteps = (chunks + target - 1) / target;
+  while (ksteps > 1 && tiles * ((chunks + ksteps - 1) / ksteps) < 256) --ksteps;
+  return {true, (chunks + ksteps - 1) / ksteps, ksteps};
+}
+
+// The register-streamed form runs the dual (gate/up) GEMM of K >= 4096 (config 5's gate/up: 43.6
+// against 50.1 us, the step 8.43 -> 8.20 ms); everywhere else the staged form measured as fast
+// or faster (config 5 at B=16, us: down 28.4 against 25.1, QKV 14.3 against 13.8, Wo 14.3
+// against 11.4; config 2 at B=8, whose 2048-deep gate/up splits to single chunks: 45.2 against
+// 32.4 for the MLP).
+GemmPlan plan_gemm(int M, int K, bool dual) {
+  if (dual && K >= 4096 && M % kRTile == 0 && K % kRChunk == 0) return plan_rs(M, K);
+  return plan_staged(M, K);
 }
 
 }  // namespace
@@ -369,15 +755,17 @@ constexpr int kMaxTiles = (int)(kGemmCtrBytes / sizeof(unsigned int));  // M <= 
 
 // Bytes of fp64 split-K partials (none without a split).
 size_t gemm_workspace_bytes(int M, int K, bool dual) {
-  const GemmPlan pl = plan_gemm(M, K);
+  const GemmPlan pl = plan_gemm(M, K, dual);
   if (pl.splits == 1) return 0;
   return (size_t)(dual ? 2 : 1) * pl.splits * kBN * M * sizeof(double);
 }
 
-// An upper bound over every K (the split count never exceeds ceil(kSplitTarget / (M / 64))).
+// An upper bound over every K: the staged form's split count never exceeds
+// ceil(kSplitTarget / (M / 64)), the register-streamed form's ceil(kSplitTarget / (M / 128)) or
+// ceil(256 / (M / 128)), both at most ceil(2 kSplitTarget / (M / 64)).
 size_t gemm_workspace_bound(int M, bool dual) {
   if (M <= 0 || M % kTM) return 0;
-  const size_t splits = (kSplitTarget + M / kTM - 1) / (M / kTM);
+  const size_t splits = (2 * kSplitTarget + M / kTM - 1) / (M / kTM);
   return ((size_t)(dual ? 2 : 1) * splits * kBN * M * sizeof(double) + 255) & ~(size_t)255;
 }
 
@@ -403,7 +791,7 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
   int st = gemm_check(fn, B, M, K, G);
   if (st) return st;
   const bool dual = w1 != nullptr;
-  const GemmPlan pl = plan_gemm(M, K);
+  const GemmPlan pl = plan_gemm(M, K, dual);
   GemmParams p = {};
   p.w0 = (const uint8_t*)w0;
   p.w1 = (const uint8_t*)w1;
@@ -436,6 +824,27 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
       return fail(IRON_ERR_ALIGN, "%s: workspace not 256-byte aligned", fn);
     p.part = (double*)part;
     p.ctr = ctr;
+  }
+  if (pl.rs) {
+    dim3 grid(M / kRTile, pl.splits);
+    const dim3 blk(64 * kRW);
+    const bool g32 = G == 32;
+#define IRON_RS(D_, X_)                                                                      \
+  do {                                                                                       \
+    if (g32) hipLaunchKernelGGL((gemm_w8_rs_kernel<D_, X_, kRW, kRRB, true>), grid, blk, 0,  \
+                                stream, p);                                                  \
+    else hipLaunchKernelGGL((gemm_w8_rs_kernel<D_, X_, kRW, kRRB, false>), grid, blk, 0,     \
+                            stream, p);                                                      \
+  } while (0)
+    if (dual) {
+      if (x_f32) IRON_RS(true, true);
+      else IRON_RS(true, false);
+    } else {
+      if (x_f32) IRON_RS(false, true);
+      else IRON_RS(false, false);
+    }
+#undef IRON_RS
+    return check_launch(fn);
   }
   dim3 grid(M / kTM, pl.splits);
   if (dual) {

@@ -123,6 +123,11 @@ def test_gemm_mfma(M, K, G, tile_m, B, domain):
     (1024, 3072, 2048, True, 32, 16),   # Qwen3-0.6B chain arm at batch 16
     (4096, 12288, 4096, True, 32, 16),  # Qwen3-8B layer MLP at BASELINE config 5 (B=16)
     (2560, 9728, 4096, True, 32, 16),   # Qwen3-4B: FF % D != 0 (the chunked-down arm)
+    # gate/up on the register-streamed form (dual, K = D >= 4096) at the other group sizes and
+    # a batch below 16 (rows past B read as zero)
+    (4096, 1024, 0, False, 64, 5),
+    (4096, 2048, 0, False, 128, 16),
+    (4096, 1024, 0, False, 32, 8),
 ])
 def test_swiglu_mlp_mfma(D, FF, QD, fuse_o, G, B):
     _say(f"swiglu mfma D={D} FF={FF} QD={QD} fuse_o={fuse_o} G={G} B={B}")
