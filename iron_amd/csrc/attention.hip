@@ -806,12 +806,18 @@ struct SplitPlan {
   int nsplit, chunk, hb;
 };
 
-SplitPlan plan_split(int B, int H, int KV, int max_ctx) {
+SplitPlan plan_split(int B, int H, int KV, int max_ctx, bool f32) {
   SplitPlan sp;
   const int HG = H / KV;
   sp.hb = HG >= 4 ? 4 : HG;
   const int wg_per_split = B * KV * (HG / sp.hb);
-  const int target_wgs = 512;
+  // About 512 workgroups; with the fp64 core, 256 where 512 would take more than 32 splits (B=1):
+  // the last split's merge of 64 partials then costs more than the longer tiles of 32 splits
+  // (config 3 at B=1: 12.5 -> 10.5 us; B=8 ragged at a 256 target: 22.6 -> 23.0 us). The fp32
+  // core keeps 64 splits (9.9 -> 9.0 us at 32): its result depends on the split boundaries, and
+  // 32 splits moved enough logits of the 128-step Qwen3-0.6B greedy run to flip 7 of its 124
+  // decided tokens against the exact chain, where 64 splits agree on all of them.
+  const int target_wgs = !f32 && 512 / wg_per_split > 32 ? 256 : 512;
   const int max_ns = (max_ctx + kTile - 1) / kTile;
   int ns = (target_wgs + wg_per_split - 1) / wg_per_split;
   if (ns > max_ns) ns = max_ns;
@@ -829,7 +835,7 @@ SplitPlan plan_split(int B, int H, int KV, int max_ctx) {
 // The split workspace: the merge's arrival counters (kAttnCtrBytes, zero before the first call
 // and after every call), then the partials.
 size_t attn_ws_bytes(int B, int H, int KV, int max_ctx) {
-  const SplitPlan sp = plan_split(B, H, KV, max_ctx);
+  const SplitPlan sp = plan_split(B, H, KV, max_ctx, true);  // the larger of the two plans
   if (sp.nsplit == 1) return 0;
   return kAttnCtrBytes +
          ((((size_t)B * H * sp.nsplit * (kD + 2) * sizeof(double)) + 255) & ~(size_t)255);
@@ -856,7 +862,7 @@ int launch_attention(AttnParams p, bool fused, int acc, int B, void* part_ws, si
     return iron::fail(IRON_ERR_SHAPE, "%s: unknown accumulation mode %d", fn, acc);
   const bool f32 = acc == IRON_ACCUM_F32;
   p.scale2 = (float)(p.scale * 1.4426950408889634);
-  const SplitPlan sp = plan_split(B, p.H, p.KV, p.max_ctx);
+  const SplitPlan sp = plan_split(B, p.H, p.KV, p.max_ctx, f32);
   p.HG = p.H / p.KV;
   p.HB = sp.hb;
   p.ctr = nullptr;

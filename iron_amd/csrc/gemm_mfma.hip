@@ -378,17 +378,6 @@ IRON_DEV bf16x8 u8_to_bf16u(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// LDS stores of this wavefront complete, then the workgroup barrier (no global-memory fence: the
-// weight loads in flight must not be waited for).
-// sched_barrier mask: every instruction class may cross except VMEM reads (whose issue order
-// the ring's waits count on)
-constexpr int kSchedAllButVmemRead = 0x7CF;
-
-IRON_DEV void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 template <bool DUAL, bool XPL, int W, int RB, bool G32>
 __global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
@@ -535,7 +524,7 @@ __global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
   __builtin_amdgcn_sched_barrier(0);
   xload(min(1, nc - 1));
   __builtin_amdgcn_sched_barrier(0);
-  lds_barrier();
+  __syncthreads();
   for (int ch = 0; ch < nc; ++ch) {
     const int buf = ch & 1;
 #pragma unroll
@@ -602,7 +591,7 @@ __global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
     __builtin_amdgcn_sched_barrier(0);
     xload(min(ch + 2, nc - 1));
     __builtin_amdgcn_sched_barrier(0);
-    lds_barrier();
+    __syncthreads();
   }
 
   if (p.splits == 1) {

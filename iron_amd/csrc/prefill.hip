@@ -195,7 +195,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   auto iteration = [&](int kbi, KVRegs& fetch, KVRegs& stage) {
     const int buf = kbi & 1;
     const int kb0 = kbi * KB;
-    if (kbi + 2 < nkb) pf_gload<D, KB>(src, kbi + 2, fetch);
+    // unconditional (past the last block it re-reads it): a load in a branch would make the
+    // compiler's wait before the staging below count it as the youngest load, draining the fetch
+    pf_gload<D, KB>(src, min(kbi + 2, nkb - 1), fetch);
     // tile t takes part while the block starts at or before its last row (wave-uniform)
     const bool act[2] = {live && !twin && kb0 <= r0[0] + 15, live && kb0 <= r0[1] + 15};
     f32x4 st[2][NKT];
@@ -277,10 +279,12 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
     if (kbi + 1 < nkb) pf_lstore<D, KB>(s_k[buf ^ 1], s_vt[buf ^ 1], sx, stage);
     __syncthreads();
   };
-  for (int kbi = 0; kbi < nkb; kbi += 2) {
+  int kbi = 0;
+  for (; kbi + 1 < nkb; kbi += 2) {  // no branch around an iteration's loads inside the loop
     iteration(kbi, ra, rb);
-    if (kbi + 1 < nkb) iteration(kbi + 1, rb, ra);
+    iteration(kbi + 1, rb, ra);
   }
+  if (kbi < nkb) iteration(kbi, ra, rb);
 
   // row sums: the four lane quarters hold disjoint keys of the same query
   if (!live) return;
