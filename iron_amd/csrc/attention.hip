@@ -186,6 +186,24 @@ IRON_DEV void load_kv_tile(const AttnParams& p, const AttnCoords& c, int t0, int
   }
 }
 
+// One lane's 16 bytes from global memory into LDS at m0 + 16 * lane (global_load_lds_dwordx4;
+// lds is wave-uniform), and one 16-byte LDS read. Inline asm so that the compiler, which would
+// otherwise wait for every outstanding LDS-DMA before any LDS read, leaves the waits to the caller:
+// a ring slot is read after s_waitcnt vmcnt(N) for the N loads issued after its own, and the
+// read's result is used after s_waitcnt lgkmcnt(0).
+IRON_DEV void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
+  __asm__ volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                   :
+                   : "v"(off), "s"(base), "s"(lds)
+                   : "memory");
+}
+
+IRON_DEV iron_u32x4 lds_read16(uint32_t addr) {
+  iron_u32x4 v;
+  __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
 // The query-side loads, issued before any K/V tile. Fused mode: the raw q row this wave rotates
 // (xq[0]), the current token's raw K and V rows, the two norm weights and the angle
 // row (e = {n_qn, n_kn, raw k, raw v, angles lo, angles hi}); plain mode: the q rows. Returns the
@@ -452,16 +470,71 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnParams p) {
   }
 
   __shared__ double s_mx[2][4][HB];
+  // the end-of-kernel sums' staging (attn_finish_f64); with four query heads also the K/V ring
+  __shared__ __align__(16) double s_ro[16][HB][kAttnD];
   if constexpr (HB >= 4) {
     // Four query heads hold 128 fp64 values per lane (q and the outputs): one register set of
-    // K/V rows keeps the kernel within half the register file, so two workgroups share each CU
-    // and one's tile loads overlap the other's arithmetic.
-    if (!p.spec && t_begin < t_end) load_kv_tile(p, c, t_begin, t_lim, kr, vr);
-    int it = 0;
-    for (int t0 = t_begin; t0 < t_end; t0 += kTile, ++it) {
-      if (t0 > t_begin) load_kv_tile(p, c, t0, t_lim, kr, vr);
-      attn_tile_f64<HB, FUSED>(kr, vr, t0, t_end, has_new, pos, s_new, qf, p.scale, it, m, l, o,
-                               s_mx, wave, lane, row, dl);
+    // K/V rows keeps the kernel within half the register file (two workgroups per CU). The
+    // tiles after it come through LDS instead: each lane's 16-byte K and V rows of a tile go by
+    // global_load_lds into the lane's own slots of a two-tile ring (32 KiB a tile, in s_ro's
+    // 64 KiB), so while a tile is processed from registers the next two are in flight. A lane
+    // reads back only what it loaded, so its own load count orders the ring (no barrier): the
+    // loads and the reads are inline asm, which the compiler does not see as an LDS store (it
+    // would otherwise wait for every such load before any LDS read) and the waits are explicit.
+    if (p.spec || t_begin >= t_end) {  // B = 1: the first tile already went out with the query
+      if (!p.spec && t_begin < t_end) load_kv_tile(p, c, t_begin, t_lim, kr, vr);
+      int it = 0;
+      for (int t0 = t_begin; t0 < t_end; t0 += kTile, ++it) {
+        if (t0 > t_begin) load_kv_tile(p, c, t0, t_lim, kr, vr);
+        attn_tile_f64<HB, FUSED>(kr, vr, t0, t_end, has_new, pos, s_new, qf, p.scale, it, m, l,
+                                 o, s_mx, wave, lane, row, dl);
+      }
+    } else {
+      static_assert(sizeof(s_ro) >= 2 * 4 * 8 * 1024, "the ring fits in the sums' staging");
+      const uint32_t ring = (uint32_t)(uintptr_t)&s_ro[0][0][0];
+      auto slot = [&](int s, int j) {  // wave-uniform: slot of row j (K 2u, V 2u + 1), ring half s
+        return (uint32_t)__builtin_amdgcn_readfirstlane(ring + ((s * 4 + wave) * 8 + j) * 1024);
+      };
+      // byte offsets from the K and V bases (one 32-bit offset serves both: the same strides)
+      const uint16_t* kb = p.k + (size_t)b * p.sb + (size_t)c.kv * p.sh;
+      const uint16_t* vb = p.v + (size_t)b * p.sb + (size_t)c.kv * p.sh;
+      auto dma_tile = [&](int t0, int s) {  // rows clamped below t_lim, as load_kv_tile's
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          int t = t0 + u * 16 + wave * 4 + row;
+          t = t < t_lim ? t : t_lim - 1;
+          const uint32_t off = (uint32_t)(t * p.st + dl * 8) * 2u;
+          lds_dma16(kb, off, slot(s, 2 * u));
+          lds_dma16(vb, off, slot(s, 2 * u + 1));
+        }
+      };
+      auto read_tile = [&](int s) {  // the older of the two tiles in flight (8 loads each)
+        __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        iron_u32x4* const k4 = reinterpret_cast<iron_u32x4*>(kr);
+        iron_u32x4* const v4 = reinterpret_cast<iron_u32x4*>(vr);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          k4[u] = lds_read16(slot(s, 2 * u) + lane * 16);
+          v4[u] = lds_read16(slot(s, 2 * u + 1) + lane * 16);
+        }
+        __asm__ volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(k4[0]), "+v"(k4[1]), "+v"(k4[2]), "+v"(k4[3]), "+v"(v4[0]),
+                           "+v"(v4[1]), "+v"(v4[2]), "+v"(v4[3])
+                         :
+                         : "memory");
+      };
+      dma_tile(t_begin, 0);
+      dma_tile(t_begin + kTile, 1);
+      int it = 0;
+      for (int t0 = t_begin; t0 < t_end; t0 += kTile, ++it) {
+        read_tile(it & 1);                        // tile it (tile it + 1 may be in flight)
+        dma_tile(t0 + 2 * kTile, it & 1);         // tile it + 2 into the half just read
+        attn_tile_f64<HB, FUSED>(kr, vr, t0, t_end, has_new, pos, s_new, qf, p.scale, it, m, l,
+                                 o, s_mx, wave, lane, row, dl);
+      }
+      // every lane's ring loads have landed before s_ro is rewritten
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
     }
   } else {
     // Tiles alternate between two register sets, the next tile's rows in flight while one is
@@ -481,7 +554,7 @@ __global__ __launch_bounds__(256, 2) void decode_attn_kernel(AttnParams p) {
     }
   }
 
-  attn_finish_f64<HB>(m, l, o, wave, row, dl, [&](int oh, int od, double O, double L, double M) {
+  attn_finish_f64<HB>(m, l, o, wave, row, dl, s_ro, [&](int oh, int od, double O, double L, double M) {
     const int hq = h0 + oh;
     if (q.ns == 1) {
       p.out[((size_t)b * p.H + hq) * kD + od] = f64_to_bf16(L > 0.0 ? O / L : 0.0);

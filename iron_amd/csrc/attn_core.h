@@ -267,11 +267,11 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, b
 // The end of the exact core: the 16 token rows of a workgroup (4 per wavefront) hold partial sums
 // under the same offsets m, so they add. For every (head oh, dim od) of the HB heads the
 // workgroup's unnormalised output O, its sum L and maximum M go to emit(oh, od, O, L, M), called
-// once per pair by one thread.
+// once per pair by one thread. s_o is the caller's LDS (16 x HB x kAttnD doubles), free on entry.
 template <int HB, class Emit>
 IRON_DEV void attn_finish_f64(const double (&m)[HB], const double (&l)[HB],
-                              const double (&o)[HB][8], int wave, int row, int dl, Emit emit) {
-  __shared__ double s_o[16][HB][kAttnD];
+                              const double (&o)[HB][8], int wave, int row, int dl,
+                              double (*s_o)[HB][kAttnD], Emit emit) {
   __shared__ double s_l[16][HB];
   __shared__ double s_mm[HB];  // m is the workgroup's (s_mx): thread 0's copy, read by index
   const int rr = wave * 4 + row;
