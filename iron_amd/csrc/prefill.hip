@@ -11,21 +11,33 @@
 // Mapping: a wavefront owns 32 query rows (two 16-row tiles) of one head; a workgroup (4
 // wavefronts) owns 4 heads of one GQA group for the same rows (or, for groups smaller than 4,
 // more query blocks), so the K/V blocks it stages in LDS (16 KiB each: 64 keys at d = 128, 128 at
-// d = 64; double buffered, V transposed) serve every wavefront. Per key block a wavefront computes
-// S^T = K Q^T per 16-key tile (each K operand read serves both query tiles): lane l then holds the
-// scores of query l%16 for keys (l/16)*4 + i of the tile, which is exactly the B-operand layout of
-// P^T for O^T = V^T P^T when a 32-key step takes its keys in the order (tile 2s: 4 keys, tile
-// 2s+1: 4 keys) per lane quarter; the V^T operand reads those keys with two 8-byte LDS reads. In
-// O^T's layout lane l also owns query l%16, so the softmax correction and the final division need
-// no cross-lane exchange. Query blocks run latest (longest) first.
+// d = 64) serve every wavefront. Per key block a wavefront computes S^T = K Q^T per 16-key tile
+// (each K operand read serves both query tiles): lane l then holds the scores of query l%16 for
+// keys (l/16)*4 + i of the tile, which is exactly the B-operand layout of P^T for O^T = V^T P^T
+// when a 32-key step takes its keys in the order (tile 2s: 4 keys, tile 2s+1: 4 keys) per lane
+// quarter. In O^T's layout lane l also owns query l%16, so the softmax correction and the final
+// division need no cross-lane exchange. Query blocks run latest (longest) first.
+//
+// Staging: K and V blocks go from memory straight into LDS (global_load_lds_dwordx4, no staging
+// registers), both in their natural row-major layout with the 16-byte chunks of each row
+// XOR-swizzled by row (conflict-free operand reads). The V^T operand is read with gfx950's
+// transposing LDS load (ds_read_tr16_b64: within each 16 lanes, lane j receives element j & 3 of
+// the 8 bytes that lanes 4k + j / 4 address, k = 0..3). Block i + 1 is loaded while block i is
+// computed (two LDS halves each for K and V). Which of a wavefront's two tiles take part in a
+// block is decided once per block (a wave-uniform branch between a two-tile and a one-tile copy
+// of the block's code), not per MFMA: per-MFMA branches split the block into basic blocks the
+// scheduler cannot interleave, and the values live across them spill.
+#include <type_traits>
+
 #include "common.h"
 #include "internal.h"
 
 namespace {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
-
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 struct PrefillParams {
   const uint16_t* q;   // [B][H][S][D]
@@ -38,72 +50,41 @@ struct PrefillParams {
 
 IRON_DEV bf16x8 as_bf16x8(const uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
-// Staging of one key block (keys clamped to the sequence). K rows go to LDS as they are; V goes
-// transposed, the 4 keys of one dim in one 8-byte write.
-// The staging registers of one key block (four K and four V slices of 8 dims), as native vectors
-// so that they stay in registers.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-struct KVRegs {
-  u32x4 k0, k1, k2, k3, v0, v1, v2, v3;
-};
-
-// Staging coordinates: K is copied by thread -> (keys 4 kg .. +4, dims kd .. +8) with the dims
-// fastest across lanes (whole rows per 16 lanes: conflict-free row writes); V by thread -> (keys
-// 4 vg .. +4, dims vd .. +8) with the key groups fastest across lanes, so that the 8-byte V^T
-// writes of a wavefront spread over the LDS banks.
-struct StageIdx {
-  int kg, kd, vg, vd;
-};
-
-template <int D, int KB>
-IRON_DEV StageIdx stage_idx(int tid) {
-  constexpr int TPG = D / 8;   // threads per key row
-  constexpr int NG = KB / 4;   // key groups per block
-  return StageIdx{tid / TPG, (tid % TPG) * 8, tid % NG, (tid / NG) * 8};
+// One lane's 16 bytes from global memory (base + off bytes) into LDS at m0 + 16 * lane
+// (global_load_lds_dwordx4; lds wave-uniform). Inline asm: seeing an LDS-DMA store, the compiler
+// would wait for every one outstanding (vmcnt(0)) before any LDS read; the kernel orders the
+// staging itself (s_waitcnt vmcnt(0) and a barrier once per block).
+IRON_DEV void pf_dma16(const void* base, uint32_t off, uint32_t lds) {
+  __asm__ volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                   :
+                   : "v"(off), "s"(base), "s"(lds)
+                   : "memory");
 }
 
-// The K and V of one (sequence, KV head) as raw buffers of S rows: a block's loads take its byte
-// offset as the scalar operand and each thread's fixed offset (rows 4 g .. +3 of the block,
-// dims d .. +8; the row steps are immediates), so a block costs no address arithmetic. Keys past
-// S (the last block at D = 64 when S is not a multiple of 128) read as zero: they lie past every
-// query, so the causal mask drops their scores and their probabilities are zero.
-struct KVSrc {
-  __amdgpu_buffer_rsrc_t k, v;
-  int koff, voff;  // this thread's byte offsets within a block
-};
+// The 16-byte chunk c of row r of a staged block lives at chunk c ^ swz(r) (NCH chunks a row):
+// K rows by r (the 16 rows of an operand read hit 16 distinct chunks), V rows by 2r (the
+// transposing read takes a chunk pair of 16 consecutive rows: pairs stay adjacent).
+template <int NCH> IRON_DEV int swz_k(int r) { return r & (NCH - 1); }
+template <int NCH> IRON_DEV int swz_v(int r) { return (2 * r) & (NCH - 1); }
 
-template <int D, int KB>
-IRON_DEV void pf_gload(const KVSrc& src, int kb, KVRegs& r) {
-  const int sb = kb * KB * D * 2;
-  r.k0 = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.koff, sb, 0);
-  r.k1 = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.koff + D * 2, sb, 0);
-  r.k2 = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.koff + 2 * D * 2, sb, 0);
-  r.k3 = __builtin_amdgcn_raw_buffer_load_b128(src.k, src.koff + 3 * D * 2, sb, 0);
-  r.v0 = __builtin_amdgcn_raw_buffer_load_b128(src.v, src.voff, sb, 0);
-  r.v1 = __builtin_amdgcn_raw_buffer_load_b128(src.v, src.voff + D * 2, sb, 0);
-  r.v2 = __builtin_amdgcn_raw_buffer_load_b128(src.v, src.voff + 2 * D * 2, sb, 0);
-  r.v3 = __builtin_amdgcn_raw_buffer_load_b128(src.v, src.voff + 3 * D * 2, sb, 0);
-}
-
-// dims dc + 2w (low halves) and dc + 2w + 1 (high halves) of the 4 keys, one 8-byte write each
-IRON_DEV void pf_vt_pair(uint16_t* lo_row, uint16_t* hi_row, uint32_t a0, uint32_t a1, uint32_t a2,
-                         uint32_t a3) {
-  *(uint2*)lo_row = make_uint2((a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16));
-  *(uint2*)hi_row = make_uint2((a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u));
-}
-
-template <int D, int KB>
-IRON_DEV void pf_lstore(uint16_t (*s_k)[D + 8], uint16_t (*s_vt)[KB + 4], const StageIdx& x,
-                        const KVRegs& r) {
-  *(u32x4*)&s_k[4 * x.kg][x.kd] = r.k0;
-  *(u32x4*)&s_k[4 * x.kg + 1][x.kd] = r.k1;
-  *(u32x4*)&s_k[4 * x.kg + 2][x.kd] = r.k2;
-  *(u32x4*)&s_k[4 * x.kg + 3][x.kd] = r.k3;
-  const int c = 4 * x.vg, dc = x.vd;
-  pf_vt_pair(&s_vt[dc][c], &s_vt[dc + 1][c], r.v0.x, r.v1.x, r.v2.x, r.v3.x);
-  pf_vt_pair(&s_vt[dc + 2][c], &s_vt[dc + 3][c], r.v0.y, r.v1.y, r.v2.y, r.v3.y);
-  pf_vt_pair(&s_vt[dc + 4][c], &s_vt[dc + 5][c], r.v0.z, r.v1.z, r.v2.z, r.v3.z);
-  pf_vt_pair(&s_vt[dc + 6][c], &s_vt[dc + 7][c], r.v0.w, r.v1.w, r.v2.w, r.v3.w);
+// One block of KB keys (K or V) from rows kb0.. of a [S][D] slab into LDS: four instructions per
+// thread; instruction i of wavefront w fills bytes i*4096 + w*1024 .. +1024 of the block, lane l
+// its 16-byte chunk position (that offset + 16 l) % (2 D) of row (that offset + 16 l) / (2 D),
+// loading the global chunk the swizzle maps there. Rows past S repeat row S - 1 (they lie past
+// every query: the causal mask drops them).
+template <int D, bool IS_V>
+IRON_DEV void pf_dma_block(const uint16_t* slab, int kb0, int S, uint32_t lds_block, int wave,
+                           int lane) {
+  constexpr int NCH = D / 8;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int byte = i * 4096 + wave * 1024 + lane * 16;
+    const int r = byte / (2 * D), p = (byte % (2 * D)) / 16;
+    const int g = p ^ (IS_V ? swz_v<NCH>(r) : swz_k<NCH>(r));
+    const int row = min(kb0 + r, S - 1);
+    pf_dma16(slab, (uint32_t)(row * D + g * 8) * 2u,
+             (uint32_t)__builtin_amdgcn_readfirstlane(lds_block + i * 4096 + wave * 1024));
+  }
 }
 
 typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
@@ -120,17 +101,17 @@ IRON_DEV uint32_t pack_bf16(float lo, float hi) {
 template <int D, int HW>
 __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   constexpr int KB = 8192 / D;         // keys per block (16 KiB of K)
+  constexpr int NCH = D / 8;           // 16-byte chunks per row
   constexpr int NKT = KB / 16;         // 16-key tiles per block
   constexpr int NKS = KB / 32;         // 32-key P.V steps per block
   constexpr int NJ = D / 32;           // 32-wide head-dim steps of Q K^T
   constexpr int ND = D / 16;           // 16-wide head-dim tiles of O
   constexpr int PW = 4 / HW;           // tile pairs per workgroup
-  __shared__ __align__(16) uint16_t s_k[2][KB][D + 8];
-  // V^T rows of KB + 4 elements (34 dwords at D = 128): the 8-byte reads of 16 consecutive rows
-  // hit distinct banks (at KB + 8 rows r and r + 8 shared them: 3x the bank-conflict cycles)
-  __shared__ __align__(16) uint16_t s_vt[2][D][KB + 4];
+  __shared__ __align__(16) uint16_t s_k[2][KB * D];
+  __shared__ __align__(16) uint16_t s_v[2][KB * D];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
   const int quarter = lane >> 4, col = lane & 15;
   const int HG = p.H / p.KV;
   // 1-D grid, head groups fastest: consecutive workgroups go to consecutive XCDs, so with a
@@ -155,6 +136,8 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   const int nkb = (16 * (NT - 1 - pmin) + 15) / KB + 1;
 
   const size_t kvo = ((size_t)b * p.KV + kv) * S * D;
+  const uint16_t* kslab = p.k + kvo;
+  const uint16_t* vslab = p.v + kvo;
 
   // Q^T operands: lane l holds query row r0[t] + l%16 (clamped), d = 32 j + (l/16)*8 .. +8
   uint4 qf[2][NJ];
@@ -166,16 +149,6 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
     for (int j = 0; j < NJ; ++j) qf[t][j] = *(const uint4*)(qrow + 32 * j + quarter * 8);
   }
 
-  const StageIdx sx = stage_idx<D, KB>(tid);
-  KVSrc src;
-  src.k = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.k + kvo), 0, S * D * 2,
-                                            kBufferDword3);
-  src.v = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.v + kvo), 0, S * D * 2,
-                                            kBufferDword3);
-  src.koff = (4 * sx.kg * D + sx.kd) * 2;
-  src.voff = (4 * sx.vg * D + sx.vd) * 2;
-  KVRegs ra, rb;  // two register sets: block i + 2 is fetched while block i + 1 waits
-
   // O^T accumulators: tile (t, dt) is 16 dims x 16 queries; lane l holds query r0[t] + l%16,
   // dims 16 dt + (l/16)*4 + i
   f32x4 o[2][ND];
@@ -185,40 +158,59 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
     for (int dt = 0; dt < ND; ++dt) o[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};  // this lane's share of query stats
   const float c = p.scale_log2;
+  // tile t takes part in block kbi while the block starts at or before its last row
+  auto active = [&](int kbi, int t) {
+    return live && !(t == 0 && twin) && kbi * KB <= r0[t] + 15;
+  };
+  const uint32_t kbase = (uint32_t)(uintptr_t)&s_k[0][0], vbase = (uint32_t)(uintptr_t)&s_v[0][0];
+  auto k_block = [&](int kbi) { return kbase + (uint32_t)((kbi & 1) * KB * D * 2); };
+  auto v_block = [&](int kbi) { return vbase + (uint32_t)((kbi & 1) * KB * D * 2); };
 
-  pf_gload<D, KB>(src, 0, ra);
-  if (nkb > 1) pf_gload<D, KB>(src, 1, rb);
-  pf_lstore<D, KB>(s_k[0], s_vt[0], sx, ra);
-  __syncthreads();
-  // iteration kbi: fetch block kbi + 2 into the set that held block kbi, compute block kbi, then
-  // stage block kbi + 1 (fetched an iteration earlier) into the other LDS buffer
-  auto iteration = [&](int kbi, KVRegs& fetch, KVRegs& stage) {
-    const int buf = kbi & 1;
-    const int kb0 = kbi * KB;
-    // unconditional (past the last block it re-reads it): a load in a branch would make the
-    // compiler's wait before the staging below count it as the youngest load, draining the fetch
-    pf_gload<D, KB>(src, min(kbi + 2, nkb - 1), fetch);
-    // tile t takes part while the block starts at or before its last row (wave-uniform)
-    const bool act[2] = {live && !twin && kb0 <= r0[0] + 15, live && kb0 <= r0[1] + 15};
-    f32x4 st[2][NKT];
+  // S^T of block kbi for tiles T0..1 (K from its LDS half)
+  auto qk = [&](auto t0c, int kbi, f32x4 (&st)[2][NKT]) {
+    constexpr int T0 = decltype(t0c)::value;
+    const uint16_t* kb = &s_k[kbi & 1][0];
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < NKT; ++kt) {
+      const int r = 16 * kt + col;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const bf16x8 a = as_bf16x8(*(const uint4*)&s_k[buf][16 * kt + col][32 * j + quarter * 8]);
-        if (act[0])
-          st[0][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[0][j]),
-                                                              j ? st[0][kt] : zero, 0, 0, 0);
-        if (act[1])
-          st[1][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[1][j]),
-                                                              j ? st[1][kt] : zero, 0, 0, 0);
+        const int ch = (4 * j + quarter) ^ swz_k<NCH>(r);
+        const bf16x8 a = as_bf16x8(*(const uint4*)&kb[r * D + ch * 8]);
+#pragma unroll
+        for (int t = T0; t < 2; ++t)
+          st[t][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(qf[t][j]),
+                                                              j ? st[t][kt] : zero, 0, 0, 0);
       }
     }
+  };
+  // The V^T operand of (32-key step ks, dim tile dt): lane (q, j) gets dims 16 dt + j of keys
+  // 32 ks + 4 q + 0..3 and 32 ks + 16 + 4 q + 0..3, by two transposing reads in which lane s
+  // addresses the 4 dims 16 dt + 4 (s & 3) .. +3 of key 32 ks + 4 q + s / 4 (+ 16).
+  auto vt_operand = [&](const uint16_t* vb, int ks, int dt) {
+    const int s = col;
+    const int dcol = 16 * dt + 4 * (s & 3);
+    bf16x4 h[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int r = 32 * ks + 16 * hh + 4 * quarter + (s >> 2);
+      const int ch = (dcol >> 3) ^ swz_v<NCH>(r);
+      const uint16_t* a = &vb[r * D + ch * 8 + (dcol & 7)];
+      h[hh] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(const_cast<uint16_t*>(a))));
+    }
+    return __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  // the online softmax of block kbi's scores for tiles T0..1, then O^T += V^T P^T (V from its
+  // LDS half)
+  auto softmax_pv = [&](auto t0c, int kbi, f32x4 (&st)[2][NKT]) {
+    constexpr int T0 = decltype(t0c)::value;
+    const uint16_t* vb = &s_v[kbi & 1][0];
+    const int kb0 = kbi * KB;
     bf16x8 pb[2][NKS];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      if (!act[t]) continue;
+    for (int t = T0; t < 2; ++t) {
       const int qi = r0[t] + col;
       const bool diag = kb0 + KB - 1 > r0[t];  // some key may lie past some query: mask
       if (diag) {  // wave-uniform: only the blocks that reach past a query need the mask
@@ -269,22 +261,42 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
     for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt) {
-        const uint16_t* vr = &s_vt[buf][16 * dt + col][32 * ks + quarter * 4];
-        const uint2 v0 = *(const uint2*)vr;
-        const uint2 v1 = *(const uint2*)(vr + 16);
-        const bf16x8 a = as_bf16x8(make_uint4(v0.x, v0.y, v1.x, v1.y));
-        if (act[0]) o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][ks], o[0][dt], 0, 0, 0);
-        if (act[1]) o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][ks], o[1][dt], 0, 0, 0);
+        const bf16x8 a = vt_operand(vb, ks, dt);
+#pragma unroll
+        for (int t = T0; t < 2; ++t)
+          o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t][ks], o[t][dt], 0, 0, 0);
       }
-    if (kbi + 1 < nkb) pf_lstore<D, KB>(s_k[buf ^ 1], s_vt[buf ^ 1], sx, stage);
+  };
+  // start of iteration kbi (after the previous barrier): block kbi + 1 into the halves block
+  // kbi - 1 was read from
+  auto fetch = [&](int kbi) {
+    if (kbi + 1 < nkb) {
+      pf_dma_block<D, false>(kslab, (kbi + 1) * KB, S, k_block(kbi + 1), wave, lane);
+      pf_dma_block<D, true>(vslab, (kbi + 1) * KB, S, v_block(kbi + 1), wave, lane);
+    }
+  };
+  // end of iteration: this thread's block loads have landed, then every thread's have
+  auto land = [&]() {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   };
-  int kbi = 0;
-  for (; kbi + 1 < nkb; kbi += 2) {  // no branch around an iteration's loads inside the loop
-    iteration(kbi, ra, rb);
-    iteration(kbi + 1, rb, ra);
+
+  pf_dma_block<D, false>(kslab, 0, S, k_block(0), wave, lane);
+  pf_dma_block<D, true>(vslab, 0, S, v_block(0), wave, lane);
+  land();
+  for (int kbi = 0; kbi < nkb; ++kbi) {
+    f32x4 st[2][NKT];
+    fetch(kbi);
+    // tile 0 active implies tile 1 active (its rows come later): one branch per block
+    if (active(kbi, 0)) {
+      qk(std::integral_constant<int, 0>(), kbi, st);
+      softmax_pv(std::integral_constant<int, 0>(), kbi, st);
+    } else if (active(kbi, 1)) {
+      qk(std::integral_constant<int, 1>(), kbi, st);
+      softmax_pv(std::integral_constant<int, 1>(), kbi, st);
+    }
+    land();
   }
-  if (kbi < nkb) iteration(kbi, ra, rb);
 
   // row sums: the four lane quarters hold disjoint keys of the same query
   if (!live) return;
