@@ -27,6 +27,10 @@
 // block is decided once per block (a wave-uniform branch between a two-tile and a one-tile copy
 // of the block's code), not per MFMA: per-MFMA branches split the block into basic blocks the
 // scheduler cannot interleave, and the values live across them spill.
+//
+// Two wavefronts share each SIMD (two workgroups per CU). A wavefront raises its priority
+// (s_setprio 1) while it issues its P.V MFMAs, so the SIMD's other wavefront fills the MFMA's
+// cycles with its softmax VALU work instead of both contending for the same phase.
 #include <type_traits>
 
 #include "common.h"
@@ -107,6 +111,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
   constexpr int NJ = D / 32;           // 32-wide head-dim steps of Q K^T
   constexpr int ND = D / 16;           // 16-wide head-dim tiles of O
   constexpr int PW = 4 / HW;           // tile pairs per workgroup
+  constexpr float kLazy = 8.f;         // how far the softmax reference may trail the maximum
   __shared__ __align__(16) uint16_t s_k[2][KB * D];
   __shared__ __align__(16) uint16_t s_v[2][KB * D];
 
@@ -202,6 +207,17 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
     }
     return __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3, 4, 5, 6, 7);
   };
+  // max over the four lane quarters (lanes l, l ^ 16, l ^ 32, l ^ 48) by two lane swaps:
+  // v_permlane16_swap exchanges the odd 16-lane rows of its first operand with the even rows of
+  // its second, v_permlane32_swap the upper half of the first with the lower half of the second
+  auto quarter_max = [](float x) __attribute__((always_inline)) {
+    const uint32_t u = __float_as_uint(x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t w = __float_as_uint(x);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  };
   // the online softmax of block kbi's scores for tiles T0..1, then O^T += V^T P^T (V from its
   // LDS half)
   auto softmax_pv = [&](auto t0c, int kbi, f32x4 (&st)[2][NKT]) {
@@ -209,28 +225,52 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
     const uint16_t* vb = &s_v[kbi & 1][0];
     const int kb0 = kbi * KB;
     bf16x8 pb[2][NKS];
+    float mx[2];
 #pragma unroll
     for (int t = T0; t < 2; ++t) {
-      const int qi = r0[t] + col;
       const bool diag = kb0 + KB - 1 > r0[t];  // some key may lie past some query: mask
       if (diag) {  // wave-uniform: only the blocks that reach past a query need the mask
+        // key kb0 + 16 kt + 4 quarter + i lies past query r0[t] + col
+        const int lim = r0[t] + col - kb0 - 4 * quarter;
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (kb0 + 16 * kt + quarter * 4 + i > qi) st[t][kt][i] = -INFINITY;
+            if (16 * kt + i > lim) st[t][kt][i] = -INFINITY;
       }
-      float mx = -INFINITY;
+      float x = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[t][kt][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      // running maximum in the exp2 domain (scale > 0, so the raw maximum maps to it)
-      const float mn = fmaxf(m[t], mx * c);  // finite: every query has a key in block 0
-      const float corr = __builtin_amdgcn_exp2f(m[t] - mn);  // m = -inf on the first block
-      m[t] = mn;
+        for (int i = 0; i < 4; ++i) x = fmaxf(x, st[t][kt][i]);
+      mx[t] = quarter_max(x) * c;  // the block's maximum in the exp2 domain (scale > 0)
+    }
+    // The probabilities are taken against a reference m[t] that may trail the running maximum
+    // by up to kLazy (so they reach 2^kLazy at most: no overflow in fp32 or bf16, and the final
+    // division by the row sum cancels the reference). The reference moves, and O and the row sums
+    // are rescaled, only when some lane's maximum passes it by more: after the first blocks that
+    // is rare (the rescale costs 32 multiplies per tile, twice the block's 16 scores per lane).
+    // m = -inf before block 0, and every query has a key in block 0, so the first block always
+    // sets it.
+    bool grow = false;
+#pragma unroll
+    for (int t = T0; t < 2; ++t) grow |= mx[t] > m[t] + kLazy;
+    if (__ballot(grow)) {
+#pragma unroll
+      for (int t = T0; t < 2; ++t) {
+        const float mn = fmaxf(m[t], mx[t]);
+        const float corr = __builtin_amdgcn_exp2f(m[t] - mn);  // 0 on the first block
+        m[t] = mn;
+        lsum[t] *= corr;
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[t][dt][i] *= corr;
+      }
+    }
+#pragma unroll
+    for (int t = T0; t < 2; ++t) {
+      const float mn = m[t];
       float ps = 0.f;
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
@@ -248,15 +288,10 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
         }
         pb[t][ks] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
       }
-      lsum[t] = lsum[t] * corr + ps;
-      if (__ballot(corr != 1.f)) {  // no lane's maximum moved: every factor is exactly 1
-#pragma unroll
-        for (int dt = 0; dt < ND; ++dt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[t][dt][i] *= corr;
-      }
+      lsum[t] += ps;
     }
     // O^T += V^T P^T; each V^T operand serves both query tiles
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
@@ -266,6 +301,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillParams p) {
         for (int t = T0; t < 2; ++t)
           o[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[t][ks], o[t][dt], 0, 0, 0);
       }
+    __builtin_amdgcn_s_setprio(0);
   };
   // start of iteration kbi (after the previous barrier): block kbi + 1 into the halves block
   // kbi - 1 was read from

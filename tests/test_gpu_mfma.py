@@ -325,6 +325,7 @@ def test_qwen3_8b_layer_b16_context_8192():
     (8, 8, 128, 128, "normal"),     # plain MHA
     (16, 8, 512, 64, "normal"),     # GQA 2
     (4, 1, 192, 128, "normal"),     # S padded from 150 (the reference's 64-padding)
+    (8, 2, 512, 128, "ramp"),       # scores rising by ~20 (log2) a block: every block rescales
 ])
 def test_prefill_attention(H, KV, S, D, dist, oracle_provider):
     _say(f"prefill H={H} KV={KV} S={S} D={D} {dist}")
@@ -340,6 +341,9 @@ def test_prefill_attention(H, KV, S, D, dist, oracle_provider):
         return torch.randn(*shape, generator=gen).to(torch.bfloat16)
 
     q, k, v = draw(H, Sp, D), draw(KV, Sp, D), draw(KV, Sp, D)
+    if dist == "ramp":  # key j's scores grow with j: each block's maximum passes the last one's
+        q = q.float().abs().to(torch.bfloat16)
+        k = (k.float().abs() * (torch.arange(Sp).float() / 32).reshape(1, Sp, 1)).to(torch.bfloat16)
     o = torch.zeros(H * Sp * D, dtype=torch.bfloat16, device=DEV)
     op.get_callable()(q.reshape(-1).to(DEV), k.reshape(-1).to(DEV), v.reshape(-1).to(DEV), o)
     torch.cuda.synchronize()
