@@ -60,6 +60,12 @@ struct GemmParams {
   const uint16_t* r1;
   const uint16_t* r2;
   int r_stride;
+  // the folded residual RMSNorm (iron::GemmResNorm): the tile sums of squares the producer writes
+  // and the consumer reads; for the consumer also the norm weight, D / 64 and eps (cur, a: r1, r2)
+  double* ssq;
+  const uint16_t* n_w;
+  int n_tiles;
+  float n_eps;
 };
 
 IRON_DEV double silu_mul_d(double g, double u) {
@@ -325,6 +331,19 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
           if (s0 + j < p.splits) a[mi] += v[j];
       }
     store_out(p, b, m, a[0], a[1]);
+    if (p.ssq) {  // x1 = f32(cur + bf16(y)) of the folded RMSNorm, squared (exact in fp64)
+      const float x1 = bf16_to_f32(p.r1[(size_t)b * p.r_stride + m]) +
+                       bf16_to_f32(f64_to_bf16(a[0]));
+      s_part[0][b][t % kTM] = (double)x1 * (double)x1;
+    }
+  }
+  if (p.ssq) {  // the tile's sum per batch row, in row order (s_part is free past the counts)
+    __syncthreads();
+    if (tid < p.B) {
+      double ss = 0.0;
+      for (int r = 0; r < kTM; ++r) ss += s_part[0][tid][r];
+      p.ssq[(size_t)blockIdx.x * kBN + tid] = ss;
+    }
   }
   if (tid == 0) __hip_atomic_store(p.ctr + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -379,10 +398,13 @@ IRON_DEV bf16x8 u8_to_bf16u(uint32_t lo, uint32_t hi) {
 }
 
 
-template <bool DUAL, bool XPL, int W, int RB, bool G32>
+// NORM: x is the folded residual RMSNorm's hf (iron::GemmResNorm), staged from cur (r1), a (r2)
+// and the norm weight (n_w): the three buffers take the places of the three planes.
+template <bool DUAL, bool XPL, int W, int RB, bool G32, bool NORM = false>
 __global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
   constexpr int NM = DUAL ? 2 : 1;
   constexpr int NX = XPL ? 3 : 1;
+  static_assert(!NORM || XPL, "the folded RMSNorm stages fp32 hf as three planes");
   constexpr int NT = 64 * W;                      // threads
   constexpr int TILE = 16 * RB * W;
   constexpr int XP = kBN * kRChunk * 2 / (NT * 16);  // 16-byte x pieces per plane and thread
@@ -421,16 +443,48 @@ __global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
   // scale of the chunk's first group; reads past a row's own groups land in the wire or past its
   // end, where the buffer returns zero, and are never used)
   __amdgpu_buffer_rsrc_t xr[NX];
+  if constexpr (NORM) {  // cur, a (rows of x_stride = D elements) and the norm weight
+    xr[0] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.r1), 0,
+                                              p.B * p.x_stride * 2, kBufferDword3);
+    xr[1] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.r2), 0,
+                                              p.B * p.x_stride * 2, kBufferDword3);
+    xr[2] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.n_w), 0, p.K * 2,
+                                              kBufferDword3);
+  } else {
 #pragma unroll
-  for (int xi = 0; xi < NX; ++xi)
-    xr[xi] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x + xi * p.x_plane), 0,
-                                               p.B * p.x_stride * 2, kBufferDword3);
+    for (int xi = 0; xi < NX; ++xi)
+      xr[xi] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x + xi * p.x_plane), 0,
+                                                 p.B * p.x_stride * 2, kBufferDword3);
+  }
   int xvo[XP];
 #pragma unroll
   for (int h = 0; h < XP; ++h) {
     const int idx = tid + NT * h;
     xvo[h] = ((idx >> 5) * p.x_stride + (idx & 31) * 8) * 2;
   }
+  // NORM: 1 / RMS of every batch row from the producer's D / 64 tile sums (up to 128): lane j of
+  // the 32 that serve batch row b = tid / 32 loads tiles j, j + 32, .. (issued first, ahead of the
+  // first chunk and the ring), and after the ring is issued the 32 lanes add in a fixed tree
+  // order. Rows past B get 0 (their cur and a read as zero).
+  __shared__ double s_inv[kBN];
+  double nv[4];
+  auto norm_issue = [&]() {
+    static_assert(NT >= 32 * kBN, "32 lanes per batch row");
+    const int b = (tid >> 5) & (kBN - 1), j = tid & 31;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int t = j + 32 * k;
+      nv[k] = tid < 32 * kBN && b < p.B && t < p.n_tiles ? p.ssq[(size_t)t * kBN + b] : 0.0;
+    }
+  };
+  auto norm_finish = [&]() {
+    const int b = (tid >> 5) & (kBN - 1), j = tid & 31;
+    double ss = (nv[0] + nv[1]) + (nv[2] + nv[3]);
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 32);
+    if (tid < 32 * kBN && j == 0) s_inv[b] = b < p.B ? inv_rms(ss, p.K, (double)p.n_eps) : 0.0;
+    __syncthreads();
+  };
   const int sf = tid * SB;
   // the matrix is the same across a wavefront (W / NM whole wavefronts per matrix): a uniform
   // value keeps the buffer descriptor in scalar registers (else every load loops over lanes)
@@ -456,8 +510,11 @@ __global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
 #pragma unroll
     for (int xi = 0; xi < NX; ++xi)
 #pragma unroll
-      for (int h = 0; h < XP; ++h)
-        xs[xi][h] = __builtin_amdgcn_raw_buffer_load_b128(xr[xi], xvo[h], kc * 2, 0);
+      for (int h = 0; h < XP; ++h) {
+        // NORM's norm weight has no batch rows: element k of the piece's row at every row
+        const int vo = NORM && xi == 2 ? ((tid + NT * h) & 31) * 16 : xvo[h];
+        xs[xi][h] = __builtin_amdgcn_raw_buffer_load_b128(xr[xi], vo, kc * 2, 0);
+      }
     const int so = (kc >> p.gshift) * 2;
     if constexpr (SB == 16) ss4 = __builtin_amdgcn_raw_buffer_load_b128(sr, svo, so, 0);
     else if constexpr (SB == 8) ss2 = __builtin_amdgcn_raw_buffer_load_b64(sr, svo, so, 0);
@@ -467,14 +524,40 @@ __global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
 #pragma unroll
     for (int h = 0; h < XP; ++h) {
       const int idx = tid + NT * h;
+      iron_u32x4 xp[NX];  // the piece's planes
+      if constexpr (NORM) {
+        // hf = f32((f32(cur + a) * inv) * w), evaluated in fp64 and split into three exact
+        // planes: the values and roundings of the separate residual-RMSNorm kernel (api.hip)
+        const double inv = s_inv[idx >> 5];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          uint16_t pl[2][3];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const uint32_t sh = hh ? 0xffff0000u : 0u;
+            auto el = [&](uint32_t d) {
+              return __uint_as_float(hh ? (d & sh) : (d << 16));
+            };
+            const float x1 = el(xs[0][h][e]) + el(xs[1][h][e]);
+            const double y = ((double)x1 * inv) * (double)el(xs[2][h][e]);
+            split3_bf16((float)y, pl[hh][0], pl[hh][1], pl[hh][2]);
+          }
+#pragma unroll
+          for (int xi = 0; xi < 3; ++xi)
+            xp[xi][e] = (uint32_t)pl[0][xi] | ((uint32_t)pl[1][xi] << 16);
+        }
+      } else {
+#pragma unroll
+        for (int xi = 0; xi < NX; ++xi) xp[xi] = xs[xi][h];
+      }
       double sx = 0.0;  // this piece's x (every plane), then the group's over its 4 G/32 lanes
 #pragma unroll
       for (int xi = 0; xi < NX; ++xi) {
-        *(iron_u32x4*)&s_x[buf][xi][idx >> 5][(idx & 31) * 8] = xs[xi][h];
+        *(iron_u32x4*)&s_x[buf][xi][idx >> 5][(idx & 31) * 8] = xp[xi];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          sx += (double)__uint_as_float(xs[xi][h][e] << 16);
-          sx += (double)__uint_as_float(xs[xi][h][e] & 0xffff0000u);
+          sx += (double)__uint_as_float(xp[xi][e] << 16);
+          sx += (double)__uint_as_float(xp[xi][e] & 0xffff0000u);
         }
       }
       sx += dpp_d<0xb1>(sx);  // quad_perm [1,0,3,2]
@@ -513,6 +596,10 @@ __global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
   // block's MFMAs then counts the later blocks' loads. (A branch around a load, or the scheduler
   // hoisting a later load above an earlier one, drops the compiler's wait to zero and drains the
   // ring every block.)
+  if constexpr (NORM) {
+    norm_issue();
+    __builtin_amdgcn_sched_barrier(0);
+  }
   xload(0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -520,6 +607,7 @@ __global__ __launch_bounds__(64 * W, 4) void gemm_w8_rs_kernel(GemmParams p) {
     wload(ring[u], min(u, nb - 1));
     __builtin_amdgcn_sched_barrier(0);
   }
+  if constexpr (NORM) norm_finish();
   xstore(0);
   __builtin_amdgcn_sched_barrier(0);
   xload(min(1, nc - 1));
@@ -772,15 +860,29 @@ int gemm_check(const char* fn, int B, int M, int K, int G) {
   return IRON_OK;
 }
 
+bool gemm_resnorm_foldable(int D, int QD, int FF) {
+  if (D <= 0 || QD <= 0 || FF <= 0 || D % kTM || D / kTM > 32 * 4 || QD % kKS) return false;
+  const GemmPlan po = plan_gemm(D, QD, false), pg = plan_gemm(FF, D, true);
+  return !po.rs && po.splits > 1 && pg.rs;
+}
+
 int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile_m, int domain,
                    const uint16_t* x, size_t x_plane, int B, int x_stride, int epi, void* y,
                    int y_stride, size_t y_plane, const uint16_t* r1, const uint16_t* r2,
                    int r_stride, unsigned int* ctr, void* part, size_t part_bytes,
-                   hipStream_t stream, const char* fn) {
+                   hipStream_t stream, const char* fn, const GemmResNorm* rn) {
   int st = gemm_check(fn, B, M, K, G);
   if (st) return st;
   const bool dual = w1 != nullptr;
   const GemmPlan pl = plan_gemm(M, K, dual);
+  // the folded residual RMSNorm: the producer (no a) splits K and has the bf16 epilogue; the
+  // consumer is the register-streamed dual GEMM over the norm's D
+  const bool rn_prod = rn && !rn->a, rn_cons = rn && rn->a;
+  if (rn && (!rn->ssq || !rn->cur || !aligned(rn->ssq, 8) ||
+             (rn_prod && (pl.rs || pl.splits < 2 || epi != GEMM_EPI_BF16 || M != rn->D)) ||
+             (rn_cons && (!pl.rs || !dual || !rn->w || K != rn->D || rn->D % kTM ||
+                          rn->D / kTM > 32 * 4))))
+    return fail(IRON_ERR_UNSUPPORTED, "%s: the folded RMSNorm does not fit this GEMM plan", fn);
   GemmParams p = {};
   p.w0 = (const uint8_t*)w0;
   p.w1 = (const uint8_t*)w1;
@@ -805,6 +907,19 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
   p.r1 = r1;
   p.r2 = r2;
   p.r_stride = r_stride;
+  if (rn_prod) {
+    p.ssq = rn->ssq;
+    p.r1 = rn->cur;
+    p.r_stride = rn->D;
+  } else if (rn_cons) {
+    p.ssq = rn->ssq;
+    p.r1 = rn->cur;
+    p.r2 = rn->a;
+    p.x_stride = rn->D;
+    p.n_w = rn->w;
+    p.n_tiles = rn->D / kTM;
+    p.n_eps = rn->eps;
+  }
   if (pl.splits > 1) {
     const size_t need = gemm_workspace_bytes(M, K, dual);
     if (!part || !ctr || part_bytes < need)
@@ -825,7 +940,12 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
     else hipLaunchKernelGGL((gemm_w8_rs_kernel<D_, X_, kRW, kRRB, false>), grid, blk, 0,     \
                             stream, p);                                                      \
   } while (0)
-    if (dual) {
+    if (rn_cons) {
+      if (g32) hipLaunchKernelGGL((gemm_w8_rs_kernel<true, true, kRW, kRRB, true, true>), grid,
+                                  blk, 0, stream, p);
+      else hipLaunchKernelGGL((gemm_w8_rs_kernel<true, true, kRW, kRRB, false, true>), grid, blk,
+                              0, stream, p);
+    } else if (dual) {
       if (x_f32) IRON_RS(true, true);
       else IRON_RS(true, false);
     } else {

@@ -29,7 +29,8 @@ static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Layout: the GEMM's split-K counters (kGemmCtrBytes, for every B), then for B <= 4 (GEMV):
 // gh (fp32 [B][FF]) | a (bf16 [B][D]); for B > 4 (MFMA): gh (three bf16 planes [3][B][FF] of
-// the fp32 values) | a (bf16 [B][D]) | hf (planes [3][B][D]) | the split-K partials (shared by
+// the fp32 values) | a (bf16 [B][D]) | hf (planes [3][B][D]; with the folded RMSNorm, the
+// producer's tile sums of squares [D / 64][16] fp64 instead) | the split-K partials (shared by
 // the GEMMs, which run in sequence).
 size_t iron_swiglu_mlp_workspace(int B, int D, int FF) {
   if (B <= 0 || D <= 0 || FF <= 0) return 0;
@@ -80,7 +81,8 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
   workspace_bytes -= iron::kGemmCtrBytes;
   if (B > iron::kGemvMaxBatch) {
     // MFMA path: the prologue (x1 = cur + a, hf = RMSNorm(x1) * n_pf in fp32) runs once per
-    // row in its own kernel, then three GEMMs with the SwiGLU / residual epilogues
+    // row in its own kernel, or (with Wo, when the plans allow) folds into Wo's epilogue and the
+    // gate/up GEMM's staging; then the GEMMs with the SwiGLU / residual epilogues
     if ((st = iron::gemm_check(fn, B, FF, D, G)) || (st = iron::gemm_check(fn, B, D, FF, G)))
       return st;
     if (wo && (st = iron::gemm_check(fn, B, D, QD, G))) return st;
@@ -90,19 +92,30 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
     char* part = (char*)hf + round256((size_t)3 * B * D * 2);
     const size_t part_bytes = workspace_bytes - (size_t)(part - base);
     const uint16_t* a = cx_or_a;
+    // with the output projection, the residual RMSNorm folds into it and the gate/up GEMM when
+    // their plans allow (iron::GemmResNorm; its tile sums take hf's place in the workspace)
+    const bool fold = wo && iron::gemm_resnorm_foldable(D, QD, FF);
+    iron::GemmResNorm rn = {(double*)hf, cur, nullptr, n_pf, D, eps};
     if (wo) {
       uint16_t* dst = a_out ? a_out : a_buf;
       st = iron::gemm_w8_launch(wo, nullptr, D, QD, G, tile_m_o, domain, cx_or_a, 0, B, QD,
                                 iron::GEMM_EPI_BF16, dst, D, 0, nullptr, nullptr, 0, ctr, part,
-                                part_bytes, s, fn);
+                                part_bytes, s, fn, fold ? &rn : nullptr);
       if (st) return st;
       a = dst;
     }
-    st = iron::res_rmsnorm_planes_launch(cur, a, n_pf, hf, B, D, eps, s);
-    if (st) return st;
-    st = iron::gemm_w8_launch(wg, wu, FF, D, G, tile_m_gu, domain, hf, (size_t)B * D, B, D,
-                              iron::GEMM_EPI_SWIGLU_PLANES, gh, FF, (size_t)B * FF, nullptr,
-                              nullptr, 0, ctr, part, part_bytes, s, fn);
+    if (fold) {
+      rn.a = a;
+      st = iron::gemm_w8_launch(wg, wu, FF, D, G, tile_m_gu, domain, nullptr, 0, B, D,
+                                iron::GEMM_EPI_SWIGLU_PLANES, gh, FF, (size_t)B * FF, nullptr,
+                                nullptr, 0, ctr, part, part_bytes, s, fn, &rn);
+    } else {
+      st = iron::res_rmsnorm_planes_launch(cur, a, n_pf, hf, B, D, eps, s);
+      if (st) return st;
+      st = iron::gemm_w8_launch(wg, wu, FF, D, G, tile_m_gu, domain, hf, (size_t)B * D, B, D,
+                                iron::GEMM_EPI_SWIGLU_PLANES, gh, FF, (size_t)B * FF, nullptr,
+                                nullptr, 0, ctr, part, part_bytes, s, fn);
+    }
     if (st) return st;
     return iron::gemm_w8_launch(wd, nullptr, D, FF, G, tile_m_d, domain, gh, (size_t)B * FF, B,
                                 FF, iron::GEMM_EPI_RES_BF16, nxt, D, 0, cur, a, D, ctr, part,

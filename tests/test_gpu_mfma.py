@@ -128,6 +128,10 @@ def test_gemm_mfma(M, K, G, tile_m, B, domain):
     (4096, 1024, 0, False, 64, 5),
     (4096, 2048, 0, False, 128, 16),
     (4096, 1024, 0, False, 32, 8),
+    # the residual RMSNorm folded into Wo (tile sums of squares) and the register-streamed gate/up
+    # (hf staged from cur, a and the norm weight), at other group sizes and batches below 16
+    (4096, 1024, 2048, True, 64, 5),
+    (4096, 2048, 4096, True, 128, 9),
 ])
 def test_swiglu_mlp_mfma(D, FF, QD, fuse_o, G, B):
     _say(f"swiglu mfma D={D} FF={FF} QD={QD} fuse_o={fuse_o} G={G} B={B}")
