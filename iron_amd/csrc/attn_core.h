@@ -187,6 +187,12 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, b
   }
   const int si = dl % N, sh = si % HB;
   const bool sv = t0 + (si / HB) * 16 + wave * 4 + row < t_end;
+  // Two workgroups share each CU, so two wavefronts each SIMD. A wavefront raises its priority
+  // over the tile's dependent chain (the transpose sum, the maximum and its barrier, the
+  // exponentials and their broadcast) and drops it for the FMA-heavy dot products and P.V, so the
+  // SIMD's other wavefront fills the chain's latency with its own FMAs (config 5: 7.84 -> 7.78 ms
+  // per step).
+  __builtin_amdgcn_s_setprio(1);
   double tot = row16_transpose_sum<N>(part, dl);
   // The exchange must run with every lane of the row active: its DPP moves read partner lanes,
   // and the compiler would otherwise sink it into the branch on sv below (sv differs between the
@@ -227,6 +233,7 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, b
   const double ev = sc == -INFINITY ? 0.0 : exp(sc - mn_s);
   double pe[U][HB];
   share_all<HB, U>(ev, pe, std::make_integer_sequence<int, 16>{});
+  __builtin_amdgcn_s_setprio(0);
   // rescale the running sums (the first tile starts from zero): lane h has head h's factor.
   // Skipped when no maximum moved (every factor would be e^0 = 1 exactly); workgroup-uniform.
   bool moved = false;
