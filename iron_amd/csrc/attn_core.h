@@ -171,6 +171,12 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, b
     }
     if (t >= t_end) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // rows past the context may hold NaNs
   }
+  // Two workgroups share each CU, so two wavefronts each SIMD. A wavefront raises its priority
+  // from the q.k dot products through the tile's dependent chain (the transpose sum, the maximum
+  // and its barrier, the exponentials and their broadcast) and drops it for P.V, so the SIMD's
+  // other wavefront fills the chain's latency with its own P.V FMAs (config 5: 7.84 -> 7.68 ms
+  // per step; config 3 B=8: 22.3 -> 21.3 us).
+  __builtin_amdgcn_s_setprio(1);
   // this lane's 8-dim partials of every (u, h), then the row sums, score (u, h) in lane u HB + h
   double part[N];
 #pragma unroll
@@ -187,12 +193,6 @@ IRON_DEV void attn_tile_f64(uint4 (&kr)[U], uint4 (&vr)[U], int t0, int t_end, b
   }
   const int si = dl % N, sh = si % HB;
   const bool sv = t0 + (si / HB) * 16 + wave * 4 + row < t_end;
-  // Two workgroups share each CU, so two wavefronts each SIMD. A wavefront raises its priority
-  // over the tile's dependent chain (the transpose sum, the maximum and its barrier, the
-  // exponentials and their broadcast) and drops it for the FMA-heavy dot products and P.V, so the
-  // SIMD's other wavefront fills the chain's latency with its own FMAs (config 5: 7.84 -> 7.78 ms
-  // per step).
-  __builtin_amdgcn_s_setprio(1);
   double tot = row16_transpose_sum<N>(part, dl);
   // The exchange must run with every lane of the row active: its DPP moves read partner lanes,
   // and the compiler would otherwise sink it into the branch on sv below (sv differs between the
