@@ -313,8 +313,11 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
   // device-scope (sc1) buffer loads, eight in flight per thread; the sum runs in split order.
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       p.part, 0, NM * p.splits * kBN * p.M * (int)sizeof(double), kBufferDword3);
-  for (int t = tid; t < kTM * p.B; t += 512) {
+  static_assert(kTM == 64, "a wavefront's lanes are one batch row's tile rows");
+  for (int t = tid; t < kTM * p.B; t += 512) {  // whole wavefronts: kTM * B is a multiple of 64
     const int b = t / kTM, m = row0 + t % kTM;
+    // the folded RMSNorm's residual input, loaded ahead of the partials (in flight with them)
+    const uint16_t cur = p.ssq ? p.r1[(size_t)b * p.r_stride + m] : (uint16_t)0;
     double a[2] = {0.0, 0.0};
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi)
@@ -331,18 +334,13 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
           if (s0 + j < p.splits) a[mi] += v[j];
       }
     store_out(p, b, m, a[0], a[1]);
-    if (p.ssq) {  // x1 = f32(cur + bf16(y)) of the folded RMSNorm, squared (exact in fp64)
-      const float x1 = bf16_to_f32(p.r1[(size_t)b * p.r_stride + m]) +
-                       bf16_to_f32(f64_to_bf16(a[0]));
-      s_part[0][b][t % kTM] = (double)x1 * (double)x1;
-    }
-  }
-  if (p.ssq) {  // the tile's sum per batch row, in row order (s_part is free past the counts)
-    __syncthreads();
-    if (tid < p.B) {
-      double ss = 0.0;
-      for (int r = 0; r < kTM; ++r) ss += s_part[0][tid][r];
-      p.ssq[(size_t)blockIdx.x * kBN + tid] = ss;
+    if (p.ssq) {
+      // x1 = f32(cur + bf16(y)) of the folded RMSNorm, squared (exact in fp64): a wavefront's 64
+      // lanes are the tile's 64 rows of one batch row (kTM = 64, t = 64 w + lane), so the tile's
+      // sum is a wavefront sum in wave_sum_d's fixed order
+      const float x1 = bf16_to_f32(cur) + bf16_to_f32(f64_to_bf16(a[0]));
+      const double ss = wave_sum_d((double)x1 * (double)x1);
+      if (lane == 0) p.ssq[(size_t)blockIdx.x * kBN + b] = ss;
     }
   }
   if (tid == 0) __hip_atomic_store(p.ctr + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
