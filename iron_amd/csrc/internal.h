@@ -76,7 +76,8 @@ size_t gemm_workspace_bound(int M, bool dual);
 // The MLP's residual RMSNorm folded into the GEMM pair around it (hf = f32((x1 * inv_rms(x1)) *
 // w), x1 = f32(cur + a), a = bf16(Wo . cx)). The producer (Wo: bf16 epilogue, split K) also
 // writes, for each of its 64-row tiles and each batch row, the fp64 sum of x1^2 over the tile's
-// rows, in row order, to ssq [D / 64][16]. The consumer (gate/up, register-streamed form) sums a
+// rows (a fixed-order wavefront sum) to ssq [D / 64][16]. The consumer (gate/up, register-
+// streamed form) sums a
 // batch row's D / 64 tile sums in a fixed order and stages hf's three bf16 planes from cur, a and
 // w chunk by chunk, where it otherwise reads the planes a separate kernel wrote.
 struct GemmResNorm {
