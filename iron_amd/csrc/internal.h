@@ -70,16 +70,12 @@ int gemm_check(const char* fn, int B, int M, int K, int G);
 constexpr size_t kGemmCtrBytes = 16384;
 // Bytes of fp64 split-K partials a GEMM of M rows needs, over every K.
 size_t gemm_workspace_bound(int M, bool dual);
-// x: bf16 [B][x_stride], or (x_plane > 0) an fp32 activation as three exact bf16 planes
-// [3][B][x_stride] with plane stride x_plane elements. y_plane: the plane stride of the planes
-// epilogue's output.
 // The MLP's residual RMSNorm folded into the GEMM pair around it (hf = f32((x1 * inv_rms(x1)) *
 // w), x1 = f32(cur + a), a = bf16(Wo . cx)). The producer (Wo: bf16 epilogue, split K) also
 // writes, for each of its 64-row tiles and each batch row, the fp64 sum of x1^2 over the tile's
-// rows (a fixed-order wavefront sum) to ssq [D / 64][16]. The consumer (gate/up, register-
-// streamed form) sums a
-// batch row's D / 64 tile sums in a fixed order and stages hf's three bf16 planes from cur, a and
-// w chunk by chunk, where it otherwise reads the planes a separate kernel wrote.
+// rows (a fixed-order wavefront sum) to ssq [D / 64][16]. The consumer (gate/up, register-streamed
+// form) sums a batch row's D / 64 tile sums in a fixed order and stages hf's three bf16 planes
+// from cur, a and w chunk by chunk, where it otherwise reads the planes a separate kernel wrote.
 struct GemmResNorm {
   double* ssq;
   const uint16_t* cur;  // [B][D]
@@ -91,6 +87,9 @@ struct GemmResNorm {
 // Whether the fold applies to an MLP of these shapes: the producer splits K (its last split sums
 // a tile's outputs) and the consumer runs the register-streamed form.
 bool gemm_resnorm_foldable(int D, int QD, int FF);
+// x: bf16 [B][x_stride], or (x_plane > 0) an fp32 activation as three exact bf16 planes
+// [3][B][x_stride] with plane stride x_plane elements. y_plane: the plane stride of the planes
+// epilogue's output. rn: the folded RMSNorm's producer or consumer side, or null.
 int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile_m, int domain,
                    const uint16_t* x, size_t x_plane, int B, int x_stride, int epi, void* y,
                    int y_stride, size_t y_plane, const uint16_t* r1, const uint16_t* r2,
