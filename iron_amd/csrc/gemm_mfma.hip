@@ -112,13 +112,25 @@ IRON_DEV bf16x8 u8_to_bf16q(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
-template <bool DUAL, bool XPL>
+// NORM: x is the residual RMSNorm's hf (iron::GemmResNorm without tile sums). Every workgroup
+// sums x1^2 over each whole batch row (2 B x K bf16 from the L2), then writes hf's three planes
+// for its split's K range (at most kNormSteps steps) into LDS once, from cur (r1), a (r2) and the
+// norm weight (n_w); the step loop then loads and stages weights only. Staging the planes step by
+// step instead, between the step's loads and its barrier, measured 2-4 us slower on config 2.
+constexpr int kNormSteps = 4;
+constexpr int kHRow = kNormSteps * kKS + 8;  // bf16 per plane row of hf (padded like s_x's rows)
+template <bool DUAL, bool XPL, bool NORM = false>
 __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
+  static_assert(!NORM || (DUAL && XPL), "the residual RMSNorm feeds the dual GEMM's fp32 planes");
   constexpr int NM = DUAL ? 2 : 1;
   constexpr int NX = XPL ? 3 : 1;    // bf16 planes of x (fp32 x: hi, mid, lo)
   __shared__ __align__(16) uint8_t s_w[2][NM][kTM][kWRow];
   __shared__ __align__(16) uint16_t s_s[2][NM][kTM][kKS / 32];
   __shared__ __align__(16) uint16_t s_x[2][NX][kBN][kXRow];
+  // NORM: hf's planes [3][B][kHRow] in the launch's dynamic LDS (B rows only: at B <= 8 two
+  // workgroups fit on a CU)
+  extern __shared__ __align__(16) uint16_t s_hf[];
+  __shared__ double s_inv[kBN];
   // the upper half's sums at the end, in the weight tiles' space past the split-K staging (s_part
   // below): 16 KiB less LDS, so two dual workgroups fit on a CU (measured neutral: the kernel is
   // bound by its issue, not its occupancy)
@@ -173,8 +185,8 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
       wb0 = *(const uint4*)(wsrc1 + k0_ + lpart * 16);                                         \
       sb = ssrc1[gi_];                                                                         \
     }                                                                                          \
-    rx0 = *(const uint4*)(p.x + xrow + k0_ + xk);                                              \
-    if (XPL) {                                                                                 \
+    if (!NORM) rx0 = *(const uint4*)(p.x + xrow + k0_ + xk);                                   \
+    if (XPL && !NORM) {                                                                        \
       rx1 = *(const uint4*)(p.x + p.x_plane + xrow + k0_ + xk);                                \
       rx2 = *(const uint4*)(p.x + 2 * p.x_plane + xrow + k0_ + xk);                            \
     }                                                                                          \
@@ -187,7 +199,7 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
       *(uint4*)&s_w[(buf_)][NM - 1][lrow][lpart * 16] = wb0;                                   \
       if (lpart < kKS / 32) s_s[(buf_)][NM - 1][lrow][lpart] = (uint16_t)sb;                   \
     }                                                                                          \
-    if (tid < 256) {                                                                           \
+    if (!NORM && tid < 256) {                                                                  \
       *(uint4*)&s_x[(buf_)][0][xb][xk] = xb < p.B ? rx0 : make_uint4(0u, 0u, 0u, 0u);          \
       if (XPL) {                                                                               \
         *(uint4*)&s_x[(buf_)][NX - 2][xb][xk] = xb < p.B ? rx1 : make_uint4(0u, 0u, 0u, 0u);   \
@@ -211,8 +223,97 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
   const int kq = (lane >> 4) * 8;                // k offset of this lane in a 32-step
   const int bcol = lane & 15;                    // B operand / C column (batch)
   const int crow = wrow + (lane >> 4) * 4;       // first C row
+  // NORM: the plane row of this lane's batch column (columns past B read row 0; their outputs are
+  // never stored)
+  const int hrow = bcol < p.B ? bcol : 0;
 
   GEMM_GLOAD(step0);
+  if constexpr (NORM) {
+    // the split's pieces of cur, a and the norm weight (8 elements each, at most two per thread:
+    // B x nsteps x 16 <= 1024), loaded together with the row sums' inputs below
+    const int n8 = nsteps * (kKS / 8);  // 8-element pieces per row
+    const int kb = step0 * kKS;
+    uint4 hc[2], ha[2], hw[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + 512 * u, b = i / n8, c = (i - b * n8) * 8;
+      if (i < p.B * n8) {
+        const size_t o = (size_t)b * p.x_stride + kb + c;
+        hc[u] = *(const uint4*)(p.r1 + o);
+        ha[u] = *(const uint4*)(p.r2 + o);
+        hw[u] = *(const uint4*)(p.n_w + kb + c);
+      }
+    }
+    // 1 / RMS of every batch row over the whole of x1 = f32(cur + a) (K = D elements): wavefront
+    // w sums rows w and w + 8, each lane 8 elements of every 512, all of a round's loads in flight
+    // together. The squares and their fp64 sums are exact (see sum_sq_tree), so this order gives
+    // the separate kernel's value.
+    for (int b = __builtin_amdgcn_readfirstlane(wave); b < p.B; b += 8) {
+      const uint16_t* cr = p.r1 + (size_t)b * p.x_stride;
+      const uint16_t* ar = p.r2 + (size_t)b * p.x_stride;
+      double sq[4] = {0.0, 0.0, 0.0, 0.0};
+      for (int k0 = lane * 8; k0 < p.K; k0 += 2048) {
+        uint4 c4[4], a4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int k = k0 + 512 * q;
+          c4[q] = k < p.K ? *(const uint4*)(cr + k) : make_uint4(0u, 0u, 0u, 0u);
+          a4[q] = k < p.K ? *(const uint4*)(ar + k) : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t cw[4] = {c4[q].x, c4[q].y, c4[q].z, c4[q].w};
+          const uint32_t aw[4] = {a4[q].x, a4[q].y, a4[q].z, a4[q].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float lo = __uint_as_float(cw[e] << 16) + __uint_as_float(aw[e] << 16);
+            const float hi = __uint_as_float(cw[e] & 0xffff0000u) +
+                             __uint_as_float(aw[e] & 0xffff0000u);
+            sq[e] = fma((double)lo, (double)lo, sq[e]);
+            sq[e] = fma((double)hi, (double)hi, sq[e]);
+          }
+        }
+      }
+      const double ss = wave_sum_d((sq[0] + sq[1]) + (sq[2] + sq[3]));
+      if (lane == 0) s_inv[b] = inv_rms(ss, p.K, (double)p.n_eps);
+    }
+    __syncthreads();
+    // hf = f32((f32(cur + a) * inv) * w), evaluated in fp64 (the separate kernel's roundings),
+    // as three exact bf16 planes over the split's K range
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + 512 * u, b = i / n8, c = (i - b * n8) * 8;
+      if (i >= p.B * n8) break;
+      uint4 pl[3];
+      {
+        const uint4 c4 = hc[u], a4 = ha[u], w4 = hw[u];
+        const double inv = s_inv[b];
+        const uint32_t cw[4] = {c4.x, c4.y, c4.z, c4.w}, aw[4] = {a4.x, a4.y, a4.z, a4.w};
+        const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
+        uint32_t pw[3][4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          uint16_t h[2][3];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            auto el = [&](uint32_t d) {
+              return __uint_as_float(hh ? (d & 0xffff0000u) : (d << 16));
+            };
+            const float x1 = el(cw[e]) + el(aw[e]);
+            const double y = ((double)x1 * inv) * (double)el(ww[e]);
+            split3_bf16((float)y, h[hh][0], h[hh][1], h[hh][2]);
+          }
+#pragma unroll
+          for (int xi = 0; xi < 3; ++xi)
+            pw[xi][e] = (uint32_t)h[0][xi] | ((uint32_t)h[1][xi] << 16);
+        }
+#pragma unroll
+        for (int xi = 0; xi < 3; ++xi) pl[xi] = make_uint4(pw[xi][0], pw[xi][1], pw[xi][2], pw[xi][3]);
+      }
+#pragma unroll
+      for (int xi = 0; xi < 3; ++xi) *(uint4*)&s_hf[(xi * p.B + b) * kHRow + c] = pl[xi];
+    }
+  }
   GEMM_LSTORE(0);
   __syncthreads();
   for (int it = 0; it < nsteps; ++it) {
@@ -227,7 +328,9 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
       bf16x8 bx[NX];
 #pragma unroll
       for (int xi = 0; xi < NX; ++xi)
-        bx[xi] = __builtin_bit_cast(bf16x8, *(const uint4*)&s_x[buf][xi][bcol][32 * j + kq]);
+        bx[xi] = __builtin_bit_cast(
+            bf16x8, NORM ? *(const uint4*)&s_hf[(xi * p.B + hrow) * kHRow + it * kKS + 32 * j + kq]
+                         : *(const uint4*)&s_x[buf][xi][bcol][32 * j + kq]);
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) {
         const uint2 qa = *(const uint2*)&s_w[buf][mi][arow][32 * j + kq];
@@ -864,6 +967,14 @@ bool gemm_resnorm_foldable(int D, int QD, int FF) {
   return !po.rs && po.splits > 1 && pg.rs;
 }
 
+bool gemm_selfnorm_foldable(int B, int D, int FF) {
+  // up to 8 batch rows: the planes' LDS then leaves room for two workgroups per CU (config 2:
+  // B = 5 31.6 -> 30.6 us, B = 8 32.4 -> 31.9 us; at B = 16, one workgroup per CU, 37.7 -> 43.5)
+  if (B < 1 || B > 8 || D <= 0 || FF <= 0 || D % kKS || FF % kTM) return false;
+  const GemmPlan pg = plan_gemm(FF, D, true);
+  return !pg.rs && pg.ksteps <= kNormSteps;
+}
+
 int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile_m, int domain,
                    const uint16_t* x, size_t x_plane, int B, int x_stride, int epi, void* y,
                    int y_stride, size_t y_plane, const uint16_t* r1, const uint16_t* r2,
@@ -875,11 +986,17 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
   const GemmPlan pl = plan_gemm(M, K, dual);
   // the folded residual RMSNorm: the producer (no a) splits K and has the bf16 epilogue; the
   // consumer is the register-streamed dual GEMM over the norm's D
-  const bool rn_prod = rn && !rn->a, rn_cons = rn && rn->a;
-  if (rn && (!rn->ssq || !rn->cur || !aligned(rn->ssq, 8) ||
+  // consumer; without tile sums, the staged dual GEMM of at most kNormSteps steps per split sums
+  // each batch row itself
+  const bool rn_self = rn && !rn->ssq;
+  const bool rn_prod = rn && rn->ssq && !rn->a, rn_cons = rn && rn->ssq && rn->a;
+  if (rn && (!rn->cur || !aligned(rn->ssq, 8) ||
              (rn_prod && (pl.rs || pl.splits < 2 || epi != GEMM_EPI_BF16 || M != rn->D)) ||
              (rn_cons && (!pl.rs || !dual || !rn->w || K != rn->D || rn->D % kTM ||
-                          rn->D / kTM > 32 * 4))))
+                          rn->D / kTM > 32 * 4)) ||
+             (rn_self && (pl.rs || pl.ksteps > kNormSteps || !dual || !rn->a || !rn->w ||
+                          K != rn->D || !aligned(rn->cur, 16) || !aligned(rn->a, 16) ||
+                          !aligned(rn->w, 16)))))
     return fail(IRON_ERR_UNSUPPORTED, "%s: the folded RMSNorm does not fit this GEMM plan", fn);
   GemmParams p = {};
   p.w0 = (const uint8_t*)w0;
@@ -909,7 +1026,7 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
     p.ssq = rn->ssq;
     p.r1 = rn->cur;
     p.r_stride = rn->D;
-  } else if (rn_cons) {
+  } else if (rn_cons || rn_self) {
     p.ssq = rn->ssq;
     p.r1 = rn->cur;
     p.r2 = rn->a;
@@ -954,7 +1071,10 @@ int gemm_w8_launch(const void* w0, const void* w1, int M, int K, int G, int tile
     return check_launch(fn);
   }
   dim3 grid(M / kTM, pl.splits);
-  if (dual) {
+  if (rn_self) {
+    hipLaunchKernelGGL((gemm_w8_mfma_kernel<true, true, true>), grid, dim3(512),
+                       (size_t)3 * B * kHRow * sizeof(uint16_t), stream, p);
+  } else if (dual) {
     if (x_f32) hipLaunchKernelGGL((gemm_w8_mfma_kernel<true, true>), grid, dim3(512), 0, stream, p);
     else hipLaunchKernelGGL((gemm_w8_mfma_kernel<true, false>), grid, dim3(512), 0, stream, p);
   } else {

@@ -84,9 +84,14 @@ struct GemmResNorm {
   int D;
   float eps;
 };
+// ssq null: no producer; the consumer (gate/up, staged form, at most 4 steps per split, B <= 8)
+// sums x1^2 over each whole batch row in every workgroup and stages hf's planes for its K range
+// once.
 // Whether the fold applies to an MLP of these shapes: the producer splits K (its last split sums
 // a tile's outputs) and the consumer runs the register-streamed form.
 bool gemm_resnorm_foldable(int D, int QD, int FF);
+// Whether the consumer-only fold (no tile sums) applies to the gate/up GEMM of these shapes.
+bool gemm_selfnorm_foldable(int B, int D, int FF);
 // x: bf16 [B][x_stride], or (x_plane > 0) an fp32 activation as three exact bf16 planes
 // [3][B][x_stride] with plane stride x_plane elements. y_plane: the plane stride of the planes
 // epilogue's output. rn: the folded RMSNorm's producer or consumer side, or null.

@@ -80,9 +80,10 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
   char* const base = (char*)workspace + iron::kGemmCtrBytes;
   workspace_bytes -= iron::kGemmCtrBytes;
   if (B > iron::kGemvMaxBatch) {
-    // MFMA path: the prologue (x1 = cur + a, hf = RMSNorm(x1) * n_pf in fp32) runs once per
-    // row in its own kernel, or (with Wo, when the plans allow) folds into Wo's epilogue and the
-    // gate/up GEMM's staging; then the GEMMs with the SwiGLU / residual epilogues
+    // MFMA path: the prologue (x1 = cur + a, hf = RMSNorm(x1) * n_pf in fp32) folds into Wo's
+    // epilogue and the gate/up GEMM's staging (with Wo, when the plans allow), or into the
+    // staged gate/up GEMM alone, or runs once per row in its own kernel; then the GEMMs with the
+    // SwiGLU / residual epilogues
     if ((st = iron::gemm_check(fn, B, FF, D, G)) || (st = iron::gemm_check(fn, B, D, FF, G)))
       return st;
     if (wo && (st = iron::gemm_check(fn, B, D, QD, G))) return st;
@@ -109,6 +110,12 @@ int iron_swiglu_mlp(const uint16_t* cur, const uint16_t* cx_or_a, const uint16_t
       st = iron::gemm_w8_launch(wg, wu, FF, D, G, tile_m_gu, domain, nullptr, 0, B, D,
                                 iron::GEMM_EPI_SWIGLU_PLANES, gh, FF, (size_t)B * FF, nullptr,
                                 nullptr, 0, ctr, part, part_bytes, s, fn, &rn);
+    } else if (iron::gemm_selfnorm_foldable(B, D, FF)) {
+      // no producer to fold into: the gate/up GEMM sums each row's squares itself
+      const iron::GemmResNorm rs = {nullptr, cur, a, n_pf, D, eps};
+      st = iron::gemm_w8_launch(wg, wu, FF, D, G, tile_m_gu, domain, nullptr, 0, B, D,
+                                iron::GEMM_EPI_SWIGLU_PLANES, gh, FF, (size_t)B * FF, nullptr,
+                                nullptr, 0, ctr, part, part_bytes, s, fn, &rs);
     } else {
       st = iron::res_rmsnorm_planes_launch(cur, a, n_pf, hf, B, D, eps, s);
       if (st) return st;
