@@ -227,13 +227,25 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
   // never stored)
   const int hrow = bcol < p.B ? bcol : 0;
 
-  GEMM_GLOAD(step0);
+  // NORM: the row sums' inputs of the first 2048 elements of row `wave` and the split's pieces
+  // of cur, a and the norm weight are loaded ahead of the first step's weights, so that their
+  // wait does not include the weights' (the counts are in order)
+  const int n8 = nsteps * (kKS / 8);  // NORM: 8-element pieces per row of the split's K range
+  const int kb = step0 * kKS;
+  const int bw = __builtin_amdgcn_readfirstlane(wave);
+  uint4 hc[2], ha[2], hw[2], rc[4], ra[4];
+  auto load_round = [&](int b, int k0, uint4 (&c4)[4], uint4 (&a4)[4]) __attribute__((always_inline)) {
+    const uint16_t* cr = p.r1 + (size_t)b * p.x_stride;
+    const uint16_t* ar = p.r2 + (size_t)b * p.x_stride;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int k = k0 + 512 * q;
+      c4[q] = k < p.K ? *(const uint4*)(cr + k) : make_uint4(0u, 0u, 0u, 0u);
+      a4[q] = k < p.K ? *(const uint4*)(ar + k) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
   if constexpr (NORM) {
-    // the split's pieces of cur, a and the norm weight (8 elements each, at most two per thread:
-    // B x nsteps x 16 <= 1024), loaded together with the row sums' inputs below
-    const int n8 = nsteps * (kKS / 8);  // 8-element pieces per row
-    const int kb = step0 * kKS;
-    uint4 hc[2], ha[2], hw[2];
+    // the split's pieces (8 elements each, at most two per thread: B x nsteps x 16 <= 1024)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int i = tid + 512 * u, b = i / n8, c = (i - b * n8) * 8;
@@ -244,22 +256,17 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
         hw[u] = *(const uint4*)(p.n_w + kb + c);
       }
     }
+    if (bw < p.B) load_round(bw, lane * 8, rc, ra);
+  }
+  GEMM_GLOAD(step0);
+  if constexpr (NORM) {
     // 1 / RMS of every batch row over the whole of x1 = f32(cur + a) (K = D elements): wavefront
-    // w sums rows w and w + 8, each lane 8 elements of every 512, all of a round's loads in flight
-    // together. The squares and their fp64 sums are exact (see sum_sq_tree), so this order gives
-    // the separate kernel's value.
-    for (int b = __builtin_amdgcn_readfirstlane(wave); b < p.B; b += 8) {
-      const uint16_t* cr = p.r1 + (size_t)b * p.x_stride;
-      const uint16_t* ar = p.r2 + (size_t)b * p.x_stride;
+    // w sums rows w and w + 8, each lane 8 elements of every 512, a round of 2048 elements'
+    // loads in flight together. The squares and their fp64 sums are exact (see sum_sq_tree), so
+    // this order gives the separate kernel's value.
+    for (int b = bw; b < p.B; b += 8) {
       double sq[4] = {0.0, 0.0, 0.0, 0.0};
-      for (int k0 = lane * 8; k0 < p.K; k0 += 2048) {
-        uint4 c4[4], a4[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int k = k0 + 512 * q;
-          c4[q] = k < p.K ? *(const uint4*)(cr + k) : make_uint4(0u, 0u, 0u, 0u);
-          a4[q] = k < p.K ? *(const uint4*)(ar + k) : make_uint4(0u, 0u, 0u, 0u);
-        }
+      auto accum = [&](const uint4 (&c4)[4], const uint4 (&a4)[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t cw[4] = {c4[q].x, c4[q].y, c4[q].z, c4[q].w};
@@ -273,6 +280,18 @@ __global__ __launch_bounds__(512) void gemm_w8_mfma_kernel(GemmParams p) {
             sq[e] = fma((double)hi, (double)hi, sq[e]);
           }
         }
+      };
+      if (b == bw) {
+        accum(rc, ra);
+      } else {
+        uint4 c4[4], a4[4];
+        load_round(b, lane * 8, c4, a4);
+        accum(c4, a4);
+      }
+      for (int k0 = lane * 8 + 2048; k0 < p.K; k0 += 2048) {
+        uint4 c4[4], a4[4];
+        load_round(b, k0, c4, a4);
+        accum(c4, a4);
       }
       const double ss = wave_sum_d((sq[0] + sq[1]) + (sq[2] + sq[3]));
       if (lane == 0) s_inv[b] = inv_rms(ss, p.K, (double)p.n_eps);
